@@ -1,0 +1,218 @@
+"""Benchmark: gpt-oss-120B-shape MoE layer decode on one MI355X.
+
+Workload: one MoE layer, hidden = intermediate = 2880, 128 MXFP4 experts,
+top-4, router 2880 -> 128, executor-default float32 expert matmuls, bf16
+activations ~ N(0, 1), seeded synthetic weights (codes uniform, E8M0 scales
+uniform in 118..124).  A step is one layer forward over one batch of B tokens
+(router -> top-k/softmax -> dispatch -> gate_up + SwiGLU -> down -> combine),
+inputs already resident in HBM.  Steps rotate over --layers independent
+layers (1.69 GB of packed experts each), so expert bytes come from HBM and not
+from a cache left warm by the previous step.
+
+Prints one JSON line.  ``value`` is microseconds per token at the headline
+batch (64); ``per_batch`` holds B = 1, 8, 64.  ``roofline`` is for the
+dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
+experts the batch touches + activations in + SwiGLU output) over its average
+duration measured with HIP events recorded by the library between its
+kernels, in a second timed pass over the same steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "kcapw-klcquant_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HIDDEN = 2880
+INTER = 2880
+EXPERTS = 128
+TOPK = 4
+WORKLOAD = 2  # seed namespace of the 120B-shape decode workload
+HBM_PEAK_GBPS = 8000.0
+GATE_UP_EXPERT_BYTES = 2 * INTER * (HIDDEN // 32) * 17  # 8,812,800: codes + E8M0 scales
+DOWN_EXPERT_BYTES = HIDDEN * (INTER // 32) * 17  # 4,406,400
+KERNELS = ["router_logits", "topk_softmax", "dispatch", "gate_up", "down", "combine"]
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batches", default="1,8,64")
+    ap.add_argument("--headline-batch", type=int, default=64)
+    ap.add_argument("--layers", type=int, default=8, help="independent layers the steps rotate over")
+    ap.add_argument("--inputs", type=int, default=16, help="distinct input batches the steps rotate over")
+    ap.add_argument("--cpu-tokens", type=int, default=6, help="tokens in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16"])
+    return ap.parse_args()
+
+
+def layer_bytes(unique_experts: int, n_tok: int) -> int:
+    """Algorithmic HBM bytes of one layer step."""
+    weights = unique_experts * (GATE_UP_EXPERT_BYTES + DOWN_EXPERT_BYTES)
+    biases = unique_experts * (2 * INTER + HIDDEN) * 2
+    router = EXPERTS * HIDDEN * 2 + EXPERTS * 2
+    acts = n_tok * HIDDEN * 2 * 2  # hidden in, output out (bf16)
+    return weights + biases + router + acts
+
+
+def gate_up_bytes(unique_experts: int, n_tok: int) -> int:
+    """Algorithmic bytes of one gate_up launch: weights + bias + fp32 activations + fp32 SwiGLU output."""
+    return (unique_experts * (GATE_UP_EXPERT_BYTES + 2 * INTER * 2) + n_tok * HIDDEN * 4
+            + n_tok * TOPK * INTER * 4)
+
+
+def cpu_baseline(n_tokens: int) -> dict:
+    """The oracle (numpy port of the reference path) on single-token route calls."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from klcquant import moe
+    from oracle import layer as olayer
+
+    host = moe.synthetic_host_layer(WORKLOAD, 0, HIDDEN, INTER, EXPERTS)
+    xs = moe.synthetic_hidden(WORKLOAD, n_tokens, HIDDEN, step=12345)
+    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    t0 = time.perf_counter()
+    for i in range(n_tokens):
+        olayer.moe_layer(xs[i:i + 1], host["router_weight"], host["router_bias"], host["gate_up_blocks"],
+                         host["gate_up_scales"], host["gate_up_bias"], host["down_blocks"], host["down_scales"],
+                         host["down_bias"], k=TOPK)
+    dt = time.perf_counter() - t0
+    del host
+    return {
+        "value": round(dt / n_tokens * 1e6, 1),
+        "unit": "us/token",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"{n_tokens} single-token route() calls (B=1, as the reference routes one token per call) "
+                   "through the numpy oracle: router, top-4, then each selected expert dequantized from MXFP4 "
+                   "and applied in float32 math, same 120B-shape layer"),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    from klcquant import _native, moe
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    _native.load()
+    dev = torch.device("cuda:0")
+    batches = [int(b) for b in args.batches.split(",") if b]
+    print(f"[bench] building {args.layers} layers of {EXPERTS} experts on {torch.cuda.get_device_name(0)}",
+          file=sys.stderr, flush=True)
+    layers = [moe.MoELayer(moe.MoELayerWeights.synthetic(WORKLOAD, l, HIDDEN, INTER, EXPERTS, dev), TOPK, 7.0,
+                           args.precision) for l in range(args.layers)]
+    torch.cuda.synchronize()
+
+    per_batch = []
+    for n_tok in batches:
+        xs = [torch.from_numpy(moe.synthetic_hidden(WORKLOAD, n_tok, HIDDEN, step=s).view(np.int16))
+              .view(torch.bfloat16).to(dev) for s in range(args.inputs)]
+        out = torch.empty((n_tok, HIDDEN), dtype=torch.bfloat16, device=dev)
+        ids = torch.empty((args.steps, n_tok, TOPK), dtype=torch.int32, device=dev)
+        for s in range(args.warmup):
+            layers[s % args.layers].forward(xs[s % args.inputs], out=out)
+        torch.cuda.synchronize()
+        # pass 1: the headline timing, no events between kernels
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            layers[s % args.layers].forward(xs[s % args.inputs], out=out, ids=ids[s])
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        # pass 2: same steps with events around each kernel
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(_native.LAYER_EVENTS)] for _ in range(args.steps)]
+        for row in evs:
+            for e in row:
+                e.record()
+        torch.cuda.synchronize()
+        for s in range(args.steps):
+            layers[s % args.layers].forward(xs[s % args.inputs], out=out, events=evs[s])
+        torch.cuda.synchronize()
+        kern_ms = np.array([[evs[s][i].elapsed_time(evs[s][i + 1]) for i in range(len(KERNELS))]
+                            for s in range(args.steps)])
+        ids_np = ids.cpu().numpy()
+        uniq = np.array([len(np.unique(ids_np[s])) for s in range(args.steps)])
+        ms_step = dt * 1e3 / args.steps
+        bytes_total = float(sum(layer_bytes(int(u), n_tok) for u in uniq))
+        gu_bytes = float(sum(gate_up_bytes(int(u), n_tok) for u in uniq))
+        gu_ms = float(kern_ms[:, 3].sum())
+        rec = {
+            "batch": n_tok,
+            "us_per_token": round(ms_step * 1e3 / n_tok, 3),
+            "us_per_step": round(ms_step * 1e3, 3),
+            "tokens_per_s": round(n_tok / (ms_step * 1e-3), 1),
+            "unique_experts_mean": round(float(uniq.mean()), 2),
+            "layer_hbm_gbps": round(bytes_total / (dt * 1e9 / 1.0) / 1.0, 1),
+            "layer_frac_of_peak": round(bytes_total / dt / 1e9 / HBM_PEAK_GBPS, 4),
+            "kernel_us_mean": {k: round(float(kern_ms[:, i].mean()) * 1e3, 3) for i, k in enumerate(KERNELS)},
+            "gate_up_gbps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+        }
+        per_batch.append(rec)
+        print(f"[bench] B={n_tok}: {rec['us_per_step']} us/step, {rec['us_per_token']} us/token, "
+              f"{rec['layer_hbm_gbps']} GB/s layer, gate_up {rec['gate_up_gbps']} GB/s, "
+              f"kernels {rec['kernel_us_mean']}", file=sys.stderr, flush=True)
+
+    head = next((r for r in per_batch if r["batch"] == args.headline_batch), per_batch[-1])
+    gu_achieved = head["gate_up_gbps"]
+    result = {
+        "metric": "MoE layer us/token & HBM GB/s (% of peak), 120B shape, batch 1-64",
+        "value": head["us_per_token"],
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_step"] / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "gpt-oss-120B-shape MoE layer decode: H=I=2880, 128 MXFP4 experts, top-4, fp32 expert math",
+            "global_batch": head["batch"],
+            "batches": batches,
+            "layers_rotated": args.layers,
+            "precision": args.precision,
+            "parallelism": "single GPU",
+        },
+        "hbm_gbps": head["layer_hbm_gbps"],
+        "hbm_frac_of_peak": head["layer_frac_of_peak"],
+        "per_batch": per_batch,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "moe_gemv_kernel<gate_up>",
+            "achieved": gu_achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gu_achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+        },
+    }
+    if args.cpu_tokens > 0:
+        print(f"[bench] CPU baseline: {args.cpu_tokens} tokens through the oracle", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,178 @@
+/*
+ * klc_moe.h — C ABI of the MI355X (gfx950) MoE expert path.
+ *
+ * The reference (KLCquant) is pure Python on PyTorch: its "interface" for this
+ * path is the Python API of mxfp4_expert.py and streamed_moe_router.py, and
+ * there is no FFI.  Each entry point below replaces the torch-eager code at
+ * the cited reference lines; the Python package `klcquant` (mxfp4_expert.py,
+ * streamed_moe_router.py) binds these through ctypes and keeps the reference's
+ * Python signatures.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise.
+ *   - bfloat16 data is passed as 16-bit patterns (uint16_t), float32 as float.
+ *   - Nothing here allocates device memory: outputs and scratch are passed in.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
+ *     is asynchronous; calls are stream-ordered and thread-safe (state is per
+ *     call, the error message is per calling thread).
+ *   - Return value: KLC_OK (0) or a negative KLC_ERR_* code; klc_last_error()
+ *     then describes the failure.  Argument checks happen before any launch.
+ */
+#ifndef KLC_MOE_H_
+#define KLC_MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KLC_ABI_VERSION 1
+
+#define KLC_OK 0
+#define KLC_ERR_ARGUMENT (-1)    /* null pointer or non-positive size */
+#define KLC_ERR_SHAPE (-2)       /* a shape constraint is violated */
+#define KLC_ERR_UNSUPPORTED (-3) /* valid but unsupported configuration */
+#define KLC_ERR_HIP (-4)         /* HIP launch / runtime error */
+
+#define KLC_DTYPE_BF16 0
+#define KLC_DTYPE_F16 1
+#define KLC_DTYPE_F32 2
+
+#define KLC_PRECISION_FP32 0 /* expert_matmul_precision="fp32" */
+#define KLC_PRECISION_BF16 1 /* expert_matmul_precision="bf16" */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* klc_last_error(void);
+/* KLC_ABI_VERSION of the built library. */
+int klc_abi_version(void);
+
+/* ---- MXFP4 weights --------------------------------------------------------
+ * Checkpoint layout (gpt-oss safetensors, read at mxfp4_expert.py:481-486):
+ *   blocks[n_mat][out_dim][groups][16] uint8  (low nibble = even input column)
+ *   scales[n_mat][out_dim][groups]     uint8  (E8M0, bias 127)
+ */
+
+/* Replaces dequantize_mxfp4_matrix (mxfp4_expert.py:357-379) for a batch of
+ * n_mat matrices: writes out[n_mat][groups*32][out_dim] (the transposed
+ * [in, out] layout) in out_dtype (KLC_DTYPE_*).  Bit-exact with torch.ldexp's
+ * float32 product rounded to the dtype, including +-0, subnormals, +-inf and
+ * the NaN of a zero code at scale 255. */
+int klc_mxfp4_dequant(const void* blocks, const void* scales, void* out, int64_t n_mat, int64_t out_dim,
+                      int64_t groups, int out_dtype, void* stream);
+
+/* Bytes of one matrix in the packed row-tile layout consumed by the expert
+ * kernels (out_dim must be a multiple of 64); negative on bad arguments. */
+int64_t klc_mxfp4_packed_bytes(int64_t out_dim, int64_t groups);
+
+/* Repacks checkpoint-layout matrices into the row-tile layout, matrix i at
+ * packed + i * klc_mxfp4_packed_bytes(out_dim, groups).  Replaces the
+ * host-side staging of _materialize_expert_matrix (mxfp4_expert.py:478-507),
+ * which keeps the packed bytes instead of a dequantized copy. */
+int klc_mxfp4_pack(const void* blocks, const void* scales, void* packed, int64_t n_mat, int64_t out_dim,
+                   int64_t groups, void* stream);
+
+/* dequantize_mxfp4_matrix (mxfp4_expert.py:357-379) applied to matrices held
+ * in the packed layout (as Mxfp4ExpertStore.load_expert_matrix returns them,
+ * mxfp4_expert.py:416-422); same output and semantics as klc_mxfp4_dequant. */
+int klc_mxfp4_dequant_packed(const void* packed, void* out, int64_t n_mat, int64_t out_dim, int64_t groups,
+                             int out_dtype, void* stream);
+
+/* ---- Router -------------------------------------------------------------- */
+
+/* Router logits, F.linear(hidden, W, b) in bfloat16
+ * (streamed_moe_router.py:268-269): x[n_tokens][hidden], w[n_experts][hidden],
+ * b[n_experts] bfloat16 -> logits[n_tokens][n_experts] bfloat16, computed as
+ * bf16(f32(x . w) + b) with the dot product accumulated in float64.  If x_f32
+ * is not NULL, also writes x as float32 [n_tokens][hidden] (the activation
+ * read by klc_moe_gate_up). */
+int klc_moe_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32,
+                          int64_t n_tokens, int64_t hidden, int64_t n_experts, void* stream);
+
+/* Top-k selection and routing weights (streamed_moe_router.py:270-284,
+ * 442-451, with routing locality disabled): per token, ids[t][j] (int32) of
+ * the k largest logits in descending order (NaN largest; equal values: lower
+ * expert index first), their float32 values, and weights = softmax over the
+ * k values rounded to bfloat16.  k <= 32, n_experts <= 1024. */
+int klc_moe_topk_softmax(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tokens,
+                         int64_t n_experts, int64_t k, void* stream);
+
+/* Expert-sorted dispatch (no reference counterpart: the reference routes one
+ * token per call, streamed_moe_router.py:499).  Pairs p = t*k + j are
+ * counting-sorted by expert, ties by p: offsets[n_experts+1],
+ * sorted_pairs[n_pairs], active[n_experts] (experts with >= 1 pair,
+ * ascending, then -1 padding) and *n_active.  n_experts <= 256. */
+int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
+                     int32_t* sorted_pairs, int32_t* active, int32_t* n_active, void* stream);
+
+/* ---- Experts ------------------------------------------------------------- */
+
+/* gate_up GEMV + bias + clamped SwiGLU for every routed pair
+ * (streamed_moe_router.py:500-506, 524-529).  w_gate_up is a device array of
+ * n_experts pointers to packed [2*inter rows][hidden/32 groups] matrices;
+ * bias is bfloat16 [n_experts][2*inter]; x_f32 is [n_tokens][hidden].
+ * Writes gated[n_pairs][inter] (the down input: rounded to bfloat16 under
+ * KLC_PRECISION_BF16) and, if gated_raw is not NULL, the unrounded SwiGLU
+ * output.  max_active bounds *n_active (normally min(n_experts, n_pairs)). */
+int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const float* x_f32, int64_t k,
+                    const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
+                    const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
+                    float swiglu_limit, int precision, float* gated, float* gated_raw, void* stream);
+
+/* down GEMV + bias (streamed_moe_router.py:507-511): w_down is a device array
+ * of n_experts pointers to packed [hidden rows][inter/32 groups] matrices;
+ * bias bfloat16 [n_experts][hidden]; gated [n_pairs][inter] ->
+ * expert_out[n_pairs][hidden] float32. */
+int klc_moe_down(const void* const* w_down, const void* bias, const float* gated, const int32_t* offsets,
+                 const int32_t* sorted_pairs, const int32_t* active, const int32_t* n_active, int64_t max_active,
+                 int64_t hidden, int64_t inter, int precision, float* expert_out, void* stream);
+
+/* Weighted combine in top-k order (streamed_moe_router.py:497, 512-513):
+ * out[t] = bf16 sum over j of bf16(bf16(expert_out[t*k+j]) * weights[t][j]),
+ * every step rounded to bfloat16. */
+int klc_moe_combine(const float* expert_out, const void* weights, int64_t n_tokens, int64_t k, int64_t hidden,
+                    void* out, void* stream);
+
+/* Bias-only fallback (streamed_moe_router.py:317-322):
+ * out[t] = bf16(sum_j bf16(down_bias[ids[t][j]] * weights[t][j])), float32 sum. */
+int klc_moe_bias_combine(const void* down_bias, const int32_t* ids, const void* weights, int64_t n_tokens,
+                         int64_t k, int64_t hidden, void* out, void* stream);
+
+/* L2 norms of the per-pair SwiGLU output and expert output, the expert_logs
+ * diagnostics of streamed_moe_router.py:518-519: norms[p] = {|gated[p]|,
+ * |expert_out[p]|}. */
+int klc_moe_pair_norms(const float* gated, const float* expert_out, int64_t n_pairs, int64_t inter,
+                       int64_t hidden, float* norms, void* stream);
+
+/* ---- One MoE layer --------------------------------------------------------- */
+
+/* Scratch bytes klc_moe_layer needs for n_tokens tokens. */
+int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k);
+
+/* One MoE layer for a batch of tokens — the route() + _execute_mxfp4_experts
+ * path (streamed_moe_router.py:257-315, 483-522) for every row of x:
+ * router logits -> top-k/softmax -> dispatch -> gate_up/SwiGLU -> down ->
+ * combine, all enqueued on `stream` with no host synchronisation.  Writes
+ * out[n_tokens][hidden] bfloat16; ids/weights (optional, may be NULL) receive
+ * the routing.  workspace must be 256-byte aligned and hold
+ * klc_moe_workspace_bytes() bytes.  events: optional host array of
+ * KLC_LAYER_EVENTS hipEvent_t handles recorded on `stream` before each of the
+ * six kernels and after the last (NULL: no events). */
+#define KLC_LAYER_EVENTS 7
+int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                  const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
+                  int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
+                  void* workspace, int64_t workspace_bytes, void* out, int32_t* ids, void* weights,
+                  void* const* events, void* stream);
+
+/* ---- Synthetic inputs -------------------------------------------------------
+ * Counter-based SplitMix64 stream, identical to klcquant/synth.py:
+ * mode 0: n random bytes; mode 1: n bytes uniform in [lo, hi]. */
+int klc_synth_fill(void* dst, int64_t n, uint64_t seed, int mode, int lo, int hi, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KLC_MOE_H_ */

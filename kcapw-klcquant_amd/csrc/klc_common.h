@@ -1,0 +1,92 @@
+// Shared device helpers and host error plumbing for the KLC MoE library (gfx950).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "klc_moe.h"
+
+namespace klc {
+
+// ---- host side -------------------------------------------------------------
+
+// Records a formatted message for klc_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Converts the last HIP launch error (if any) into a status.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define KLC_REQUIRE(cond, code, ...)                 \
+  do {                                               \
+    if (!(cond)) return ::klc::set_error((code), __VA_ARGS__); \
+  } while (0)
+
+constexpr int kWave = 64;
+
+// Packed ("row-tile") MXFP4 layout used by the expert GEMV kernels.  One
+// matrix of `rows` x `groups` MX blocks is stored as
+//   blocks: [rows / 64][groups][64 rows][16 bytes]
+//   scales: [rows / 64][ceil(groups / 4)][64 rows][4 bytes]   (byte g % 4)
+// so one wave-wide 16-byte load fetches group g of 64 consecutive rows as
+// 1 KiB of contiguous memory.
+constexpr int kTileRows = 64;
+inline int64_t packed_block_bytes(int64_t rows, int64_t groups) { return (rows / kTileRows) * groups * 1024; }
+inline int64_t packed_scale_bytes(int64_t rows, int64_t groups) {
+  return (rows / kTileRows) * ((groups + 3) / 4) * 256;
+}
+inline int64_t packed_matrix_bytes(int64_t rows, int64_t groups) {
+  return packed_block_bytes(rows, groups) + packed_scale_bytes(rows, groups);
+}
+
+// ---- device side -----------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// float32 -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
+
+// Exact float32 bit pattern of FP4_VALUES[code] * 2^(e - 127), as
+// torch.ldexp produces it in float32: +-inf on overflow, NaN for a zero code
+// with e = 255 (0 * inf), float32 subnormals for the smallest scales.
+// E2M1 magnitude m = code & 7 is (1 + f/2) * 2^q with q = (m >> 1) - 1 and
+// f = m & 1 for m >= 2; m = 1 is 0.5 (q = -1, f = 0).
+__device__ __forceinline__ uint32_t mxfp4_f32_bits(uint32_t code, uint32_t e) {
+  const uint32_t sign = (code & 8u) << 28;
+  const uint32_t m = code & 7u;
+  if (e == 255u) return m == 0u ? 0x7fc00000u : (sign | 0x7f800000u);
+  if (m == 0u) return sign;
+  const int q = (int)(m >> 1) - 1;
+  const uint32_t f = (m > 1u) ? (m & 1u) : 0u;
+  const int biased = q + (int)e;
+  if (biased >= 255) return sign | 0x7f800000u;
+  if (biased >= 1) return sign | ((uint32_t)biased << 23) | (f << 22);
+  // biased in {-1, 0}: subnormal, value (2 + f) * 2^(biased - 128) = mant * 2^-149
+  return sign | ((2u + f) << (biased + 21));
+}
+
+// 2^(e - 127) as float32 for an E8M0 byte (e = 255 -> NaN, the "no scale" code).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  if (e == 0u) return __uint_as_float(0x00400000u);
+  if (e == 255u) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float(e << 23);
+}
+
+// Two E2M1 codes of byte `sel` of `word` as float32 (low nibble first),
+// unscaled.  Uses gfx950's v_cvt_scalef32_pk_f32_fp4 with scale 1.0.
+template <int kSel>
+__device__ __forceinline__ float2 fp4x2_to_f32(uint32_t word) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  f2v v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, kSel);
+  return make_float2(v.x, v.y);
+}
+
+}  // namespace klc

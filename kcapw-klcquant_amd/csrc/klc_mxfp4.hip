@@ -1,0 +1,245 @@
+// MXFP4 -> dense dequant and checkpoint -> row-tile repack (gfx950).
+//
+// Dequant is HBM bound (1 byte of codes + 1/32 byte of scale in, 2 bytes out
+// per value for bfloat16), so the kernel is built around coalesced traffic:
+// a workgroup owns a strip of 64 output columns (64 checkpoint rows, i.e. a
+// contiguous 64 x groups x 16-byte region) and walks the input dimension in
+// chunks of 4 groups.  Packed bytes are staged in LDS, then every thread
+// decodes a 4 (input rows) x 8 (output columns) block and writes four 16-byte
+// rows, so each wave-wide store covers full 128-byte lines of the transposed
+// [in, out] output.  Values are built with integer arithmetic
+// (mxfp4_f32_bits), which is exact for every (code, scale) pair.
+#include "klc_common.h"
+
+namespace klc {
+namespace {
+
+constexpr int kDqThreads = 256;
+constexpr int kDqCols = 64;      // output columns (= checkpoint rows) per workgroup
+constexpr int kDqGroups = 4;     // MX groups (32 inputs each) per chunk
+constexpr int kLdsStride = 17;   // dwords per staged row: 16 data + 1 pad (bank spread)
+constexpr int kSclStride = 5;    // dwords per staged scale row
+
+// Converts one exact float32 bit pattern to the output dtype's bits.
+template <int kDtype>
+__device__ __forceinline__ uint32_t to_out_bits(uint32_t f32bits) {
+  if constexpr (kDtype == KLC_DTYPE_BF16) {
+    return f32bits >> 16;  // every finite MXFP4 value is exact in bfloat16
+  } else if constexpr (kDtype == KLC_DTYPE_F16) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(__uint_as_float(f32bits)));
+  } else {
+    return f32bits;
+  }
+}
+
+template <int kDtype, bool kPacked>
+__global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __restrict__ blocks,
+                                                             const uint8_t* __restrict__ scales,
+                                                             void* __restrict__ out, int rows, int groups,
+                                                             int64_t packed_stride) {
+  __shared__ uint32_t s_blk[kDqCols * kLdsStride];
+  __shared__ uint32_t s_scl[kDqCols * kSclStride];
+
+  const int strips = (rows + kDqCols - 1) / kDqCols;
+  const int m = blockIdx.x / strips;
+  const int col0 = (blockIdx.x - m * strips) * kDqCols;
+  const int tid = threadIdx.x;
+  const int in_dim = groups * 32;
+
+  // load mapping: one 16-byte chunk (row, gi) per thread
+  const int l_row = tid >> 2;
+  const int l_gi = tid & 3;
+  // compute mapping: 4 input rows x 8 output columns per thread
+  const int c_oc = tid & 7;
+  const int c_iq = tid >> 3;          // 0..31 quads of input rows
+  const int c_gi = c_iq >> 3;         // group within the chunk
+  const int c_q4 = c_iq & 7;          // quad within the group
+  const int col = col0 + c_oc * 8;
+
+  const uint8_t* mat = blocks;
+  int64_t scale_base = 0;
+  const int tiles = rows / kTileRows;
+  const int g4 = (groups + 3) >> 2;
+  if constexpr (kPacked) {
+    mat = blocks + (int64_t)m * packed_stride;
+    scale_base = (int64_t)tiles * groups * 1024;
+  }
+
+  for (int g0 = 0; g0 < groups; g0 += kDqGroups) {
+    const int ng = min(kDqGroups, groups - g0);
+    {
+      const int r = col0 + l_row;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      uint32_t e = 127u;
+      if (r < rows && l_gi < ng) {
+        const int g = g0 + l_gi;
+        if constexpr (kPacked) {
+          const uint8_t* src = mat + ((int64_t)(r / kTileRows) * groups + g) * 1024 + (r % kTileRows) * 16;
+          v = *reinterpret_cast<const uint4*>(src);
+          e = mat[scale_base + ((int64_t)(r / kTileRows) * g4 + (g >> 2)) * 256 + (r % kTileRows) * 4 + (g & 3)];
+        } else {
+          const int64_t chunk = ((int64_t)m * rows + r) * groups + g;
+          v = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
+          e = scales[chunk];
+        }
+      }
+      uint32_t* dst = s_blk + l_row * kLdsStride + l_gi * 4;
+      dst[0] = v.x;
+      dst[1] = v.y;
+      dst[2] = v.z;
+      dst[3] = v.w;
+      s_scl[l_row * kSclStride + l_gi] = e;
+    }
+    __syncthreads();
+
+    if (c_gi < ng) {
+      uint32_t bits[4][8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int lr = c_oc * 8 + j;
+        const uint32_t word = s_blk[lr * kLdsStride + c_gi * 4 + (c_q4 >> 1)];
+        const uint32_t v16 = (word >> ((c_q4 & 1) * 16)) & 0xffffu;
+        const uint32_t e = s_scl[lr * kSclStride + c_gi];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bits[r][j] = to_out_bits<kDtype>(mxfp4_f32_bits((v16 >> (4 * r)) & 0xfu, e));
+      }
+      const int i0 = (g0 + c_gi) * 32 + c_q4 * 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row_off = ((int64_t)m * in_dim + i0 + r) * rows;
+        if constexpr (kDtype == KLC_DTYPE_F32) {
+          float* o = static_cast<float*>(out) + row_off + col;
+          if (col + 8 <= rows && (rows & 3) == 0) {
+            reinterpret_cast<uint4*>(o)[0] = make_uint4(bits[r][0], bits[r][1], bits[r][2], bits[r][3]);
+            reinterpret_cast<uint4*>(o)[1] = make_uint4(bits[r][4], bits[r][5], bits[r][6], bits[r][7]);
+          } else {
+            for (int j = 0; j < 8; ++j)
+              if (col + j < rows) o[j] = __uint_as_float(bits[r][j]);
+          }
+        } else {
+          uint16_t* o = static_cast<uint16_t*>(out) + row_off + col;
+          if (col + 8 <= rows && (rows & 7) == 0) {
+            *reinterpret_cast<uint4*>(o) =
+                make_uint4(bits[r][0] | (bits[r][1] << 16), bits[r][2] | (bits[r][3] << 16),
+                           bits[r][4] | (bits[r][5] << 16), bits[r][6] | (bits[r][7] << 16));
+          } else {
+            for (int j = 0; j < 8; ++j)
+              if (col + j < rows) o[j] = (uint16_t)bits[r][j];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Checkpoint layout -> row-tile layout.  One thread per (matrix, tile, group
+// slot, row in tile); group slots run to ceil(groups/4)*4 so the scale padding
+// is written (as zero) too.  Writes are coalesced; this runs once per load.
+__global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ blocks,
+                                                   const uint8_t* __restrict__ scales, uint8_t* __restrict__ packed,
+                                                   int64_t n_mat, int rows, int groups, int64_t packed_stride) {
+  const int tiles = rows / kTileRows;
+  const int g4 = (groups + 3) >> 2;
+  const int gslots = g4 * 4;
+  const int64_t total = n_mat * tiles * gslots * kTileRows;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int rr = (int)(idx % kTileRows);
+    int64_t rest = idx / kTileRows;
+    const int g = (int)(rest % gslots);
+    rest /= gslots;
+    const int tile = (int)(rest % tiles);
+    const int64_t m = rest / tiles;
+    const int r = tile * kTileRows + rr;
+    uint8_t* base = packed + m * packed_stride;
+    uint8_t e = 0;
+    if (g < groups) {
+      const int64_t chunk = (m * rows + r) * groups + g;
+      const uint4 v = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
+      *reinterpret_cast<uint4*>(base + ((int64_t)tile * groups + g) * 1024 + rr * 16) = v;
+      e = scales[chunk];
+    }
+    base[(int64_t)tiles * groups * 1024 + ((int64_t)tile * g4 + (g >> 2)) * 256 + rr * 4 + (g & 3)] = e;
+  }
+}
+
+template <bool kPacked>
+int launch_dequant(const void* blocks, const void* scales, void* out, int64_t n_mat, int64_t rows, int64_t groups,
+                   int dtype, int64_t packed_stride, hipStream_t stream) {
+  const int64_t strips = (rows + kDqCols - 1) / kDqCols;
+  const int64_t grid = n_mat * strips;
+  KLC_REQUIRE(grid <= 0x7fffffff, KLC_ERR_UNSUPPORTED, "dequant: too many matrices (%lld)", (long long)n_mat);
+  const auto* b = static_cast<const uint8_t*>(blocks);
+  const auto* s = static_cast<const uint8_t*>(scales);
+  switch (dtype) {
+    case KLC_DTYPE_BF16:
+      dequant_kernel<KLC_DTYPE_BF16, kPacked><<<(unsigned)grid, kDqThreads, 0, stream>>>(b, s, out, (int)rows, (int)groups, packed_stride);
+      break;
+    case KLC_DTYPE_F16:
+      dequant_kernel<KLC_DTYPE_F16, kPacked><<<(unsigned)grid, kDqThreads, 0, stream>>>(b, s, out, (int)rows, (int)groups, packed_stride);
+      break;
+    case KLC_DTYPE_F32:
+      dequant_kernel<KLC_DTYPE_F32, kPacked><<<(unsigned)grid, kDqThreads, 0, stream>>>(b, s, out, (int)rows, (int)groups, packed_stride);
+      break;
+    default:
+      return set_error(KLC_ERR_ARGUMENT, "dequant: unknown dtype %d", dtype);
+  }
+  return check_launch("dequant_kernel");
+}
+
+}  // namespace
+}  // namespace klc
+
+using namespace klc;
+
+extern "C" int klc_mxfp4_dequant(const void* blocks, const void* scales, void* out, int64_t n_mat, int64_t out_dim,
+                                 int64_t groups, int out_dtype, void* stream) {
+  KLC_REQUIRE(blocks && scales && out, KLC_ERR_ARGUMENT, "klc_mxfp4_dequant: null pointer");
+  KLC_REQUIRE(n_mat >= 0 && out_dim > 0 && groups > 0, KLC_ERR_ARGUMENT,
+              "klc_mxfp4_dequant: bad sizes n_mat=%lld out_dim=%lld groups=%lld", (long long)n_mat,
+              (long long)out_dim, (long long)groups);
+  KLC_REQUIRE(out_dim < (1 << 30) && groups < (1 << 24), KLC_ERR_UNSUPPORTED, "klc_mxfp4_dequant: matrix too large");
+  if (n_mat == 0) return KLC_OK;
+  return launch_dequant<false>(blocks, scales, out, n_mat, out_dim, groups, out_dtype, 0, as_stream(stream));
+}
+
+extern "C" int64_t klc_mxfp4_packed_bytes(int64_t out_dim, int64_t groups) {
+  if (out_dim <= 0 || groups <= 0)
+    return set_error(KLC_ERR_ARGUMENT, "klc_mxfp4_packed_bytes: bad sizes out_dim=%lld groups=%lld",
+                     (long long)out_dim, (long long)groups);
+  if (out_dim % kTileRows)
+    return set_error(KLC_ERR_SHAPE, "klc_mxfp4_packed_bytes: out_dim=%lld is not a multiple of %d",
+                     (long long)out_dim, kTileRows);
+  return packed_matrix_bytes(out_dim, groups);
+}
+
+extern "C" int klc_mxfp4_pack(const void* blocks, const void* scales, void* packed, int64_t n_mat, int64_t out_dim,
+                              int64_t groups, void* stream) {
+  KLC_REQUIRE(blocks && scales && packed, KLC_ERR_ARGUMENT, "klc_mxfp4_pack: null pointer");
+  const int64_t stride = klc_mxfp4_packed_bytes(out_dim, groups);
+  if (stride < 0) return (int)stride;
+  KLC_REQUIRE(n_mat >= 0, KLC_ERR_ARGUMENT, "klc_mxfp4_pack: n_mat=%lld", (long long)n_mat);
+  KLC_REQUIRE(out_dim < (1 << 30) && groups < (1 << 24), KLC_ERR_UNSUPPORTED, "klc_mxfp4_pack: matrix too large");
+  if (n_mat == 0) return KLC_OK;
+  const int64_t total = n_mat * (out_dim / kTileRows) * ((groups + 3) / 4) * 4 * kTileRows;
+  const int64_t blocks_needed = (total + 255) / 256;
+  const unsigned grid = (unsigned)(blocks_needed < 65536 ? blocks_needed : 65536);
+  pack_kernel<<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint8_t*>(blocks),
+                                                     static_cast<const uint8_t*>(scales),
+                                                     static_cast<uint8_t*>(packed), n_mat, (int)out_dim, (int)groups,
+                                                     stride);
+  return check_launch("pack_kernel");
+}
+
+extern "C" int klc_mxfp4_dequant_packed(const void* packed, void* out, int64_t n_mat, int64_t out_dim,
+                                        int64_t groups, int out_dtype, void* stream) {
+  KLC_REQUIRE(packed && out, KLC_ERR_ARGUMENT, "klc_mxfp4_dequant_packed: null pointer");
+  const int64_t stride = klc_mxfp4_packed_bytes(out_dim, groups);
+  if (stride < 0) return (int)stride;
+  KLC_REQUIRE(n_mat >= 0, KLC_ERR_ARGUMENT, "klc_mxfp4_dequant_packed: n_mat=%lld", (long long)n_mat);
+  KLC_REQUIRE(out_dim < (1 << 30) && groups < (1 << 24), KLC_ERR_UNSUPPORTED,
+              "klc_mxfp4_dequant_packed: matrix too large");
+  if (n_mat == 0) return KLC_OK;
+  return launch_dequant<true>(packed, packed, out, n_mat, out_dim, groups, out_dtype, stride, as_stream(stream));
+}

@@ -1,0 +1,339 @@
+// Router logits, top-k + softmax, and expert-sorted dispatch (gfx950).
+//
+// Logits: one wave per (expert, block of 8 tokens).  Lanes stride the hidden
+// dimension with 16-byte loads; each bfloat16 product is exact in float32 and
+// is accumulated in float64, so the only roundings are the reference's own:
+// float32 of the dot product, float32 bias add, bfloat16 result
+// (streamed_moe_router.py:269).
+//
+// Top-k: one wave per token.  Each logit becomes a 64-bit key (ordered value
+// bits, then inverted expert index), so a wave-wide max picks the largest
+// value and, among equal values, the lowest expert index; k rounds of that
+// give the descending top-k.  The softmax over the k values is evaluated in
+// float64 and rounded to float32, then to bfloat16.
+//
+// Dispatch: one workgroup performs a stable counting sort of the (token, slot)
+// pairs by expert: per-chunk histograms in LDS, an exclusive scan over chunks
+// and experts, then an in-order scatter.
+#include "klc_common.h"
+
+namespace klc {
+namespace {
+
+constexpr int kRouterTok = 8;
+
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ b,
+                                                            uint16_t* __restrict__ logits, float* __restrict__ x_f32,
+                                                            int n_tok, int hidden, int n_exp) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t0 = blockIdx.y * kRouterTok;
+  const int nt = min(kRouterTok, n_tok - t0);
+
+  if (x_f32 != nullptr && blockIdx.x == 0) {
+    const int64_t base = (int64_t)t0 * hidden;
+    for (int i = threadIdx.x; i < nt * hidden; i += blockDim.x) x_f32[base + i] = bf16_to_f32(x[base + i]);
+  }
+
+  const int e = blockIdx.x * 4 + wave;
+  if (e >= n_exp) return;
+
+  double acc[kRouterTok];
+#pragma unroll
+  for (int j = 0; j < kRouterTok; ++j) acc[j] = 0.0;
+
+  const uint16_t* wr = w + (int64_t)e * hidden;
+  if ((hidden & 7) == 0) {
+    const int nchunk = hidden >> 3;
+    for (int c = lane; c < nchunk; c += kWave) {
+      const uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 8);
+      const uint32_t wwords[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int j = 0; j < kRouterTok; ++j) {
+        if (j < nt) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + j) * hidden + c * 8);
+          const uint32_t xwords[4] = {xv.x, xv.y, xv.z, xv.w};
+          double s = 0.0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float w0 = __uint_as_float(wwords[q] << 16), w1 = __uint_as_float(wwords[q] & 0xffff0000u);
+            const float x0 = __uint_as_float(xwords[q] << 16), x1 = __uint_as_float(xwords[q] & 0xffff0000u);
+            s += (double)(x0 * w0);
+            s += (double)(x1 * w1);
+          }
+          acc[j] += s;
+        }
+      }
+    }
+  } else {
+    for (int h = lane; h < hidden; h += kWave) {
+      const float wf = bf16_to_f32(wr[h]);
+#pragma unroll
+      for (int j = 0; j < kRouterTok; ++j)
+        if (j < nt) acc[j] += (double)(bf16_to_f32(x[(int64_t)(t0 + j) * hidden + h]) * wf);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRouterTok; ++j) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off);
+  }
+  if (lane == 0) {
+    const float bias = bf16_to_f32(b[e]);
+    for (int j = 0; j < nt; ++j)
+      logits[(int64_t)(t0 + j) * n_exp + e] = (uint16_t)f32_to_bf16_rne((float)acc[j] + bias);
+  }
+}
+
+// Orderable key: larger key = larger logit; NaN is the largest value; -0 == +0;
+// among equal values the lower expert index has the larger key.
+__device__ __forceinline__ uint64_t logit_key(uint32_t bf16bits, int idx) {
+  uint32_t u = bf16bits << 16;
+  uint32_t k32;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    k32 = 0xffffffffu;
+  } else {
+    if ((u & 0x7fffffffu) == 0u) u = 0u;
+    k32 = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return ((uint64_t)k32 << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+
+constexpr int kTopkMaxPerLane = 16;  // n_experts <= 1024
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = __shfl_xor(v, off);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
+                                                           int32_t* __restrict__ ids, float* __restrict__ values,
+                                                           uint16_t* __restrict__ weights, int n_tok, int n_exp,
+                                                           int k) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= n_tok) return;
+  const uint16_t* row = logits + (int64_t)t * n_exp;
+  uint64_t keys[kTopkMaxPerLane];
+#pragma unroll
+  for (int s = 0; s < kTopkMaxPerLane; ++s) {
+    const int idx = lane + s * kWave;
+    keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;
+  }
+  // lane r keeps the r-th selection
+  int my_id = 0;
+  float my_val = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = 0ull;
+#pragma unroll
+    for (int s = 0; s < kTopkMaxPerLane; ++s) best = keys[s] > best ? keys[s] : best;
+    best = wave_max_u64(best);
+#pragma unroll
+    for (int s = 0; s < kTopkMaxPerLane; ++s)
+      if (keys[s] == best) keys[s] = 0ull;
+    if (lane == r) {
+      my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+      my_val = bf16_to_f32(row[my_id]);
+    }
+  }
+  // softmax over the k values: max is the first selection (NaN propagates),
+  // exponentials summed in selection order, all in float64
+  const double mx = (double)__shfl(my_val, 0);
+  double sum = 0.0;
+  for (int r = 0; r < k; ++r) sum += exp((double)__shfl(my_val, r) - mx);
+  if (lane < k) {
+    const int64_t o = (int64_t)t * k + lane;
+    ids[o] = my_id;
+    if (values) values[o] = my_val;
+    weights[o] = (uint16_t)f32_to_bf16_rne((float)(exp((double)my_val - mx) / sum));
+  }
+}
+
+constexpr int kDispatchThreads = 256;
+constexpr int kDispatchMaxExperts = 256;
+
+// Exclusive prefix sum of LDS array `v[n]` (n <= 256) by the whole block;
+// total written to *total.  Uses one wave, 4 entries per lane.
+__device__ void block_exclusive_scan_256(int32_t* v, int n, int32_t* total) {
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    int32_t local[4];
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = lane * 4 + i;
+      local[i] = idx < n ? v[idx] : 0;
+      s += local[i];
+    }
+    int32_t incl = s;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int32_t o = __shfl_up(incl, off);
+      if (lane >= off) incl += o;
+    }
+    int32_t run = incl - s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = lane * 4 + i;
+      if (idx < n) v[idx] = run;
+      run += local[i];
+    }
+    if (lane == kWave - 1) *total = incl;
+  }
+}
+
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_t* __restrict__ ids, int n_pairs,
+                                                                    int n_exp, int32_t* __restrict__ offsets,
+                                                                    int32_t* __restrict__ sorted,
+                                                                    int32_t* __restrict__ active,
+                                                                    int32_t* __restrict__ n_active) {
+  // cnt[e * chunks + c]: pairs of expert e in chunk c (then its exclusive prefix)
+  __shared__ uint16_t cnt[kDispatchMaxExperts * kDispatchThreads];
+  __shared__ int32_t total[kDispatchMaxExperts];
+  __shared__ int32_t flags[kDispatchMaxExperts];
+  __shared__ int32_t sums[2];
+
+  const int tid = threadIdx.x;
+  const int chunks = n_pairs < kDispatchThreads ? n_pairs : kDispatchThreads;
+  const int per = (n_pairs + chunks - 1) / chunks;
+
+  for (int i = tid; i < n_exp * chunks; i += kDispatchThreads) cnt[i] = 0;
+  __syncthreads();
+  if (tid < chunks) {
+    const int p_end = min(n_pairs, (tid + 1) * per);
+    for (int p = tid * per; p < p_end; ++p) {
+      const int e = ids[p];
+      if (e >= 0 && e < n_exp) cnt[e * chunks + tid] += 1;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < n_exp; e += kDispatchThreads) {
+    int32_t run = 0;
+    uint16_t* c = cnt + e * chunks;
+    for (int i = 0; i < chunks; ++i) {
+      const int32_t v = c[i];
+      c[i] = (uint16_t)run;
+      run += v;
+    }
+    total[e] = run;
+    flags[e] = run > 0 ? 1 : 0;
+  }
+  __syncthreads();
+  // total[] becomes the expert offsets, flags[] the active-list positions
+  block_exclusive_scan_256(total, n_exp, &sums[0]);
+  __syncthreads();
+  block_exclusive_scan_256(flags, n_exp, &sums[1]);
+  __syncthreads();
+  if (tid < chunks) {
+    const int p_end = min(n_pairs, (tid + 1) * per);
+    for (int p = tid * per; p < p_end; ++p) {
+      const int e = ids[p];
+      if (e >= 0 && e < n_exp) {
+        const int pos = total[e] + cnt[e * chunks + tid];
+        cnt[e * chunks + tid] += 1;
+        sorted[pos] = p;
+      }
+    }
+  }
+  for (int e = tid; e < n_exp; e += kDispatchThreads) {
+    offsets[e] = total[e];
+    const int next = e + 1 < n_exp ? total[e + 1] : sums[0];
+    if (next > total[e]) active[flags[e]] = e;
+    if (e >= sums[1]) active[e] = -1;
+  }
+  if (tid == 0) {
+    offsets[n_exp] = sums[0];
+    *n_active = sums[1];
+  }
+}
+
+}  // namespace
+
+int launch_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32, int64_t n_tok,
+                         int64_t hidden, int64_t n_exp, hipStream_t stream) {
+  const dim3 grid((unsigned)((n_exp + 3) / 4), (unsigned)((n_tok + kRouterTok - 1) / kRouterTok));
+  router_logits_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                                                 static_cast<const uint16_t*>(b), static_cast<uint16_t*>(logits),
+                                                 x_f32, (int)n_tok, (int)hidden, (int)n_exp);
+  return check_launch("router_logits_kernel");
+}
+
+int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
+                int64_t k, hipStream_t stream) {
+  topk_softmax_kernel<<<(unsigned)((n_tok + 3) / 4), 256, 0, stream>>>(
+      static_cast<const uint16_t*>(logits), ids, values, static_cast<uint16_t*>(weights), (int)n_tok, (int)n_exp,
+      (int)k);
+  return check_launch("topk_softmax_kernel");
+}
+
+int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
+                    int32_t* active, int32_t* n_active, hipStream_t stream) {
+  dispatch_kernel<<<1, kDispatchThreads, 0, stream>>>(ids, (int)n_pairs, (int)n_exp, offsets, sorted, active,
+                                                      n_active);
+  return check_launch("dispatch_kernel");
+}
+
+int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp) {
+  KLC_REQUIRE(n_tok > 0 && hidden > 0 && n_exp > 0, KLC_ERR_ARGUMENT,
+              "router: bad sizes n_tokens=%lld hidden=%lld n_experts=%lld", (long long)n_tok, (long long)hidden,
+              (long long)n_exp);
+  KLC_REQUIRE(n_tok <= (int64_t)65535 * kRouterTok && hidden < (1 << 28) && n_exp <= 1024, KLC_ERR_UNSUPPORTED,
+              "router: unsupported sizes n_tokens=%lld hidden=%lld n_experts=%lld (n_experts <= 1024)",
+              (long long)n_tok, (long long)hidden, (long long)n_exp);
+  return KLC_OK;
+}
+
+int check_topk_args(int64_t n_tok, int64_t n_exp, int64_t k) {
+  KLC_REQUIRE(n_tok > 0 && n_exp > 0 && k > 0, KLC_ERR_ARGUMENT, "topk: bad sizes n_tokens=%lld n_experts=%lld k=%lld",
+              (long long)n_tok, (long long)n_exp, (long long)k);
+  KLC_REQUIRE(k <= n_exp, KLC_ERR_SHAPE, "topk: k=%lld exceeds n_experts=%lld", (long long)k, (long long)n_exp);
+  KLC_REQUIRE(k <= 32 && n_exp <= 1024 && n_tok < ((int64_t)1 << 31) / 4, KLC_ERR_UNSUPPORTED,
+              "topk: unsupported k=%lld n_experts=%lld (k <= 32, n_experts <= 1024)", (long long)k,
+              (long long)n_exp);
+  return KLC_OK;
+}
+
+int check_dispatch_args(int64_t n_pairs, int64_t n_exp) {
+  KLC_REQUIRE(n_pairs > 0 && n_exp > 0, KLC_ERR_ARGUMENT, "dispatch: bad sizes n_pairs=%lld n_experts=%lld",
+              (long long)n_pairs, (long long)n_exp);
+  KLC_REQUIRE(n_exp <= kDispatchMaxExperts, KLC_ERR_UNSUPPORTED, "dispatch: n_experts=%lld > %d", (long long)n_exp,
+              kDispatchMaxExperts);
+  KLC_REQUIRE(n_pairs <= (int64_t)kDispatchThreads * 65535, KLC_ERR_UNSUPPORTED, "dispatch: n_pairs=%lld too large",
+              (long long)n_pairs);
+  return KLC_OK;
+}
+
+}  // namespace klc
+
+using namespace klc;
+
+extern "C" int klc_moe_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32,
+                                     int64_t n_tokens, int64_t hidden, int64_t n_experts, void* stream) {
+  KLC_REQUIRE(x && w && b && logits, KLC_ERR_ARGUMENT, "klc_moe_router_logits: null pointer");
+  const int rc = check_router_args(n_tokens, hidden, n_experts);
+  if (rc) return rc;
+  return launch_router_logits(x, w, b, logits, x_f32, n_tokens, hidden, n_experts, as_stream(stream));
+}
+
+extern "C" int klc_moe_topk_softmax(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tokens,
+                                    int64_t n_experts, int64_t k, void* stream) {
+  KLC_REQUIRE(logits && ids && weights, KLC_ERR_ARGUMENT, "klc_moe_topk_softmax: null pointer");
+  const int rc = check_topk_args(n_tokens, n_experts, k);
+  if (rc) return rc;
+  return launch_topk(logits, ids, values, weights, n_tokens, n_experts, k, as_stream(stream));
+}
+
+extern "C" int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
+                                int32_t* sorted_pairs, int32_t* active, int32_t* n_active, void* stream) {
+  KLC_REQUIRE(ids && offsets && sorted_pairs && active && n_active, KLC_ERR_ARGUMENT, "klc_moe_dispatch: null pointer");
+  const int rc = check_dispatch_args(n_pairs, n_experts);
+  if (rc) return rc;
+  return launch_dispatch(ids, n_pairs, n_experts, offsets, sorted_pairs, active, n_active, as_stream(stream));
+}

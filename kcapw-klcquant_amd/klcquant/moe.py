@@ -1,0 +1,216 @@
+"""One MoE layer with every expert resident in HBM in the packed row-tile layout.
+
+This is the batched form of the reference's per-token path
+(streamed_moe_router.py:257-315 and :483-522 for each row of ``hidden``):
+router logits -> top-k/softmax -> expert-sorted dispatch -> gate_up + SwiGLU
+-> down -> weighted combine, enqueued on the current stream with no host
+synchronisation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from . import ops, synth
+
+
+@dataclass
+class MoELayerWeights:
+    """Device-resident weights of one MoE layer (E experts, hidden H, intermediate I)."""
+
+    router_weight: torch.Tensor  # [E, H] bf16
+    router_bias: torch.Tensor  # [E] bf16
+    gate_up: torch.Tensor  # [E, packed bytes of a [2I rows, H/32 groups] matrix] uint8
+    gate_up_bias: torch.Tensor  # [E, 2I] bf16
+    down: torch.Tensor  # [E, packed bytes of a [H rows, I/32 groups] matrix] uint8
+    down_bias: torch.Tensor  # [E, H] bf16
+    hidden: int
+    inter: int
+    gate_up_table: torch.Tensor = field(init=False)
+    down_table: torch.Tensor = field(init=False)
+
+    def __post_init__(self) -> None:
+        dev = self.router_weight.device
+        self.gate_up_table = ops.pointer_table(self.gate_up, dev)
+        self.down_table = ops.pointer_table(self.down, dev)
+
+    @property
+    def n_experts(self) -> int:
+        return int(self.router_weight.shape[0])
+
+    @property
+    def device(self) -> torch.device:
+        return self.router_weight.device
+
+    def expert_bytes(self) -> int:
+        """Packed bytes of one expert (gate_up + down, blocks + scales)."""
+        return int(self.gate_up.shape[1] + self.down.shape[1])
+
+    @classmethod
+    def from_checkpoint(cls, router_weight, router_bias, gate_up_blocks, gate_up_scales, gate_up_bias, down_blocks,
+                        down_scales, down_bias, device: torch.device | str = "cuda") -> "MoELayerWeights":
+        """Packs checkpoint-layout tensors (``[E, out, G, 16]`` / ``[E, out, G]``)."""
+        dev = torch.device(device)
+
+        def to_dev(t, dtype):
+            return torch.as_tensor(t).to(device=dev, dtype=dtype).contiguous()
+
+        e = router_weight.shape[0]
+        hidden = router_weight.shape[1]
+        inter = down_blocks.shape[2] * 32
+        if tuple(gate_up_blocks.shape[:2]) != (e, 2 * inter) or gate_up_blocks.shape[2] * 32 != hidden:
+            raise ValueError(f"gate_up blocks shape {tuple(gate_up_blocks.shape)} does not match E={e} H={hidden} I={inter}")
+        if tuple(down_blocks.shape[:2]) != (e, hidden):
+            raise ValueError(f"down blocks shape {tuple(down_blocks.shape)} does not match E={e} H={hidden}")
+        gu = ops.mxfp4_pack(to_dev(gate_up_blocks, torch.uint8), to_dev(gate_up_scales, torch.uint8))
+        dn = ops.mxfp4_pack(to_dev(down_blocks, torch.uint8), to_dev(down_scales, torch.uint8))
+        return cls(to_dev(router_weight, torch.bfloat16), to_dev(router_bias, torch.bfloat16), gu,
+                   to_dev(gate_up_bias, torch.bfloat16), dn, to_dev(down_bias, torch.bfloat16), hidden, inter)
+
+    @classmethod
+    def synthetic(cls, workload: int, layer: int, hidden: int, inter: int, n_experts: int,
+                  device: torch.device | str = "cuda", router_bias_override: np.ndarray | None = None
+                  ) -> "MoELayerWeights":
+        """Seeded synthetic layer, bit-identical to :func:`synthetic_host_layer`.
+
+        MXFP4 codes and scales are generated on the GPU (klc_synth_fill) in
+        checkpoint layout and packed; the normal-distributed tensors are small
+        and generated on the host.
+        """
+        dev = torch.device(device)
+        seeds = {name: synth.tensor_seed(workload, name, layer) for name in synth.TENSOR_IDS}
+        rw = synth.random_normal_bf16(seeds["router_weight"], n_experts * hidden, 0.0, 0.02).reshape(n_experts, hidden)
+        rb = synth.random_normal_bf16(seeds["router_bias"], n_experts, 0.0, 0.01)
+        if router_bias_override is not None:
+            rb = np.asarray(router_bias_override, dtype=np.uint16)
+        gub = synth.random_normal_bf16(seeds["gate_up_bias"], n_experts * 2 * inter, 0.0, 0.01).reshape(n_experts, -1)
+        db = synth.random_normal_bf16(seeds["down_bias"], n_experts * hidden, 0.0, 0.01).reshape(n_experts, -1)
+
+        def bf16_dev(a):
+            return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
+
+        def packed(rows, in_dim, seed_b, seed_s):
+            groups = in_dim // 32
+            blocks = torch.empty((n_experts, rows, groups, 16), dtype=torch.uint8, device=dev)
+            scales = torch.empty((n_experts, rows, groups), dtype=torch.uint8, device=dev)
+            ops.synth_fill(blocks, seed_b, 0)
+            ops.synth_fill(scales, seed_s, 1, 118, 124)
+            out = ops.mxfp4_pack(blocks, scales)
+            del blocks, scales  # the checkpoint-layout staging copy is not kept
+            return out
+
+        gu = packed(2 * inter, hidden, seeds["gate_up_blocks"], seeds["gate_up_scales"])
+        dn = packed(hidden, inter, seeds["down_blocks"], seeds["down_scales"])
+        return cls(bf16_dev(rw), bf16_dev(rb), gu, bf16_dev(gub), dn, bf16_dev(db), hidden, inter)
+
+
+def synthetic_host_layer(workload: int, layer: int, hidden: int, inter: int, n_experts: int,
+                         router_bias_override: np.ndarray | None = None) -> dict:
+    """The same seeded layer as :meth:`MoELayerWeights.synthetic`, as numpy arrays in checkpoint layout."""
+    seeds = {name: synth.tensor_seed(workload, name, layer) for name in synth.TENSOR_IDS}
+    rb = synth.random_normal_bf16(seeds["router_bias"], n_experts, 0.0, 0.01)
+    if router_bias_override is not None:
+        rb = np.asarray(router_bias_override, dtype=np.uint16)
+    gub, gus = synth.mxfp4_expert_tensors(seeds["gate_up_blocks"], seeds["gate_up_scales"], n_experts, 2 * inter, hidden)
+    db, ds = synth.mxfp4_expert_tensors(seeds["down_blocks"], seeds["down_scales"], n_experts, hidden, inter)
+    return {
+        "router_weight": synth.random_normal_bf16(seeds["router_weight"], n_experts * hidden, 0.0, 0.02).reshape(n_experts, hidden),
+        "router_bias": rb,
+        "gate_up_blocks": gub,
+        "gate_up_scales": gus,
+        "gate_up_bias": synth.random_normal_bf16(seeds["gate_up_bias"], n_experts * 2 * inter, 0.0, 0.01).reshape(n_experts, -1),
+        "down_blocks": db,
+        "down_scales": ds,
+        "down_bias": synth.random_normal_bf16(seeds["down_bias"], n_experts * hidden, 0.0, 0.01).reshape(n_experts, -1),
+    }
+
+
+def synthetic_hidden(workload: int, n_tokens: int, hidden: int, step: int = 0) -> np.ndarray:
+    """bf16 bit patterns ``[n_tokens, hidden]`` of N(0, 1) activations."""
+    seed = synth.tensor_seed(workload, "hidden") + 7919 * step
+    return synth.random_normal_bf16(seed, n_tokens * hidden).reshape(n_tokens, hidden)
+
+
+class MoELayer:
+    """Runs one MoE layer on batches of tokens (bf16 ``[B, H]`` in, bf16 ``[B, H]`` out)."""
+
+    def __init__(self, weights: MoELayerWeights, experts_per_token: int = 4, swiglu_limit: float = 7.0,
+                 precision: str = "fp32") -> None:
+        if precision not in ops.PRECISIONS:
+            raise ValueError(f"unknown matmul precision {precision!r}")
+        self.w = weights
+        self.k = min(int(experts_per_token), weights.n_experts)
+        self.limit = float(swiglu_limit)
+        self.precision = precision
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def workspace(self, n_tokens: int) -> torch.Tensor:
+        ws = self._ws.get(n_tokens)
+        if ws is None:
+            nbytes = ops.workspace_bytes(n_tokens, self.w.hidden, self.w.inter, self.w.n_experts, self.k)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=self.w.device)
+            self._ws[n_tokens] = ws
+        return ws
+
+    def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
+                weights: torch.Tensor | None = None, events: list | None = None) -> torch.Tensor:
+        """Fused layer (klc_moe_layer); optional ``ids``/``weights`` receive the routing.
+
+        ``events``: optional list of ``KLC_LAYER_EVENTS`` recorded
+        ``torch.cuda.Event`` objects, re-recorded around the six kernels.
+        """
+        ops._check_gpu("hidden", x, torch.bfloat16, 2)
+        n_tok, hidden = x.shape
+        if hidden != self.w.hidden:
+            raise ValueError(f"hidden size {hidden} != layer hidden {self.w.hidden}")
+        if out is None:
+            out = torch.empty_like(x)
+        ws = self.workspace(n_tok)
+        w = self.w
+        ev = None
+        if events is not None:
+            if len(events) != nat.LAYER_EVENTS:
+                raise ValueError(f"need {nat.LAYER_EVENTS} events, got {len(events)}")
+            ev = (ctypes.c_void_p * nat.LAYER_EVENTS)(*[e.cuda_event for e in events])
+        nat.call("klc_moe_layer", ops._ptr(x), ops._ptr(w.router_weight), ops._ptr(w.router_bias),
+                 ops._ptr(w.gate_up_table), ops._ptr(w.gate_up_bias), ops._ptr(w.down_table), ops._ptr(w.down_bias),
+                 n_tok, hidden, w.inter, w.n_experts, self.k, self.limit, ops.PRECISIONS[self.precision],
+                 ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(ids), ops._ptr(weights), ev,
+                 ops._stream(x.device))
+        return out
+
+    __call__ = forward
+
+    def forward_detailed(self, x: torch.Tensor, routing: tuple[torch.Tensor, torch.Tensor] | None = None) -> dict:
+        """Step-by-step path exposing every intermediate (same kernels as :meth:`forward`).
+
+        ``routing`` optionally supplies precomputed ``(ids int32 [B, k],
+        weights bf16 [B, k])`` (the routing-locality path decides the experts on
+        the host); otherwise the GPU router selects them.
+        """
+        w = self.w
+        logits, x_f32 = ops.router_logits(x, w.router_weight, w.router_bias, want_f32=True)
+        values = None
+        if routing is None:
+            ids, values, weights = ops.topk_softmax(logits, self.k)
+        else:
+            ids, weights = routing
+            ops._check_gpu("ids", ids, torch.int32, 2)
+            ops._check_gpu("weights", weights, torch.bfloat16, 2)
+        k = ids.shape[1]
+        offsets, sorted_pairs, active, n_active = ops.dispatch(ids, w.n_experts)
+        max_active = min(w.n_experts, ids.numel())
+        gated, gated_raw = ops.gate_up(w.gate_up_table, w.gate_up_bias, x_f32, k, offsets, sorted_pairs, active,
+                                       n_active, max_active, w.hidden, w.inter, self.limit, self.precision,
+                                       want_raw=True)
+        eo = ops.down(w.down_table, w.down_bias, gated, offsets, sorted_pairs, active, n_active, max_active, w.hidden,
+                      w.inter, self.precision)
+        out = ops.combine(eo, weights, x.shape[0], k)
+        return {"out": out, "logits": logits, "ids": ids, "values": values, "weights": weights,
+                "offsets": offsets, "sorted_pairs": sorted_pairs, "active": active, "n_active": n_active,
+                "gated": gated_raw, "gated_act": gated, "expert_out": eo}

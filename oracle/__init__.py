@@ -1,0 +1,34 @@
+"""CPU oracle for the MoE expert path — TEST INFRASTRUCTURE ONLY.
+
+This package restates, in numpy, the arithmetic of the reference's MoE expert
+path (``mxfp4_expert.py`` and ``streamed_moe_router.py``) so that the HIP
+kernels can be checked against it on identical seeded inputs.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it, and only as the checker: nothing in the product path
+(``kcapw-klcquant_amd/``) imports or calls it, and there is no CPU fallback.
+
+Modules and what pins them (tests/test_oracle_*.py):
+
+* ``numerics``  — float32 -> bfloat16 / float16 rounding.  Pinned against
+  hand-worked bit patterns (ties to even, overflow, subnormals, NaN) and
+  against numpy's own float16 cast.
+* ``mxfp4``     — MXFP4 -> dense dequant (mxfp4_expert.py:17-34, 357-379).
+  Pinned against the E2M1/E8M0 definitions of the OCP MX v1.0 spec evaluated
+  with ``math.ldexp`` for all 16 codes x 256 scale bytes, the reference's
+  FP4_VALUES table, and single-nibble probes for the layout.
+* ``router``    — router logits, top-k, softmax, dispatch
+  (streamed_moe_router.py:268-284, 365-375).  Pinned by exact rational
+  dot products (``fractions``), brute-force selection and closed-form
+  softmax cases.
+* ``experts``   — gate_up / clamped SwiGLU / down / weighted combine
+  (streamed_moe_router.py:483-529) and the bias-only fallback (:317-322).
+  Pinned by clamp special cases, exact rational GEMVs on tiny shapes and
+  order-sensitive bfloat16 combine cases.
+* ``layer``     — one MoE layer for a batch of tokens, composing the above.
+* ``rmsnorm``   — streamed_attention.py:27-28 (the stacked workload only).
+
+Parity of every function above is pinned; no function is "parity unpinned".
+The one documented divergence is the top-k tie rule: equal bfloat16 logits
+are ordered by lower expert index first, where torch.topk's order on ties is
+implementation defined.
+"""

@@ -1,0 +1,92 @@
+"""GPU parity: router logits, top-k/softmax and dispatch against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_bits, bf16_tensor
+from klcquant import ops, synth
+from oracle import router as orr
+from oracle.numerics import f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def router_inputs(seed, n_tok, hidden, n_exp):
+    x = synth.random_normal_bf16(seed + 1, n_tok * hidden).reshape(n_tok, hidden)
+    w = synth.random_normal_bf16(seed + 2, n_exp * hidden, 0.0, 0.02).reshape(n_exp, hidden)
+    b = synth.random_normal_bf16(seed + 3, n_exp, 0.0, 0.01)
+    return x, w, b
+
+
+@pytest.mark.parametrize("n_tok,hidden,n_exp", [(1, 2880, 32), (64, 2880, 128), (13, 2880, 128), (5, 100, 7),
+                                                (9, 64, 1024)])
+def test_logits_bit_exact(gpu, n_tok, hidden, n_exp):
+    x, w, b = router_inputs(100 + n_tok, n_tok, hidden, n_exp)
+    logits, x_f32 = ops.router_logits(bf16_tensor(x, gpu), bf16_tensor(w, gpu), bf16_tensor(b, gpu), want_f32=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(logits), orr.router_logits(x, w, b))
+    assert np.array_equal(x_f32.cpu().numpy(), (x.astype(np.uint32) << 16).view(np.float32))
+
+
+def test_topk_on_gpu_logits_bit_exact_and_softmax(gpu):
+    n_tok, hidden, n_exp, k = 2048, 2880, 128, 4
+    x, w, b = router_inputs(7, n_tok, hidden, n_exp)
+    logits = ops.router_logits(bf16_tensor(x, gpu), bf16_tensor(w, gpu), bf16_tensor(b, gpu))
+    ids, values, weights = ops.topk_softmax(logits, k)
+    torch.cuda.synchronize()
+    lb = bf16_bits(logits)
+    want_ids, want_vals = orr.topk(lb, k)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    assert np.array_equal(values.cpu().numpy(), want_vals)
+    assert np.array_equal(bf16_bits(weights), orr.softmax_weights(want_vals))
+    # this input has boundary ties (4th == 5th logit); the tie rule decides them
+    srt = -np.sort(-(lb.astype(np.uint32) << 16).view(np.float32), axis=1)
+    assert (srt[:, k - 1] == srt[:, k]).sum() > 0
+
+
+def test_topk_ties_nan_and_signed_zero(gpu):
+    f = np.array([[0, 2, 1, 2, 2, 3, 2, 0, 0, 0],
+                  [-0.0, 0.0, -1, -1, -2, -3, -4, -5, -6, -7],
+                  [1, np.nan, 5, 5, 0, 0, 0, 0, 0, np.nan],
+                  [-np.inf, -np.inf, -np.inf, -np.inf, -np.inf, -np.inf, -np.inf, -np.inf, -np.inf, 7]],
+                 dtype=np.float32)
+    bits = f32_to_bf16(f)
+    ids, values, weights = ops.topk_softmax(bf16_tensor(bits, gpu), 3)
+    torch.cuda.synchronize()
+    assert ids.cpu().numpy().tolist() == [[5, 1, 3], [0, 1, 2], [1, 9, 2], [9, 0, 1]]
+    want_ids, want_vals = orr.topk(bits, 3)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    w = bf16_bits(weights)
+    ow = orr.softmax_weights(want_vals)
+    gn = (w & 0x7FFF) > 0x7F80
+    assert np.array_equal(gn, (ow & 0x7FFF) > 0x7F80)
+    assert np.array_equal(w[~gn], ow[~gn])
+
+
+@pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 128), (64, 4, 128), (2048, 4, 128), (7, 3, 5), (300, 2, 256),
+                                           (64, 4, 32)])
+def test_dispatch_matches_stable_counting_sort(gpu, n_tok, k, n_exp):
+    rng_ids = synth.random_ints(900 + n_tok, n_tok * k, 0, n_exp - 1).reshape(n_tok, k).astype(np.int32)
+    offsets, sorted_pairs, active, n_active = ops.dispatch(torch.from_numpy(rng_ids).to(gpu), n_exp)
+    torch.cuda.synchronize()
+    counts, w_off, w_order, w_active = orr.dispatch(rng_ids, n_exp)
+    assert np.array_equal(offsets.cpu().numpy(), w_off)
+    assert np.array_equal(sorted_pairs.cpu().numpy(), w_order)
+    na = int(n_active.item())
+    assert na == len(w_active)
+    a = active.cpu().numpy()
+    assert np.array_equal(a[:na], w_active)
+    assert (a[na:] == -1).all()
+
+
+def test_router_rejects_bad_shapes(gpu):
+    x = torch.zeros((2, 64), dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros((8, 32), dtype=torch.bfloat16, device=gpu)
+    b = torch.zeros(8, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        ops.router_logits(x, w, b)
+    with pytest.raises(Exception):
+        ops.topk_softmax(torch.zeros((2, 8), dtype=torch.bfloat16, device=gpu), 9)
