@@ -111,11 +111,13 @@ int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int
 /* gate_up GEMV + bias + clamped SwiGLU for every routed pair
  * (streamed_moe_router.py:500-506, 524-529).  w_gate_up is a device array of
  * n_experts pointers to packed [2*inter rows][hidden/32 groups] matrices;
- * bias is bfloat16 [n_experts][2*inter]; x_f32 is [n_tokens][hidden].
- * Writes gated[n_pairs][inter] (the down input: rounded to bfloat16 under
- * KLC_PRECISION_BF16) and, if gated_raw is not NULL, the unrounded SwiGLU
- * output.  max_active bounds *n_active (normally min(n_experts, n_pairs)). */
-int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const float* x_f32, int64_t k,
+ * bias is bfloat16 [n_experts][2*inter]; x is the bfloat16 hidden state
+ * [n_tokens][hidden].  Writes gated[n_pairs][inter] (the down input: rounded
+ * to bfloat16 under KLC_PRECISION_BF16) and, if gated_raw is not NULL, the
+ * unrounded SwiGLU output.  max_active bounds *n_active (normally
+ * min(n_experts, n_pairs)).  hidden and inter must be <= 3072; hidden a
+ * multiple of 64, inter of 32. */
+int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t k,
                     const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
                     const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
                     float swiglu_limit, int precision, float* gated, float* gated_raw, void* stream);

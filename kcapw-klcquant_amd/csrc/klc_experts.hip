@@ -29,35 +29,34 @@ int check_dispatch_args(int64_t n_pairs, int64_t n_exp);
 
 namespace {
 
-constexpr int kGemvWaves = 4;
+constexpr int kGemvWaves = 4;                 // 4 x 16 rows = one 64-row tile per workgroup
 constexpr int kGemvThreads = kGemvWaves * kWave;
-constexpr int kGemvTok = 4;   // tokens per pass over the weights
-constexpr int kGemvBatch = 24;  // groups loaded per batch per wave (<= 96 VGPRs)
+constexpr int kVRows = 8;                     // activation rows (MFMA N columns) staged per pass
+constexpr int kMaxSteps = 24;                 // 4-group steps per row (inputs <= 3072)
 
-// The activations are read-only for the whole kernel and every lane of a wave
-// reads the same slice, so they are addressed through the constant address
-// space, which lets the compiler fetch them with scalar loads into SGPRs.
-typedef const float __attribute__((address_space(4)))* const_f32_ptr;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Expert matrices arrive through a pointer table; they live in global memory.
 typedef const uint8_t __attribute__((address_space(1)))* global_u8_ptr;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef const u32x4 __attribute__((address_space(1)))* global_u32x4_ptr;
 typedef const uint32_t __attribute__((address_space(1)))* global_u32_ptr;
 
-// Decodes one 16-byte chunk (32 codes, input order) to float32.
-__device__ __forceinline__ void decode_chunk(const u32x4& v, float* wf) {
-  const uint32_t words[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float2 a = fp4x2_to_f32<0>(words[q]);
-    float2 b = fp4x2_to_f32<1>(words[q]);
-    float2 c = fp4x2_to_f32<2>(words[q]);
-    float2 d = fp4x2_to_f32<3>(words[q]);
-    wf[q * 8 + 0] = a.x; wf[q * 8 + 1] = a.y;
-    wf[q * 8 + 2] = b.x; wf[q * 8 + 3] = b.y;
-    wf[q * 8 + 4] = c.x; wf[q * 8 + 5] = c.y;
-    wf[q * 8 + 6] = d.x; wf[q * 8 + 7] = d.y;
-  }
+// 2^(e-127) as the float32 scale operand of v_cvt_scalef32_pk_bf16_fp4; the
+// conversion is exact for e = 0..254 (e = 0 is a float32 subnormal).
+__device__ __forceinline__ float cvt_scale(uint32_t e) {
+  return __uint_as_float(e == 0u ? 0x00400000u : (e == 255u ? 0x7f800000u : (e << 23)));
+}
+
+// Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
+__device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {
+  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+  return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3),
+                                 __builtin_shufflevector(p2, p3, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
@@ -68,13 +67,24 @@ __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
   return (up + 1.0f) * glu;
 }
 
-template <bool kGateUp>
-__global__ __launch_bounds__(kGemvThreads) void moe_gemv_kernel(
-    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const float* __restrict__ act,
+__device__ __forceinline__ uint16_t bf16_bits_rne(float f) { return (uint16_t)f32_to_bf16_rne(f); }
+
+// Expert GEMV on MFMA.  Workgroup = (64-row tile, active expert); wave w owns
+// rows [16w, 16w + 16) of the tile over the whole input dimension.  Per
+// 4-group step a lane holds the 16 code bytes of (row l % 16, group 4s + l/16)
+// -- exactly the A operand of four v_mfma_f32_16x16x32_bf16 (k = 8 * (l/16) + i)
+// once decoded -- and the B operand is read from the activations staged in
+// LDS as bfloat16 rows (the same k mapping).  Columns are up to kVRows
+// activation rows: gate_up stages one row per token (x is bfloat16, exact);
+// down stages hi = bf16(g) and lo = bf16(g - hi) per token so the float32
+// SwiGLU output enters the product with a 2^-17 relative residual.
+template <bool kDown>
+__global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
+    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const void* __restrict__ act,
     float* __restrict__ out, float* __restrict__ out_raw, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ pairs, const int32_t* __restrict__ active, const int32_t* __restrict__ n_active,
     int rows, int groups, int k_top, float limit, int precision) {
-  __shared__ float red[kGemvWaves][kGemvTok][kWave];
+  extern __shared__ uint16_t xs[];  // [kVRows][row_stride] bfloat16 bits
 
   const int u = blockIdx.y;
   if (u >= *n_active) return;
@@ -83,91 +93,133 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_kernel(
   const int np = offsets[e + 1] - pb;
   const int tile = blockIdx.x;
   const int tiles = rows / kTileRows;
-  const int g4 = (groups + 3) >> 2;
+  const int g4 = (groups + 3) >> 2;             // 4-group steps
   const int in_dim = groups * 32;
-  // wave index made provably uniform so group addressing stays scalar
+  const int row_stride = g4 * 128 + 8;          // bf16 elements per staged row (zero padded)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int g_lo = wave * groups / kGemvWaves;
-  const int g_hi = (wave + 1) * groups / kGemvWaves;
+  const int lr = lane & 15;                     // row within the wave's 16 (A) / column n (B, D)
+  const int lq = lane >> 4;                     // k-quarter: group 4s + lq
 
+  // ---- issue all weight loads of this lane first ----
   const global_u8_ptr mat = (global_u8_ptr)wptr[e];
-  const global_u8_ptr blk = mat + (int64_t)tile * groups * 1024 + lane * 16;
-  const global_u8_ptr scl = mat + (int64_t)tiles * groups * 1024 + (int64_t)tile * g4 * 256 + lane * 4;
-  const int row = tile * kTileRows + lane;
-  const float bias_v = bf16_to_f32(bias[(int64_t)e * rows + row]);
-
-  for (int tc = 0; tc < np; tc += kGemvTok) {
-    const int nt = min(kGemvTok, np - tc);
-    const float* xrow[kGemvTok];
+  const int trow = wave * 16 + lr;              // row inside the 64-row tile
+  const global_u8_ptr blk = mat + (int64_t)tile * groups * 1024 + trow * 16;
+  const global_u8_ptr scl = mat + (int64_t)tiles * groups * 1024 + (int64_t)tile * g4 * 256 + trow * 4;
+  u32x4 wv[kMaxSteps];
+  uint32_t sv[kMaxSteps];
 #pragma unroll
-    for (int j = 0; j < kGemvTok; ++j) {
-      const int pair = pairs[pb + tc + min(j, nt - 1)];
-      const int src = kGateUp ? pair / k_top : pair;
-      xrow[j] = act + (int64_t)src * in_dim;
+  for (int s = 0; s < kMaxSteps; ++s) {
+    if (s < g4) {
+      const int g = 4 * s + lq;
+      wv[s] = g < groups ? *(global_u32x4_ptr)(blk + (int64_t)g * 1024) : u32x4{0u, 0u, 0u, 0u};
+      sv[s] = *(global_u32_ptr)(scl + (int64_t)s * 256);
     }
-    float acc[kGemvTok];
-#pragma unroll
-    for (int j = 0; j < kGemvTok; ++j) acc[j] = 0.0f;
+  }
 
-    for (int gb = g_lo; gb < g_hi; gb += kGemvBatch) {
-      const int ng = min(kGemvBatch, g_hi - gb);
-      u32x4 wv[kGemvBatch];
+  const int tok_per_pass = kDown ? kVRows / 2 : kVRows;
+  for (int tc = 0; tc < np; tc += tok_per_pass) {
+    const int nt = min(tok_per_pass, np - tc);
+    const int nrows = kDown ? 2 * nt : nt;
+    // ---- stage activation rows (bf16) into LDS ----
+    __syncthreads();  // previous pass finished reading xs
+    if constexpr (!kDown) {
+      const uint16_t* x = static_cast<const uint16_t*>(act);
+      const int chunks = in_dim / 8;            // 16-byte chunks per row
+      for (int i = threadIdx.x; i < nrows * chunks; i += kGemvThreads) {
+        const int r = i / chunks, c = i - r * chunks;
+        const int tok = pairs[pb + tc + r] / k_top;
+        *reinterpret_cast<uint4*>(xs + r * row_stride + c * 8) =
+            *reinterpret_cast<const uint4*>(x + (int64_t)tok * in_dim + c * 8);
+      }
+    } else {
+      const float* g = static_cast<const float*>(act);
+      const int chunks = in_dim / 4;            // 4 floats per thread-step
+      for (int i = threadIdx.x; i < nt * chunks; i += kGemvThreads) {
+        const int t = i / chunks, c = i - t * chunks;
+        const float4 v = *reinterpret_cast<const float4*>(g + (int64_t)pairs[pb + tc + t] * in_dim + c * 4);
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        uint32_t hi[2], lo[2];
 #pragma unroll
-      for (int i = 0; i < kGemvBatch; ++i)
-        if (i < ng) wv[i] = *(global_u32x4_ptr)(blk + (int64_t)(gb + i) * 1024);
+        for (int h = 0; h < 2; ++h) {
+          const uint16_t h0 = bf16_bits_rne(f[2 * h]), h1 = bf16_bits_rne(f[2 * h + 1]);
+          const uint16_t l0 = bf16_bits_rne(f[2 * h] - bf16_to_f32(h0));
+          const uint16_t l1 = bf16_bits_rne(f[2 * h + 1] - bf16_to_f32(h1));
+          hi[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+          lo[h] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+        }
+        *reinterpret_cast<uint2*>(xs + (2 * t) * row_stride + c * 4) = make_uint2(hi[0], hi[1]);
+        *reinterpret_cast<uint2*>(xs + (2 * t + 1) * row_stride + c * 4) = make_uint2(lo[0], lo[1]);
+      }
+    }
+    // zero the padding beyond in_dim (its A operand is zero; keep 0 * pad finite)
+    const int pad = g4 * 128 - in_dim;
+    for (int i = threadIdx.x; i < nrows * pad; i += kGemvThreads) {
+      const int r = i / pad;
+      xs[r * row_stride + in_dim + (i - r * pad)] = 0;
+    }
+    __syncthreads();
+
+    // ---- MFMA main loop ----
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool has_col = lr < nrows;
+    const uint16_t* xrow = xs + lr * row_stride + lq * 32;
 #pragma unroll
-      for (int i = 0; i < kGemvBatch; ++i) {
-        if (i < ng) {
-          const int g = gb + i;
-          const uint32_t sw = *(global_u32_ptr)(scl + (int64_t)(g >> 2) * 256);
-          const float s = e8m0_to_f32((sw >> ((g & 3) * 8)) & 0xffu);
-          float wf[32];
-          decode_chunk(wv[i], wf);
+    for (int s = 0; s < kMaxSteps; ++s) {
+      if (s < g4) {
+        const float scale = cvt_scale((sv[s] >> (8 * lq)) & 0xffu);
+        const uint32_t words[4] = {wv[s].x, wv[s].y, wv[s].z, wv[s].w};
 #pragma unroll
-          for (int j = 0; j < kGemvTok; ++j) {
-            if (j < nt) {
-              const const_f32_ptr xr = (const_f32_ptr)(xrow[j] + g * 32);
-              float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-              for (int q = 0; q < 32; q += 2) {
-                a0 = fmaf(wf[q], xr[q], a0);
-                a1 = fmaf(wf[q + 1], xr[q + 1], a1);
-              }
-              acc[j] = fmaf(a0 + a1, s, acc[j]);
-            }
-          }
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8_t a = decode8(words[j], scale);
+          bf16x8_t b = {};
+          if (has_col) b = *reinterpret_cast<const bf16x8_t*>(xrow + s * 128 + j * 8);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
         }
       }
     }
 
+    // ---- epilogue: lane holds rows 4*lq + v (v = 0..3) of the wave's 16, column lr ----
+    const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
+    float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if constexpr (!kDown) {
+      if (lr < nt) {
+        const int pair = pairs[pb + tc + lr];
+        const int half = rows >> 1;
 #pragma unroll
-    for (int j = 0; j < kGemvTok; ++j) red[wave][j][lane] = acc[j];
-    __syncthreads();
-    if (wave == 0) {
-      for (int j = 0; j < nt; ++j) {
-        float v = red[0][j][lane];
-#pragma unroll
-        for (int w = 1; w < kGemvWaves; ++w) v += red[w][j][lane];
-        if (precision == KLC_PRECISION_BF16) v = round_bf16(v);
-        v += bias_v;
-        const int pair = pairs[pb + tc + j];
-        if constexpr (kGateUp) {
-          const float up = __shfl_xor(v, 1);
-          if ((lane & 1) == 0) {
-            const float y = swiglu(v, up, limit);
-            const int64_t idx = (int64_t)pair * (rows >> 1) + (row >> 1);
-            if (out_raw) out_raw[idx] = y;
-            out[idx] = precision == KLC_PRECISION_BF16 ? round_bf16(y) : y;
+        for (int h = 0; h < 2; ++h) {
+          float gate = v[2 * h], up = v[2 * h + 1];
+          if (precision == KLC_PRECISION_BF16) {
+            gate = round_bf16(gate);
+            up = round_bf16(up);
           }
-        } else {
-          out[(int64_t)pair * rows + row] = v;
+          gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
+          up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
+          const float y = swiglu(gate, up, limit);
+          const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
+          if (out_raw) out_raw[idx] = y;
+          out[idx] = precision == KLC_PRECISION_BF16 ? round_bf16(y) : y;
         }
       }
+    } else {
+      // column 2t holds the hi part of token t, column 2t + 1 the lo part
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
+      if ((lr & 1) == 0 && (lr >> 1) < nt) {
+        const int pair = pairs[pb + tc + (lr >> 1)];
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float t = precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i];
+          o[i] = t + bf16_to_f32(bias[(int64_t)e * rows + row0 + i]);
+        }
+        *reinterpret_cast<float4*>(out + (int64_t)pair * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
+      }
     }
-    __syncthreads();
   }
 }
+
+size_t gemv_lds_bytes(int groups) { return (size_t)kVRows * (((groups + 3) / 4) * 128 + 8) * 2; }
 
 // out[t][h] over k slots in order; every step rounded to bfloat16.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ eo, const uint16_t* __restrict__ w,
@@ -233,30 +285,30 @@ int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t max_active) {
   KLC_REQUIRE(hidden % 64 == 0 && inter % 32 == 0 && (2 * inter) % 64 == 0, KLC_ERR_SHAPE,
               "experts: hidden=%lld must be a multiple of 64 and inter=%lld a multiple of 32", (long long)hidden,
               (long long)inter);
-  KLC_REQUIRE(max_active <= 65535 && hidden < (1 << 24) && inter < (1 << 24), KLC_ERR_UNSUPPORTED,
-              "experts: unsupported sizes");
+  KLC_REQUIRE(max_active <= 65535 && hidden <= 32 * 4 * kMaxSteps && inter <= 32 * 4 * kMaxSteps,
+              KLC_ERR_UNSUPPORTED, "experts: unsupported sizes (hidden, inter <= %d)", 32 * 4 * kMaxSteps);
   return KLC_OK;
 }
 
-int launch_gate_up(const void* const* w, const void* bias, const float* x_f32, int64_t k, const int32_t* offsets,
+int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_t k, const int32_t* offsets,
                    const int32_t* pairs, const int32_t* active, const int32_t* n_active, int64_t max_active,
                    int64_t hidden, int64_t inter, float limit, int precision, float* gated, float* gated_raw,
                    hipStream_t stream) {
   const dim3 grid((unsigned)(2 * inter / kTileRows), (unsigned)max_active);
-  moe_gemv_kernel<true><<<grid, kGemvThreads, 0, stream>>>(
-      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), x_f32, gated, gated_raw,
+  moe_gemv_mfma_kernel<false><<<grid, kGemvThreads, gemv_lds_bytes((int)(hidden / 32)), stream>>>(
+      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), x, gated, gated_raw,
       offsets, pairs, active, n_active, (int)(2 * inter), (int)(hidden / 32), (int)k, limit, precision);
-  return check_launch("moe_gemv_kernel<gate_up>");
+  return check_launch("moe_gemv_mfma_kernel<gate_up>");
 }
 
 int launch_down(const void* const* w, const void* bias, const float* gated, const int32_t* offsets,
                 const int32_t* pairs, const int32_t* active, const int32_t* n_active, int64_t max_active,
                 int64_t hidden, int64_t inter, int precision, float* eo, hipStream_t stream) {
   const dim3 grid((unsigned)(hidden / kTileRows), (unsigned)max_active);
-  moe_gemv_kernel<false><<<grid, kGemvThreads, 0, stream>>>(
+  moe_gemv_mfma_kernel<true><<<grid, kGemvThreads, gemv_lds_bytes((int)(inter / 32)), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), gated, eo, nullptr, offsets,
       pairs, active, n_active, (int)hidden, (int)(inter / 32), 1, 0.0f, precision);
-  return check_launch("moe_gemv_kernel<down>");
+  return check_launch("moe_gemv_mfma_kernel<down>");
 }
 
 int launch_combine(const float* eo, const void* w, int64_t n_tok, int64_t k, int64_t hidden, void* out,
@@ -270,7 +322,7 @@ int launch_combine(const float* eo, const void* w, int64_t n_tok, int64_t k, int
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 struct LayerScratch {
-  int64_t logits, x_f32, ids, values, weights, offsets, sorted, active, n_active, gated, eo, total;
+  int64_t logits, ids, values, weights, offsets, sorted, active, n_active, gated, eo, total;
 };
 
 LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k) {
@@ -278,7 +330,6 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
   const int64_t pairs = n_tok * k;
   int64_t off = 0;
   s.logits = off;   off += align256(n_tok * n_exp * 2);
-  s.x_f32 = off;    off += align256(n_tok * hidden * 4);
   s.ids = off;      off += align256(pairs * 4);
   s.values = off;   off += align256(pairs * 4);
   s.weights = off;  off += align256(pairs * 2);
@@ -297,18 +348,18 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
 
 using namespace klc;
 
-extern "C" int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const float* x_f32, int64_t k,
+extern "C" int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t k,
                                const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
                                const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
                                float swiglu_limit, int precision, float* gated, float* gated_raw, void* stream) {
-  KLC_REQUIRE(w_gate_up && bias && x_f32 && offsets && sorted_pairs && active && n_active && gated, KLC_ERR_ARGUMENT,
+  KLC_REQUIRE(w_gate_up && bias && x && offsets && sorted_pairs && active && n_active && gated, KLC_ERR_ARGUMENT,
               "klc_moe_gate_up: null pointer");
   KLC_REQUIRE(k > 0, KLC_ERR_ARGUMENT, "klc_moe_gate_up: k=%lld", (long long)k);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "klc_moe_gate_up: unknown precision %d", precision);
   const int rc = check_gemv_shapes(hidden, inter, max_active);
   if (rc) return rc;
-  return launch_gate_up(w_gate_up, bias, x_f32, k, offsets, sorted_pairs, active, n_active, max_active, hidden, inter,
+  return launch_gate_up(w_gate_up, bias, x, k, offsets, sorted_pairs, active, n_active, max_active, hidden, inter,
                         swiglu_limit, precision, gated, gated_raw, as_stream(stream));
 }
 
@@ -390,7 +441,6 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
 
   char* ws = static_cast<char*>(workspace);
   void* logits = ws + s.logits;
-  float* x_f32 = reinterpret_cast<float*>(ws + s.x_f32);
   int32_t* ids_buf = ids ? ids : reinterpret_cast<int32_t*>(ws + s.ids);
   float* values = reinterpret_cast<float*>(ws + s.values);
   void* w_buf = weights ? weights : static_cast<void*>(ws + s.weights);
@@ -408,13 +458,13 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   };
 
   if ((rc = mark(0))) return rc;
-  if ((rc = launch_router_logits(x, router_w, router_b, logits, x_f32, n_tokens, hidden, n_experts, st))) return rc;
+  if ((rc = launch_router_logits(x, router_w, router_b, logits, nullptr, n_tokens, hidden, n_experts, st))) return rc;
   if ((rc = mark(1))) return rc;
   if ((rc = launch_topk(logits, ids_buf, values, w_buf, n_tokens, n_experts, k, st))) return rc;
   if ((rc = mark(2))) return rc;
   if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, st))) return rc;
   if ((rc = mark(3))) return rc;
-  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x_f32, k, offsets, sorted, active, n_active, max_active, hidden,
+  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, k, offsets, sorted, active, n_active, max_active, hidden,
                            inter, swiglu_limit, precision, gated, nullptr, st)))
     return rc;
   if ((rc = mark(4))) return rc;

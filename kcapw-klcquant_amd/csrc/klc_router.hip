@@ -20,70 +20,86 @@
 namespace klc {
 namespace {
 
-constexpr int kRouterTok = 8;
+constexpr int kRouterTok = 8;     // tokens per workgroup
+constexpr int kRouterChunks = 8;  // 16-byte weight chunks per lane: hidden <= 64 * 8 * 8 = 4096
 
+// One wave per (expert, block of up to 8 tokens).  The workgroup stages the
+// block's hidden rows in LDS; every lane first issues all of its weight-row
+// loads, then accumulates float64 sums of exact float32 products per token.
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
                                                             const uint16_t* __restrict__ b,
                                                             uint16_t* __restrict__ logits, float* __restrict__ x_f32,
                                                             int n_tok, int hidden, int n_exp) {
+  extern __shared__ uint16_t xs[];  // [kRouterTok][hidden]
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int t0 = blockIdx.y * kRouterTok;
   const int nt = min(kRouterTok, n_tok - t0);
-
-  if (x_f32 != nullptr && blockIdx.x == 0) {
-    const int64_t base = (int64_t)t0 * hidden;
-    for (int i = threadIdx.x; i < nt * hidden; i += blockDim.x) x_f32[base + i] = bf16_to_f32(x[base + i]);
-  }
-
   const int e = blockIdx.x * 4 + wave;
+  const int nchunk = hidden >> 3;  // hidden % 8 == 0 (checked on the host)
+
+  uint4 wv[kRouterChunks];
+  if (e < n_exp) {
+    const uint16_t* wr = w + (int64_t)e * hidden;
+#pragma unroll
+    for (int i = 0; i < kRouterChunks; ++i) {
+      const int c = lane + i * kWave;
+      wv[i] = c < nchunk ? *reinterpret_cast<const uint4*>(wr + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  const int64_t base = (int64_t)t0 * hidden;
+  for (int i = threadIdx.x; i < nt * nchunk; i += blockDim.x) {
+    const uint4 v = *reinterpret_cast<const uint4*>(x + base + (int64_t)i * 8);
+    *reinterpret_cast<uint4*>(xs + i * 8) = v;
+    if (x_f32 != nullptr && blockIdx.x == 0) {
+      const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+      float4* dst = reinterpret_cast<float4*>(x_f32 + base + (int64_t)i * 8);
+      dst[0] = make_float4(__uint_as_float(words[0] << 16), __uint_as_float(words[0] & 0xffff0000u),
+                           __uint_as_float(words[1] << 16), __uint_as_float(words[1] & 0xffff0000u));
+      dst[1] = make_float4(__uint_as_float(words[2] << 16), __uint_as_float(words[2] & 0xffff0000u),
+                           __uint_as_float(words[3] << 16), __uint_as_float(words[3] & 0xffff0000u));
+    }
+  }
+  __syncthreads();
   if (e >= n_exp) return;
 
   double acc[kRouterTok];
 #pragma unroll
-  for (int j = 0; j < kRouterTok; ++j) acc[j] = 0.0;
-
-  const uint16_t* wr = w + (int64_t)e * hidden;
-  if ((hidden & 7) == 0) {
-    const int nchunk = hidden >> 3;
-    for (int c = lane; c < nchunk; c += kWave) {
-      const uint4 wv = *reinterpret_cast<const uint4*>(wr + c * 8);
-      const uint32_t wwords[4] = {wv.x, wv.y, wv.z, wv.w};
+  for (int j = 0; j < kRouterTok; ++j) {
+    acc[j] = 0.0;
+    if (j < nt) {
+      double s = 0.0;
 #pragma unroll
-      for (int j = 0; j < kRouterTok; ++j) {
-        if (j < nt) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(x + (int64_t)(t0 + j) * hidden + c * 8);
-          const uint32_t xwords[4] = {xv.x, xv.y, xv.z, xv.w};
-          double s = 0.0;
+      for (int i = 0; i < kRouterChunks; ++i) {
+        const int c = lane + i * kWave;
+        if (c < nchunk) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xs + j * hidden + c * 8);
+          const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+          const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const float w0 = __uint_as_float(wwords[q] << 16), w1 = __uint_as_float(wwords[q] & 0xffff0000u);
-            const float x0 = __uint_as_float(xwords[q] << 16), x1 = __uint_as_float(xwords[q] & 0xffff0000u);
-            s += (double)(x0 * w0);
-            s += (double)(x1 * w1);
+            s += (double)(__uint_as_float(xw[q] << 16) * __uint_as_float(ww[q] << 16));
+            s += (double)(__uint_as_float(xw[q] & 0xffff0000u) * __uint_as_float(ww[q] & 0xffff0000u));
           }
-          acc[j] += s;
         }
       }
-    }
-  } else {
-    for (int h = lane; h < hidden; h += kWave) {
-      const float wf = bf16_to_f32(wr[h]);
-#pragma unroll
-      for (int j = 0; j < kRouterTok; ++j)
-        if (j < nt) acc[j] += (double)(bf16_to_f32(x[(int64_t)(t0 + j) * hidden + h]) * wf);
+      acc[j] = s;
     }
   }
 #pragma unroll
   for (int j = 0; j < kRouterTok; ++j) {
+    if (j < nt) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off);
+      for (int off = 32; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off);
+    }
   }
-  if (lane == 0) {
-    const float bias = bf16_to_f32(b[e]);
-    for (int j = 0; j < nt; ++j)
-      logits[(int64_t)(t0 + j) * n_exp + e] = (uint16_t)f32_to_bf16_rne((float)acc[j] + bias);
+  if (lane < nt) {
+    double mine = 0.0;
+#pragma unroll
+    for (int j = 0; j < kRouterTok; ++j)
+      if (j == lane) mine = acc[j];
+    logits[(int64_t)(t0 + lane) * n_exp + e] = (uint16_t)f32_to_bf16_rne((float)mine + bf16_to_f32(b[e]));
   }
 }
 
@@ -259,7 +275,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
 int launch_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32, int64_t n_tok,
                          int64_t hidden, int64_t n_exp, hipStream_t stream) {
   const dim3 grid((unsigned)((n_exp + 3) / 4), (unsigned)((n_tok + kRouterTok - 1) / kRouterTok));
-  router_logits_kernel<<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+  const size_t lds = (size_t)kRouterTok * hidden * sizeof(uint16_t);
+  router_logits_kernel<<<grid, 256, lds, stream>>>(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
                                                  static_cast<const uint16_t*>(b), static_cast<uint16_t*>(logits),
                                                  x_f32, (int)n_tok, (int)hidden, (int)n_exp);
   return check_launch("router_logits_kernel");
@@ -284,9 +301,11 @@ int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp) {
   KLC_REQUIRE(n_tok > 0 && hidden > 0 && n_exp > 0, KLC_ERR_ARGUMENT,
               "router: bad sizes n_tokens=%lld hidden=%lld n_experts=%lld", (long long)n_tok, (long long)hidden,
               (long long)n_exp);
-  KLC_REQUIRE(n_tok <= (int64_t)65535 * kRouterTok && hidden < (1 << 28) && n_exp <= 1024, KLC_ERR_UNSUPPORTED,
-              "router: unsupported sizes n_tokens=%lld hidden=%lld n_experts=%lld (n_experts <= 1024)",
-              (long long)n_tok, (long long)hidden, (long long)n_exp);
+  KLC_REQUIRE(hidden % 8 == 0, KLC_ERR_SHAPE, "router: hidden=%lld must be a multiple of 8", (long long)hidden);
+  KLC_REQUIRE(n_tok <= (int64_t)65535 * kRouterTok && hidden <= 64 * 8 * kRouterChunks && n_exp <= 1024,
+              KLC_ERR_UNSUPPORTED,
+              "router: unsupported sizes n_tokens=%lld hidden=%lld n_experts=%lld (hidden <= %d, n_experts <= 1024)",
+              (long long)n_tok, (long long)hidden, (long long)n_exp, 64 * 8 * kRouterChunks);
   return KLC_OK;
 }
 

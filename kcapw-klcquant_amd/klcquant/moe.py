@@ -194,7 +194,7 @@ class MoELayer:
         the host); otherwise the GPU router selects them.
         """
         w = self.w
-        logits, x_f32 = ops.router_logits(x, w.router_weight, w.router_bias, want_f32=True)
+        logits = ops.router_logits(x, w.router_weight, w.router_bias)
         values = None
         if routing is None:
             ids, values, weights = ops.topk_softmax(logits, self.k)
@@ -205,7 +205,7 @@ class MoELayer:
         k = ids.shape[1]
         offsets, sorted_pairs, active, n_active = ops.dispatch(ids, w.n_experts)
         max_active = min(w.n_experts, ids.numel())
-        gated, gated_raw = ops.gate_up(w.gate_up_table, w.gate_up_bias, x_f32, k, offsets, sorted_pairs, active,
+        gated, gated_raw = ops.gate_up(w.gate_up_table, w.gate_up_bias, x, k, offsets, sorted_pairs, active,
                                        n_active, max_active, w.hidden, w.inter, self.limit, self.precision,
                                        want_raw=True)
         eo = ops.down(w.down_table, w.down_bias, gated, offsets, sorted_pairs, active, n_active, max_active, w.hidden,

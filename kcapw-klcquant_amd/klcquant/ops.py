@@ -172,14 +172,15 @@ def pointer_table(mats: list[torch.Tensor] | torch.Tensor, device: torch.device)
     return torch.tensor(addrs, dtype=torch.int64).to(device)
 
 
-def gate_up(table: torch.Tensor, bias: torch.Tensor, x_f32: torch.Tensor, k: int, offsets, sorted_pairs, active,
+def gate_up(table: torch.Tensor, bias: torch.Tensor, x: torch.Tensor, k: int, offsets, sorted_pairs, active,
             n_active, max_active: int, hidden: int, inter: int, limit: float = 7.0, precision: str = "fp32",
             want_raw: bool = False):
-    dev = x_f32.device
+    _check_gpu("hidden", x, torch.bfloat16, 2)
+    dev = x.device
     n_pairs = sorted_pairs.numel()
     gated = torch.empty((n_pairs, inter), dtype=torch.float32, device=dev)
     raw = torch.empty_like(gated) if want_raw else None
-    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x_f32), k, _ptr(offsets), _ptr(sorted_pairs),
+    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), k, _ptr(offsets), _ptr(sorted_pairs),
              _ptr(active), _ptr(n_active), max_active, hidden, inter, float(limit), PRECISIONS[precision],
              _ptr(gated), _ptr(raw), _stream(dev))
     return (gated, raw) if want_raw else gated

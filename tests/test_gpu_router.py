@@ -21,8 +21,8 @@ def router_inputs(seed, n_tok, hidden, n_exp):
     return x, w, b
 
 
-@pytest.mark.parametrize("n_tok,hidden,n_exp", [(1, 2880, 32), (64, 2880, 128), (13, 2880, 128), (5, 100, 7),
-                                                (9, 64, 1024)])
+@pytest.mark.parametrize("n_tok,hidden,n_exp", [(1, 2880, 32), (64, 2880, 128), (13, 2880, 128), (5, 104, 7),
+                                                (9, 64, 1024), (17, 4096, 5)])
 def test_logits_bit_exact(gpu, n_tok, hidden, n_exp):
     x, w, b = router_inputs(100 + n_tok, n_tok, hidden, n_exp)
     logits, x_f32 = ops.router_logits(bf16_tensor(x, gpu), bf16_tensor(w, gpu), bf16_tensor(b, gpu), want_f32=True)
@@ -88,5 +88,10 @@ def test_router_rejects_bad_shapes(gpu):
     b = torch.zeros(8, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(ValueError):
         ops.router_logits(x, w, b)
+    from klcquant._native import KlcError
+    x2 = torch.zeros((2, 100), dtype=torch.bfloat16, device=gpu)
+    w2 = torch.zeros((8, 100), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(KlcError, match="multiple of 8"):
+        ops.router_logits(x2, w2, b)
     with pytest.raises(Exception):
         ops.topk_softmax(torch.zeros((2, 8), dtype=torch.bfloat16, device=gpu), 9)
