@@ -112,23 +112,26 @@ int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int
  * (streamed_moe_router.py:500-506, 524-529).  w_gate_up is a device array of
  * n_experts pointers to packed [2*inter rows][hidden/32 groups] matrices;
  * bias is bfloat16 [n_experts][2*inter]; x is the bfloat16 hidden state
- * [n_tokens][hidden].  Writes gated[n_pairs][inter] (the down input: rounded
- * to bfloat16 under KLC_PRECISION_BF16) and, if gated_raw is not NULL, the
- * unrounded SwiGLU output.  max_active bounds *n_active (normally
- * min(n_experts, n_pairs)).  hidden and inter must be <= 3072; hidden a
- * multiple of 64, inter of 32. */
-int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t k,
+ * [n_tokens][hidden]; pairs p = t*k + j come from klc_moe_dispatch.
+ * Writes the down input to gated_split as two bfloat16 planes
+ * [2][n_tokens*k][inter]: hi = bf16(y) and lo = bf16(y - hi) of the float32
+ * SwiGLU output y (under KLC_PRECISION_BF16, where the reference rounds y to
+ * bfloat16, lo = 0), and, if gated_raw is not NULL, y itself as float32
+ * [n_tokens*k][inter].  max_active bounds *n_active (normally
+ * min(n_experts, n_tokens*k)).  hidden and inter must be <= 3072, hidden a
+ * multiple of 64 and inter of 32. */
+int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens, int64_t k,
                     const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
                     const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
-                    float swiglu_limit, int precision, float* gated, float* gated_raw, void* stream);
+                    float swiglu_limit, int precision, void* gated_split, float* gated_raw, void* stream);
 
 /* down GEMV + bias (streamed_moe_router.py:507-511): w_down is a device array
  * of n_experts pointers to packed [hidden rows][inter/32 groups] matrices;
- * bias bfloat16 [n_experts][hidden]; gated [n_pairs][inter] ->
- * expert_out[n_pairs][hidden] float32. */
-int klc_moe_down(const void* const* w_down, const void* bias, const float* gated, const int32_t* offsets,
-                 const int32_t* sorted_pairs, const int32_t* active, const int32_t* n_active, int64_t max_active,
-                 int64_t hidden, int64_t inter, int precision, float* expert_out, void* stream);
+ * bias bfloat16 [n_experts][hidden]; gated_split as written by
+ * klc_moe_gate_up for n_pairs pairs -> expert_out[n_pairs][hidden] float32. */
+int klc_moe_down(const void* const* w_down, const void* bias, const void* gated_split, int64_t n_pairs,
+                 const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active, const int32_t* n_active,
+                 int64_t max_active, int64_t hidden, int64_t inter, int precision, float* expert_out, void* stream);
 
 /* Weighted combine in top-k order (streamed_moe_router.py:497, 512-513):
  * out[t] = bf16 sum over j of bf16(bf16(expert_out[t*k+j]) * weights[t][j]),
@@ -149,16 +152,20 @@ int klc_moe_pair_norms(const float* gated, const float* expert_out, int64_t n_pa
 
 /* ---- One MoE layer --------------------------------------------------------- */
 
-/* Scratch bytes klc_moe_layer needs for n_tokens tokens. */
+/* Scratch bytes klc_moe_layer needs for n_tokens tokens.  The workspace must
+ * be zero-filled once before its first use (it holds completion counters that
+ * every call leaves at zero again); calls that share a workspace must be
+ * ordered on one stream. */
 int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k);
 
 /* One MoE layer for a batch of tokens — the route() + _execute_mxfp4_experts
  * path (streamed_moe_router.py:257-315, 483-522) for every row of x:
  * router logits -> top-k/softmax -> dispatch -> gate_up/SwiGLU -> down ->
- * combine, all enqueued on `stream` with no host synchronisation.  Writes
+ * combine, all enqueued on `stream` with no host synchronisation (batches of
+ * up to 64 tokens run the router, top-k and dispatch as one launch).  Writes
  * out[n_tokens][hidden] bfloat16; ids/weights (optional, may be NULL) receive
- * the routing.  workspace must be 256-byte aligned and hold
- * klc_moe_workspace_bytes() bytes.  events: optional host array of
+ * the routing.  workspace must be 256-byte aligned, hold
+ * klc_moe_workspace_bytes() bytes and be zero-filled before its first use.  events: optional host array of
  * KLC_LAYER_EVENTS hipEvent_t handles recorded on `stream` before each of the
  * six kernels and after the last (NULL: no events). */
 #define KLC_LAYER_EVENTS 7

@@ -27,18 +27,28 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 constexpr int kWave = 64;
 
 // Packed ("row-tile") MXFP4 layout used by the expert GEMV kernels.  One
-// matrix of `rows` x `groups` MX blocks is stored as
+// matrix of `rows` x `groups` MX blocks (rows a multiple of 64) is stored as
 //   blocks: [rows / 64][groups][64 rows][16 bytes]
-//   scales: [rows / 64][ceil(groups / 4)][64 rows][4 bytes]   (byte g % 4)
+//   scales: [rows / 64][64 rows][4 quarters][S bytes],  S = round_up(ceil(groups / 4), 8)
 // so one wave-wide 16-byte load fetches group g of 64 consecutive rows as
-// 1 KiB of contiguous memory.
+// 1 KiB of contiguous memory, and the scale of (row r, group g) is byte g / 4
+// of the record (r, g % 4): a GEMV lane that works on groups q, q + 4, ...
+// of one row finds all of its scales in one S-byte record.
 constexpr int kTileRows = 64;
-inline int64_t packed_block_bytes(int64_t rows, int64_t groups) { return (rows / kTileRows) * groups * 1024; }
-inline int64_t packed_scale_bytes(int64_t rows, int64_t groups) {
-  return (rows / kTileRows) * ((groups + 3) / 4) * 256;
+__host__ __device__ inline int64_t packed_steps(int64_t groups) { return (groups + 3) / 4; }
+__host__ __device__ inline int64_t packed_scale_record(int64_t groups) { return (packed_steps(groups) + 7) / 8 * 8; }
+__host__ __device__ inline int64_t packed_block_bytes(int64_t rows, int64_t groups) { return (rows / kTileRows) * groups * 1024; }
+__host__ __device__ inline int64_t packed_scale_bytes(int64_t rows, int64_t groups) {
+  return (rows / kTileRows) * kTileRows * 4 * packed_scale_record(groups);
 }
-inline int64_t packed_matrix_bytes(int64_t rows, int64_t groups) {
+__host__ __device__ inline int64_t packed_matrix_bytes(int64_t rows, int64_t groups) {
   return packed_block_bytes(rows, groups) + packed_scale_bytes(rows, groups);
+}
+// Byte offset of the scale of (row, group) inside a packed matrix.
+__host__ __device__ __forceinline__ int64_t packed_scale_offset(int rows, int groups, int row, int group) {
+  const int64_t rec = ((groups + 3) / 4 + 7) / 8 * 8;
+  return (int64_t)(rows / kTileRows) * groups * 1024 +
+         ((int64_t)row * 4 + (group & 3)) * rec + (group >> 2);
 }
 
 // ---- device side -----------------------------------------------------------

@@ -23,6 +23,9 @@ int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, 
                 int64_t k, hipStream_t stream);
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
                     int32_t* active, int32_t* n_active, hipStream_t stream);
+int launch_router_fused(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
+                        int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
+                        int32_t* sorted, int32_t* active, int32_t* n_active, uint32_t* done, hipStream_t stream);
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp);
 int check_topk_args(int64_t n_tok, int64_t n_exp, int64_t k);
 int check_dispatch_args(int64_t n_pairs, int64_t n_exp);
@@ -38,10 +41,14 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-// Expert matrices arrive through a pointer table; they live in global memory.
-typedef const uint8_t __attribute__((address_space(1)))* global_u8_ptr;
-typedef const u32x4 __attribute__((address_space(1)))* global_u32x4_ptr;
-typedef const uint32_t __attribute__((address_space(1)))* global_u32_ptr;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// Raw buffer descriptor word 3 for gfx9-family buffer loads (32-bit data, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
+// A per-lane buffer offset (VGPR voffset) past every matrix: such raw-buffer
+// loads are out of range, return 0 and touch no memory.  Only voffset is ever
+// set to it; the uniform soffset always stays a valid in-matrix offset, so the
+// sum cannot wrap (matrices are far below 1 GiB).
+constexpr uint32_t kOutOfRange = 0x40000000u;
 
 // 2^(e-127) as the float32 scale operand of v_cvt_scalef32_pk_bf16_fp4; the
 // conversion is exact for e = 0..254 (e = 0 is a float32 subnormal).
@@ -67,23 +74,37 @@ __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
   return (up + 1.0f) * glu;
 }
 
-__device__ __forceinline__ uint16_t bf16_bits_rne(float f) { return (uint16_t)f32_to_bf16_rne(f); }
+// Expert GEMV on MFMA.  A workgroup streams `tpw` consecutive 64-row tiles of
+// one active expert; wave w owns rows [16w, 16w + 16) of each tile over the
+// whole input dimension.  Per 4-group step a lane holds the 16 code bytes of
+// (row l % 16, group 4s + l/16) -- the A operand of four
+// v_mfma_f32_16x16x32_bf16 (k = 8 * (l/16) + i) once decoded -- and reads the
+// matching B operand from activation rows staged once in LDS as bfloat16.
+//
+// Weight chunks stream through a ring of kRing registers: step s's slot is
+// refilled with the chunk kRing steps ahead (in this tile or the next) right
+// after it is consumed, so every wave keeps kRing KiB of HBM reads in flight
+// across tile boundaries.  kSteps is a template constant and every load is
+// unconditional straight-line code, which lets the compiler wait for exactly
+// one chunk per step (vector loads retire in order).  Past the last tile the
+// refills read the expert's first chunk again (an L2 hit, no HBM traffic).
+// The activation-row loads are issued before the ring prologue, so waiting
+// for them (the oldest loads) does not wait for any weight chunk.
+//
+// Columns are up to kVRows activation rows.  gate_up stages one row per token
+// (the bfloat16 hidden state, exact).  down stages two rows per token, the hi
+// and lo bfloat16 planes written by gate_up (hi = bf16(y), lo = bf16(y - hi)),
+// so the float32 SwiGLU output enters the product with a 2^-17 residual.  An
+// expert with more tokens than one pass holds streams its tiles once per pass.
+constexpr int kRing = 8;  // every compiled kSteps >= kRing is a multiple of it (slot s % kRing is step s of any tile)
 
-// Expert GEMV on MFMA.  Workgroup = (64-row tile, active expert); wave w owns
-// rows [16w, 16w + 16) of the tile over the whole input dimension.  Per
-// 4-group step a lane holds the 16 code bytes of (row l % 16, group 4s + l/16)
-// -- exactly the A operand of four v_mfma_f32_16x16x32_bf16 (k = 8 * (l/16) + i)
-// once decoded -- and the B operand is read from the activations staged in
-// LDS as bfloat16 rows (the same k mapping).  Columns are up to kVRows
-// activation rows: gate_up stages one row per token (x is bfloat16, exact);
-// down stages hi = bf16(g) and lo = bf16(g - hi) per token so the float32
-// SwiGLU output enters the product with a 2^-17 relative residual.
-template <bool kDown>
+template <bool kDown, int kSteps>
 __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
-    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const void* __restrict__ act,
-    float* __restrict__ out, float* __restrict__ out_raw, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ pairs, const int32_t* __restrict__ active, const int32_t* __restrict__ n_active,
-    int rows, int groups, int k_top, float limit, int precision) {
+    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
+    int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
+    float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
+    const int32_t* __restrict__ active, const int32_t* __restrict__ n_active, int rows, int groups, int k_top,
+    float limit, int precision, int tpw) {
   extern __shared__ uint16_t xs[];  // [kVRows][row_stride] bfloat16 bits
 
   const int u = blockIdx.y;
@@ -91,135 +112,259 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   const int e = active[u];
   const int pb = offsets[e];
   const int np = offsets[e + 1] - pb;
-  const int tile = blockIdx.x;
   const int tiles = rows / kTileRows;
-  const int g4 = (groups + 3) >> 2;             // 4-group steps
+  const int tile0 = blockIdx.x * tpw;
+  const int ntile = min(tpw, tiles - tile0);
+  if (ntile <= 0) return;
   const int in_dim = groups * 32;
-  const int row_stride = g4 * 128 + 8;          // bf16 elements per staged row (zero padded)
+  const int cpr = groups * 4;                   // 16-byte activation chunks per row
+  const int row_stride = kSteps * 128 + 8;      // bf16 elements per staged row (zero padded)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int lr = lane & 15;                     // row within the wave's 16 (A) / column n (B, D)
-  const int lq = lane >> 4;                     // k-quarter: group 4s + lq
-
-  // ---- issue all weight loads of this lane first ----
-  const global_u8_ptr mat = (global_u8_ptr)wptr[e];
-  const int trow = wave * 16 + lr;              // row inside the 64-row tile
-  const global_u8_ptr blk = mat + (int64_t)tile * groups * 1024 + trow * 16;
-  const global_u8_ptr scl = mat + (int64_t)tiles * groups * 1024 + (int64_t)tile * g4 * 256 + trow * 4;
-  u32x4 wv[kMaxSteps];
-  uint32_t sv[kMaxSteps];
-#pragma unroll
-  for (int s = 0; s < kMaxSteps; ++s) {
-    if (s < g4) {
-      const int g = 4 * s + lq;
-      wv[s] = g < groups ? *(global_u32x4_ptr)(blk + (int64_t)g * 1024) : u32x4{0u, 0u, 0u, 0u};
-      sv[s] = *(global_u32_ptr)(scl + (int64_t)s * 256);
-    }
-  }
-
+  const int lq = lane >> 4;                     // k-quarter: groups 4s + lq
+  constexpr int kLoads = (kVRows * kSteps * 16 + kGemvThreads - 1) / kGemvThreads;  // staging chunks per thread
+  constexpr int kR = kRing < kSteps ? kRing : kSteps;
+  static_assert(kSteps % kR == 0, "the ring must divide the step count");
   const int tok_per_pass = kDown ? kVRows / 2 : kVRows;
+  const int trow = wave * 16 + lr;              // row inside a 64-row tile
+  const int rec = ((groups + 3) / 4 + 7) / 8 * 8;
+  const uint32_t tile_bytes = (uint32_t)groups * 1024u;
+  // the expert matrix as a buffer: weight chunks and scale records are read
+  // with a per-lane VGPR offset and a uniform (SGPR) step offset
+  const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)wptr[e], (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
+  // chunk of step t in a tile = tile offset + 4096 t + voff.  kSteps is a
+  // multiple of the ring size and may exceed the real step count g4: lanes
+  // whose group 4t + lq is past the last group read out of range (0, no
+  // memory traffic) and decode with scale 0.
+  const int g4 = (groups + 3) >> 2;
+  const uint32_t voff = (uint32_t)(lq * 1024 + trow * 16);
+  const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;  // step g4 - 1
+  auto chunk = [&](uint32_t tile_off, int t, bool valid) -> u32x4 {
+    const uint32_t v = !valid || t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
+    return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, 0);
+  };
+  const uint32_t rec_voff = (uint32_t)((trow * 4 + lq) * rec);
+  const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
+
   for (int tc = 0; tc < np; tc += tok_per_pass) {
     const int nt = min(tok_per_pass, np - tc);
     const int nrows = kDown ? 2 * nt : nt;
-    // ---- stage activation rows (bf16) into LDS ----
-    __syncthreads();  // previous pass finished reading xs
-    if constexpr (!kDown) {
-      const uint16_t* x = static_cast<const uint16_t*>(act);
-      const int chunks = in_dim / 8;            // 16-byte chunks per row
-      for (int i = threadIdx.x; i < nrows * chunks; i += kGemvThreads) {
-        const int r = i / chunks, c = i - r * chunks;
-        const int tok = pairs[pb + tc + r] / k_top;
-        *reinterpret_cast<uint4*>(xs + r * row_stride + c * 8) =
-            *reinterpret_cast<const uint4*>(x + (int64_t)tok * in_dim + c * 8);
-      }
-    } else {
-      const float* g = static_cast<const float*>(act);
-      const int chunks = in_dim / 4;            // 4 floats per thread-step
-      for (int i = threadIdx.x; i < nt * chunks; i += kGemvThreads) {
-        const int t = i / chunks, c = i - t * chunks;
-        const float4 v = *reinterpret_cast<const float4*>(g + (int64_t)pairs[pb + tc + t] * in_dim + c * 4);
-        const float f[4] = {v.x, v.y, v.z, v.w};
-        uint32_t hi[2], lo[2];
+    if (tc > 0) __syncthreads();  // the previous pass finished reading xs
+
+    // ---- 1. activation-row loads (row sources are uniform: scalar loads) ----
+    int src[kVRows];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint16_t h0 = bf16_bits_rne(f[2 * h]), h1 = bf16_bits_rne(f[2 * h + 1]);
-          const uint16_t l0 = bf16_bits_rne(f[2 * h] - bf16_to_f32(h0));
-          const uint16_t l1 = bf16_bits_rne(f[2 * h + 1] - bf16_to_f32(h1));
-          hi[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-          lo[h] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-        }
-        *reinterpret_cast<uint2*>(xs + (2 * t) * row_stride + c * 4) = make_uint2(hi[0], hi[1]);
-        *reinterpret_cast<uint2*>(xs + (2 * t + 1) * row_stride + c * 4) = make_uint2(lo[0], lo[1]);
+    for (int r = 0; r < kVRows; ++r) {
+      const int rr = min(r, nrows - 1);
+      if constexpr (kDown) {
+        src[r] = pairs[pb + tc + (rr >> 1)];
+      } else {
+        src[r] = pairs[pb + tc + rr] / k_top;
       }
     }
-    // zero the padding beyond in_dim (its A operand is zero; keep 0 * pad finite)
-    const int pad = g4 * 128 - in_dim;
-    for (int i = threadIdx.x; i < nrows * pad; i += kGemvThreads) {
-      const int r = i / pad;
-      xs[r * row_stride + in_dim + (i - r * pad)] = 0;
+    u32x4 xv[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int id = min((int)threadIdx.x + i * kGemvThreads, nrows * cpr - 1);
+      const int r = id / cpr;
+      const int c = id - r * cpr;
+      int srow = src[0];
+#pragma unroll
+      for (int q = 1; q < kVRows; ++q) srow = r == q ? src[q] : srow;
+      const uint16_t* p = act + (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim + c * 8;
+      xv[i] = *reinterpret_cast<const u32x4*>(p);
+    }
+
+    // ---- 2. scale record of the first tile, then the ring prologue ----
+    // scale record of (row, quarter) in a tile: byte s = scale of group 4s + lq
+    constexpr int kRecWords = (kSteps + 7) / 8 * 2;
+    auto load_rec = [&](int tile, uint32_t* dst) {
+      const uint32_t soff = scale_base + (uint32_t)(tile * kTileRows * 4 * rec);
+#pragma unroll
+      for (int i = 0; i < kRecWords / 2; ++i) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, rec_voff + 8u * min(i, rec / 8 - 1), soff, 0);
+        dst[2 * i] = v.x;
+        dst[2 * i + 1] = v.y;
+      }
+    };
+    uint32_t sc[kRecWords], sc_next[kRecWords];
+    load_rec(tile0, sc);
+    uint32_t tb = (uint32_t)tile0 * tile_bytes;
+    u32x4 ring[kR];
+#pragma unroll
+    for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
+
+    // ---- 3. activation rows into LDS (waits only for the oldest loads) ----
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int id = (int)threadIdx.x + i * kGemvThreads;
+      const int r = id / cpr;
+      const int c = id - r * cpr;
+      // ids past the staged rows land in row 0's spare 16-byte slot, which nothing reads
+      const int dst = id < nrows * cpr ? r * row_stride + c * 8 : row_stride - 8;
+      *reinterpret_cast<u32x4*>(xs + dst) = xv[i];
+    }
+    {
+      const int pad = kSteps * 128 - in_dim;  // zero: its A operand is zero, keep 0 * pad finite
+      for (int i = threadIdx.x; i < nrows * pad; i += kGemvThreads) {
+        const int r = i / pad;
+        xs[r * row_stride + in_dim + (i - r * pad)] = 0;
+      }
     }
     __syncthreads();
 
-    // ---- MFMA main loop ----
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    const bool has_col = lr < nrows;
-    const uint16_t* xrow = xs + lr * row_stride + lq * 32;
+    // B operand rows: column n = lr reads staged row min(n, kVRows - 1) without
+    // masking; columns past the live rows produce outputs nobody stores (an
+    // MFMA output column depends only on its own B column)
+    const uint16_t* xrow = xs + min(lr, kVRows - 1) * row_stride + lq * 32;
+    for (int ti = 0; ti < ntile; ++ti) {
+      const int tile = tile0 + ti;
+      // refills past this tile read the next one; past the last tile they read
+      // out of range (0, no memory traffic) at a valid tile offset
+      const bool has_next = ti + 1 < ntile;
+      const uint32_t nb = has_next ? tb + tile_bytes : tb;
+      // the next tile's scale record is issued before the first refill that
+      // reads the next tile, so waiting for it never waits for a ring load
+      const int next_tile = has_next ? tile + 1 : tile;
+      if constexpr (kSteps <= kR) load_rec(next_tile, sc_next);
+
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      // B operands are read one step ahead of their MFMAs (LDS latency)
+      bf16x8_t bcur[4], bnext[4];
 #pragma unroll
-    for (int s = 0; s < kMaxSteps; ++s) {
-      if (s < g4) {
-        const float scale = cvt_scale((sv[s] >> (8 * lq)) & 0xffu);
-        const uint32_t words[4] = {wv[s].x, wv[s].y, wv[s].z, wv[s].w};
+      for (int j = 0; j < 4; ++j) bcur[j] = *reinterpret_cast<const bf16x8_t*>(xrow + j * 8);
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        __builtin_amdgcn_sched_barrier(0);  // keep each step's decode next to its MFMAs
+        if constexpr (kSteps > kR) {
+          if (s == kSteps - kR) load_rec(next_tile, sc_next);
+        }
+        // the chunk is invariant across passes; an empty asm "modifying" it
+        // keeps the decode inside the loop instead of hoisting every step's
+        // decoded operands (16 registers each) out of it
+        asm volatile("" : "+v"(ring[s % kR]));
+        const u32x4 w = ring[s % kR];
+        {
+          const int t = s + kR;  // refill: kR steps ahead
+          ring[s % kR] = t < kSteps ? chunk(tb, t, true) : chunk(nb, t - kSteps, has_next);
+        }
+        if (s + 1 < kSteps) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            bnext[j] = *reinterpret_cast<const bf16x8_t*>(xrow + (s + 1) * 128 + j * 8);
+        }
+        // 2^(e-127) as float32 bits (e = 0: the subnormal 2^-127; e = 255: inf,
+        // which the conversion reads as the MX NaN scale); a lane past the
+        // last group uses scale 0 (finite E2M1 values times 0 are +-0)
+        const uint32_t eb = (sc[s >> 2] >> (8 * (s & 3))) & 0xffu;
+        uint32_t sbits = eb == 0u ? 0x00400000u : (eb << 23);
+        sbits = 4 * s + lq < groups ? sbits : 0u;
+        const float scale = __uint_as_float(sbits);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const bf16x8_t a = decode8(words[j], scale);
-          bf16x8_t b = {};
-          if (has_col) b = *reinterpret_cast<const bf16x8_t*>(xrow + s * 128 + j * 8);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+          const bf16x8_t a = decode8(w[j], scale);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bcur[j], acc, 0, 0, 0);
+        }
+        if (s + 1 < kSteps) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bcur[j] = bnext[j];
         }
       }
-    }
+      tb = nb;
+#pragma unroll
+      for (int i = 0; i < kRecWords; ++i) sc[i] = sc_next[i];
 
-    // ---- epilogue: lane holds rows 4*lq + v (v = 0..3) of the wave's 16, column lr ----
-    const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
-    float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-    if constexpr (!kDown) {
-      if (lr < nt) {
-        const int pair = pairs[pb + tc + lr];
-        const int half = rows >> 1;
+      // ---- epilogue: lane holds rows 4*lq + v (v = 0..3) of the wave's 16, column lr ----
+      const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
+      float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+      if constexpr (!kDown) {
+        if (lr < nt) {
+          const int pair = pairs[pb + tc + lr];
+          const int half = rows >> 1;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float gate = v[2 * h], up = v[2 * h + 1];
-          if (precision == KLC_PRECISION_BF16) {
-            gate = round_bf16(gate);
-            up = round_bf16(up);
+          for (int h = 0; h < 2; ++h) {
+            float gate = v[2 * h], up = v[2 * h + 1];
+            if (precision == KLC_PRECISION_BF16) {
+              gate = round_bf16(gate);
+              up = round_bf16(up);
+            }
+            gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
+            up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
+            const float y = swiglu(gate, up, limit);
+            const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
+            if (out_raw) out_raw[idx] = y;
+            // down input: hi/lo bfloat16 planes (lo = 0 when the reference rounds to bf16)
+            const uint32_t hi = f32_to_bf16_rne(y);
+            const uint32_t lo = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y - bf16_to_f32(hi));
+            out_split[idx] = (uint16_t)hi;
+            out_split[out_plane + idx] = (uint16_t)lo;
           }
-          gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
-          up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
-          const float y = swiglu(gate, up, limit);
-          const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
-          if (out_raw) out_raw[idx] = y;
-          out[idx] = precision == KLC_PRECISION_BF16 ? round_bf16(y) : y;
         }
-      }
-    } else {
-      // column 2t holds the hi part of token t, column 2t + 1 the lo part
+      } else {
+        // column 2t holds the hi part of token t, column 2t + 1 the lo part
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
-      if ((lr & 1) == 0 && (lr >> 1) < nt) {
-        const int pair = pairs[pb + tc + (lr >> 1)];
-        float o[4];
+        for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
+        if ((lr & 1) == 0 && (lr >> 1) < nt) {
+          const int pair = pairs[pb + tc + (lr >> 1)];
+          float o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float t = precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i];
-          o[i] = t + bf16_to_f32(bias[(int64_t)e * rows + row0 + i]);
+          for (int i = 0; i < 4; ++i) {
+            const float t = precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i];
+            o[i] = t + bf16_to_f32(bias[(int64_t)e * rows + row0 + i]);
+          }
+          *reinterpret_cast<float4*>(out + (int64_t)pair * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
         }
-        *reinterpret_cast<float4*>(out + (int64_t)pair * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
       }
     }
   }
 }
 
-size_t gemv_lds_bytes(int groups) { return (size_t)kVRows * (((groups + 3) / 4) * 128 + 8) * 2; }
+// Step counts with a compiled kernel; other shapes round up (the extra steps
+// read out of range and decode to zero).  Each is <= kRing or a multiple of it.
+constexpr int kStepSizes[] = {1, 2, 3, 4, 6, 8, 16, 24};
+
+int gemv_steps(int groups) {
+  const int g4 = (groups + 3) / 4;
+  for (int s : kStepSizes)
+    if (s >= g4) return s;
+  return -1;
+}
+
+template <bool kDown>
+using GemvKernel = void (*)(const uint8_t* const*, const uint16_t*, const uint16_t*, int64_t, float*, uint16_t*,
+                            int64_t, float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int,
+                            int, float, int, int);
+
+template <bool kDown>
+GemvKernel<kDown> gemv_kernel_for(int steps) {
+  switch (steps) {
+    case 1: return moe_gemv_mfma_kernel<kDown, 1>;
+    case 2: return moe_gemv_mfma_kernel<kDown, 2>;
+    case 3: return moe_gemv_mfma_kernel<kDown, 3>;
+    case 4: return moe_gemv_mfma_kernel<kDown, 4>;
+    case 6: return moe_gemv_mfma_kernel<kDown, 6>;
+    case 8: return moe_gemv_mfma_kernel<kDown, 8>;
+    case 16: return moe_gemv_mfma_kernel<kDown, 16>;
+    case 24: return moe_gemv_mfma_kernel<kDown, 24>;
+    default: return nullptr;
+  }
+}
+
+size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * (steps * 128 + 8) * 2; }
+
+// Tiles each workgroup streams: enough workgroups to give every CU about three
+// (the LDS-limited residency), fewer tiles per workgroup when few experts are
+// active.  max_active is an upper bound of the active experts.
+int tiles_per_workgroup(int tiles, int64_t max_active) {
+  const int64_t target = 3 * 256;
+  int64_t tpw = (int64_t)tiles * max_active / target;
+  if (tpw < 1) tpw = 1;
+  if (tpw > tiles) tpw = tiles;
+  return (int)tpw;
+}
+
 
 // out[t][h] over k slots in order; every step rounded to bfloat16.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ eo, const uint16_t* __restrict__ w,
@@ -290,24 +435,33 @@ int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t max_active) {
   return KLC_OK;
 }
 
-int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_t k, const int32_t* offsets,
-                   const int32_t* pairs, const int32_t* active, const int32_t* n_active, int64_t max_active,
-                   int64_t hidden, int64_t inter, float limit, int precision, float* gated, float* gated_raw,
-                   hipStream_t stream) {
-  const dim3 grid((unsigned)(2 * inter / kTileRows), (unsigned)max_active);
-  moe_gemv_mfma_kernel<false><<<grid, kGemvThreads, gemv_lds_bytes((int)(hidden / 32)), stream>>>(
-      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), x, gated, gated_raw,
-      offsets, pairs, active, n_active, (int)(2 * inter), (int)(hidden / 32), (int)k, limit, precision);
+int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k,
+                   const int32_t* offsets, const int32_t* pairs, const int32_t* active, const int32_t* n_active,
+                   int64_t max_active, int64_t hidden, int64_t inter, float limit, int precision, void* gated_split,
+                   float* gated_raw, hipStream_t stream) {
+  const int tiles = (int)(2 * inter / kTileRows);
+  const int tpw = tiles_per_workgroup(tiles, max_active);
+  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)max_active);
+  const int steps = gemv_steps((int)(hidden / 32));
+  gemv_kernel_for<false>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
+      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
+      static_cast<const uint16_t*>(x), 0, nullptr, static_cast<uint16_t*>(gated_split), n_tok * k * inter,
+      gated_raw, offsets, pairs, active, n_active, (int)(2 * inter), (int)(hidden / 32), (int)k, limit, precision,
+      tpw);
   return check_launch("moe_gemv_mfma_kernel<gate_up>");
 }
 
-int launch_down(const void* const* w, const void* bias, const float* gated, const int32_t* offsets,
-                const int32_t* pairs, const int32_t* active, const int32_t* n_active, int64_t max_active,
-                int64_t hidden, int64_t inter, int precision, float* eo, hipStream_t stream) {
-  const dim3 grid((unsigned)(hidden / kTileRows), (unsigned)max_active);
-  moe_gemv_mfma_kernel<true><<<grid, kGemvThreads, gemv_lds_bytes((int)(inter / 32)), stream>>>(
-      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), gated, eo, nullptr, offsets,
-      pairs, active, n_active, (int)hidden, (int)(inter / 32), 1, 0.0f, precision);
+int launch_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs,
+                const int32_t* offsets, const int32_t* pairs, const int32_t* active, const int32_t* n_active,
+                int64_t max_active, int64_t hidden, int64_t inter, int precision, float* eo, hipStream_t stream) {
+  const int tiles = (int)(hidden / kTileRows);
+  const int tpw = tiles_per_workgroup(tiles, max_active);
+  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)max_active);
+  const int steps = gemv_steps((int)(inter / 32));
+  gemv_kernel_for<true>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
+      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
+      static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs, active,
+      n_active, (int)hidden, (int)(inter / 32), 1, 0.0f, precision, tpw);
   return check_launch("moe_gemv_mfma_kernel<down>");
 }
 
@@ -321,14 +475,17 @@ int launch_combine(const float* eo, const void* w, int64_t n_tok, int64_t k, int
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
+constexpr int64_t kFusedRouterTokens = 2;  // batches up to this size use the one-launch router
+
 struct LayerScratch {
-  int64_t logits, ids, values, weights, offsets, sorted, active, n_active, gated, eo, total;
+  int64_t counters, logits, ids, values, weights, offsets, sorted, active, n_active, gated, eo, total;
 };
 
 LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k) {
   LayerScratch s{};
   const int64_t pairs = n_tok * k;
   int64_t off = 0;
+  s.counters = off; off += 256;  // self-resetting completion counters (zero before first use)
   s.logits = off;   off += align256(n_tok * n_exp * 2);
   s.ids = off;      off += align256(pairs * 4);
   s.values = off;   off += align256(pairs * 4);
@@ -337,7 +494,7 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
   s.sorted = off;   off += align256(pairs * 4);
   s.active = off;   off += align256(n_exp * 4);
   s.n_active = off; off += align256(4);
-  s.gated = off;    off += align256(pairs * inter * 4);
+  s.gated = off;    off += align256(pairs * inter * 4);  // hi and lo bf16 planes
   s.eo = off;       off += align256(pairs * hidden * 4);
   s.total = off;
   return s;
@@ -348,33 +505,35 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
 
 using namespace klc;
 
-extern "C" int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t k,
-                               const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
+extern "C" int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens,
+                               int64_t k, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
                                const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
-                               float swiglu_limit, int precision, float* gated, float* gated_raw, void* stream) {
-  KLC_REQUIRE(w_gate_up && bias && x && offsets && sorted_pairs && active && n_active && gated, KLC_ERR_ARGUMENT,
-              "klc_moe_gate_up: null pointer");
-  KLC_REQUIRE(k > 0, KLC_ERR_ARGUMENT, "klc_moe_gate_up: k=%lld", (long long)k);
+                               float swiglu_limit, int precision, void* gated_split, float* gated_raw, void* stream) {
+  KLC_REQUIRE(w_gate_up && bias && x && offsets && sorted_pairs && active && n_active && gated_split,
+              KLC_ERR_ARGUMENT, "klc_moe_gate_up: null pointer");
+  KLC_REQUIRE(n_tokens > 0 && k > 0, KLC_ERR_ARGUMENT, "klc_moe_gate_up: n_tokens=%lld k=%lld", (long long)n_tokens,
+              (long long)k);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "klc_moe_gate_up: unknown precision %d", precision);
   const int rc = check_gemv_shapes(hidden, inter, max_active);
   if (rc) return rc;
-  return launch_gate_up(w_gate_up, bias, x, k, offsets, sorted_pairs, active, n_active, max_active, hidden, inter,
-                        swiglu_limit, precision, gated, gated_raw, as_stream(stream));
+  return launch_gate_up(w_gate_up, bias, x, n_tokens, k, offsets, sorted_pairs, active, n_active, max_active, hidden,
+                        inter, swiglu_limit, precision, gated_split, gated_raw, as_stream(stream));
 }
 
-extern "C" int klc_moe_down(const void* const* w_down, const void* bias, const float* gated, const int32_t* offsets,
-                            const int32_t* sorted_pairs, const int32_t* active, const int32_t* n_active,
-                            int64_t max_active, int64_t hidden, int64_t inter, int precision, float* expert_out,
-                            void* stream) {
-  KLC_REQUIRE(w_down && bias && gated && offsets && sorted_pairs && active && n_active && expert_out,
+extern "C" int klc_moe_down(const void* const* w_down, const void* bias, const void* gated_split, int64_t n_pairs,
+                            const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
+                            const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter, int precision,
+                            float* expert_out, void* stream) {
+  KLC_REQUIRE(w_down && bias && gated_split && offsets && sorted_pairs && active && n_active && expert_out,
               KLC_ERR_ARGUMENT, "klc_moe_down: null pointer");
+  KLC_REQUIRE(n_pairs > 0, KLC_ERR_ARGUMENT, "klc_moe_down: n_pairs=%lld", (long long)n_pairs);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "klc_moe_down: unknown precision %d", precision);
   const int rc = check_gemv_shapes(hidden, inter, max_active);
   if (rc) return rc;
-  return launch_down(w_down, bias, gated, offsets, sorted_pairs, active, n_active, max_active, hidden, inter,
-                     precision, expert_out, as_stream(stream));
+  return launch_down(w_down, bias, gated_split, n_pairs, offsets, sorted_pairs, active, n_active, max_active, hidden,
+                     inter, precision, expert_out, as_stream(stream));
 }
 
 extern "C" int klc_moe_combine(const float* expert_out, const void* weights, int64_t n_tokens, int64_t k,
@@ -448,8 +607,9 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   int32_t* sorted = reinterpret_cast<int32_t*>(ws + s.sorted);
   int32_t* active = reinterpret_cast<int32_t*>(ws + s.active);
   int32_t* n_active = reinterpret_cast<int32_t*>(ws + s.n_active);
-  float* gated = reinterpret_cast<float*>(ws + s.gated);
+  void* gated = ws + s.gated;
   float* eo = reinterpret_cast<float*>(ws + s.eo);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(ws + s.counters);
   hipStream_t st = as_stream(stream);
   auto mark = [&](int i) -> int {
     if (events == nullptr) return KLC_OK;
@@ -458,18 +618,28 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   };
 
   if ((rc = mark(0))) return rc;
-  if ((rc = launch_router_logits(x, router_w, router_b, logits, nullptr, n_tokens, hidden, n_experts, st))) return rc;
-  if ((rc = mark(1))) return rc;
-  if ((rc = launch_topk(logits, ids_buf, values, w_buf, n_tokens, n_experts, k, st))) return rc;
-  if ((rc = mark(2))) return rc;
-  if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, st))) return rc;
+  if (n_tokens <= kFusedRouterTokens) {
+    // decode batches: logits, top-k and dispatch in one launch
+    if ((rc = launch_router_fused(x, router_w, router_b, logits, n_tokens, hidden, n_experts, k, ids_buf, values,
+                                  w_buf, offsets, sorted, active, n_active, counters, st)))
+      return rc;
+    if ((rc = mark(1))) return rc;
+    if ((rc = mark(2))) return rc;
+  } else {
+    if ((rc = launch_router_logits(x, router_w, router_b, logits, nullptr, n_tokens, hidden, n_experts, st)))
+      return rc;
+    if ((rc = mark(1))) return rc;
+    if ((rc = launch_topk(logits, ids_buf, values, w_buf, n_tokens, n_experts, k, st))) return rc;
+    if ((rc = mark(2))) return rc;
+    if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, st))) return rc;
+  }
   if ((rc = mark(3))) return rc;
-  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, k, offsets, sorted, active, n_active, max_active, hidden,
-                           inter, swiglu_limit, precision, gated, nullptr, st)))
+  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, offsets, sorted, active, n_active, max_active,
+                           hidden, inter, swiglu_limit, precision, gated, nullptr, st)))
     return rc;
   if ((rc = mark(4))) return rc;
-  if ((rc = launch_down(w_down, down_bias, gated, offsets, sorted, active, n_active, max_active, hidden, inter,
-                        precision, eo, st)))
+  if ((rc = launch_down(w_down, down_bias, gated, n_tokens * k, offsets, sorted, active, n_active, max_active, hidden,
+                        inter, precision, eo, st)))
     return rc;
   if ((rc = mark(5))) return rc;
   if ((rc = launch_combine(eo, w_buf, n_tokens, k, hidden, out, st))) return rc;

@@ -57,13 +57,7 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
   const int col = col0 + c_oc * 8;
 
   const uint8_t* mat = blocks;
-  int64_t scale_base = 0;
-  const int tiles = rows / kTileRows;
-  const int g4 = (groups + 3) >> 2;
-  if constexpr (kPacked) {
-    mat = blocks + (int64_t)m * packed_stride;
-    scale_base = (int64_t)tiles * groups * 1024;
-  }
+  if constexpr (kPacked) mat = blocks + (int64_t)m * packed_stride;
 
   for (int g0 = 0; g0 < groups; g0 += kDqGroups) {
     const int ng = min(kDqGroups, groups - g0);
@@ -76,7 +70,7 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
         if constexpr (kPacked) {
           const uint8_t* src = mat + ((int64_t)(r / kTileRows) * groups + g) * 1024 + (r % kTileRows) * 16;
           v = *reinterpret_cast<const uint4*>(src);
-          e = mat[scale_base + ((int64_t)(r / kTileRows) * g4 + (g >> 2)) * 256 + (r % kTileRows) * 4 + (g & 3)];
+          e = mat[packed_scale_offset(rows, groups, r, g)];
         } else {
           const int64_t chunk = ((int64_t)m * rows + r) * groups + g;
           v = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
@@ -133,34 +127,45 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
   }
 }
 
-// Checkpoint layout -> row-tile layout.  One thread per (matrix, tile, group
-// slot, row in tile); group slots run to ceil(groups/4)*4 so the scale padding
-// is written (as zero) too.  Writes are coalesced; this runs once per load.
-__global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ blocks,
-                                                   const uint8_t* __restrict__ scales, uint8_t* __restrict__ packed,
-                                                   int64_t n_mat, int rows, int groups, int64_t packed_stride) {
+// Checkpoint layout -> row-tile layout: one thread per (matrix, tile, group,
+// row in tile) 16-byte chunk, writes coalesced; runs once per load.
+__global__ __launch_bounds__(256) void pack_blocks_kernel(const uint8_t* __restrict__ blocks,
+                                                          uint8_t* __restrict__ packed, int64_t n_mat, int rows,
+                                                          int groups, int64_t packed_stride) {
   const int tiles = rows / kTileRows;
-  const int g4 = (groups + 3) >> 2;
-  const int gslots = g4 * 4;
-  const int64_t total = n_mat * tiles * gslots * kTileRows;
+  const int64_t total = n_mat * tiles * groups * kTileRows;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int rr = (int)(idx % kTileRows);
     int64_t rest = idx / kTileRows;
-    const int g = (int)(rest % gslots);
-    rest /= gslots;
+    const int g = (int)(rest % groups);
+    rest /= groups;
     const int tile = (int)(rest % tiles);
     const int64_t m = rest / tiles;
     const int r = tile * kTileRows + rr;
-    uint8_t* base = packed + m * packed_stride;
-    uint8_t e = 0;
-    if (g < groups) {
-      const int64_t chunk = (m * rows + r) * groups + g;
-      const uint4 v = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
-      *reinterpret_cast<uint4*>(base + ((int64_t)tile * groups + g) * 1024 + rr * 16) = v;
-      e = scales[chunk];
-    }
-    base[(int64_t)tiles * groups * 1024 + ((int64_t)tile * g4 + (g >> 2)) * 256 + rr * 4 + (g & 3)] = e;
+    const uint4 v = *reinterpret_cast<const uint4*>(blocks + ((m * rows + r) * groups + g) * 16);
+    *reinterpret_cast<uint4*>(packed + m * packed_stride + ((int64_t)tile * groups + g) * 1024 + rr * 16) = v;
+  }
+}
+
+// Scale records: one thread per (matrix, row, quarter, step) byte, padding zero.
+__global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ scales,
+                                                          uint8_t* __restrict__ packed, int64_t n_mat, int rows,
+                                                          int groups, int64_t packed_stride) {
+  const int rec = (int)packed_scale_record(groups);
+  const int64_t total = n_mat * rows * 4 * rec;
+  const int64_t scale_base = packed_block_bytes(rows, groups);
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int s = (int)(idx % rec);
+    int64_t rest = idx / rec;
+    const int q = (int)(rest % 4);
+    rest /= 4;
+    const int r = (int)(rest % rows);
+    const int64_t m = rest / rows;
+    const int g = 4 * s + q;
+    const uint8_t e = g < groups ? scales[(m * rows + r) * groups + g] : (uint8_t)0;
+    packed[m * packed_stride + scale_base + ((int64_t)r * 4 + q) * rec + s] = e;
   }
 }
 
@@ -222,14 +227,18 @@ extern "C" int klc_mxfp4_pack(const void* blocks, const void* scales, void* pack
   KLC_REQUIRE(n_mat >= 0, KLC_ERR_ARGUMENT, "klc_mxfp4_pack: n_mat=%lld", (long long)n_mat);
   KLC_REQUIRE(out_dim < (1 << 30) && groups < (1 << 24), KLC_ERR_UNSUPPORTED, "klc_mxfp4_pack: matrix too large");
   if (n_mat == 0) return KLC_OK;
-  const int64_t total = n_mat * (out_dim / kTileRows) * ((groups + 3) / 4) * 4 * kTileRows;
-  const int64_t blocks_needed = (total + 255) / 256;
-  const unsigned grid = (unsigned)(blocks_needed < 65536 ? blocks_needed : 65536);
-  pack_kernel<<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint8_t*>(blocks),
-                                                     static_cast<const uint8_t*>(scales),
-                                                     static_cast<uint8_t*>(packed), n_mat, (int)out_dim, (int)groups,
-                                                     stride);
-  return check_launch("pack_kernel");
+  hipStream_t st = as_stream(stream);
+  const int64_t chunks = n_mat * out_dim * groups;
+  const unsigned grid_b = (unsigned)((chunks + 255) / 256 < 65536 ? (chunks + 255) / 256 : 65536);
+  pack_blocks_kernel<<<grid_b, 256, 0, st>>>(static_cast<const uint8_t*>(blocks), static_cast<uint8_t*>(packed), n_mat,
+                                             (int)out_dim, (int)groups, stride);
+  const int rc = check_launch("pack_blocks_kernel");
+  if (rc) return rc;
+  const int64_t bytes = n_mat * out_dim * 4 * packed_scale_record(groups);
+  const unsigned grid_s = (unsigned)((bytes + 255) / 256 < 65536 ? (bytes + 255) / 256 : 65536);
+  pack_scales_kernel<<<grid_s, 256, 0, st>>>(static_cast<const uint8_t*>(scales), static_cast<uint8_t*>(packed),
+                                             n_mat, (int)out_dim, (int)groups, stride);
+  return check_launch("pack_scales_kernel");
 }
 
 extern "C" int klc_mxfp4_dequant_packed(const void* packed, void* out, int64_t n_mat, int64_t out_dim,

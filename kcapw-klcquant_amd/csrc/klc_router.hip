@@ -26,12 +26,9 @@ constexpr int kRouterChunks = 8;  // 16-byte weight chunks per lane: hidden <= 6
 // One wave per (expert, block of up to 8 tokens).  The workgroup stages the
 // block's hidden rows in LDS; every lane first issues all of its weight-row
 // loads, then accumulates float64 sums of exact float32 products per token.
-__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ b,
-                                                            uint16_t* __restrict__ logits, float* __restrict__ x_f32,
-                                                            int n_tok, int hidden, int n_exp) {
-  extern __shared__ uint16_t xs[];  // [kRouterTok][hidden]
+__device__ void router_logits_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                   const uint16_t* __restrict__ b, uint16_t* logits, float* __restrict__ x_f32,
+                                   int n_tok, int hidden, int n_exp, uint16_t* xs /* LDS [kRouterTok][hidden] */) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int t0 = blockIdx.y * kRouterTok;
@@ -62,7 +59,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     }
   }
   __syncthreads();
-  if (e >= n_exp) return;
+  if (e >= n_exp) return;  // the caller synchronises the block only after this function
 
   double acc[kRouterTok];
 #pragma unroll
@@ -103,6 +100,15 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
   }
 }
 
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ b,
+                                                            uint16_t* __restrict__ logits, float* __restrict__ x_f32,
+                                                            int n_tok, int hidden, int n_exp) {
+  extern __shared__ uint16_t rxs[];
+  router_logits_tile(x, w, b, logits, x_f32, n_tok, hidden, n_exp, rxs);
+}
+
 // Orderable key: larger key = larger logit; NaN is the largest value; -0 == +0;
 // among equal values the lower expert index has the larger key.
 __device__ __forceinline__ uint64_t logit_key(uint32_t bf16bits, int idx) {
@@ -128,15 +134,10 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
-                                                           int32_t* __restrict__ ids, float* __restrict__ values,
-                                                           uint16_t* __restrict__ weights, int n_tok, int n_exp,
-                                                           int k) {
-  const int wave = threadIdx.x >> 6;
+// Top-k + softmax of one token's logits row by one wave.
+__device__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t, int32_t* __restrict__ ids,
+                                 float* __restrict__ values, uint16_t* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= n_tok) return;
-  const uint16_t* row = logits + (int64_t)t * n_exp;
   uint64_t keys[kTopkMaxPerLane];
 #pragma unroll
   for (int s = 0; s < kTopkMaxPerLane; ++s) {
@@ -165,11 +166,20 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __res
   double sum = 0.0;
   for (int r = 0; r < k; ++r) sum += exp((double)__shfl(my_val, r) - mx);
   if (lane < k) {
-    const int64_t o = (int64_t)t * k + lane;
+    const int64_t o = t * k + lane;
     ids[o] = my_id;
     if (values) values[o] = my_val;
     weights[o] = (uint16_t)f32_to_bf16_rne((float)(exp((double)my_val - mx) / sum));
   }
+}
+
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
+                                                           int32_t* __restrict__ ids, float* __restrict__ values,
+                                                           uint16_t* __restrict__ weights, int n_tok, int n_exp,
+                                                           int k) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= n_tok) return;
+  topk_softmax_row(logits + (int64_t)t * n_exp, n_exp, k, t, ids, values, weights);
 }
 
 constexpr int kDispatchThreads = 256;
@@ -205,20 +215,25 @@ __device__ void block_exclusive_scan_256(int32_t* v, int n, int32_t* total) {
   }
 }
 
-__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_t* __restrict__ ids, int n_pairs,
-                                                                    int n_exp, int32_t* __restrict__ offsets,
-                                                                    int32_t* __restrict__ sorted,
-                                                                    int32_t* __restrict__ active,
-                                                                    int32_t* __restrict__ n_active) {
-  // cnt[e * chunks + c]: pairs of expert e in chunk c (then its exclusive prefix)
-  __shared__ uint16_t cnt[kDispatchMaxExperts * kDispatchThreads];
-  __shared__ int32_t total[kDispatchMaxExperts];
-  __shared__ int32_t flags[kDispatchMaxExperts];
-  __shared__ int32_t sums[2];
+// LDS bytes block_dispatch needs for n_pairs pairs over n_exp experts.
+__host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int n_exp) {
+  return (size_t)n_exp * (n_pairs < kDispatchThreads ? n_pairs : kDispatchThreads) * sizeof(uint16_t) +
+         2 * kDispatchMaxExperts * sizeof(int32_t) + 2 * sizeof(int32_t);
+}
 
+// Stable counting sort of the pairs by expert, by one 256-thread block.
+// lds holds dispatch_lds_bytes(n_pairs, n_exp) bytes.
+__device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
+                               int32_t* __restrict__ sorted, int32_t* __restrict__ active,
+                               int32_t* __restrict__ n_active, char* lds) {
   const int tid = threadIdx.x;
   const int chunks = n_pairs < kDispatchThreads ? n_pairs : kDispatchThreads;
   const int per = (n_pairs + chunks - 1) / chunks;
+  // cnt[e * chunks + c]: pairs of expert e in chunk c (then its exclusive prefix)
+  uint16_t* cnt = reinterpret_cast<uint16_t*>(lds);
+  int32_t* total = reinterpret_cast<int32_t*>(lds + (size_t)n_exp * chunks * sizeof(uint16_t));
+  int32_t* flags = total + kDispatchMaxExperts;
+  int32_t* sums = flags + kDispatchMaxExperts;
 
   for (int i = tid; i < n_exp * chunks; i += kDispatchThreads) cnt[i] = 0;
   __syncthreads();
@@ -270,6 +285,53 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
   }
 }
 
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_t* __restrict__ ids, int n_pairs,
+                                                                    int n_exp, int32_t* __restrict__ offsets,
+                                                                    int32_t* __restrict__ sorted,
+                                                                    int32_t* __restrict__ active,
+                                                                    int32_t* __restrict__ n_active) {
+  extern __shared__ char dlds[];
+  block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, dlds);
+}
+
+// Router for decode batches in one launch: every workgroup computes its
+// (4 experts x 8 tokens) logits tile; the last workgroup to finish (counted
+// in *done, which it resets to 0) then selects the top-k of every token and
+// builds the expert-sorted dispatch.  Release/acquire fences at agent scope
+// make the other workgroups' logits visible across XCDs.
+__global__ __launch_bounds__(256) void router_fused_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ b, uint16_t* logits,
+                                                           int n_tok, int hidden, int n_exp, int k, int32_t* ids,
+                                                           float* __restrict__ values, uint16_t* __restrict__ weights,
+                                                           int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
+                                                           int32_t* __restrict__ active,
+                                                           int32_t* __restrict__ n_active, uint32_t* done) {
+  extern __shared__ char flds[];
+  router_logits_tile(x, w, b, logits, nullptr, n_tok, hidden, n_exp, reinterpret_cast<uint16_t*>(flds));
+  __shared__ uint32_t last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const uint32_t n_blocks = gridDim.x * gridDim.y;
+    const uint32_t prev = atomicAdd(done, 1u);
+    last = prev == n_blocks - 1 ? 1u : 0u;
+    if (last) {
+      *done = 0u;  // ready for the next launch
+      __threadfence();
+    }
+  }
+  __syncthreads();
+  if (!last) return;
+  for (int t = threadIdx.x >> 6; t < n_tok; t += 4) {
+    const uint16_t* row = logits + (int64_t)t * n_exp;
+    topk_softmax_row(row, n_exp, k, t, ids, values, weights);
+  }
+  __threadfence_block();
+  __syncthreads();
+  block_dispatch(ids, n_tok * k, n_exp, offsets, sorted, active, n_active, flds);
+}
+
 }  // namespace
 
 int launch_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32, int64_t n_tok,
@@ -292,9 +354,22 @@ int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, 
 
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
                     int32_t* active, int32_t* n_active, hipStream_t stream) {
-  dispatch_kernel<<<1, kDispatchThreads, 0, stream>>>(ids, (int)n_pairs, (int)n_exp, offsets, sorted, active,
-                                                      n_active);
+  dispatch_kernel<<<1, kDispatchThreads, dispatch_lds_bytes((int)n_pairs, (int)n_exp), stream>>>(
+      ids, (int)n_pairs, (int)n_exp, offsets, sorted, active, n_active);
   return check_launch("dispatch_kernel");
+}
+
+int launch_router_fused(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
+                        int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
+                        int32_t* sorted, int32_t* active, int32_t* n_active, uint32_t* done, hipStream_t stream) {
+  const dim3 grid((unsigned)((n_exp + 3) / 4), (unsigned)((n_tok + kRouterTok - 1) / kRouterTok));
+  const size_t lds_logits = (size_t)kRouterTok * hidden * sizeof(uint16_t);
+  const size_t lds_dispatch = dispatch_lds_bytes((int)(n_tok * k), (int)n_exp);
+  router_fused_kernel<<<grid, 256, lds_logits > lds_dispatch ? lds_logits : lds_dispatch, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
+      static_cast<uint16_t*>(logits), (int)n_tok, (int)hidden, (int)n_exp, (int)k, ids, values,
+      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, done);
+  return check_launch("router_fused_kernel");
 }
 
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp) {

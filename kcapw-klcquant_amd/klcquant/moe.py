@@ -153,7 +153,8 @@ class MoELayer:
         ws = self._ws.get(n_tokens)
         if ws is None:
             nbytes = ops.workspace_bytes(n_tokens, self.w.hidden, self.w.inter, self.w.n_experts, self.k)
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=self.w.device)
+            # zero-filled once: it carries completion counters that every call resets
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=self.w.device)
             self._ws[n_tokens] = ws
         return ws
 

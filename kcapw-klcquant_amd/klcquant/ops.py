@@ -175,23 +175,26 @@ def pointer_table(mats: list[torch.Tensor] | torch.Tensor, device: torch.device)
 def gate_up(table: torch.Tensor, bias: torch.Tensor, x: torch.Tensor, k: int, offsets, sorted_pairs, active,
             n_active, max_active: int, hidden: int, inter: int, limit: float = 7.0, precision: str = "fp32",
             want_raw: bool = False):
+    """Returns the down input as bf16 hi/lo planes ``[2, B * k, I]`` (and the float32 SwiGLU output)."""
     _check_gpu("hidden", x, torch.bfloat16, 2)
     dev = x.device
-    n_pairs = sorted_pairs.numel()
-    gated = torch.empty((n_pairs, inter), dtype=torch.float32, device=dev)
-    raw = torch.empty_like(gated) if want_raw else None
-    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), k, _ptr(offsets), _ptr(sorted_pairs),
+    n_tok = x.shape[0]
+    split = torch.empty((2, n_tok * k, inter), dtype=torch.bfloat16, device=dev)
+    raw = torch.empty((n_tok * k, inter), dtype=torch.float32, device=dev) if want_raw else None
+    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), n_tok, k, _ptr(offsets), _ptr(sorted_pairs),
              _ptr(active), _ptr(n_active), max_active, hidden, inter, float(limit), PRECISIONS[precision],
-             _ptr(gated), _ptr(raw), _stream(dev))
-    return (gated, raw) if want_raw else gated
+             _ptr(split), _ptr(raw), _stream(dev))
+    return (split, raw) if want_raw else split
 
 
-def down(table: torch.Tensor, bias: torch.Tensor, gated: torch.Tensor, offsets, sorted_pairs, active, n_active,
+def down(table: torch.Tensor, bias: torch.Tensor, gated_split: torch.Tensor, offsets, sorted_pairs, active, n_active,
          max_active: int, hidden: int, inter: int, precision: str = "fp32") -> torch.Tensor:
-    dev = gated.device
-    eo = torch.empty((gated.shape[0], hidden), dtype=torch.float32, device=dev)
-    nat.call("klc_moe_down", _ptr(table), _ptr(bias), _ptr(gated), _ptr(offsets), _ptr(sorted_pairs), _ptr(active),
-             _ptr(n_active), max_active, hidden, inter, PRECISIONS[precision], _ptr(eo), _stream(dev))
+    _check_gpu("gated_split", gated_split, torch.bfloat16, 3)
+    dev = gated_split.device
+    n_pairs = gated_split.shape[1]
+    eo = torch.empty((n_pairs, hidden), dtype=torch.float32, device=dev)
+    nat.call("klc_moe_down", _ptr(table), _ptr(bias), _ptr(gated_split), n_pairs, _ptr(offsets), _ptr(sorted_pairs),
+             _ptr(active), _ptr(n_active), max_active, hidden, inter, PRECISIONS[precision], _ptr(eo), _stream(dev))
     return eo
 
 

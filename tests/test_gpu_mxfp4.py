@@ -98,15 +98,21 @@ def test_pack_layout_positions(gpu):
     rows, groups = 128, 5
     blocks, scales = synth.mxfp4_expert_tensors(31, 32, 1, rows, groups * 32, 0, 255)
     packed = ops.mxfp4_pack(torch.from_numpy(blocks).to(gpu), torch.from_numpy(scales).to(gpu)).cpu().numpy()[0]
-    g4 = (groups + 3) // 4
+    rec = ((groups + 3) // 4 + 7) // 8 * 8  # scale record bytes per (row, group % 4)
     blk_bytes = rows // 64 * groups * 1024
+    assert packed.size == blk_bytes + rows * 4 * rec
     for r in (0, 1, 63, 64, 127):
         for g in range(groups):
             t, rr = divmod(r, 64)
             off = (t * groups + g) * 1024 + rr * 16
             assert np.array_equal(packed[off:off + 16], blocks[0, r, g])
-            soff = blk_bytes + (t * g4 + g // 4) * 256 + rr * 4 + g % 4
+            soff = blk_bytes + (r * 4 + g % 4) * rec + g // 4
             assert packed[soff] == scales[0, r, g]
+        # record bytes beyond the last group are zero
+        for q in range(4):
+            for s in range(rec):
+                if 4 * s + q >= groups:
+                    assert packed[blk_bytes + (r * 4 + q) * rec + s] == 0
 
 
 def test_synth_fill_matches_host_generator(gpu):
