@@ -1,0 +1,97 @@
+"""Pins the oracle's router logits, top-k, softmax weights and dispatch."""
+
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+
+import numpy as np
+
+from klcquant import synth
+from oracle import router
+from oracle.numerics import bf16_to_f32, f32_to_bf16
+
+
+def exact_logit_bits(x_row, w_row, b):
+    """bf16(f32(f32(exact dot) + b)) with the dot product as an exact rational."""
+    xs = bf16_to_f32(x_row).astype(np.float64)
+    ws = bf16_to_f32(w_row).astype(np.float64)
+    exact = sum((Fraction(float(a)) * Fraction(float(c)) for a, c in zip(xs, ws)), Fraction(0))
+    acc32 = np.float32(float(exact))  # float(Fraction) rounds correctly to float64; then to float32
+    s = np.float32(acc32 + np.float32(bf16_to_f32(np.array([b], np.uint16))[0]))
+    return int(f32_to_bf16(np.array([s]))[0])
+
+
+def test_logits_match_exact_rational_dot_products():
+    n_tok, hidden, n_exp = 3, 96, 7
+    x = synth.random_normal_bf16(1, n_tok * hidden).reshape(n_tok, hidden)
+    w = synth.random_normal_bf16(2, n_exp * hidden, 0, 0.02).reshape(n_exp, hidden)
+    b = synth.random_normal_bf16(3, n_exp, 0, 0.01)
+    got = router.router_logits(x, w, b)
+    for t in range(n_tok):
+        for e in range(n_exp):
+            assert got[t, e] == exact_logit_bits(x[t], w[e], b[e])
+
+
+def test_logits_at_full_width_match_fsum():
+    """H = 2880: float64 accumulation must round like the exact sum (math.fsum)."""
+    n_tok, hidden, n_exp = 4, 2880, 16
+    x = synth.random_normal_bf16(11, n_tok * hidden).reshape(n_tok, hidden)
+    w = synth.random_normal_bf16(12, n_exp * hidden, 0, 0.02).reshape(n_exp, hidden)
+    b = synth.random_normal_bf16(13, n_exp, 0, 0.01)
+    got = router.router_logits(x, w, b)
+    xf = bf16_to_f32(x).astype(np.float64)
+    wf = bf16_to_f32(w).astype(np.float64)
+    bf = bf16_to_f32(b)
+    for t in range(n_tok):
+        for e in range(n_exp):
+            acc = np.float32(math.fsum(xf[t] * wf[e]))  # products are exact in float64
+            assert got[t, e] == f32_to_bf16(np.array([np.float32(acc + bf[e])]))[0]
+
+
+def test_topk_tie_rule_and_order():
+    bits = f32_to_bf16(np.array([[0, 2, 1, 2, 2, 3, 2]], dtype=np.float32))
+    ids, vals = router.topk(bits, 3)
+    # value-descending, equal values by lower expert index (torch leaves ties implementation defined)
+    assert ids.tolist() == [[5, 1, 3]]
+    assert vals.tolist() == [[3.0, 2.0, 2.0]]
+
+
+def test_topk_matches_brute_force_without_ties():
+    rng = np.random.default_rng(3)
+    vals = rng.permutation(np.arange(-64, 64, dtype=np.float32))[None, :].repeat(5, 0)
+    for i in range(5):
+        vals[i] = rng.permutation(vals[i])
+    bits = f32_to_bf16(vals)
+    ids, v = router.topk(bits, 4)
+    for i in range(5):
+        want = sorted(range(128), key=lambda j: -vals[i, j])[:4]
+        assert ids[i].tolist() == want
+
+
+def test_topk_k_larger_than_experts_is_clamped():
+    ids, _ = router.topk(f32_to_bf16(np.array([[1.0, 3.0]], np.float32)), 4)
+    assert ids.tolist() == [[1, 0]]
+
+
+def test_softmax_closed_forms():
+    w = router.softmax_weights(np.array([[0.5, 0.5, 0.5, 0.5]], dtype=np.float32))
+    assert w.tolist() == [[0x3E80] * 4]  # exactly 0.25
+    w = router.softmax_weights(np.array([[7.0, -np.inf, -np.inf]], dtype=np.float32))
+    assert bf16_to_f32(w).tolist() == [[1.0, 0.0, 0.0]]
+    v = np.array([[2.0, 1.0, 0.0, -1.0]], dtype=np.float32)
+    e = np.exp(v.astype(np.float64) - 2.0)
+    want = f32_to_bf16((e / e.sum()).astype(np.float32))
+    assert np.array_equal(router.softmax_weights(v), want)
+    assert np.isnan(bf16_to_f32(router.softmax_weights(np.array([[np.nan, 1.0]], np.float32)))).all()
+
+
+def test_dispatch_is_a_stable_counting_sort():
+    ids = synth.random_ints(5, 64 * 4, 0, 9).reshape(64, 4)
+    counts, offsets, order, active = router.dispatch(ids, 12)
+    flat = ids.reshape(-1)
+    assert order.tolist() == sorted(range(flat.size), key=lambda p: (flat[p], p))
+    assert counts.tolist() == [int((flat == e).sum()) for e in range(12)]
+    assert offsets[0] == 0 and offsets[-1] == flat.size
+    assert active.tolist() == [e for e in range(12) if counts[e] > 0]
+    assert 10 not in active and 11 not in active
