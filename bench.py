@@ -22,6 +22,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -40,6 +41,10 @@ HBM_PEAK_GBPS = 8000.0
 GATE_UP_EXPERT_BYTES = 2 * INTER * (HIDDEN // 32) * 17  # 8,812,800: codes + E8M0 scales
 DOWN_EXPERT_BYTES = HIDDEN * (INTER // 32) * 17  # 4,406,400
 KERNELS = ["router_logits", "topk_softmax", "dispatch", "gate_up", "down", "combine"]
+# rocprofv3 FETCH_SIZE + WRITE_SIZE of the gate_up launches at B = 64, scaled by
+# the same counters on a copy kernel of known size (written by hand from the
+# counter runs; the file states the commands)
+TRAFFIC_PROFILE = ROOT / "profiles" / "moe_gemv_gate_up_120b_b64_hbm_traffic.txt"
 
 
 def parse_args():
@@ -53,7 +58,31 @@ def parse_args():
     ap.add_argument("--inputs", type=int, default=16, help="distinct input batches the steps rotate over")
     ap.add_argument("--cpu-tokens", type=int, default=6, help="tokens in the CPU baseline sample (0 = skip)")
     ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16"])
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB -> 1 GiB float32 copy kernel 5 times (HBM counter calibration)")
     return ap.parse_args()
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per gate_up launch (B = 64, fp32) from the committed counter summary, if present."""
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(torch, dev) -> None:
+    n = 1 << 28  # float32 elements: 1 GiB read and 1 GiB written per launch
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        torch.mul(src, 2.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_kernel": "torch.mul(float32 [2^28], 2.0)", "bytes_read": n * 4, "bytes_written": n * 4,
+                      "launches": 5}), flush=True)
 
 
 def layer_bytes(unique_experts: int, n_tok: int) -> int:
@@ -116,6 +145,9 @@ def main() -> int:
         return 2
     _native.load()
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(torch, dev)
+        return 0
     batches = [int(b) for b in args.batches.split(",") if b]
     print(f"[bench] building {args.layers} layers of {EXPERTS} experts on {torch.cuda.get_device_name(0)}",
           file=sys.stderr, flush=True)
@@ -165,6 +197,7 @@ def main() -> int:
             "layer_frac_of_peak": round(bytes_total / dt / 1e9 / HBM_PEAK_GBPS, 4),
             "kernel_us_mean": {k: round(float(kern_ms[:, i].mean()) * 1e3, 3) for i, k in enumerate(KERNELS)},
             "gate_up_gbps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+            "gate_up_bytes_per_launch": round(gu_bytes / args.steps),
         }
         per_batch.append(rec)
         print(f"[bench] B={n_tok}: {rec['us_per_step']} us/step, {rec['us_per_token']} us/token, "
@@ -199,12 +232,13 @@ def main() -> int:
         "per_batch": per_batch,
         "roofline": {
             "bound": "hbm",
-            "kernel": "moe_gemv_kernel<gate_up>",
+            "kernel": "moe_gemv_mfma_kernel<gate_up>",
             "achieved": gu_achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gu_achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic() if head["batch"] == 64 and args.precision == "fp32" else None,
+            "algorithmic_bytes_per_launch": round(head["gate_up_bytes_per_launch"]),
         },
     }
     if args.cpu_tokens > 0:

@@ -98,6 +98,12 @@ int klc_moe_router_logits(const void* x, const void* w, const void* b, void* log
 int klc_moe_topk_softmax(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tokens,
                          int64_t n_experts, int64_t k, void* stream);
 
+/* Routing weights for experts chosen on the host (streamed_moe_router.py:281-282
+ * when routing locality is enabled and the selection of :331-394 is made by
+ * the caller): weights[t][j] = bf16(softmax(values[t][:])[j]) with the maximum
+ * propagating NaN and the sum taken in slot order in float64.  k <= 1024. */
+int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens, int64_t k, void* stream);
+
 /* Expert-sorted dispatch (no reference counterpart: the reference routes one
  * token per call, streamed_moe_router.py:499).  Pairs p = t*k + j are
  * counting-sorted by expert, ties by p: offsets[n_experts+1],

@@ -50,12 +50,6 @@ constexpr int kBufferWord3 = 0x00020000;
 // sum cannot wrap (matrices are far below 1 GiB).
 constexpr uint32_t kOutOfRange = 0x40000000u;
 
-// 2^(e-127) as the float32 scale operand of v_cvt_scalef32_pk_bf16_fp4; the
-// conversion is exact for e = 0..254 (e = 0 is a float32 subnormal).
-__device__ __forceinline__ float cvt_scale(uint32_t e) {
-  return __uint_as_float(e == 0u ? 0x00400000u : (e == 255u ? 0x7f800000u : (e << 23)));
-}
-
 // Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
 __device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {
   const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);

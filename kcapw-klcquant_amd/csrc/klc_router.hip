@@ -182,6 +182,25 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __res
   topk_softmax_row(logits + (int64_t)t * n_exp, n_exp, k, t, ids, values, weights);
 }
 
+// Softmax of caller-chosen scores (one thread per token): the routing-locality
+// path picks the experts on the host and hands over their fp32 scores.  The
+// maximum propagates NaN; exponentials are summed in slot order in float64.
+__global__ __launch_bounds__(256) void softmax_weights_kernel(const float* __restrict__ values,
+                                                              uint16_t* __restrict__ weights, int n_tok, int k) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_tok) return;
+  const float* v = values + (int64_t)t * k;
+  double mx = (double)v[0];
+  for (int r = 1; r < k; ++r) {
+    const double x = (double)v[r];
+    mx = (x != x || x > mx) ? x : mx;
+  }
+  double sum = 0.0;
+  for (int r = 0; r < k; ++r) sum += exp((double)v[r] - mx);
+  for (int r = 0; r < k; ++r)
+    weights[(int64_t)t * k + r] = (uint16_t)f32_to_bf16_rne((float)(exp((double)v[r] - mx) / sum));
+}
+
 constexpr int kDispatchThreads = 256;
 constexpr int kDispatchMaxExperts = 256;
 
@@ -422,6 +441,16 @@ extern "C" int klc_moe_topk_softmax(const void* logits, int32_t* ids, float* val
   const int rc = check_topk_args(n_tokens, n_experts, k);
   if (rc) return rc;
   return launch_topk(logits, ids, values, weights, n_tokens, n_experts, k, as_stream(stream));
+}
+
+extern "C" int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens, int64_t k,
+                                       void* stream) {
+  KLC_REQUIRE(values && weights, KLC_ERR_ARGUMENT, "klc_moe_softmax_weights: null pointer");
+  KLC_REQUIRE(n_tokens > 0 && k > 0 && n_tokens < ((int64_t)1 << 31) && k <= 1024, KLC_ERR_ARGUMENT,
+              "klc_moe_softmax_weights: bad sizes n_tokens=%lld k=%lld", (long long)n_tokens, (long long)k);
+  softmax_weights_kernel<<<(unsigned)((n_tokens + 255) / 256), 256, 0, as_stream(stream)>>>(
+      values, static_cast<uint16_t*>(weights), (int)n_tokens, (int)k);
+  return check_launch("softmax_weights_kernel");
 }
 
 extern "C" int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,

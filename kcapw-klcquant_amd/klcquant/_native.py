@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "klc_mxfp4_dequant_packed": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _P]),
     "klc_moe_router_logits": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "klc_moe_topk_softmax": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "klc_moe_softmax_weights": (_I32, [_P, _P, _I64, _I64, _P]),
     "klc_moe_dispatch": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "klc_moe_gate_up": (_I32, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _F32, _I32, _P, _P, _P]),
     "klc_moe_down": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _P, _P]),

@@ -145,6 +145,15 @@ def topk_softmax(logits: torch.Tensor, k: int):
     return ids, values, weights
 
 
+def softmax_weights(values: torch.Tensor) -> torch.Tensor:
+    """fp32 scores ``[B, k]`` -> bf16 softmax weights ``[B, k]``."""
+    _check_gpu("values", values, torch.float32, 2)
+    weights = torch.empty(values.shape, dtype=torch.bfloat16, device=values.device)
+    nat.call("klc_moe_softmax_weights", _ptr(values), _ptr(weights), values.shape[0], values.shape[1],
+             _stream(values.device))
+    return weights
+
+
 def dispatch(ids: torch.Tensor, n_experts: int):
     """int32 ids ``[B, k]`` -> (offsets ``[E + 1]``, sorted_pairs ``[B * k]``, active ``[E]``, n_active ``[1]``)."""
     _check_gpu("ids", ids, torch.int32)

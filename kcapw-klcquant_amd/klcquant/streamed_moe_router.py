@@ -1,0 +1,561 @@
+"""MoE routing and expert execution with the reference router's interface.
+
+``StreamedMoERouter.route`` keeps the signature, return value and telemetry of
+streamed_moe_router.py:257-329: logits -> top-k -> softmax weights -> experts
+(gate_up, clamped SwiGLU, down) -> weighted bf16 combine, plus RouterStats
+bookkeeping.  Every numeric step runs on the GPU through the C ABI
+(klc_moe_router_logits, klc_moe_topk_softmax, klc_moe_dispatch,
+klc_moe_gate_up, klc_moe_down, klc_moe_combine): experts are read packed
+(MXFP4 codes + E8M0 scales) and dequantized inside the GEMV, never
+materialised.
+
+Differences a caller can see:
+
+* ``hidden`` may also be ``[B, H]`` (a batch of tokens routed independently);
+  the route dict then holds one list per token.  ``position`` may be a list of
+  per-row positions.
+* top-k ties between equal bf16 logits go to the lower expert index (torch's
+  order on ties is unspecified).
+* all tensors must be bf16 (the dtype the executor feeds,
+  streamed_transformer_executor.py:354-355) and on the GPU.
+
+The host reads the selected experts and weights back once per call, because
+the route dict holds them as Python lists.  With a ``ResidentExpertStore`` that
+read is the last thing the call does; with a streaming ``Mxfp4ExpertStore`` the
+host needs the experts first to bring misses into HBM.
+"""
+
+from __future__ import annotations
+
+import math
+from collections import Counter, deque
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import ops
+from .mxfp4_expert import Mxfp4ExpertStore, ResidentExpertStore
+
+
+@dataclass
+class RoutingLocalityConfig:
+    """Routing-locality knobs (fields and defaults of streamed_moe_router.py:12-35)."""
+
+    enabled: bool = False
+    sticky_strength: float = 0.0
+    sticky_decay: float = 0.92
+    semantic_guard: bool = False
+    sticky_candidate_margin: float = 0.50
+    max_sticky_bonus: float = 0.25
+    min_raw_overlap: int = 2
+    max_hot_experts_per_layer: int = 0
+    active_experts_per_token_cap: int = 0
+    exploration_margin: float = 0.25
+    cache_aware_strength: float = 0.0
+    predictive_prefetch: bool = False
+    prediction_window: int = 16
+    workload_window: int = 64
+    dynamic_active_expert_cap: bool = False
+    min_active_experts_per_token: int = 1
+    max_active_experts_per_token: int = 0
+    cap_eviction_pressure_threshold: float = 0.50
+    cap_hit_rate_expand_threshold: float = 0.65
+    thrash_evictions_per_activation: float = 0.35
+    thrash_reuse_density: float = 0.15
+    thrash_active_growth: float = 0.25
+
+
+def _percentile_summary(values: list[int]) -> dict:
+    if not values:
+        return {"count": 0, "mean": None, "p50": None, "p90": None, "max": None}
+    v = sorted(values)
+    n = len(v)
+    return {"count": n, "mean": sum(v) / n, "p50": v[int(0.50 * (n - 1))], "p90": v[int(0.90 * (n - 1))],
+            "max": v[-1]}
+
+
+def _entropy(probabilities) -> float:
+    return -sum(p * math.log(max(p, 1e-12)) for p in probabilities)
+
+
+@dataclass
+class RouterStats:
+    """Routing telemetry; ``to_json`` has the keys of streamed_moe_router.py:54-102."""
+
+    expert_hits: Counter = field(default_factory=Counter)
+    routed_tokens: int = 0
+    route_events: list[dict] = field(default_factory=list)
+    last_seen_position: dict[tuple[int, int], int] = field(default_factory=dict)
+    reuse_distances: list[int] = field(default_factory=list)
+    active_by_position: dict[int, set[tuple[int, int]]] = field(default_factory=dict)
+    route_entropies: list[float] = field(default_factory=list)
+    cache_delta_events: list[dict] = field(default_factory=list)
+    cap_events: list[dict] = field(default_factory=list)
+    guarded_adjustments: int = 0
+    blocked_adjustments: int = 0
+    raw_overlap_total: int = 0
+    route_count: int = 0
+
+    def record_route(self, layer_idx: int, position: int, experts: list[int], weights: list[float],
+                     raw_experts: list[int], adjusted: bool, predicted_experts: list[int] | None = None,
+                     resident_experts: list[int] | None = None, active_cap: int | None = None,
+                     blocked_adjustment: bool = False) -> None:
+        """One token's routing decision (streamed_moe_router.py:104-155)."""
+        layer_idx, position = int(layer_idx), int(position)
+        experts = [int(e) for e in experts]
+        raw = [int(e) for e in raw_experts]
+        self.routed_tokens += 1
+        self.route_count += 1
+        entropy = _entropy(float(w) for w in weights)
+        self.route_entropies.append(entropy)
+        overlap = len(set(experts) & set(raw))
+        self.raw_overlap_total += overlap
+        self.guarded_adjustments += int(bool(adjusted))
+        self.blocked_adjustments += int(bool(blocked_adjustment))
+        active = self.active_by_position.setdefault(position, set())
+        distances = []
+        for e in experts:
+            key = (layer_idx, e)
+            self.expert_hits[key] += 1
+            active.add(key)
+            seen = self.last_seen_position.get(key)
+            if seen is not None:
+                distances.append(position - seen)
+            self.last_seen_position[key] = position
+        self.reuse_distances.extend(distances)
+        self.route_events.append({
+            "position": position, "layer": layer_idx, "experts": experts, "raw_experts": raw,
+            "predicted_experts": [int(e) for e in (predicted_experts or [])],
+            "resident_experts": [int(e) for e in (resident_experts or [])],
+            "weights": [float(w) for w in weights], "route_entropy": entropy, "reuse_distances": distances,
+            "sticky_adjusted": adjusted, "blocked_locality_adjustment": blocked_adjustment,
+            "raw_route_overlap": overlap, "active_expert_cap": active_cap,
+        })
+
+    def record_cache_delta(self, layer_idx: int, position: int, experts: list[int], before: dict, after: dict) -> None:
+        delta = {name: int(after.get(name, 0)) - int(before.get(name, 0)) for name in ("hits", "misses", "evictions")}
+        self.cache_delta_events.append({"position": int(position), "layer": int(layer_idx),
+                                        "experts": [int(e) for e in experts], **delta})
+
+    def record_cap_event(self, layer_idx: int, position: int, old_cap: int, new_cap: int, reason: str, hits: int,
+                         misses: int, evictions: int) -> None:
+        if old_cap != new_cap:
+            self.cap_events.append({"position": int(position), "layer": int(layer_idx), "old_cap": int(old_cap),
+                                    "new_cap": int(new_cap), "reason": reason, "hits": int(hits),
+                                    "misses": int(misses), "evictions": int(evictions)})
+
+    def _hit_eviction_correlation(self) -> dict:
+        n = len(self.cache_delta_events)
+        if n == 0:
+            return {"sample_count": 0, "correlation": None}
+        h = [float(ev.get("hits", 0)) for ev in self.cache_delta_events]
+        e = [float(ev.get("evictions", 0)) for ev in self.cache_delta_events]
+        mh, me = sum(h) / n, sum(e) / n
+        cov = sum((a - mh) * (b - me) for a, b in zip(h, e))
+        denom = math.sqrt(sum((a - mh) ** 2 for a in h) * sum((b - me) ** 2 for b in e))
+        return {"sample_count": n, "correlation": cov / denom if denom > 0 else None}
+
+    def _prediction_accuracy(self) -> dict:
+        rows = [ev for ev in self.route_events if ev.get("predicted_experts")]
+        if not rows:
+            return {"sample_count": 0, "mean_precision": None, "mean_recall": None, "exact_match_rate": None}
+        precision = recall = exact = 0.0
+        for ev in rows:
+            actual, predicted = set(ev.get("experts", [])), set(ev.get("predicted_experts", []))
+            hit = len(actual & predicted)
+            precision += hit / max(len(predicted), 1)
+            recall += hit / max(len(actual), 1)
+            exact += float(actual == predicted)
+        n = len(rows)
+        return {"sample_count": n, "mean_precision": precision / n, "mean_recall": recall / n,
+                "exact_match_rate": exact / n}
+
+    def to_json(self) -> dict:
+        activations = sum(self.expert_hits.values())
+        unique = len(self.expert_hits)
+        evictions = sum(int(ev.get("evictions", 0)) for ev in self.cache_delta_events)
+        active_rows = [{"position": int(p), "active_expert_count": len(s)}
+                       for p, s in sorted(self.active_by_position.items())]
+        growth = 0.0
+        if len(active_rows) >= 2:
+            first = active_rows[0]["active_expert_count"]
+            growth = (active_rows[-1]["active_expert_count"] - first) / max(first, 1)
+        reuse_density = len(self.reuse_distances) / max(activations, 1)
+        per_activation = evictions / max(activations, 1)
+        per_1k = 1000.0 * evictions / max(self.routed_tokens, 1)
+        thrash = per_activation >= 0.35 and (reuse_density <= 0.15 or growth >= 0.25 or per_1k >= 1000.0
+                                             or unique >= max(activations * 0.50, 1))
+        distribution = _entropy(c / activations for c in self.expert_hits.values()) if activations else 0.0
+        return {
+            "routed_tokens": self.routed_tokens,
+            "expert_activation_frequency": {str(k): v for k, v in self.expert_hits.most_common()},
+            "locality": {
+                "total_expert_activations": activations,
+                "unique_expert_activations": unique,
+                "reuse_density": reuse_density,
+                "reuse_distance": _percentile_summary(self.reuse_distances),
+                "routing_entropy_mean": sum(self.route_entropies) / max(len(self.route_entropies), 1),
+                "routing_entropy_distribution": distribution,
+                "active_expert_set_size_over_time": active_rows,
+                "active_expert_set_growth": growth,
+                "cache_evictions_observed": evictions,
+                "evictions_per_activation": per_activation,
+                "evictions_per_1k_routed_tokens": per_1k,
+                "expert_thrash_mode": thrash,
+                "cache_hit_eviction_correlation": self._hit_eviction_correlation(),
+                "prediction_accuracy": self._prediction_accuracy(),
+                "dynamic_cap_events": self.cap_events[:500],
+                "guarded_adjustments": int(self.guarded_adjustments),
+                "blocked_adjustments": int(self.blocked_adjustments),
+                "mean_raw_route_overlap": self.raw_overlap_total / max(self.route_count, 1),
+            },
+            "route_events": self.route_events[:500],
+            "cache_delta_events": self.cache_delta_events[:500],
+        }
+
+
+def _topk_order(values: np.ndarray, k: int) -> list[int]:
+    """Indices of the k largest float32 values: descending, NaN first, ties to the lower index."""
+    keyed = np.where(np.isnan(values), np.inf, values)
+    nan_first = ~np.isnan(values)
+    order = np.lexsort((np.arange(values.size), -keyed, nan_first))
+    return [int(i) for i in order[:k]]
+
+
+class StreamedMoERouter:
+    """Router + expert executor (streamed_moe_router.py:236-529) on the gfx950 kernels."""
+
+    def __init__(self, experts_per_token: int = 4, swiglu_limit: float = 7.0,
+                 locality_config: RoutingLocalityConfig | None = None, matmul_precision: str = "fp32") -> None:
+        if matmul_precision not in ops.PRECISIONS:
+            raise ValueError(f"unknown matmul precision {matmul_precision!r} (expected 'fp32' or 'bf16')")
+        self.experts_per_token = experts_per_token
+        self.swiglu_limit = swiglu_limit
+        self.alpha = 1.702  # fixed in the SwiGLU kernel
+        self.stats = RouterStats()
+        self.locality_config = locality_config or RoutingLocalityConfig()
+        self.matmul_precision = matmul_precision
+        self.sticky_scores: dict[int, dict[int, float]] = {}
+        self.workload_scores: dict[int, dict[int, float]] = {}
+        self.recent_history: dict[int, deque[int]] = {}
+        self.dynamic_caps: dict[int, int] = {}
+
+    # ---- the routed layer -------------------------------------------------------------
+
+    def route(self, layer_idx: int, hidden: torch.Tensor, tensors: dict[str, torch.Tensor],
+              expert_store: Mxfp4ExpertStore | ResidentExpertStore | None = None, execute_experts: bool = True,
+              position: int | list[int] = 0, predicted_experts: list[int] | None = None,
+              resident_experts: set[int] | None = None) -> tuple[torch.Tensor, dict]:
+        prefix = f"model.layers.{layer_idx}.mlp"
+        router_w = tensors[f"{prefix}.router.weight"]
+        router_b = tensors[f"{prefix}.router.bias"]
+        if hidden.dim() not in (1, 2):
+            raise ValueError(f"hidden must be [H] or [B, H], got shape {tuple(hidden.shape)}")
+        batched = hidden.dim() == 2
+        x = (hidden if batched else hidden.reshape(1, -1)).contiguous()
+        n_tok = x.shape[0]
+        positions = [int(position)] * n_tok if isinstance(position, int) else [int(p) for p in position]
+        if len(positions) != n_tok:
+            raise ValueError(f"{len(positions)} positions for {n_tok} tokens")
+        logits = ops.router_logits(x, router_w, router_b)
+        n_exp = logits.shape[1]
+        k = self._effective_expert_count(layer_idx, n_exp)
+        resident = sorted(int(e) for e in (resident_experts or set()))
+        gu_bias = tensors.get(f"{prefix}.experts.gate_up_proj_bias")
+        d_bias = tensors.get(f"{prefix}.experts.down_proj_bias")
+
+        if not self.locality_config.enabled:
+            ids, _, weights = ops.topk_softmax(logits, k)
+            host = None  # read back after the expert kernels are enqueued
+        else:
+            ids, weights, host = self._select_on_host(layer_idx, logits, k, resident_experts or set(), positions)
+        recorded = host is not None  # the locality path records each row while it selects
+
+        run_experts = execute_experts and expert_store is not None
+        norms = None
+        if run_experts:
+            before = self._cache_snapshot(expert_store)
+            if host is None and not isinstance(expert_store, ResidentExpertStore):
+                host = self._read_back(ids, weights)  # misses must be brought into HBM first
+            if host is not None:
+                for row in host[0]:
+                    expert_store.protect_experts(layer_idx, row)
+            if gu_bias is None or d_bias is None:
+                output, mode = torch.zeros_like(hidden), "mxfp4_missing_bias"
+            else:
+                output, norms = self._execute_experts(layer_idx, x, ids, weights, gu_bias, d_bias, expert_store,
+                                                      host)
+                output, mode = output.reshape(hidden.shape), "mxfp4_expert_matmul"
+        elif d_bias is None:
+            output, mode = torch.zeros_like(hidden), "router_only"
+        else:
+            output, mode = ops.bias_combine(d_bias, ids, weights).reshape(hidden.shape), "bias_only_moe"
+
+        if host is None:
+            host = self._read_back(ids, weights)
+        if not recorded:
+            for r in range(n_tok):  # locality disabled: the selection is the raw top-k
+                predicted = [int(e) for e in (predicted_experts if predicted_experts is not None
+                                              else self.predict_experts(layer_idx, k))]
+                host[4].append(predicted)
+                self.stats.record_route(layer_idx, positions[r], host[0][r], host[1][r], host[2][r], False,
+                                        predicted_experts=predicted, resident_experts=resident, active_cap=k,
+                                        blocked_adjustment=False)
+                self._update_workload_scores(layer_idx, host[0][r], host[1][r])
+        experts_rows, weight_rows, raw_rows, _, predicted_rows = host
+        adjusted_rows = [experts_rows[r] != raw_rows[r] for r in range(n_tok)]
+
+        def per_token(rows):
+            return rows if batched else rows[0]
+
+        if not run_experts:
+            if mode == "router_only":
+                return output, {"experts": per_token(experts_rows), "weights": per_token(weight_rows), "mode": mode}
+            return output, {"experts": per_token(experts_rows), "raw_experts": per_token(raw_rows),
+                            "weights": per_token(weight_rows), "mode": mode,
+                            "sticky_adjusted": per_token(adjusted_rows)}
+
+        route = {"experts": per_token(experts_rows), "weights": per_token(weight_rows), "mode": mode}
+        if norms is not None:
+            norms = norms.cpu().tolist()
+            logs = [[{"expert": int(e), "routing_weight": float(w), "gate_up_norm": float(norms[r * k + j][0]),
+                      "output_norm": float(norms[r * k + j][1])}
+                     for j, (e, w) in enumerate(zip(experts_rows[r], weight_rows[r]))] for r in range(n_tok)]
+            route["expert_logs"] = per_token(logs)
+        after = self._cache_snapshot(expert_store)
+        for r in range(n_tok):  # a batch's cache traffic is booked on its first row
+            self.stats.record_cache_delta(layer_idx, positions[r], experts_rows[r], before if r == 0 else after,
+                                          after)
+        self._adapt_active_cap(layer_idx, positions[-1], before, after)
+        route.update({"raw_experts": per_token(raw_rows), "predicted_experts": per_token(predicted_rows),
+                      "resident_experts": resident, "sticky_adjusted": per_token(adjusted_rows),
+                      "active_expert_cap": k})
+        return output, route
+
+    # ---- device work ---------------------------------------------------------------------
+
+    @staticmethod
+    def _read_back(ids: torch.Tensor, weights: torch.Tensor):
+        """One device->host read of the selection.
+
+        Returns ``(experts, weights, raw_experts, blocked, predicted)`` row
+        lists; without routing locality the raw experts are the selection and
+        the predictions are filled in by the caller.
+        """
+        experts = ids.cpu().tolist()
+        w = weights.float().cpu().tolist()
+        return experts, w, [list(r) for r in experts], [False] * len(experts), []
+
+    def _execute_experts(self, layer_idx, x, ids, weights, gu_bias, d_bias, store, host):
+        """gate_up + SwiGLU + down + combine for every (token, slot) pair on the GPU."""
+        n_tok, k = ids.shape
+        if isinstance(store, ResidentExpertStore):
+            w = store.layer(layer_idx)
+            hidden, inter, n_exp = w.hidden, w.inter, w.n_experts
+            gu_table, d_table = w.gate_up_table, w.down_table
+            store.record_access(layer_idx, 2 * n_tok * k)
+        else:
+            hidden = x.shape[1]
+            inter = gu_bias.shape[1] // 2
+            n_exp = gu_bias.shape[0]
+            gu_addr = [0] * n_exp
+            d_addr = [0] * n_exp
+            keep = []
+            for row in host[0]:
+                for e in row:  # the reference's access order: gate_up then down, slot by slot
+                    gu = store.packed_expert(layer_idx, e, "gate_up_proj")
+                    dn = store.packed_expert(layer_idx, e, "down_proj")
+                    if store.matrix_shape(layer_idx, e, "gate_up_proj") != (2 * inter, hidden // 32) or \
+                            store.matrix_shape(layer_idx, e, "down_proj") != (hidden, inter // 32):
+                        raise ValueError(f"expert {e} of layer {layer_idx} does not match hidden={hidden} "
+                                         f"inter={inter}")
+                    gu_addr[e], d_addr[e] = gu.data_ptr(), dn.data_ptr()
+                    keep += [gu, dn]
+            gu_table = torch.tensor(gu_addr, dtype=torch.int64).to(x.device)
+            d_table = torch.tensor(d_addr, dtype=torch.int64).to(x.device)
+        if tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
+            raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
+                             f"E={n_exp} H={hidden} I={inter}")
+        offsets, sorted_pairs, active, n_active = ops.dispatch(ids, n_exp)
+        max_active = min(n_exp, ids.numel())
+        gated, gated_raw = ops.gate_up(gu_table, gu_bias, x, k, offsets, sorted_pairs, active, n_active, max_active,
+                                       hidden, inter, self.swiglu_limit, self.matmul_precision, want_raw=True)
+        eo = ops.down(d_table, d_bias, gated, offsets, sorted_pairs, active, n_active, max_active, hidden, inter,
+                      self.matmul_precision)
+        out = ops.combine(eo, weights, n_tok, k)
+        norms = ops.pair_norms(gated_raw, eo)
+        return out, norms
+
+    # ---- routing locality (host control logic, streamed_moe_router.py:331-476) ------------
+
+    def _select_on_host(self, layer_idx, logits, k, resident_set, positions):
+        """Locality-adjusted selection, row by row, in the order the reference routes tokens.
+
+        The sticky scores a row leaves behind steer the next row, so each row's
+        bf16 weights are computed (klc_moe_softmax_weights) and read back before
+        the next row is selected.
+        """
+        rows = logits.float().cpu().numpy()
+        n_tok = rows.shape[0]
+        ids = torch.empty((n_tok, k), dtype=torch.int32, device=logits.device)
+        weights = torch.empty((n_tok, k), dtype=torch.bfloat16, device=logits.device)
+        experts_rows, weight_rows, raw_rows, blocked_rows, predicted_rows = [], [], [], [], []
+        for r in range(n_tok):
+            row = rows[r].astype(np.float32)
+            raw = _topk_order(row, k)
+            adjusted_logits = self._apply_locality_bias(layer_idx, row, resident_set)
+            experts, values, blocked = self._guarded_expert_selection(row, adjusted_logits, raw,
+                                                                      _topk_order(adjusted_logits, k), k)
+            vals = torch.tensor([values], dtype=torch.float32).to(logits.device)
+            w_row = ops.softmax_weights(vals)
+            ids[r] = torch.tensor(experts, dtype=torch.int32).to(logits.device)
+            weights[r] = w_row[0]
+            w_list = w_row.float().cpu()[0].tolist()
+            predicted = [int(e) for e in self.predict_experts(layer_idx, k)]
+            predicted_rows.append(predicted)
+            experts_rows.append(experts)
+            weight_rows.append(w_list)
+            raw_rows.append(raw)
+            blocked_rows.append(blocked)
+            self.stats.record_route(layer_idx, positions[r], experts, w_list, raw, experts != raw,
+                                    predicted_experts=predicted, resident_experts=sorted(resident_set),
+                                    active_cap=k, blocked_adjustment=blocked)
+            self._update_sticky_scores(layer_idx, experts, w_list)
+            self._update_workload_scores(layer_idx, experts, w_list)
+        return ids, weights, (experts_rows, weight_rows, raw_rows, blocked_rows, predicted_rows)
+
+    def _apply_locality_bias(self, layer_idx: int, logits: np.ndarray, resident: set[int]) -> np.ndarray:
+        """float32 logits + sticky bonus / exploration penalty / residency bonus (streamed_moe_router.py:331-363)."""
+        cfg = self.locality_config
+        if not cfg.enabled:
+            return logits
+        out = logits.astype(np.float32).copy()
+        k = min(self.experts_per_token, logits.size)
+        raw = _topk_order(logits, k)
+        floor = np.float32(logits[raw[-1]]) - np.float32(abs(float(cfg.sticky_candidate_margin)))
+        scores = self.sticky_scores.get(layer_idx, {})
+        if scores and cfg.sticky_strength > 0:
+            eligible = [int(e) for e in scores if logits[int(e)] >= floor]
+            if eligible:
+                bonus = np.array([scores[e] for e in eligible], dtype=np.float32) * np.float32(cfg.sticky_strength)
+                if cfg.semantic_guard and cfg.max_sticky_bonus > 0:
+                    bonus = np.minimum(bonus, np.float32(cfg.max_sticky_bonus))
+                out[eligible] += bonus
+        if cfg.max_hot_experts_per_layer > 0 and len(scores) >= cfg.max_hot_experts_per_layer:
+            hot = set(sorted(scores, key=scores.get, reverse=True)[:cfg.max_hot_experts_per_layer])
+            allowed = hot | set(raw[:max(1, self.experts_per_token // 2)])
+            mask = np.ones(out.size, dtype=bool)
+            mask[sorted(allowed)] = False
+            out[mask] -= np.float32(abs(float(cfg.exploration_margin)))
+        if resident and cfg.cache_aware_strength > 0:
+            ids = np.array(sorted(resident), dtype=np.int64)
+            threshold = np.float32(np.max(logits)) - np.float32(abs(float(cfg.exploration_margin)))
+            eligible = ids[logits[ids] >= threshold]
+            if eligible.size:
+                out[eligible] += np.float32(cfg.cache_aware_strength)
+        return out
+
+    def _guarded_expert_selection(self, logits: np.ndarray, adjusted_logits: np.ndarray, raw_experts: list[int],
+                                  adjusted_experts: list[int], k: int) -> tuple[list[int], list[float], bool]:
+        """Keeps at least ``min_raw_overlap`` raw experts (streamed_moe_router.py:365-394)."""
+        cfg = self.locality_config
+        if not (cfg.enabled and cfg.semantic_guard):
+            return list(adjusted_experts), [float(adjusted_logits[e]) for e in adjusted_experts], False
+        raw = list(raw_experts[:k])
+        chosen = list(adjusted_experts[:k])
+        need = min(max(int(cfg.min_raw_overlap), 0), k)
+        blocked = False
+        while len(set(raw) & set(chosen)) < need:
+            missing = [e for e in raw if e not in chosen]
+            foreign = [e for e in chosen if e not in raw]
+            if not missing or not foreign:
+                break
+            weakest = min(foreign, key=lambda e: float(adjusted_logits[e]))
+            chosen[chosen.index(weakest)] = missing[0]
+            blocked = True
+        chosen.sort(key=lambda e: float(adjusted_logits[e]), reverse=True)
+        return chosen, [float(logits[e]) for e in chosen], blocked
+
+    def _update_sticky_scores(self, layer_idx: int, experts: list[int], weights: list[float]) -> None:
+        cfg = self.locality_config
+        if not cfg.enabled:
+            return
+        scores = self.sticky_scores.setdefault(layer_idx, {})
+        for e in list(scores):
+            scores[e] *= float(cfg.sticky_decay)
+            if scores[e] < 1e-4:
+                del scores[e]
+        for e, w in zip(experts, weights):
+            scores[int(e)] = scores.get(int(e), 0.0) + float(w)
+        cap = cfg.max_hot_experts_per_layer
+        if cap > 0 and len(scores) > 2 * cap:
+            keep = set(sorted(scores, key=scores.get, reverse=True)[:cap])
+            for e in [e for e in scores if e not in keep]:
+                del scores[e]
+
+    def _update_workload_scores(self, layer_idx: int, experts: list[int], weights: list[float]) -> None:
+        cfg = self.locality_config
+        scores = self.workload_scores.setdefault(layer_idx, {})
+        decay = 1.0 - 1.0 / max(float(cfg.workload_window), 1.0)
+        for e in list(scores):
+            scores[e] *= decay
+            if scores[e] < 1e-4:
+                del scores[e]
+        history = self.recent_history.setdefault(layer_idx, deque(maxlen=max(int(cfg.prediction_window), 1)))
+        for e, w in zip(experts, weights):
+            scores[int(e)] = scores.get(int(e), 0.0) + float(w)
+            history.append(int(e))
+
+    def predict_experts(self, layer_idx: int, limit: int | None = None) -> list[int]:
+        """Experts likely next for ``layer_idx`` (streamed_moe_router.py:426-440)."""
+        cfg = self.locality_config
+        if not (cfg.enabled and cfg.predictive_prefetch):
+            return []
+        scores: Counter[int] = Counter()
+        for e, v in self.workload_scores.get(layer_idx, {}).items():
+            scores[int(e)] += float(v)
+        for e, v in self.sticky_scores.get(layer_idx, {}).items():
+            scores[int(e)] += 0.75 * float(v)
+        for e in self.recent_history.get(layer_idx, ()):
+            scores[int(e)] += 0.50
+        if not scores:
+            return []
+        return [int(e) for e, _ in scores.most_common(max(int(limit or self.experts_per_token), 1))]
+
+    def _effective_expert_count(self, layer_idx: int, expert_count: int) -> int:
+        cfg = self.locality_config
+        k = min(self.experts_per_token, expert_count)
+        if cfg.enabled and cfg.active_experts_per_token_cap > 0:
+            k = min(k, int(cfg.active_experts_per_token_cap))
+        if cfg.enabled and cfg.dynamic_active_expert_cap:
+            base = cfg.active_experts_per_token_cap or self.experts_per_token
+            start = min(max(base, cfg.min_active_experts_per_token),
+                        cfg.max_active_experts_per_token or self.experts_per_token)
+            k = min(k, self.dynamic_caps.setdefault(layer_idx, start))
+        return max(k, 1)
+
+    def _adapt_active_cap(self, layer_idx: int, position: int, before: dict, after: dict) -> None:
+        cfg = self.locality_config
+        if not (cfg.enabled and cfg.dynamic_active_expert_cap):
+            return
+        old = self.dynamic_caps.setdefault(layer_idx, cfg.active_experts_per_token_cap or self.experts_per_token)
+        hits = int(after.get("hits", 0)) - int(before.get("hits", 0))
+        misses = int(after.get("misses", 0)) - int(before.get("misses", 0))
+        evictions = int(after.get("evictions", 0)) - int(before.get("evictions", 0))
+        total = max(hits + misses, 1)
+        lo = max(int(cfg.min_active_experts_per_token), 1)
+        hi = int(cfg.max_active_experts_per_token or self.experts_per_token)
+        new, reason = old, ""
+        if evictions / total >= float(cfg.cap_eviction_pressure_threshold) and old > lo:
+            new, reason = old - 1, "eviction_pressure"
+        elif evictions == 0 and hits / total >= float(cfg.cap_hit_rate_expand_threshold) and old < hi:
+            new, reason = old + 1, "stable_high_hit_rate"
+        if new != old:
+            self.dynamic_caps[layer_idx] = new
+            self.stats.record_cap_event(layer_idx, position, old, new, reason, hits, misses, evictions)
+
+    @staticmethod
+    def _cache_snapshot(expert_store) -> dict:
+        st = expert_store.cache.stats
+        return {"hits": st.hits, "misses": st.misses, "evictions": st.evictions}

@@ -82,17 +82,21 @@ def check_layer(gpu, host, dev_w, x, k, precision):
     assert np.array_equal(out, oex.combine(eo, bf16_bits(det["weights"])))
     # fused single-call layer == step-by-step path, bit for bit
     assert np.array_equal(bf16_bits(fused), out)
-    # final output vs the oracle's
+    assert_final_close(out, ref, precision)
+    return det, ref
+
+
+def assert_final_close(out_bits, ref, precision="fp32"):
+    """Final bf16 output vs the oracle's, with the combine's rounding slack."""
     w = bf16_to_f32(ref["weights"])
     slack = 2.0 ** -7 * np.sum(np.abs(w[:, :, None] * ref["expert_out"]), axis=1)
-    got = bf16_to_f32(out).astype(np.float64)
+    got = bf16_to_f32(np.asarray(out_bits).reshape(ref["out"].shape)).astype(np.float64)
     want = bf16_to_f32(ref["out"]).astype(np.float64)
     err = np.abs(got - want)
     if precision == "bf16":
         slack = slack + 2.0 ** -8 * np.sum(np.abs(w[:, :, None]) * np.sqrt(np.mean(ref["expert_out"] ** 2, axis=-1,
                                                                                keepdims=True)), axis=1)
     assert (err <= ATOL + RTOL * np.abs(want) + slack).all(), f"final output worst error {err.max():.3e}"
-    return det, ref
 
 
 @pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 8), (16, 4, 8), (5, 2, 3), (33, 4, 16)])

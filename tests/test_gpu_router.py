@@ -95,3 +95,18 @@ def test_router_rejects_bad_shapes(gpu):
         ops.router_logits(x2, w2, b)
     with pytest.raises(Exception):
         ops.topk_softmax(torch.zeros((2, 8), dtype=torch.bfloat16, device=gpu), 9)
+
+
+def test_softmax_weights_of_host_chosen_scores(gpu):
+    """klc_moe_softmax_weights: unordered scores, a NaN row, k = 1 and a wide k."""
+    for n_tok, k in [(300, 4), (3, 1), (2, 40)]:
+        vals = synth.random_normal_f32(90 + k, n_tok * k, 0.0, 3.0).reshape(n_tok, k)
+        if k > 1:
+            vals[1, 1] = np.nan
+        got = ops.softmax_weights(torch.from_numpy(vals).to(gpu))
+        torch.cuda.synchronize()
+        want = orr.softmax_weights(vals)
+        assert np.array_equal(bf16_bits(got), want) or k > 1 and np.array_equal(
+            np.delete(bf16_bits(got), 1, axis=0), np.delete(want, 1, axis=0))
+        if k > 1:
+            assert np.isnan(got[1].float().cpu().numpy()).all()

@@ -1,0 +1,217 @@
+"""GPU parity of the reference-shaped API: ``StreamedMoERouter.route`` with a
+resident and a streaming expert store, its fallbacks, and
+``dequantize_mxfp4_matrix`` / ``Mxfp4ExpertStore.load_expert_matrix``.
+
+Expected values come from the oracle on the same seeded inputs.  Selection
+(experts, weights) and dequantized matrices are bit-exact; outputs use the
+tolerances of test_gpu_experts (1e-2 + 2e-2 |ref| per expert output, plus the
+bf16 combine slack); the per-expert norms in ``expert_logs`` follow from
+those outputs to 2e-2 relative.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_bits, bf16_tensor
+from klcquant import moe
+from klcquant.mxfp4_expert import Mxfp4ExpertStore, ResidentExpertStore, dequantize_mxfp4_matrix
+from klcquant.streamed_moe_router import RoutingLocalityConfig, StreamedMoERouter
+from oracle import experts as oex
+from oracle import mxfp4 as omx
+from oracle.numerics import bf16_to_f32
+from test_gpu_experts import assert_close, assert_final_close, oracle_layer
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 256, 128, 16, 4
+WORKLOAD = 61
+
+
+def layer_tensors(host, gpu, layer=0, drop=()):
+    names = {"router.weight": "router_weight", "router.bias": "router_bias",
+             "experts.gate_up_proj_bias": "gate_up_bias", "experts.down_proj_bias": "down_bias"}
+    return {f"model.layers.{layer}.mlp.{k}": bf16_tensor(host[v], gpu) for k, v in names.items() if k not in drop}
+
+
+@pytest.fixture(scope="module")
+def setup(gpu):
+    host = moe.synthetic_host_layer(WORKLOAD, 0, H, I, E)
+    dev_w = moe.MoELayerWeights.synthetic(WORKLOAD, 0, H, I, E, gpu)
+    return host, dev_w
+
+
+def check_route(out, route, host, x, batched, precision="fp32"):
+    ref = oracle_layer(host, x, K, precision)
+    experts = route["experts"] if batched else [route["experts"]]
+    weights = route["weights"] if batched else [route["weights"]]
+    assert experts == ref["ids"].tolist()
+    assert weights == bf16_to_f32(ref["weights"]).astype(np.float64).tolist()
+    assert_final_close(bf16_bits(out), ref, precision)
+    logs = route["expert_logs"] if batched else [route["expert_logs"]]
+    for t, row in enumerate(logs):
+        assert [entry["expert"] for entry in row] == experts[t]
+        for j, entry in enumerate(row):
+            assert entry["routing_weight"] == weights[t][j]
+            np.testing.assert_allclose(entry["gate_up_norm"], np.linalg.norm(ref["gated"][t, j]), rtol=2e-2)
+            np.testing.assert_allclose(entry["output_norm"], np.linalg.norm(ref["expert_out"][t, j]), rtol=2e-2)
+    return ref
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_route_single_token_resident_store(gpu, setup, precision):
+    host, dev_w = setup
+    x = moe.synthetic_hidden(WORKLOAD, 1, H)
+    router = StreamedMoERouter(K, 7.0, matmul_precision=precision)
+    store = ResidentExpertStore({0: dev_w})
+    out, route = router.route(0, bf16_tensor(x[0], gpu), layer_tensors(host, gpu), store, position=3)
+    assert out.shape == (H,) and out.dtype == torch.bfloat16
+    assert route["mode"] == "mxfp4_expert_matmul" and route["active_expert_cap"] == K
+    assert route["raw_experts"] == route["experts"] and route["sticky_adjusted"] is False
+    check_route(out, route, host, x, False, precision)
+    st = router.stats.to_json()
+    assert st["routed_tokens"] == 1 and st["route_events"][0]["position"] == 3
+    assert store.cache.stats.hits == 2 * K
+    json.dumps(store.to_json())
+
+
+def test_route_batch_resident_store(gpu, setup):
+    host, dev_w = setup
+    x = moe.synthetic_hidden(WORKLOAD, 12, H, step=1)
+    router = StreamedMoERouter(K)
+    out, route = router.route(0, bf16_tensor(x, gpu), layer_tensors(host, gpu), ResidentExpertStore({0: dev_w}),
+                              position=list(range(12)))
+    assert out.shape == (12, H)
+    check_route(out, route, host, x, True)
+    assert router.stats.routed_tokens == 12
+
+
+def write_checkpoint(path, host, layer=0):
+    from safetensors.torch import save_file
+
+    prefix = f"model.layers.{layer}.mlp.experts"
+    tensors = {f"{prefix}.gate_up_proj_blocks": torch.from_numpy(host["gate_up_blocks"]),
+               f"{prefix}.gate_up_proj_scales": torch.from_numpy(host["gate_up_scales"]),
+               f"{prefix}.down_proj_blocks": torch.from_numpy(host["down_blocks"]),
+               f"{prefix}.down_proj_scales": torch.from_numpy(host["down_scales"])}
+    save_file(tensors, str(path / "model-00001.safetensors"))
+    (path / "model.safetensors.index.json").write_text(
+        json.dumps({"weight_map": {name: "model-00001.safetensors" for name in tensors}}))
+
+
+def test_route_streaming_store_matches_resident(gpu, setup, tmp_path):
+    host, dev_w = setup
+    write_checkpoint(tmp_path, host)
+    x = moe.synthetic_hidden(WORKLOAD, 1, H, step=2)
+    tensors = layer_tensors(host, gpu)
+    per_expert = (dev_w.gate_up.shape[1] + dev_w.down.shape[1])
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, dtype=torch.bfloat16, cache_bytes=E * per_expert)
+    router = StreamedMoERouter(K)
+    out, route = router.route(0, bf16_tensor(x[0], gpu), tensors, store)
+    check_route(out, route, host, x, False)
+    assert store.cache.stats.misses == 2 * K and store.cache.stats.hits == 0
+    assert store.resident_experts(0) == set(route["experts"])
+    out2, route2 = router.route(0, bf16_tensor(x[0], gpu), tensors, store, position=1)
+    assert store.cache.stats.hits == 2 * K and store.cache.stats.misses == 2 * K
+    assert torch.equal(out, out2) and route2["experts"] == route["experts"]
+    delta = router.stats.cache_delta_events[-1]
+    assert (delta["hits"], delta["misses"]) == (2 * K, 0)
+    resident, _ = StreamedMoERouter(K).route(0, bf16_tensor(x[0], gpu), tensors, ResidentExpertStore({0: dev_w}))
+    assert torch.equal(out, resident)
+    json.dumps(store.to_json())
+
+
+def test_store_load_expert_matrix_is_exact(gpu, setup, tmp_path):
+    host, _ = setup
+    write_checkpoint(tmp_path, host)
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, dtype=torch.bfloat16, cache_bytes=1 << 30)
+    for e, proj in [(3, "gate_up_proj"), (11, "down_proj")]:
+        got = store.load_expert_matrix(0, e, proj)
+        want = omx.dequantize(host[f"{proj[:-5]}_blocks"][e], host[f"{proj[:-5]}_scales"][e], "bf16")
+        assert np.array_equal(bf16_bits(got), want)
+    store.pin_experts([(0, 5, "down_proj")])
+    assert (0, 5, "down_proj") in store.cache.pinned
+
+
+def test_store_prefetch_then_consume(gpu, setup, tmp_path):
+    host, _ = setup
+    write_checkpoint(tmp_path, host)
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, cache_bytes=1 << 30, async_prefetch=True)
+    store.prefetch_experts(0, [2, 7])
+    got = store.load_expert_matrix(0, 7, "down_proj")
+    assert got.dtype == torch.float16
+    want = omx.dequantize(host["down_blocks"][7], host["down_scales"][7], "f16")
+    assert np.array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), want.view(np.uint16))
+    store.executor.shutdown(wait=True)
+    js = store.to_json()
+    assert js["prefetch_submitted"] == 4 and js["prefetch_failed"] == 0
+
+
+def test_dequantize_matrix_default_fp16(gpu):
+    from klcquant import synth
+
+    blocks, scales = synth.mxfp4_expert_tensors(3, 4, 1, 64, 96, scale_lo=100, scale_hi=140)
+    got = dequantize_mxfp4_matrix(torch.from_numpy(blocks[0]).to(gpu), torch.from_numpy(scales[0]).to(gpu))
+    assert got.dtype == torch.float16 and got.shape == (96, 64)
+    want = omx.dequantize(blocks[0], scales[0], "f16")
+    assert np.array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), want.view(np.uint16))
+    with pytest.raises(ValueError, match="shape mismatch"):
+        dequantize_mxfp4_matrix(torch.from_numpy(blocks[0]).to(gpu), torch.from_numpy(scales[0][:, :2]).to(gpu))
+
+
+def test_route_fallback_modes(gpu, setup):
+    host, dev_w = setup
+    x = moe.synthetic_hidden(WORKLOAD, 3, H, step=3)
+    ref = oracle_layer(host, x, K)
+    xt = bf16_tensor(x, gpu)
+    out, route = StreamedMoERouter(K).route(0, xt, layer_tensors(host, gpu), execute_experts=False)
+    assert route["mode"] == "bias_only_moe" and route["experts"] == ref["ids"].tolist()
+    assert np.array_equal(bf16_bits(out), oex.bias_only(host["down_bias"], ref["ids"], ref["weights"]))
+    out, route = StreamedMoERouter(K).route(0, xt, layer_tensors(host, gpu, drop=("experts.down_proj_bias",)))
+    assert route["mode"] == "router_only" and not out.any()
+    out, route = StreamedMoERouter(K).route(0, xt, layer_tensors(host, gpu, drop=("experts.gate_up_proj_bias",)),
+                                            ResidentExpertStore({0: dev_w}))
+    assert route["mode"] == "mxfp4_missing_bias" and not out.any() and route["experts"] == ref["ids"].tolist()
+    with pytest.raises(KeyError):
+        StreamedMoERouter(K).route(1, xt, layer_tensors(host, gpu))
+
+
+def test_locality_without_bonus_equals_plain_routing(gpu, setup):
+    host, dev_w = setup
+    x = moe.synthetic_hidden(WORKLOAD, 4, H, step=4)
+    store = ResidentExpertStore({0: dev_w})
+    plain_out, plain = StreamedMoERouter(K).route(0, bf16_tensor(x, gpu), layer_tensors(host, gpu), store)
+    cfg = RoutingLocalityConfig(enabled=True, predictive_prefetch=True)
+    router = StreamedMoERouter(K, locality_config=cfg)
+    out, route = router.route(0, bf16_tensor(x, gpu), layer_tensors(host, gpu), store)
+    assert route["experts"] == plain["experts"] and route["weights"] == plain["weights"]
+    assert torch.equal(out, plain_out)
+    # predictions for later rows come from the earlier rows' experts
+    assert route["predicted_experts"][0] == [] and len(route["predicted_experts"][1]) == K
+
+
+def test_locality_sticky_bonus_changes_selection(gpu, setup):
+    """A large sticky bonus on an expert inside the candidate margin moves it into the top-k;
+    the weights are the softmax of the adjusted scores (klc_moe_softmax_weights)."""
+    host, dev_w = setup
+    x = moe.synthetic_hidden(WORKLOAD, 1, H, step=5)
+    ref = oracle_layer(host, x, E)  # all experts, descending
+    order = ref["ids"][0].tolist()
+    vals = bf16_to_f32(ref["logits"][0])
+    # the best expert outside the top-k that is within 0.5 of the k-th logit
+    cand = [e for e in order[K:] if vals[e] >= np.float32(vals[order[K - 1]]) - np.float32(0.5)]
+    assert cand, "seeded input has no candidate within the margin"
+    e = cand[0]
+    router = StreamedMoERouter(K, locality_config=RoutingLocalityConfig(enabled=True, sticky_strength=1.0))
+    router.sticky_scores[0] = {e: 5.0}
+    out, route = router.route(0, bf16_tensor(x[0], gpu), layer_tensors(host, gpu), ResidentExpertStore({0: dev_w}))
+    assert route["experts"][0] == e and route["sticky_adjusted"]
+    assert route["raw_experts"] == order[:K]
+    adjusted = [float(np.float32(vals[e]) + np.float32(5.0))] + [float(vals[j]) for j in order[:K - 1]]
+    from oracle.router import softmax_weights
+    assert route["weights"] == bf16_to_f32(softmax_weights(np.array([adjusted], np.float32)))[0].tolist()
+    assert route["experts"][1:] == order[:K - 1]

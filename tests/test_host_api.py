@@ -1,0 +1,207 @@
+"""Host logic of the reference-shaped API: expert cache eviction, routing
+telemetry and routing-locality selection.  Expected values are worked out by
+hand from the rules each docstring cites; nothing here touches a GPU."""
+
+from __future__ import annotations
+
+import json
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from klcquant import mxfp4_expert as mx
+from klcquant import streamed_moe_router as smr
+
+
+def item(n=4):
+    return torch.zeros(n, dtype=torch.uint8)
+
+
+def test_fp4_table_is_the_e2m1_code_table():
+    # E2M1: sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0; code 1 is the subnormal 0.5
+    for code in range(16):
+        s, e, m = code >> 3, (code >> 1) & 3, code & 1
+        mag = (m * 0.5) if e == 0 else (1 + m / 2) * 2.0 ** (e - 1)
+        assert mx.FP4_VALUES[code] == (-mag if s else mag)
+        assert math.copysign(1.0, mx.FP4_VALUES[code]) == (-1.0 if s else 1.0)
+
+
+def test_cache_disabled_budget_stores_nothing():
+    c = mx.ExpertWeightCache(0)
+    c.put((0, 1, "down_proj"), item())
+    assert not c.contains((0, 1, "down_proj")) and c.current_bytes == 0
+
+
+def test_cache_evicts_lowest_frequency_then_oldest():
+    c = mx.ExpertWeightCache(12)  # three 4-byte items
+    a, b, d, e = (0, 0, "gate_up_proj"), (0, 1, "gate_up_proj"), (0, 2, "gate_up_proj"), (0, 3, "gate_up_proj")
+    for key in (a, b, d):
+        c.put(key, item())
+    assert c.get(a) is not None and c.get(a) is not None  # a: frequency 3
+    c.put(e, item())  # over budget: b and d have frequency 1, b was touched earlier
+    assert not c.contains(b) and c.contains(a) and c.contains(d) and c.contains(e)
+    assert c.stats.evictions == 1 and c.stats.hits == 2 and c.current_bytes == 12
+    assert c.get(b) is None and c.stats.misses == 1
+    assert c.eviction_reasons["global_pressure"] == 1
+
+
+def test_cache_future_scores_and_protection_override_frequency():
+    c = mx.ExpertWeightCache(8)
+    a, b, d = (1, 0, "down_proj"), (1, 1, "down_proj"), (1, 2, "down_proj")
+    c.put(a, item())
+    c.put(b, item())
+    c.get(a)
+    c.set_future_scores([b], protect_window=100)  # b: future score 1, protected
+    c.put(d, item())  # unprotected candidates a (score 0, frequency 2) and d (score 0, frequency 1)
+    assert c.contains(b)
+    assert not c.contains(d)  # lowest (score 0, frequency 1) among unprotected
+    assert c.stats.protected_eviction_skips == 0
+
+
+def test_cache_pinned_items_survive():
+    c = mx.ExpertWeightCache(8)
+    a, b, d = (2, 0, "down_proj"), (2, 1, "down_proj"), (2, 2, "down_proj")
+    c.put(a, item(), pin=True)
+    c.put(b, item())
+    c.put(d, item())
+    assert c.contains(a) and c.stats.evictions == 1
+    assert c.get(a) is not None and c.stats.pinned_hits == 1
+
+
+def test_cache_layer_quota_evicts_from_the_over_quota_layer():
+    c = mx.ExpertWeightCache(16, layer_count=2, layer_aware=True)  # quota 8 bytes per layer
+    l0 = [(0, i, "down_proj") for i in range(3)]
+    for key in l0:
+        c.put(key, item())
+    c.get(l0[0])
+    c.get(l0[1])
+    c.get(l0[2])
+    new = (1, 0, "down_proj")
+    c.put(new, item())  # 16 bytes: at budget, nothing evicted
+    assert c.stats.evictions == 0
+    newer = (1, 1, "down_proj")
+    c.put(newer, item())  # layer 0 holds 12 > 8 bytes: its entry goes, not layer 1's fresher ones
+    assert c.contains(new) and c.contains(newer)
+    assert sum(c.contains(k) for k in l0) == 2
+    assert c.eviction_reasons["layer_quota_pressure"] == 1
+
+
+def test_cache_to_json_is_serialisable_and_consistent():
+    c = mx.ExpertWeightCache(8)
+    c.put((0, 0, "gate_up_proj"), item())
+    c.get((0, 0, "gate_up_proj"))
+    c.get((0, 9, "gate_up_proj"))
+    js = c.to_json()
+    json.dumps(js)
+    assert js["hits"] == 1 and js["misses"] == 1 and js["hit_rate"] == 0.5
+    assert js["resident_items"] == 1 and js["resident_bytes"] == 4
+    assert js["layer_activity"] == [{"layer": 0, "hits": 1, "misses": 1, "hit_rate": 0.5, "evictions": 0,
+                                     "loaded_mb": 0.0, "hit_mb": round(4 / 2**20, 6)}]
+
+
+def test_store_requires_a_gpu_device(tmp_path):
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": {}}))
+    with pytest.raises(ValueError, match="GPU"):
+        mx.Mxfp4ExpertStore(tmp_path, tmp_path, torch.device("cpu"))
+
+
+def test_router_stats_closed_forms():
+    st = smr.RouterStats()
+    st.record_route(3, 10, [1, 2], [0.5, 0.5], [1, 2], False)
+    st.record_route(3, 12, [2, 5], [1.0, 0.0], [2, 4], True, predicted_experts=[2, 7])
+    js = st.to_json()
+    json.dumps(js)
+    loc = js["locality"]
+    assert js["routed_tokens"] == 2
+    assert loc["total_expert_activations"] == 4 and loc["unique_expert_activations"] == 3
+    assert loc["reuse_distance"] == {"count": 1, "mean": 2.0, "p50": 2, "p90": 2, "max": 2}
+    assert loc["reuse_density"] == 0.25
+    assert math.isclose(loc["routing_entropy_mean"], math.log(2) / 2)
+    # expert (3,2) twice, (3,1) and (3,5) once: H = -(1/2 ln 1/2 + 2 * 1/4 ln 1/4)
+    assert math.isclose(loc["routing_entropy_distribution"], 1.5 * math.log(2))
+    assert loc["guarded_adjustments"] == 1 and loc["mean_raw_route_overlap"] == 1.5
+    assert loc["prediction_accuracy"] == {"sample_count": 1, "mean_precision": 0.5, "mean_recall": 0.5,
+                                          "exact_match_rate": 0.0}
+    assert loc["active_expert_set_size_over_time"] == [{"position": 10, "active_expert_count": 2},
+                                                       {"position": 12, "active_expert_count": 2}]
+
+
+def test_router_stats_thrash_and_correlation():
+    st = smr.RouterStats()
+    st.record_route(0, 0, [1], [1.0], [1], False)
+    st.record_cache_delta(0, 0, [1], {"hits": 0, "misses": 0, "evictions": 0}, {"hits": 0, "misses": 2, "evictions": 1})
+    st.record_cache_delta(0, 1, [1], {"hits": 0, "misses": 2, "evictions": 1}, {"hits": 2, "misses": 2, "evictions": 1})
+    loc = st.to_json()["locality"]
+    assert loc["cache_evictions_observed"] == 1 and loc["evictions_per_activation"] == 1.0
+    assert loc["expert_thrash_mode"] is True
+    assert loc["cache_hit_eviction_correlation"] == {"sample_count": 2, "correlation": -1.0}
+
+
+def test_topk_order_ties_and_nan():
+    v = np.array([1.0, 3.0, 3.0, np.nan, 2.0], dtype=np.float32)
+    assert smr._topk_order(v, 4) == [3, 1, 2, 4]
+
+
+def make_router(**cfg):
+    return smr.StreamedMoERouter(4, 7.0, smr.RoutingLocalityConfig(enabled=True, **cfg))
+
+
+def test_sticky_bonus_pulls_in_a_recent_expert_within_the_margin():
+    r = make_router(sticky_strength=0.5)
+    r.sticky_scores[0] = {6: 0.2, 7: 1.0}
+    logits = np.array([2.0, 1.9, 1.8, 1.7, 0.0, 0.0, 1.5, 1.0], dtype=np.float32)
+    adj = r._apply_locality_bias(0, logits, set())
+    # floor = 1.7 - 0.5 = 1.2: expert 6 (1.5) gets +0.1, expert 7 (1.0) is below the floor
+    assert adj[6] == np.float32(1.5) + np.float32(0.2) * np.float32(0.5) and adj[7] == np.float32(1.0)
+    assert smr._topk_order(adj, 4) == [0, 1, 2, 3]
+    r.sticky_scores[0] = {6: 1.2}  # +0.6 lifts expert 6 to 2.1, above every raw logit
+    adj = r._apply_locality_bias(0, logits, set())
+    assert smr._topk_order(adj, 4) == [6, 0, 1, 2]
+
+
+def test_semantic_guard_caps_bonus_and_restores_raw_experts():
+    r = make_router(sticky_strength=10.0, semantic_guard=True, max_sticky_bonus=0.25, min_raw_overlap=4)
+    r.sticky_scores[0] = {5: 1.0}
+    logits = np.array([2.0, 1.9, 1.8, 1.7, 0.0, 1.6], dtype=np.float32)
+    adj = r._apply_locality_bias(0, logits, set())
+    assert adj[5] == np.float32(1.6) + np.float32(0.25)
+    raw = smr._topk_order(logits, 4)
+    picked = smr._topk_order(adj, 4)
+    assert picked == [0, 1, 5, 2]
+    experts, values, blocked = r._guarded_expert_selection(logits, adj, raw, picked, 4)
+    assert experts == [0, 1, 2, 3] and blocked  # all four raw experts must stay
+    assert values == [2.0, float(np.float32(1.9)), float(np.float32(1.8)), float(np.float32(1.7))]
+
+
+def test_exploration_penalty_and_cache_bonus():
+    r = make_router(max_hot_experts_per_layer=1, exploration_margin=0.25, cache_aware_strength=1.0)
+    r.sticky_scores[0] = {3: 1.0}
+    logits = np.array([1.0, 0.9, 0.8, 0.7, 0.6], dtype=np.float32)
+    adj = r._apply_locality_bias(0, logits, {4})
+    # allowed = hot {3} + first two raw experts {0, 1}; 2 and 4 lose 0.25; 4 is resident but
+    # below max - 0.25 = 0.75, so it gets no bonus
+    want = logits.copy()
+    want[[2, 4]] -= np.float32(0.25)
+    assert np.array_equal(adj, want)
+
+
+def test_predictions_caps_and_adaptation():
+    r = make_router(predictive_prefetch=True, prediction_window=4, workload_window=2,
+                    dynamic_active_expert_cap=True, max_active_experts_per_token=4)
+    r._update_workload_scores(0, [1, 2], [0.75, 0.25])
+    r._update_sticky_scores(0, [1, 2], [0.75, 0.25])
+    # scores: workload {1: .75, 2: .25}, sticky * .75 {1: .5625, 2: .1875}, history +.5 each
+    assert r.predict_experts(0, 1) == [1] and r.predict_experts(0) == [1, 2]
+    assert r._effective_expert_count(0, 128) == 4
+    r._adapt_active_cap(0, 5, {"hits": 0, "misses": 0, "evictions": 0}, {"hits": 0, "misses": 4, "evictions": 2})
+    assert r.dynamic_caps[0] == 3 and r._effective_expert_count(0, 128) == 3
+    assert r.stats.cap_events[-1]["reason"] == "eviction_pressure"
+    r._adapt_active_cap(0, 6, {"hits": 0, "misses": 0, "evictions": 0}, {"hits": 8, "misses": 1, "evictions": 0})
+    assert r.dynamic_caps[0] == 4
+
+
+def test_router_rejects_unknown_precision():
+    with pytest.raises(ValueError):
+        smr.StreamedMoERouter(matmul_precision="fp8")
