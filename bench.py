@@ -105,7 +105,7 @@ def cpu_baseline(n_tokens: int) -> dict:
     import numpy as np
     from threadpoolctl import threadpool_info
 
-    from klcquant import moe
+    from klcquant_amd import moe
     from oracle import layer as olayer
 
     host = moe.synthetic_host_layer(WORKLOAD, 0, HIDDEN, INTER, EXPERTS)
@@ -138,7 +138,7 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from klcquant import _native, moe
+    from klcquant_amd import _native, moe
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

@@ -4,7 +4,7 @@
  * The reference (KLCquant) is pure Python on PyTorch: its "interface" for this
  * path is the Python API of mxfp4_expert.py and streamed_moe_router.py, and
  * there is no FFI.  Each entry point below replaces the torch-eager code at
- * the cited reference lines; the Python package `klcquant` (mxfp4_expert.py,
+ * the cited reference lines; the Python package `klcquant_amd` (mxfp4_expert.py,
  * streamed_moe_router.py) binds these through ctypes and keeps the reference's
  * Python signatures.
  *
@@ -182,7 +182,7 @@ int klc_moe_layer(const void* x, const void* router_w, const void* router_b, con
                   void* const* events, void* stream);
 
 /* ---- Synthetic inputs -------------------------------------------------------
- * Counter-based SplitMix64 stream, identical to klcquant/synth.py:
+ * Counter-based SplitMix64 stream, identical to klcquant_amd/synth.py:
  * mode 0: n random bytes; mode 1: n bytes uniform in [lo, hi]. */
 int klc_synth_fill(void* dst, int64_t n, uint64_t seed, int mode, int lo, int hi, void* stream);
 

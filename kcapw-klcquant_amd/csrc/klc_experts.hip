@@ -2,17 +2,16 @@
 // clamped SwiGLU) and down (+ bias), the weighted combine, and the one-call
 // MoE layer (gfx950).
 //
-// GEMV mapping.  A workgroup owns one 64-row tile of one active expert's
-// matrix (packed row-tile layout, see klc_common.h) and all tokens routed to
-// that expert.  Its 4 waves split the input groups; in each step every lane
-// loads 16 bytes = 32 E2M1 codes of its own row, so a wave-wide load is 1 KiB
-// of contiguous HBM.  Codes are decoded in registers with
-// v_cvt_scalef32_pk_f32_fp4; the activation slice of a group is the same for
-// all 64 lanes, so it is read through the scalar path and each weight is used
-// by every token of the expert straight from registers.  Per group the 32
-// products are summed and scaled once by 2^(e-127).  Wave partials are summed
-// in wave order through LDS, then wave 0 applies bias (+ SwiGLU on the
-// interleaved gate/up lane pairs) and writes fp32 results.
+// GEMV mapping.  Tokens are grouped by expert (klc_moe_dispatch), and one
+// workgroup streams a run of consecutive 64-row tiles of one active expert's
+// packed matrix (row-tile layout, klc_common.h) for all tokens routed to that
+// expert.  Codes are decoded in registers by v_cvt_scalef32_pk_bf16_fp4 (E2M1
+// times the E8M0 scale, exact) straight into the A operand of
+// v_mfma_f32_16x16x32_bf16; the B operand is the tokens' activation rows,
+// staged once per pass in LDS.  Each weight byte is read from HBM once per
+// pass however many tokens share the expert.  gate_up applies bias and the
+// clamped SwiGLU on interleaved row pairs in registers and writes the down
+// input; down applies bias and writes float32 expert outputs.
 #include "klc_common.h"
 
 namespace klc {

@@ -1,4 +1,4 @@
-// Counter-based SplitMix64 fill, identical to klcquant/synth.py: element i
+// Counter-based SplitMix64 fill, identical to klcquant_amd/synth.py: element i
 // uses draw(seed, i) = mix64(mix64(seed) + (i + 1) * GAMMA).
 #include "klc_common.h"
 

@@ -2,7 +2,7 @@
 
 The library is built in-tree next to this file so that it travels with the
 source tree; objects go to ``kcapw-klcquant_amd/_build``.  Run as
-``python -m klcquant._build`` (from ``kcapw-klcquant_amd``) or call
+``python -m klcquant_amd._build`` (from ``kcapw-klcquant_amd``) or call
 :func:`build_library`.
 """
 

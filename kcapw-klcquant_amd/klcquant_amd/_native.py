@@ -85,7 +85,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         p = Path(path) if path else LIB_PATH
         if not p.exists():
             raise KlcLibraryError(
-                f"{p} is missing: build it with `python -m klcquant._build` (hipcc, gfx950); "
+                f"{p} is missing: build it with `python -m klcquant_amd._build` (hipcc, gfx950); "
                 "the MoE path has no CPU fallback")
         try:
             lib = ctypes.CDLL(str(p))

@@ -243,7 +243,7 @@ def workspace_bytes(n_tokens: int, hidden: int, inter: int, n_experts: int, k: i
 
 
 def synth_fill(dst: torch.Tensor, seed: int, mode: int = 0, lo: int = 0, hi: int = 255) -> torch.Tensor:
-    """Fills a uint8 device tensor from the SplitMix64 stream (see klcquant.synth)."""
+    """Fills a uint8 device tensor from the SplitMix64 stream (see klcquant_amd.synth)."""
     _check_gpu("dst", dst, torch.uint8)
     nat.call("klc_synth_fill", _ptr(dst), dst.numel(), ctypes.c_uint64(seed & ((1 << 64) - 1)), mode, lo, hi,
              _stream(dst.device))

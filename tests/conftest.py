@@ -30,7 +30,7 @@ def gpu():
 
     if not torch.cuda.is_available():
         pytest.fail("GPU test run without a visible GPU")
-    from klcquant import _native
+    from klcquant_amd import _native
 
     _native.load()  # raises if libklcmoe.so is missing
     return torch.device("cuda:0")

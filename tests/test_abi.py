@@ -9,7 +9,7 @@ from pathlib import Path
 
 import pytest
 
-from klcquant import _native as nat
+from klcquant_amd import _native as nat
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "klc_moe.h"
 
@@ -90,7 +90,7 @@ def test_workspace_size_grows_with_tokens():
 
 def test_cpu_tensors_are_rejected():
     torch = pytest.importorskip("torch")
-    from klcquant import ops
+    from klcquant_amd import ops
 
     x = torch.zeros((2, 64), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU"):

@@ -24,7 +24,7 @@ import pytest
 import torch
 
 from conftest import bf16_bits, bf16_tensor
-from klcquant import moe, ops
+from klcquant_amd import moe, ops
 from oracle import experts as oex
 from oracle import layer as olayer
 from oracle.numerics import bf16_to_f32
@@ -129,7 +129,7 @@ def test_many_tokens_one_expert(gpu):
 
 def test_bias_only_combine(gpu):
     n_tok, k, n_exp, hidden = 9, 4, 16, 256
-    from klcquant import synth
+    from klcquant_amd import synth
     from oracle.router import topk
     dbias = synth.random_normal_bf16(5, n_exp * hidden, 0, 0.5).reshape(n_exp, hidden)
     logits = synth.random_normal_bf16(6, n_tok * n_exp).reshape(n_tok, n_exp)

@@ -8,7 +8,7 @@ import torch
 
 from conftest import bf16_bits
 from oracle import mxfp4 as omx
-from klcquant import ops, synth
+from klcquant_amd import ops, synth
 
 pytestmark = pytest.mark.gpu
 

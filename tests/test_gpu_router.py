@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from conftest import bf16_bits, bf16_tensor
-from klcquant import ops, synth
+from klcquant_amd import ops, synth
 from oracle import router as orr
 from oracle.numerics import f32_to_bf16
 
@@ -88,7 +88,7 @@ def test_router_rejects_bad_shapes(gpu):
     b = torch.zeros(8, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(ValueError):
         ops.router_logits(x, w, b)
-    from klcquant._native import KlcError
+    from klcquant_amd._native import KlcError
     x2 = torch.zeros((2, 100), dtype=torch.bfloat16, device=gpu)
     w2 = torch.zeros((8, 100), dtype=torch.bfloat16, device=gpu)
     with pytest.raises(KlcError, match="multiple of 8"):

@@ -18,9 +18,9 @@ import pytest
 import torch
 
 from conftest import bf16_bits, bf16_tensor
-from klcquant import moe
-from klcquant.mxfp4_expert import Mxfp4ExpertStore, ResidentExpertStore, dequantize_mxfp4_matrix
-from klcquant.streamed_moe_router import RoutingLocalityConfig, StreamedMoERouter
+from klcquant_amd import moe
+from klcquant_amd.mxfp4_expert import Mxfp4ExpertStore, ResidentExpertStore, dequantize_mxfp4_matrix
+from klcquant_amd.streamed_moe_router import RoutingLocalityConfig, StreamedMoERouter
 from oracle import experts as oex
 from oracle import mxfp4 as omx
 from oracle.numerics import bf16_to_f32
@@ -152,7 +152,7 @@ def test_store_prefetch_then_consume(gpu, setup, tmp_path):
 
 
 def test_dequantize_matrix_default_fp16(gpu):
-    from klcquant import synth
+    from klcquant_amd import synth
 
     blocks, scales = synth.mxfp4_expert_tensors(3, 4, 1, 64, 96, scale_lo=100, scale_hi=140)
     got = dequantize_mxfp4_matrix(torch.from_numpy(blocks[0]).to(gpu), torch.from_numpy(scales[0]).to(gpu))

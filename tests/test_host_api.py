@@ -11,8 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from klcquant import mxfp4_expert as mx
-from klcquant import streamed_moe_router as smr
+from klcquant_amd import mxfp4_expert as mx
+from klcquant_amd import streamed_moe_router as smr
 
 
 def item(n=4):

@@ -7,7 +7,7 @@ from fractions import Fraction
 
 import numpy as np
 
-from klcquant import synth
+from klcquant_amd import synth
 from oracle import experts, mxfp4
 from oracle.numerics import bf16_to_f32, f32_to_bf16
 from oracle.rmsnorm import residual_add, rms_norm

@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from klcquant import synth
+from klcquant_amd import synth
 from oracle.numerics import f32_to_bf16
 
 
