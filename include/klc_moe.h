@@ -85,8 +85,8 @@ int klc_mxfp4_dequant_packed(const void* packed, void* out, int64_t n_mat, int64
  * (streamed_moe_router.py:268-269): x[n_tokens][hidden], w[n_experts][hidden],
  * b[n_experts] bfloat16 -> logits[n_tokens][n_experts] bfloat16, computed as
  * bf16(f32(x . w) + b) with the dot product accumulated in float64.  If x_f32
- * is not NULL, also writes x as float32 [n_tokens][hidden] (the activation
- * read by klc_moe_gate_up). */
+ * is not NULL, also writes x as float32 [n_tokens][hidden] (hidden.float(),
+ * streamed_moe_router.py:505). */
 int klc_moe_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32,
                           int64_t n_tokens, int64_t hidden, int64_t n_experts, void* stream);
 
@@ -108,9 +108,20 @@ int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens
  * token per call, streamed_moe_router.py:499).  Pairs p = t*k + j are
  * counting-sorted by expert, ties by p: offsets[n_experts+1],
  * sorted_pairs[n_pairs], active[n_experts] (experts with >= 1 pair,
- * ascending, then -1 padding) and *n_active.  n_experts <= 256. */
+ * ascending, then -1 padding) and *n_active.  Also writes the GEMV work
+ * units, int32 units[klc_moe_units_size(n_pairs, n_experts)]:
+ *   units[0] = number of gate_up units, units[1] = number of down units,
+ *   then the gate_up list (capacity C8), then the down list (capacity C4),
+ *   C_m = (n_pairs + (m - 1) * min(n_pairs, n_experts)) / m.
+ * A unit is expert | (pass << 10) and covers the pass-th run of m tokens of
+ * that expert (m = 8 for gate_up, 4 for down); experts ascending, then passes.
+ * n_experts <= 256, n_pairs < 65536 and ceil(n_pairs / 64) * n_experts <= 65536. */
 int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
-                     int32_t* sorted_pairs, int32_t* active, int32_t* n_active, void* stream);
+                     int32_t* sorted_pairs, int32_t* active, int32_t* n_active, int32_t* units, void* stream);
+
+/* Number of int32 elements of the dispatch's work-unit array (or a negative
+ * status for unsupported sizes). */
+int64_t klc_moe_units_size(int64_t n_pairs, int64_t n_experts);
 
 /* ---- Experts ------------------------------------------------------------- */
 
@@ -118,26 +129,26 @@ int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int
  * (streamed_moe_router.py:500-506, 524-529).  w_gate_up is a device array of
  * n_experts pointers to packed [2*inter rows][hidden/32 groups] matrices;
  * bias is bfloat16 [n_experts][2*inter]; x is the bfloat16 hidden state
- * [n_tokens][hidden]; pairs p = t*k + j come from klc_moe_dispatch.
- * Writes the down input to gated_split as two bfloat16 planes
- * [2][n_tokens*k][inter]: hi = bf16(y) and lo = bf16(y - hi) of the float32
- * SwiGLU output y (under KLC_PRECISION_BF16, where the reference rounds y to
- * bfloat16, lo = 0), and, if gated_raw is not NULL, y itself as float32
- * [n_tokens*k][inter].  max_active bounds *n_active (normally
- * min(n_experts, n_tokens*k)).  hidden and inter must be <= 3072, hidden a
- * multiple of 64 and inter of 32. */
+ * [n_tokens][hidden]; offsets, sorted_pairs and units are klc_moe_dispatch's
+ * outputs for the n_tokens*k pairs.  Writes the down input to gated_split as
+ * two bfloat16 planes [2][n_tokens*k][inter]: hi = bf16(y) and
+ * lo = bf16(y - hi) of the float32 SwiGLU output y (under KLC_PRECISION_BF16,
+ * where the reference rounds y to bfloat16, lo = 0), and, if gated_raw is not
+ * NULL, y itself as float32 [n_tokens*k][inter].  hidden and inter must be
+ * <= 3072, hidden a multiple of 64 and inter of 32. */
 int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens, int64_t k,
-                    const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
-                    const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
-                    float swiglu_limit, int precision, void* gated_split, float* gated_raw, void* stream);
+                    int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* units,
+                    int64_t hidden, int64_t inter, float swiglu_limit, int precision, void* gated_split,
+                    float* gated_raw, void* stream);
 
 /* down GEMV + bias (streamed_moe_router.py:507-511): w_down is a device array
  * of n_experts pointers to packed [hidden rows][inter/32 groups] matrices;
  * bias bfloat16 [n_experts][hidden]; gated_split as written by
- * klc_moe_gate_up for n_pairs pairs -> expert_out[n_pairs][hidden] float32. */
+ * klc_moe_gate_up for n_pairs pairs -> expert_out[n_pairs][hidden] float32;
+ * offsets, sorted_pairs and units from klc_moe_dispatch. */
 int klc_moe_down(const void* const* w_down, const void* bias, const void* gated_split, int64_t n_pairs,
-                 const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active, const int32_t* n_active,
-                 int64_t max_active, int64_t hidden, int64_t inter, int precision, float* expert_out, void* stream);
+                 int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* units,
+                 int64_t hidden, int64_t inter, int precision, float* expert_out, void* stream);
 
 /* Weighted combine in top-k order (streamed_moe_router.py:497, 512-513):
  * out[t] = bf16 sum over j of bf16(bf16(expert_out[t*k+j]) * weights[t][j]),

@@ -51,6 +51,31 @@ __host__ __device__ __forceinline__ int64_t packed_scale_offset(int rows, int gr
          ((int64_t)row * 4 + (group & 3)) * rec + (group >> 2);
 }
 
+// Work units of the expert GEMVs.  A unit is one pass of one active expert
+// over up to kUnitTokens[kernel] of its tokens (gate_up stages 8 activation
+// rows per pass, down 4: it stages hi and lo rows per token); an expert with
+// more tokens gets several units, which run as separate workgroups.  The
+// dispatch writes both lists into one int32 array:
+//   [0] gate_up unit count, [1] down unit count,
+//   [2, 2 + cap(8))            gate_up units,
+//   [2 + cap(8), ... + cap(4)) down units,
+// a unit being expert | (pass << 10) (experts < 1024), experts ascending,
+// passes ascending.
+constexpr int kUnitTokensGateUp = 8;
+constexpr int kUnitTokensDown = 4;
+__host__ __device__ __forceinline__ int32_t make_unit(int expert, int pass) { return expert | (pass << 10); }
+__host__ __device__ __forceinline__ int unit_expert(int32_t u) { return u & 1023; }
+__host__ __device__ __forceinline__ int unit_pass(int32_t u) { return (int)((uint32_t)u >> 10); }
+// Upper bound on the units of n_pairs pairs over n_exp experts at `per`
+// tokens per unit: sum_e ceil(c_e / per) <= (n_pairs + (per - 1) * active) / per.
+__host__ __device__ inline int64_t units_capacity(int64_t n_pairs, int64_t n_exp, int per) {
+  const int64_t active = n_pairs < n_exp ? n_pairs : n_exp;
+  return (n_pairs + (per - 1) * active) / per;
+}
+__host__ __device__ inline int64_t units_size(int64_t n_pairs, int64_t n_exp) {
+  return 2 + units_capacity(n_pairs, n_exp, kUnitTokensGateUp) + units_capacity(n_pairs, n_exp, kUnitTokensDown);
+}
+
 // ---- device side -----------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }

@@ -8,8 +8,11 @@
 // expert.  Codes are decoded in registers by v_cvt_scalef32_pk_bf16_fp4 (E2M1
 // times the E8M0 scale, exact) straight into the A operand of
 // v_mfma_f32_16x16x32_bf16; the B operand is the tokens' activation rows,
-// staged once per pass in LDS.  Each weight byte is read from HBM once per
-// pass however many tokens share the expert.  gate_up applies bias and the
+// staged once in LDS.  A workgroup serves one work unit: up to 8 (gate_up)
+// or 4 (down) of the expert's tokens, so each weight byte is read from HBM
+// once per unit however many of its tokens share it; an expert with more
+// tokens has several units, run by separate workgroups side by side (see
+// klc_common.h).  gate_up applies bias and the
 // clamped SwiGLU on interleaved row pairs in registers and writes the down
 // input; down applies bias and writes float32 expert outputs.
 #include "klc_common.h"
@@ -21,10 +24,11 @@ int launch_router_logits(const void* x, const void* w, const void* b, void* logi
 int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
                 int64_t k, hipStream_t stream);
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
-                    int32_t* active, int32_t* n_active, hipStream_t stream);
+                    int32_t* active, int32_t* n_active, int32_t* units, hipStream_t stream);
 int launch_router_fused(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
                         int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
-                        int32_t* sorted, int32_t* active, int32_t* n_active, uint32_t* done, hipStream_t stream);
+                        int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* done,
+                        hipStream_t stream);
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp);
 int check_topk_args(int64_t n_tok, int64_t n_exp, int64_t k);
 int check_dispatch_args(int64_t n_pairs, int64_t n_exp);
@@ -33,7 +37,7 @@ namespace {
 
 constexpr int kGemvWaves = 4;                 // 4 x 16 rows = one 64-row tile per workgroup
 constexpr int kGemvThreads = kGemvWaves * kWave;
-constexpr int kVRows = 8;                     // activation rows (MFMA N columns) staged per pass
+constexpr int kVRows = 8;                     // activation rows (MFMA N columns) staged per unit
 constexpr int kMaxSteps = 24;                 // 4-group steps per row (inputs <= 3072)
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -80,15 +84,15 @@ __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
 // across tile boundaries.  kSteps is a template constant and every load is
 // unconditional straight-line code, which lets the compiler wait for exactly
 // one chunk per step (vector loads retire in order).  Past the last tile the
-// refills read the expert's first chunk again (an L2 hit, no HBM traffic).
+// refills are out-of-range buffer loads (they return 0 and touch no memory).
 // The activation-row loads are issued before the ring prologue, so waiting
 // for them (the oldest loads) does not wait for any weight chunk.
 //
 // Columns are up to kVRows activation rows.  gate_up stages one row per token
 // (the bfloat16 hidden state, exact).  down stages two rows per token, the hi
 // and lo bfloat16 planes written by gate_up (hi = bf16(y), lo = bf16(y - hi)),
-// so the float32 SwiGLU output enters the product with a 2^-17 residual.  An
-// expert with more tokens than one pass holds streams its tiles once per pass.
+// so the float32 SwiGLU output enters the product with a 2^-17 residual.  A
+// unit therefore holds 4 tokens in down and 8 in gate_up.
 constexpr int kRing = 8;  // every compiled kSteps >= kRing is a multiple of it (slot s % kRing is step s of any tile)
 
 template <bool kDown, int kSteps>
@@ -96,15 +100,18 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
     const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
-    const int32_t* __restrict__ active, const int32_t* __restrict__ n_active, int rows, int groups, int k_top,
+    const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
     float limit, int precision, int tpw) {
   extern __shared__ uint16_t xs[];  // [kVRows][row_stride] bfloat16 bits
 
   const int u = blockIdx.y;
-  if (u >= *n_active) return;
-  const int e = active[u];
+  if (u >= *n_units) return;
+  const int32_t unit = units[u];
+  const int e = unit_expert(unit);
   const int pb = offsets[e];
-  const int np = offsets[e + 1] - pb;
+  const int tok_per_pass = kDown ? kUnitTokensDown : kUnitTokensGateUp;
+  const int tc = unit_pass(unit) * tok_per_pass;  // first token of this unit
+  const int nt = min(tok_per_pass, offsets[e + 1] - pb - tc);
   const int tiles = rows / kTileRows;
   const int tile0 = blockIdx.x * tpw;
   const int ntile = min(tpw, tiles - tile0);
@@ -119,7 +126,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   constexpr int kLoads = (kVRows * kSteps * 16 + kGemvThreads - 1) / kGemvThreads;  // staging chunks per thread
   constexpr int kR = kRing < kSteps ? kRing : kSteps;
   static_assert(kSteps % kR == 0, "the ring must divide the step count");
-  const int tok_per_pass = kDown ? kVRows / 2 : kVRows;
+  static_assert(kUnitTokensGateUp <= kVRows && 2 * kUnitTokensDown <= kVRows, "a unit's rows fit one pass");
   const int trow = wave * 16 + lr;              // row inside a 64-row tile
   const int rec = ((groups + 3) / 4 + 7) / 8 * 8;
   const uint32_t tile_bytes = (uint32_t)groups * 1024u;
@@ -141,10 +148,8 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   const uint32_t rec_voff = (uint32_t)((trow * 4 + lq) * rec);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
 
-  for (int tc = 0; tc < np; tc += tok_per_pass) {
-    const int nt = min(tok_per_pass, np - tc);
+  {
     const int nrows = kDown ? 2 * nt : nt;
-    if (tc > 0) __syncthreads();  // the previous pass finished reading xs
 
     // ---- 1. activation-row loads (row sources are uniform: scalar loads) ----
     int src[kVRows];
@@ -234,9 +239,9 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
         if constexpr (kSteps > kR) {
           if (s == kSteps - kR) load_rec(next_tile, sc_next);
         }
-        // the chunk is invariant across passes; an empty asm "modifying" it
-        // keeps the decode inside the loop instead of hoisting every step's
-        // decoded operands (16 registers each) out of it
+        // an empty asm "modifying" the chunk pins each step's decode right
+        // here, so decoded operands (16 registers per step) are never
+        // computed early and kept live across steps
         asm volatile("" : "+v"(ring[s % kR]));
         const u32x4 w = ring[s % kR];
         {
@@ -347,12 +352,13 @@ GemvKernel<kDown> gemv_kernel_for(int steps) {
 
 size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * (steps * 128 + 8) * 2; }
 
-// Tiles each workgroup streams: enough workgroups to give every CU about three
-// (the LDS-limited residency), fewer tiles per workgroup when few experts are
-// active.  max_active is an upper bound of the active experts.
-int tiles_per_workgroup(int tiles, int64_t max_active) {
-  const int64_t target = 3 * 256;
-  int64_t tpw = (int64_t)tiles * max_active / target;
+// Tiles each workgroup streams: about three rounds of workgroups over the
+// chip (3 resident per CU x 256 CUs each round), so workgroups that finish
+// early are replaced and the tail stays short; one tile per workgroup when
+// few units exist.  max_units is an upper bound of the units.
+int tiles_per_workgroup(int tiles, int64_t max_units) {
+  const int64_t target = 3 * 3 * 256;
+  int64_t tpw = (int64_t)tiles * max_units / target;
   if (tpw < 1) tpw = 1;
   if (tpw > tiles) tpw = tiles;
   return (int)tpw;
@@ -416,45 +422,51 @@ __global__ __launch_bounds__(256) void pair_norms_kernel(const float* __restrict
   }
 }
 
-int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t max_active) {
-  KLC_REQUIRE(hidden > 0 && inter > 0 && max_active > 0, KLC_ERR_ARGUMENT,
-              "experts: bad sizes hidden=%lld inter=%lld max_active=%lld", (long long)hidden, (long long)inter,
-              (long long)max_active);
+int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t n_pairs, int64_t n_exp) {
+  KLC_REQUIRE(hidden > 0 && inter > 0 && n_pairs > 0 && n_exp > 0, KLC_ERR_ARGUMENT,
+              "experts: bad sizes hidden=%lld inter=%lld n_pairs=%lld n_experts=%lld", (long long)hidden,
+              (long long)inter, (long long)n_pairs, (long long)n_exp);
+  const int rc = check_dispatch_args(n_pairs, n_exp);
+  if (rc) return rc;
   KLC_REQUIRE(hidden % 64 == 0 && inter % 32 == 0 && (2 * inter) % 64 == 0, KLC_ERR_SHAPE,
               "experts: hidden=%lld must be a multiple of 64 and inter=%lld a multiple of 32", (long long)hidden,
               (long long)inter);
-  KLC_REQUIRE(max_active <= 65535 && hidden <= 32 * 4 * kMaxSteps && inter <= 32 * 4 * kMaxSteps,
-              KLC_ERR_UNSUPPORTED, "experts: unsupported sizes (hidden, inter <= %d)", 32 * 4 * kMaxSteps);
+  KLC_REQUIRE(units_capacity(n_pairs, n_exp, kUnitTokensDown) <= 65535 && hidden <= 32 * 4 * kMaxSteps &&
+                  inter <= 32 * 4 * kMaxSteps,
+              KLC_ERR_UNSUPPORTED, "experts: unsupported sizes (hidden, inter <= %d, <= 65535 work units)",
+              32 * 4 * kMaxSteps);
   return KLC_OK;
 }
 
-int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k,
-                   const int32_t* offsets, const int32_t* pairs, const int32_t* active, const int32_t* n_active,
-                   int64_t max_active, int64_t hidden, int64_t inter, float limit, int precision, void* gated_split,
-                   float* gated_raw, hipStream_t stream) {
+int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k, int64_t n_exp,
+                   const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
+                   float limit, int precision, void* gated_split, float* gated_raw, hipStream_t stream) {
   const int tiles = (int)(2 * inter / kTileRows);
-  const int tpw = tiles_per_workgroup(tiles, max_active);
-  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)max_active);
+  const int64_t cap = units_capacity(n_tok * k, n_exp, kUnitTokensGateUp);
+  const int tpw = tiles_per_workgroup(tiles, cap);
+  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)cap);
   const int steps = gemv_steps((int)(hidden / 32));
   gemv_kernel_for<false>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(x), 0, nullptr, static_cast<uint16_t*>(gated_split), n_tok * k * inter,
-      gated_raw, offsets, pairs, active, n_active, (int)(2 * inter), (int)(hidden / 32), (int)k, limit, precision,
+      gated_raw, offsets, pairs, units + 2, units, (int)(2 * inter), (int)(hidden / 32), (int)k, limit, precision,
       tpw);
   return check_launch("moe_gemv_mfma_kernel<gate_up>");
 }
 
-int launch_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs,
-                const int32_t* offsets, const int32_t* pairs, const int32_t* active, const int32_t* n_active,
-                int64_t max_active, int64_t hidden, int64_t inter, int precision, float* eo, hipStream_t stream) {
+int launch_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs, int64_t n_exp,
+                const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
+                int precision, float* eo, hipStream_t stream) {
   const int tiles = (int)(hidden / kTileRows);
-  const int tpw = tiles_per_workgroup(tiles, max_active);
-  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)max_active);
+  const int64_t cap = units_capacity(n_pairs, n_exp, kUnitTokensDown);
+  const int tpw = tiles_per_workgroup(tiles, cap);
+  const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)cap);
+  const int32_t* list = units + 2 + units_capacity(n_pairs, n_exp, kUnitTokensGateUp);
   const int steps = gemv_steps((int)(inter / 32));
   gemv_kernel_for<true>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
-      static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs, active,
-      n_active, (int)hidden, (int)(inter / 32), 1, 0.0f, precision, tpw);
+      static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs, list,
+      units + 1, (int)hidden, (int)(inter / 32), 1, 0.0f, precision, tpw);
   return check_launch("moe_gemv_mfma_kernel<down>");
 }
 
@@ -471,7 +483,7 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 constexpr int64_t kFusedRouterTokens = 2;  // batches up to this size use the one-launch router
 
 struct LayerScratch {
-  int64_t counters, logits, ids, values, weights, offsets, sorted, active, n_active, gated, eo, total;
+  int64_t counters, logits, ids, values, weights, offsets, sorted, active, n_active, units, gated, eo, total;
 };
 
 LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k) {
@@ -487,6 +499,7 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
   s.sorted = off;   off += align256(pairs * 4);
   s.active = off;   off += align256(n_exp * 4);
   s.n_active = off; off += align256(4);
+  s.units = off;    off += align256(units_size(pairs, n_exp) * 4);
   s.gated = off;    off += align256(pairs * inter * 4);  // hi and lo bf16 planes
   s.eo = off;       off += align256(pairs * hidden * 4);
   s.total = off;
@@ -499,34 +512,34 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
 using namespace klc;
 
 extern "C" int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens,
-                               int64_t k, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
-                               const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter,
-                               float swiglu_limit, int precision, void* gated_split, float* gated_raw, void* stream) {
-  KLC_REQUIRE(w_gate_up && bias && x && offsets && sorted_pairs && active && n_active && gated_split,
-              KLC_ERR_ARGUMENT, "klc_moe_gate_up: null pointer");
+                               int64_t k, int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs,
+                               const int32_t* units, int64_t hidden, int64_t inter, float swiglu_limit,
+                               int precision, void* gated_split, float* gated_raw, void* stream) {
+  KLC_REQUIRE(w_gate_up && bias && x && offsets && sorted_pairs && units && gated_split, KLC_ERR_ARGUMENT,
+              "klc_moe_gate_up: null pointer");
   KLC_REQUIRE(n_tokens > 0 && k > 0, KLC_ERR_ARGUMENT, "klc_moe_gate_up: n_tokens=%lld k=%lld", (long long)n_tokens,
               (long long)k);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "klc_moe_gate_up: unknown precision %d", precision);
-  const int rc = check_gemv_shapes(hidden, inter, max_active);
+  const int rc = check_gemv_shapes(hidden, inter, n_tokens * k, n_experts);
   if (rc) return rc;
-  return launch_gate_up(w_gate_up, bias, x, n_tokens, k, offsets, sorted_pairs, active, n_active, max_active, hidden,
-                        inter, swiglu_limit, precision, gated_split, gated_raw, as_stream(stream));
+  return launch_gate_up(w_gate_up, bias, x, n_tokens, k, n_experts, offsets, sorted_pairs, units, hidden, inter,
+                        swiglu_limit, precision, gated_split, gated_raw, as_stream(stream));
 }
 
 extern "C" int klc_moe_down(const void* const* w_down, const void* bias, const void* gated_split, int64_t n_pairs,
-                            const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* active,
-                            const int32_t* n_active, int64_t max_active, int64_t hidden, int64_t inter, int precision,
-                            float* expert_out, void* stream) {
-  KLC_REQUIRE(w_down && bias && gated_split && offsets && sorted_pairs && active && n_active && expert_out,
-              KLC_ERR_ARGUMENT, "klc_moe_down: null pointer");
+                            int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs,
+                            const int32_t* units, int64_t hidden, int64_t inter, int precision, float* expert_out,
+                            void* stream) {
+  KLC_REQUIRE(w_down && bias && gated_split && offsets && sorted_pairs && units && expert_out, KLC_ERR_ARGUMENT,
+              "klc_moe_down: null pointer");
   KLC_REQUIRE(n_pairs > 0, KLC_ERR_ARGUMENT, "klc_moe_down: n_pairs=%lld", (long long)n_pairs);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "klc_moe_down: unknown precision %d", precision);
-  const int rc = check_gemv_shapes(hidden, inter, max_active);
+  const int rc = check_gemv_shapes(hidden, inter, n_pairs, n_experts);
   if (rc) return rc;
-  return launch_down(w_down, bias, gated_split, n_pairs, offsets, sorted_pairs, active, n_active, max_active, hidden,
-                     inter, precision, expert_out, as_stream(stream));
+  return launch_down(w_down, bias, gated_split, n_pairs, n_experts, offsets, sorted_pairs, units, hidden, inter,
+                     precision, expert_out, as_stream(stream));
 }
 
 extern "C" int klc_moe_combine(const float* expert_out, const void* weights, int64_t n_tokens, int64_t k,
@@ -580,10 +593,7 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   if (rc) return rc;
   rc = check_topk_args(n_tokens, n_experts, k);
   if (rc) return rc;
-  rc = check_dispatch_args(n_tokens * k, n_experts);
-  if (rc) return rc;
-  const int64_t max_active = n_experts < n_tokens * k ? n_experts : n_tokens * k;
-  rc = check_gemv_shapes(hidden, inter, max_active);
+  rc = check_gemv_shapes(hidden, inter, n_tokens * k, n_experts);
   if (rc) return rc;
   KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "klc_moe_layer: n_tokens=%lld > 65535", (long long)n_tokens);
   const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
@@ -600,6 +610,7 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   int32_t* sorted = reinterpret_cast<int32_t*>(ws + s.sorted);
   int32_t* active = reinterpret_cast<int32_t*>(ws + s.active);
   int32_t* n_active = reinterpret_cast<int32_t*>(ws + s.n_active);
+  int32_t* units = reinterpret_cast<int32_t*>(ws + s.units);
   void* gated = ws + s.gated;
   float* eo = reinterpret_cast<float*>(ws + s.eo);
   uint32_t* counters = reinterpret_cast<uint32_t*>(ws + s.counters);
@@ -614,7 +625,7 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   if (n_tokens <= kFusedRouterTokens) {
     // decode batches: logits, top-k and dispatch in one launch
     if ((rc = launch_router_fused(x, router_w, router_b, logits, n_tokens, hidden, n_experts, k, ids_buf, values,
-                                  w_buf, offsets, sorted, active, n_active, counters, st)))
+                                  w_buf, offsets, sorted, active, n_active, units, counters, st)))
       return rc;
     if ((rc = mark(1))) return rc;
     if ((rc = mark(2))) return rc;
@@ -624,15 +635,16 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
     if ((rc = mark(1))) return rc;
     if ((rc = launch_topk(logits, ids_buf, values, w_buf, n_tokens, n_experts, k, st))) return rc;
     if ((rc = mark(2))) return rc;
-    if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, st))) return rc;
+    if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, units, st)))
+      return rc;
   }
   if ((rc = mark(3))) return rc;
-  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, offsets, sorted, active, n_active, max_active,
-                           hidden, inter, swiglu_limit, precision, gated, nullptr, st)))
+  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden, inter,
+                           swiglu_limit, precision, gated, nullptr, st)))
     return rc;
   if ((rc = mark(4))) return rc;
-  if ((rc = launch_down(w_down, down_bias, gated, n_tokens * k, offsets, sorted, active, n_active, max_active, hidden,
-                        inter, precision, eo, st)))
+  if ((rc = launch_down(w_down, down_bias, gated, n_tokens * k, n_experts, offsets, sorted, units, hidden, inter,
+                        precision, eo, st)))
     return rc;
   if ((rc = mark(5))) return rc;
   if ((rc = launch_combine(eo, w_buf, n_tokens, k, hidden, out, st))) return rc;

@@ -13,8 +13,8 @@
 // float64 and rounded to float32, then to bfloat16.
 //
 // Dispatch: one workgroup performs a stable counting sort of the (token, slot)
-// pairs by expert: per-chunk histograms in LDS, an exclusive scan over chunks
-// and experts, then an in-order scatter.
+// pairs by expert: per-64-pair-chunk histograms from wave ballots, an
+// exclusive scan over chunks and experts, then an in-order scatter.
 #include "klc_common.h"
 
 namespace klc {
@@ -36,26 +36,41 @@ __device__ void router_logits_tile(const uint16_t* __restrict__ x, const uint16_
   const int e = blockIdx.x * 4 + wave;
   const int nchunk = hidden >> 3;  // hidden % 8 == 0 (checked on the host)
 
+  // every load is unconditional (indices clamped into range, surplus values
+  // discarded) so all of a lane's loads are in flight together
   uint4 wv[kRouterChunks];
-  if (e < n_exp) {
-    const uint16_t* wr = w + (int64_t)e * hidden;
+  {
+    const uint16_t* wr = w + (int64_t)min(e, n_exp - 1) * hidden;
 #pragma unroll
     for (int i = 0; i < kRouterChunks; ++i) {
       const int c = lane + i * kWave;
-      wv[i] = c < nchunk ? *reinterpret_cast<const uint4*>(wr + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 v = *reinterpret_cast<const uint4*>(wr + min(c, nchunk - 1) * 8);
+      wv[i] = c < nchunk ? v : make_uint4(0u, 0u, 0u, 0u);
     }
   }
   const int64_t base = (int64_t)t0 * hidden;
-  for (int i = threadIdx.x; i < nt * nchunk; i += blockDim.x) {
-    const uint4 v = *reinterpret_cast<const uint4*>(x + base + (int64_t)i * 8);
-    *reinterpret_cast<uint4*>(xs + i * 8) = v;
-    if (x_f32 != nullptr && blockIdx.x == 0) {
-      const uint32_t words[4] = {v.x, v.y, v.z, v.w};
-      float4* dst = reinterpret_cast<float4*>(x_f32 + base + (int64_t)i * 8);
-      dst[0] = make_float4(__uint_as_float(words[0] << 16), __uint_as_float(words[0] & 0xffff0000u),
-                           __uint_as_float(words[1] << 16), __uint_as_float(words[1] & 0xffff0000u));
-      dst[1] = make_float4(__uint_as_float(words[2] << 16), __uint_as_float(words[2] & 0xffff0000u),
-                           __uint_as_float(words[3] << 16), __uint_as_float(words[3] & 0xffff0000u));
+  const int n_stage = nt * nchunk;
+  constexpr int kStage = kRouterTok * kWave * kRouterChunks / 256;  // chunks per thread (blockDim.x == 256)
+  uint4 xv[kStage];
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int i = min((int)threadIdx.x + j * 256, n_stage - 1);
+    xv[j] = *reinterpret_cast<const uint4*>(x + base + (int64_t)i * 8);
+  }
+#pragma unroll
+  for (int j = 0; j < kStage; ++j) {
+    const int i = (int)threadIdx.x + j * 256;
+    if (i < n_stage) {
+      const uint4 v = xv[j];
+      *reinterpret_cast<uint4*>(xs + i * 8) = v;
+      if (x_f32 != nullptr && blockIdx.x == 0) {
+        const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+        float4* dst = reinterpret_cast<float4*>(x_f32 + base + (int64_t)i * 8);
+        dst[0] = make_float4(__uint_as_float(words[0] << 16), __uint_as_float(words[0] & 0xffff0000u),
+                             __uint_as_float(words[1] << 16), __uint_as_float(words[1] & 0xffff0000u));
+        dst[1] = make_float4(__uint_as_float(words[2] << 16), __uint_as_float(words[2] & 0xffff0000u),
+                             __uint_as_float(words[3] << 16), __uint_as_float(words[3] & 0xffff0000u));
+      }
     }
   }
   __syncthreads();
@@ -234,62 +249,107 @@ __device__ void block_exclusive_scan_256(int32_t* v, int n, int32_t* total) {
   }
 }
 
+// Pairs are taken in chunks of 64 (one wave-wide pass); hist[c][e] counts the
+// pairs of expert e in chunk c (then, after the scan over chunks, the pairs
+// of e in chunks before c).
+constexpr int kDispatchChunk = kWave;
+constexpr int64_t kDispatchMaxHistBytes = 128 * 1024;
+
+__host__ __device__ constexpr int dispatch_chunks(int n_pairs) { return (n_pairs + kDispatchChunk - 1) / kDispatchChunk; }
+
 // LDS bytes block_dispatch needs for n_pairs pairs over n_exp experts.
 __host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int n_exp) {
-  return (size_t)n_exp * (n_pairs < kDispatchThreads ? n_pairs : kDispatchThreads) * sizeof(uint16_t) +
-         2 * kDispatchMaxExperts * sizeof(int32_t) + 2 * sizeof(int32_t);
+  return ((size_t)dispatch_chunks(n_pairs) * n_exp * sizeof(uint16_t) + 15) / 16 * 16 +
+         4 * kDispatchMaxExperts * sizeof(int32_t) + 4 * sizeof(int32_t);
 }
 
-// Stable counting sort of the pairs by expert, by one 256-thread block.
-// lds holds dispatch_lds_bytes(n_pairs, n_exp) bytes.
+// Lanes of the wave holding the same key (key < 512): the lanes that agree
+// with this lane on each of the 9 key bits.
+__device__ __forceinline__ uint64_t wave_peers(uint32_t key) {
+  uint64_t peers = ~0ull;
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    const bool bit = (key >> b) & 1u;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
+}
+
+// Stable counting sort of the pairs by expert, by one 256-thread block, and
+// the GEMV work-unit lists (klc_common.h).  Chunk c of 64 pairs is handled by
+// wave c % 4: a lane's rank among the chunk's pairs of its expert comes from
+// ballots, so no step is serial over pairs.  lds holds
+// dispatch_lds_bytes(n_pairs, n_exp) bytes.
 __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
                                int32_t* __restrict__ sorted, int32_t* __restrict__ active,
-                               int32_t* __restrict__ n_active, char* lds) {
+                               int32_t* __restrict__ n_active, int32_t* __restrict__ units, char* lds) {
   const int tid = threadIdx.x;
-  const int chunks = n_pairs < kDispatchThreads ? n_pairs : kDispatchThreads;
-  const int per = (n_pairs + chunks - 1) / chunks;
-  // cnt[e * chunks + c]: pairs of expert e in chunk c (then its exclusive prefix)
-  uint16_t* cnt = reinterpret_cast<uint16_t*>(lds);
-  int32_t* total = reinterpret_cast<int32_t*>(lds + (size_t)n_exp * chunks * sizeof(uint16_t));
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int nchunk = dispatch_chunks(n_pairs);
+  uint16_t* hist = reinterpret_cast<uint16_t*>(lds);
+  int32_t* total = reinterpret_cast<int32_t*>(lds + ((size_t)nchunk * n_exp * sizeof(uint16_t) + 15) / 16 * 16);
   int32_t* flags = total + kDispatchMaxExperts;
-  int32_t* sums = flags + kDispatchMaxExperts;
+  int32_t* ugu = flags + kDispatchMaxExperts;  // units per expert, then their prefix (gate_up)
+  int32_t* udn = ugu + kDispatchMaxExperts;    // same for down
+  int32_t* sums = udn + kDispatchMaxExperts;
+  const uint64_t below = (1ull << lane) - 1ull;
 
-  for (int i = tid; i < n_exp * chunks; i += kDispatchThreads) cnt[i] = 0;
+  for (int i = tid; i < nchunk * n_exp; i += kDispatchThreads) hist[i] = 0;
   __syncthreads();
-  if (tid < chunks) {
-    const int p_end = min(n_pairs, (tid + 1) * per);
-    for (int p = tid * per; p < p_end; ++p) {
-      const int e = ids[p];
-      if (e >= 0 && e < n_exp) cnt[e * chunks + tid] += 1;
-    }
+  // 1. per-chunk counts: the lowest lane of each expert's peer group writes them
+  for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
+    const int p = c * kDispatchChunk + lane;
+    const int e = p < n_pairs ? ids[p] : -1;
+    const bool valid = e >= 0 && e < n_exp;
+    const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
+    if (valid && (peers & below) == 0ull) hist[c * n_exp + e] = (uint16_t)__popcll(peers);
   }
   __syncthreads();
+  // 2. per expert: exclusive prefix over chunks, totals, unit counts
   for (int e = tid; e < n_exp; e += kDispatchThreads) {
     int32_t run = 0;
-    uint16_t* c = cnt + e * chunks;
-    for (int i = 0; i < chunks; ++i) {
-      const int32_t v = c[i];
-      c[i] = (uint16_t)run;
+    for (int c = 0; c < nchunk; ++c) {
+      const int32_t v = hist[c * n_exp + e];
+      hist[c * n_exp + e] = (uint16_t)run;
       run += v;
     }
     total[e] = run;
     flags[e] = run > 0 ? 1 : 0;
+    ugu[e] = (run + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
+    udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
   }
   __syncthreads();
-  // total[] becomes the expert offsets, flags[] the active-list positions
+  // total[] becomes the expert offsets, flags[] the active-list positions,
+  // ugu[]/udn[] the first unit of each expert
   block_exclusive_scan_256(total, n_exp, &sums[0]);
   __syncthreads();
   block_exclusive_scan_256(flags, n_exp, &sums[1]);
   __syncthreads();
-  if (tid < chunks) {
-    const int p_end = min(n_pairs, (tid + 1) * per);
-    for (int p = tid * per; p < p_end; ++p) {
-      const int e = ids[p];
-      if (e >= 0 && e < n_exp) {
-        const int pos = total[e] + cnt[e * chunks + tid];
-        cnt[e * chunks + tid] += 1;
-        sorted[pos] = p;
-      }
+  block_exclusive_scan_256(ugu, n_exp, &sums[2]);
+  __syncthreads();
+  block_exclusive_scan_256(udn, n_exp, &sums[3]);
+  __syncthreads();
+  // 3. scatter: position = expert offset + pairs of e in earlier chunks + rank in this chunk
+  for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
+    const int p = c * kDispatchChunk + lane;
+    const int e = p < n_pairs ? ids[p] : -1;
+    const bool valid = e >= 0 && e < n_exp;
+    const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
+    if (valid) sorted[total[e] + hist[c * n_exp + e] + __popcll(peers & below)] = p;
+  }
+  {
+    int32_t* gu_list = units + 2;
+    int32_t* dn_list = gu_list + units_capacity(n_pairs, n_exp, kUnitTokensGateUp);
+    for (int e = tid; e < n_exp; e += kDispatchThreads) {
+      const int c = (e + 1 < n_exp ? total[e + 1] : sums[0]) - total[e];
+      for (int j = 0; j * kUnitTokensGateUp < c; ++j) gu_list[ugu[e] + j] = make_unit(e, j);
+      for (int j = 0; j * kUnitTokensDown < c; ++j) dn_list[udn[e] + j] = make_unit(e, j);
+    }
+    if (tid == 0) {
+      units[0] = sums[2];
+      units[1] = sums[3];
     }
   }
   for (int e = tid; e < n_exp; e += kDispatchThreads) {
@@ -308,9 +368,10 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
                                                                     int n_exp, int32_t* __restrict__ offsets,
                                                                     int32_t* __restrict__ sorted,
                                                                     int32_t* __restrict__ active,
-                                                                    int32_t* __restrict__ n_active) {
+                                                                    int32_t* __restrict__ n_active,
+                                                                    int32_t* __restrict__ units) {
   extern __shared__ char dlds[];
-  block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, dlds);
+  block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
 }
 
 // Router for decode batches in one launch: every workgroup computes its
@@ -325,7 +386,8 @@ __global__ __launch_bounds__(256) void router_fused_kernel(const uint16_t* __res
                                                            float* __restrict__ values, uint16_t* __restrict__ weights,
                                                            int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
                                                            int32_t* __restrict__ active,
-                                                           int32_t* __restrict__ n_active, uint32_t* done) {
+                                                           int32_t* __restrict__ n_active, int32_t* __restrict__ units,
+                                                           uint32_t* done) {
   extern __shared__ char flds[];
   router_logits_tile(x, w, b, logits, nullptr, n_tok, hidden, n_exp, reinterpret_cast<uint16_t*>(flds));
   __shared__ uint32_t last;
@@ -348,7 +410,7 @@ __global__ __launch_bounds__(256) void router_fused_kernel(const uint16_t* __res
   }
   __threadfence_block();
   __syncthreads();
-  block_dispatch(ids, n_tok * k, n_exp, offsets, sorted, active, n_active, flds);
+  block_dispatch(ids, n_tok * k, n_exp, offsets, sorted, active, n_active, units, flds);
 }
 
 }  // namespace
@@ -372,22 +434,23 @@ int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, 
 }
 
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
-                    int32_t* active, int32_t* n_active, hipStream_t stream) {
+                    int32_t* active, int32_t* n_active, int32_t* units, hipStream_t stream) {
   dispatch_kernel<<<1, kDispatchThreads, dispatch_lds_bytes((int)n_pairs, (int)n_exp), stream>>>(
-      ids, (int)n_pairs, (int)n_exp, offsets, sorted, active, n_active);
+      ids, (int)n_pairs, (int)n_exp, offsets, sorted, active, n_active, units);
   return check_launch("dispatch_kernel");
 }
 
 int launch_router_fused(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
                         int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
-                        int32_t* sorted, int32_t* active, int32_t* n_active, uint32_t* done, hipStream_t stream) {
+                        int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* done,
+                        hipStream_t stream) {
   const dim3 grid((unsigned)((n_exp + 3) / 4), (unsigned)((n_tok + kRouterTok - 1) / kRouterTok));
   const size_t lds_logits = (size_t)kRouterTok * hidden * sizeof(uint16_t);
   const size_t lds_dispatch = dispatch_lds_bytes((int)(n_tok * k), (int)n_exp);
   router_fused_kernel<<<grid, 256, lds_logits > lds_dispatch ? lds_logits : lds_dispatch, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
       static_cast<uint16_t*>(logits), (int)n_tok, (int)hidden, (int)n_exp, (int)k, ids, values,
-      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, done);
+      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, units, done);
   return check_launch("router_fused_kernel");
 }
 
@@ -418,8 +481,9 @@ int check_dispatch_args(int64_t n_pairs, int64_t n_exp) {
               (long long)n_pairs, (long long)n_exp);
   KLC_REQUIRE(n_exp <= kDispatchMaxExperts, KLC_ERR_UNSUPPORTED, "dispatch: n_experts=%lld > %d", (long long)n_exp,
               kDispatchMaxExperts);
-  KLC_REQUIRE(n_pairs <= (int64_t)kDispatchThreads * 65535, KLC_ERR_UNSUPPORTED, "dispatch: n_pairs=%lld too large",
-              (long long)n_pairs);
+  KLC_REQUIRE(n_pairs < 65536 && (int64_t)dispatch_chunks((int)n_pairs) * n_exp * 2 <= kDispatchMaxHistBytes,
+              KLC_ERR_UNSUPPORTED, "dispatch: n_pairs=%lld too large for %lld experts (ceil(n_pairs / 64) * "
+              "n_experts <= 65536, n_pairs < 65536)", (long long)n_pairs, (long long)n_exp);
   return KLC_OK;
 }
 
@@ -454,9 +518,18 @@ extern "C" int klc_moe_softmax_weights(const float* values, void* weights, int64
 }
 
 extern "C" int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
-                                int32_t* sorted_pairs, int32_t* active, int32_t* n_active, void* stream) {
-  KLC_REQUIRE(ids && offsets && sorted_pairs && active && n_active, KLC_ERR_ARGUMENT, "klc_moe_dispatch: null pointer");
+                                int32_t* sorted_pairs, int32_t* active, int32_t* n_active, int32_t* units,
+                                void* stream) {
+  KLC_REQUIRE(ids && offsets && sorted_pairs && active && n_active && units, KLC_ERR_ARGUMENT,
+              "klc_moe_dispatch: null pointer");
   const int rc = check_dispatch_args(n_pairs, n_experts);
   if (rc) return rc;
-  return launch_dispatch(ids, n_pairs, n_experts, offsets, sorted_pairs, active, n_active, as_stream(stream));
+  return launch_dispatch(ids, n_pairs, n_experts, offsets, sorted_pairs, active, n_active, units,
+                         as_stream(stream));
+}
+
+extern "C" int64_t klc_moe_units_size(int64_t n_pairs, int64_t n_experts) {
+  const int rc = check_dispatch_args(n_pairs, n_experts);
+  if (rc) return rc;
+  return units_size(n_pairs, n_experts);
 }

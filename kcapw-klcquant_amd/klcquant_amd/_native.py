@@ -45,9 +45,10 @@ SIGNATURES: dict[str, tuple] = {
     "klc_moe_router_logits": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "klc_moe_topk_softmax": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "klc_moe_softmax_weights": (_I32, [_P, _P, _I64, _I64, _P]),
-    "klc_moe_dispatch": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
-    "klc_moe_gate_up": (_I32, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _F32, _I32, _P, _P, _P]),
-    "klc_moe_down": (_I32, [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I32, _P, _P]),
+    "klc_moe_dispatch": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "klc_moe_units_size": (_I64, [_I64, _I64]),
+    "klc_moe_gate_up": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _F32, _I32, _P, _P, _P]),
+    "klc_moe_down": (_I32, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I32, _P, _P]),
     "klc_moe_combine": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_bias_combine": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_pair_norms": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P]),

@@ -204,14 +204,12 @@ class MoELayer:
             ops._check_gpu("ids", ids, torch.int32, 2)
             ops._check_gpu("weights", weights, torch.bfloat16, 2)
         k = ids.shape[1]
-        offsets, sorted_pairs, active, n_active = ops.dispatch(ids, w.n_experts)
-        max_active = min(w.n_experts, ids.numel())
-        gated, gated_raw = ops.gate_up(w.gate_up_table, w.gate_up_bias, x, k, offsets, sorted_pairs, active,
-                                       n_active, max_active, w.hidden, w.inter, self.limit, self.precision,
-                                       want_raw=True)
-        eo = ops.down(w.down_table, w.down_bias, gated, offsets, sorted_pairs, active, n_active, max_active, w.hidden,
-                      w.inter, self.precision)
+        disp = ops.dispatch(ids, w.n_experts)
+        gated, gated_raw = ops.gate_up(w.gate_up_table, w.gate_up_bias, x, k, disp, w.hidden, w.inter, self.limit,
+                                       self.precision, want_raw=True)
+        eo = ops.down(w.down_table, w.down_bias, gated, disp, w.hidden, w.inter, self.precision)
         out = ops.combine(eo, weights, x.shape[0], k)
         return {"out": out, "logits": logits, "ids": ids, "values": values, "weights": weights,
-                "offsets": offsets, "sorted_pairs": sorted_pairs, "active": active, "n_active": n_active,
-                "gated": gated_raw, "gated_act": gated, "expert_out": eo}
+                "offsets": disp.offsets, "sorted_pairs": disp.sorted_pairs, "active": disp.active,
+                "n_active": disp.n_active, "units": disp.units, "gated": gated_raw, "gated_act": gated,
+                "expert_out": eo}

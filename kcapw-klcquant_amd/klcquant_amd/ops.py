@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from typing import NamedTuple
 
 import torch
 
@@ -154,8 +155,21 @@ def softmax_weights(values: torch.Tensor) -> torch.Tensor:
     return weights
 
 
-def dispatch(ids: torch.Tensor, n_experts: int):
-    """int32 ids ``[B, k]`` -> (offsets ``[E + 1]``, sorted_pairs ``[B * k]``, active ``[E]``, n_active ``[1]``)."""
+class Dispatch(NamedTuple):
+    """klc_moe_dispatch outputs: expert offsets ``[E + 1]``, pairs sorted by expert
+    ``[P]``, active experts ``[E]`` (-1 padded), their count ``[1]`` and the GEMV
+    work units (``units[0]``/``units[1]`` = gate_up/down unit counts, then the lists)."""
+
+    offsets: torch.Tensor
+    sorted_pairs: torch.Tensor
+    active: torch.Tensor
+    n_active: torch.Tensor
+    units: torch.Tensor
+    n_experts: int
+
+
+def dispatch(ids: torch.Tensor, n_experts: int) -> Dispatch:
+    """int32 ids ``[B, k]`` -> :class:`Dispatch`."""
     _check_gpu("ids", ids, torch.int32)
     dev = ids.device
     n_pairs = ids.numel()
@@ -163,9 +177,10 @@ def dispatch(ids: torch.Tensor, n_experts: int):
     sorted_pairs = torch.empty(n_pairs, dtype=torch.int32, device=dev)
     active = torch.empty(n_experts, dtype=torch.int32, device=dev)
     n_active = torch.empty(1, dtype=torch.int32, device=dev)
+    units = torch.empty(nat.call("klc_moe_units_size", n_pairs, n_experts), dtype=torch.int32, device=dev)
     nat.call("klc_moe_dispatch", _ptr(ids), n_pairs, n_experts, _ptr(offsets), _ptr(sorted_pairs), _ptr(active),
-             _ptr(n_active), _stream(dev))
-    return offsets, sorted_pairs, active, n_active
+             _ptr(n_active), _ptr(units), _stream(dev))
+    return Dispatch(offsets, sorted_pairs, active, n_active, units, n_experts)
 
 
 # ---- Experts --------------------------------------------------------------------
@@ -181,29 +196,29 @@ def pointer_table(mats: list[torch.Tensor] | torch.Tensor, device: torch.device)
     return torch.tensor(addrs, dtype=torch.int64).to(device)
 
 
-def gate_up(table: torch.Tensor, bias: torch.Tensor, x: torch.Tensor, k: int, offsets, sorted_pairs, active,
-            n_active, max_active: int, hidden: int, inter: int, limit: float = 7.0, precision: str = "fp32",
-            want_raw: bool = False):
+def gate_up(table: torch.Tensor, bias: torch.Tensor, x: torch.Tensor, k: int, disp: Dispatch, hidden: int,
+            inter: int, limit: float = 7.0, precision: str = "fp32", want_raw: bool = False):
     """Returns the down input as bf16 hi/lo planes ``[2, B * k, I]`` (and the float32 SwiGLU output)."""
     _check_gpu("hidden", x, torch.bfloat16, 2)
     dev = x.device
     n_tok = x.shape[0]
     split = torch.empty((2, n_tok * k, inter), dtype=torch.bfloat16, device=dev)
     raw = torch.empty((n_tok * k, inter), dtype=torch.float32, device=dev) if want_raw else None
-    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), n_tok, k, _ptr(offsets), _ptr(sorted_pairs),
-             _ptr(active), _ptr(n_active), max_active, hidden, inter, float(limit), PRECISIONS[precision],
+    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), n_tok, k, disp.n_experts, _ptr(disp.offsets),
+             _ptr(disp.sorted_pairs), _ptr(disp.units), hidden, inter, float(limit), PRECISIONS[precision],
              _ptr(split), _ptr(raw), _stream(dev))
     return (split, raw) if want_raw else split
 
 
-def down(table: torch.Tensor, bias: torch.Tensor, gated_split: torch.Tensor, offsets, sorted_pairs, active, n_active,
-         max_active: int, hidden: int, inter: int, precision: str = "fp32") -> torch.Tensor:
+def down(table: torch.Tensor, bias: torch.Tensor, gated_split: torch.Tensor, disp: Dispatch, hidden: int, inter: int,
+         precision: str = "fp32") -> torch.Tensor:
     _check_gpu("gated_split", gated_split, torch.bfloat16, 3)
     dev = gated_split.device
     n_pairs = gated_split.shape[1]
     eo = torch.empty((n_pairs, hidden), dtype=torch.float32, device=dev)
-    nat.call("klc_moe_down", _ptr(table), _ptr(bias), _ptr(gated_split), n_pairs, _ptr(offsets), _ptr(sorted_pairs),
-             _ptr(active), _ptr(n_active), max_active, hidden, inter, PRECISIONS[precision], _ptr(eo), _stream(dev))
+    nat.call("klc_moe_down", _ptr(table), _ptr(bias), _ptr(gated_split), n_pairs, disp.n_experts, _ptr(disp.offsets),
+             _ptr(disp.sorted_pairs), _ptr(disp.units), hidden, inter, PRECISIONS[precision], _ptr(eo),
+             _stream(dev))
     return eo
 
 

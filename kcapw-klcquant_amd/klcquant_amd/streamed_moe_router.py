@@ -377,12 +377,10 @@ class StreamedMoERouter:
         if tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
             raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
                              f"E={n_exp} H={hidden} I={inter}")
-        offsets, sorted_pairs, active, n_active = ops.dispatch(ids, n_exp)
-        max_active = min(n_exp, ids.numel())
-        gated, gated_raw = ops.gate_up(gu_table, gu_bias, x, k, offsets, sorted_pairs, active, n_active, max_active,
-                                       hidden, inter, self.swiglu_limit, self.matmul_precision, want_raw=True)
-        eo = ops.down(d_table, d_bias, gated, offsets, sorted_pairs, active, n_active, max_active, hidden, inter,
-                      self.matmul_precision)
+        disp = ops.dispatch(ids, n_exp)
+        gated, gated_raw = ops.gate_up(gu_table, gu_bias, x, k, disp, hidden, inter, self.swiglu_limit,
+                                       self.matmul_precision, want_raw=True)
+        eo = ops.down(d_table, d_bias, gated, disp, hidden, inter, self.matmul_precision)
         out = ops.combine(eo, weights, n_tok, k)
         norms = ops.pair_norms(gated_raw, eo)
         return out, norms

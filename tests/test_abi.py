@@ -63,21 +63,29 @@ def test_argument_errors_before_any_launch():
         nat.call("klc_moe_topk_softmax", fake, fake, fake, fake, 4, 8, 9, None)
     assert ei.value.status == nat.KLC_ERR_SHAPE
     with pytest.raises(nat.KlcError) as ei:
-        nat.call("klc_moe_dispatch", fake, 16, 300, fake, fake, fake, fake, None)
+        nat.call("klc_moe_dispatch", fake, 16, 300, fake, fake, fake, fake, fake, None)
     assert ei.value.status == nat.KLC_ERR_UNSUPPORTED
     with pytest.raises(nat.KlcError) as ei:
         nat.call("klc_moe_router_logits", fake, fake, fake, fake, None, 2, 100, 8, None)
     assert ei.value.status == nat.KLC_ERR_SHAPE
     with pytest.raises(nat.KlcError) as ei:
-        nat.call("klc_moe_gate_up", fake, fake, fake, 2, 4, fake, fake, fake, fake, 8, 2880, 2880, 7.0, 5, fake,
+        nat.call("klc_moe_gate_up", fake, fake, fake, 2, 4, 128, fake, fake, fake, 2880, 2880, 7.0, 5, fake,
                  None, None)
     assert ei.value.status == nat.KLC_ERR_ARGUMENT
     with pytest.raises(nat.KlcError) as ei:
-        nat.call("klc_moe_down", fake, fake, fake, 8, fake, fake, fake, fake, 8, 4096, 2880, 0, fake, None)
+        nat.call("klc_moe_down", fake, fake, fake, 8, 128, fake, fake, fake, 4096, 2880, 0, fake, None)
     assert ei.value.status == nat.KLC_ERR_UNSUPPORTED
     with pytest.raises(nat.KlcError) as ei:
         nat.call("klc_synth_fill", fake, 16, 1, 1, 10, 300, None)
     assert ei.value.status == nat.KLC_ERR_ARGUMENT
+
+
+def test_units_size():
+    lib = nat.load()
+    # 256 pairs over 128 experts: gate_up (256 + 7 * 128) // 8 = 144, down (256 + 3 * 128) // 4 = 160
+    assert lib.klc_moe_units_size(256, 128) == 2 + 144 + 160
+    assert lib.klc_moe_units_size(4, 128) == 2 + 4 + 4
+    assert lib.klc_moe_units_size(16, 300) == nat.KLC_ERR_UNSUPPORTED
 
 
 def test_workspace_size_grows_with_tokens():

@@ -70,16 +70,26 @@ def test_topk_ties_nan_and_signed_zero(gpu):
                                            (64, 4, 32)])
 def test_dispatch_matches_stable_counting_sort(gpu, n_tok, k, n_exp):
     rng_ids = synth.random_ints(900 + n_tok, n_tok * k, 0, n_exp - 1).reshape(n_tok, k).astype(np.int32)
-    offsets, sorted_pairs, active, n_active = ops.dispatch(torch.from_numpy(rng_ids).to(gpu), n_exp)
+    disp = ops.dispatch(torch.from_numpy(rng_ids).to(gpu), n_exp)
     torch.cuda.synchronize()
     counts, w_off, w_order, w_active = orr.dispatch(rng_ids, n_exp)
-    assert np.array_equal(offsets.cpu().numpy(), w_off)
-    assert np.array_equal(sorted_pairs.cpu().numpy(), w_order)
-    na = int(n_active.item())
+    assert np.array_equal(disp.offsets.cpu().numpy(), w_off)
+    assert np.array_equal(disp.sorted_pairs.cpu().numpy(), w_order)
+    na = int(disp.n_active.item())
     assert na == len(w_active)
-    a = active.cpu().numpy()
+    a = disp.active.cpu().numpy()
     assert np.array_equal(a[:na], w_active)
     assert (a[na:] == -1).all()
+    # work units: every (expert, run of 8 / 4 tokens) once, experts ascending (the ABI's documented layout)
+    u = disp.units.cpu().numpy()
+    n_pairs = n_tok * k
+    cap8 = (n_pairs + 7 * min(n_pairs, n_exp)) // 8
+    cap4 = (n_pairs + 3 * min(n_pairs, n_exp)) // 4
+    assert u.size == 2 + cap8 + cap4
+    for per, start, n in [(8, 2, int(u[0])), (4, 2 + cap8, int(u[1]))]:
+        want = [e | (j << 10) for e in range(n_exp) for j in range(-(-int(counts[e]) // per))]
+        assert u[start:start + n].tolist() == want
+        assert n <= (cap8 if per == 8 else cap4)
 
 
 def test_router_rejects_bad_shapes(gpu):
