@@ -10,7 +10,10 @@ layers (1.69 GB of packed experts each), so expert bytes come from HBM and not
 from a cache left warm by the previous step.
 
 Prints one JSON line.  ``value`` is microseconds per token at the headline
-batch (64); ``per_batch`` holds B = 1, 8, 64.  ``roofline`` is for the
+batch (64); ``per_batch`` holds B = 1, 8, 64.  ``stack`` is the 36-layer
+MoE-only decode (RMSNorm -> MoE -> residual per layer, 60.9 GB of experts
+resident, 64 sequences x 32 steps) and ``dequant`` the standalone MXFP4 ->
+bf16 dequant of 128 down_proj experts; both are extra lines of the same run.  ``roofline`` is for the
 dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
 experts the batch touches + activations in + SwiGLU output) over its average
 duration measured with HIP events recorded by the library between its
@@ -58,6 +61,9 @@ def parse_args():
     ap.add_argument("--inputs", type=int, default=16, help="distinct input batches the steps rotate over")
     ap.add_argument("--cpu-tokens", type=int, default=6, help="tokens in the CPU baseline sample (0 = skip)")
     ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16"])
+    ap.add_argument("--skip-dequant", action="store_true", help="skip the standalone dequant measurement")
+    ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
+    ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB -> 1 GiB float32 copy kernel 5 times (HBM counter calibration)")
     return ap.parse_args()
@@ -98,6 +104,79 @@ def gate_up_bytes(unique_experts: int, n_tok: int) -> int:
     """Algorithmic bytes of one gate_up launch: weights + bias + fp32 activations + fp32 SwiGLU output."""
     return (unique_experts * (GATE_UP_EXPERT_BYTES + 2 * INTER * 2) + n_tok * HIDDEN * 4
             + n_tok * TOPK * INTER * 4)
+
+
+def dequant_bench(torch, dev, reps: int = 10) -> dict:
+    """Standalone MXFP4 -> bf16 dequant of 128 down_proj experts ([2880, 90, 16] codes +
+    [2880, 90] E8M0 scales each, checkpoint layout) into [128, 2880, 2880] bf16."""
+    import numpy as np
+
+    from klcquant_amd import ops
+
+    n, rows, groups = EXPERTS, HIDDEN, INTER // 32
+    blocks = torch.empty((n, rows, groups, 16), dtype=torch.uint8, device=dev)
+    scales = torch.empty((n, rows, groups), dtype=torch.uint8, device=dev)
+    ops.synth_fill(blocks, 1000 * 1 + 7, 0)
+    ops.synth_fill(scales, 1000 * 1 + 8, 1, 118, 124)
+    out = torch.empty((n, groups * 32, rows), dtype=torch.bfloat16, device=dev)
+    from klcquant_amd import _native as nat
+
+    def launch():
+        nat.call("klc_mxfp4_dequant", ops._ptr(blocks), ops._ptr(scales), ops._ptr(out), n, rows, groups,
+                 nat.DTYPE_BF16, ops._stream(dev))
+
+    for _ in range(3):
+        launch()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(reps):
+        launch()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    us = float(np.mean([ev[i].elapsed_time(ev[i + 1]) for i in range(reps)])) * 1e3
+    moved = n * rows * groups * 17 + n * rows * groups * 32 * 2
+    del blocks, scales, out
+    return {"workload": "128 x down_proj [2880 x 2880] MXFP4 -> bf16 (checkpoint layout in, [in, out] out)",
+            "us": round(us, 2), "bytes": moved, "gbps": round(moved / (us * 1e-6) / 1e9, 1),
+            "frac_of_peak": round(moved / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def stack_bench(torch, dev, n_layers: int, n_seqs: int, n_steps: int, precision: str) -> dict:
+    """36-layer MoE-only decode: per layer h += moe(rms_norm(h)), every expert resident in HBM;
+    n_seqs sequences x n_steps decode steps (a step = one token per sequence through all layers)."""
+    import numpy as np
+
+    from klcquant_amd import moe
+
+    t0 = time.perf_counter()
+    stack = moe.MoEStack.synthetic(4, n_layers, HIDDEN, INTER, EXPERTS, dev, precision=precision)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    xs = [torch.from_numpy(moe.synthetic_hidden(4, n_seqs, HIDDEN, step=s).view(np.int16)).view(torch.bfloat16)
+          .to(dev) for s in range(n_steps)]
+    out = torch.empty_like(xs[0])
+    ids = [[torch.empty((n_seqs, TOPK), dtype=torch.int32, device=dev) for _ in range(n_layers)]
+           for _ in range(n_steps)]
+    for s in range(2):
+        stack(xs[s], out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(n_steps):
+        stack(xs[s], out=out, ids=ids[s])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    uniq = [len(np.unique(t.cpu().numpy())) for row in ids for t in row]
+    moved = float(sum(layer_bytes(u, n_seqs) for u in uniq)) + n_steps * n_layers * (HIDDEN * 2 + n_seqs * HIDDEN * 4)
+    resident = sum(int(l.w.gate_up.numel() + l.w.down.numel()) for l in stack.layers)
+    del stack
+    torch.cuda.empty_cache()
+    return {"workload": f"{n_layers}-layer MoE-only stack, gpt-oss-120B shape, rms_norm -> MoE -> residual, "
+                        f"{n_seqs} sequences x {n_steps} decode steps",
+            "tokens_per_s": round(n_seqs * n_steps / dt, 1), "ms_per_step": round(dt * 1e3 / n_steps, 3),
+            "us_per_layer": round(dt * 1e6 / n_steps / n_layers, 2), "hbm_gbps": round(moved / dt / 1e9, 1),
+            "frac_of_peak": round(moved / dt / 1e9 / HBM_PEAK_GBPS, 4), "resident_gb": round(resident / 1e9, 2),
+            "unique_experts_mean": round(float(np.mean(uniq)), 2), "build_s": round(build_s, 1)}
 
 
 def cpu_baseline(n_tokens: int) -> dict:
@@ -241,6 +320,14 @@ def main() -> int:
             "algorithmic_bytes_per_launch": round(head["gate_up_bytes_per_launch"]),
         },
     }
+    if args.stack_layers > 0:
+        del layers
+        torch.cuda.empty_cache()
+        result["stack"] = stack_bench(torch, dev, args.stack_layers, 64, args.stack_steps, args.precision)
+        print(f"[bench] stack: {result['stack']}", file=sys.stderr, flush=True)
+    if not args.skip_dequant:
+        result["dequant"] = dequant_bench(torch, dev)
+        print(f"[bench] dequant: {result['dequant']}", file=sys.stderr, flush=True)
     if args.cpu_tokens > 0:
         print(f"[bench] CPU baseline: {args.cpu_tokens} tokens through the oracle", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_tokens)

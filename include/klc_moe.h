@@ -152,9 +152,11 @@ int klc_moe_down(const void* const* w_down, const void* bias, const void* gated_
 
 /* Weighted combine in top-k order (streamed_moe_router.py:497, 512-513):
  * out[t] = bf16 sum over j of bf16(bf16(expert_out[t*k+j]) * weights[t][j]),
- * every step rounded to bfloat16. */
-int klc_moe_combine(const float* expert_out, const void* weights, int64_t n_tokens, int64_t k, int64_t hidden,
-                    void* out, void* stream);
+ * every step rounded to bfloat16.  If residual (bfloat16 [n_tokens][hidden])
+ * is not NULL, out[t] = bf16(residual[t] + out[t]), the residual add after the
+ * MoE block (streamed_transformer_executor.py:260). */
+int klc_moe_combine(const float* expert_out, const void* weights, const void* residual, int64_t n_tokens, int64_t k,
+                    int64_t hidden, void* out, void* stream);
 
 /* Bias-only fallback (streamed_moe_router.py:317-322):
  * out[t] = bf16(sum_j bf16(down_bias[ids[t][j]] * weights[t][j])), float32 sum. */
@@ -179,9 +181,10 @@ int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter,
  * path (streamed_moe_router.py:257-315, 483-522) for every row of x:
  * router logits -> top-k/softmax -> dispatch -> gate_up/SwiGLU -> down ->
  * combine, all enqueued on `stream` with no host synchronisation (batches of
- * up to 64 tokens run the router, top-k and dispatch as one launch).  Writes
- * out[n_tokens][hidden] bfloat16; ids/weights (optional, may be NULL) receive
- * the routing.  workspace must be 256-byte aligned, hold
+ * up to 2 tokens run the router, top-k and dispatch as one launch).  Writes
+ * out[n_tokens][hidden] bfloat16, plus residual (bfloat16 [n_tokens][hidden])
+ * when that is not NULL (streamed_transformer_executor.py:260; out may alias
+ * residual); ids/weights (optional, may be NULL) receive the routing.  workspace must be 256-byte aligned, hold
  * klc_moe_workspace_bytes() bytes and be zero-filled before its first use.  events: optional host array of
  * KLC_LAYER_EVENTS hipEvent_t handles recorded on `stream` before each of the
  * six kernels and after the last (NULL: no events). */
@@ -189,8 +192,16 @@ int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter,
 int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
                   const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
-                  void* workspace, int64_t workspace_bytes, void* out, int32_t* ids, void* weights,
-                  void* const* events, void* stream);
+                  void* workspace, int64_t workspace_bytes, void* out, const void* residual, int32_t* ids,
+                  void* weights, void* const* events, void* stream);
+
+/* ---- RMSNorm (stacked decode) -------------------------------------------------
+ * rms_norm(x, weight, eps) of streamed_attention.py:27-28 for bfloat16
+ * x[n_tokens][hidden] and weight[hidden]: x * rsqrt(mean(x.float()^2) + eps)
+ * .to(bfloat16) * weight, with the mean of squares rounded to float32 and each
+ * multiply rounded to bfloat16.  hidden a multiple of 8, <= 8192. */
+int klc_rms_norm(const void* x, const void* weight, void* out, int64_t n_tokens, int64_t hidden, float eps,
+                 void* stream);
 
 /* ---- Synthetic inputs -------------------------------------------------------
  * Counter-based SplitMix64 stream, identical to klcquant_amd/synth.py:

@@ -365,9 +365,12 @@ int tiles_per_workgroup(int tiles, int64_t max_units) {
 }
 
 
-// out[t][h] over k slots in order; every step rounded to bfloat16.
+// out[t][h] over k slots in order; every step rounded to bfloat16; then, if
+// residual is given, out = bf16(residual + out) (the stacked decode's
+// hidden += moe_out).
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ eo, const uint16_t* __restrict__ w,
-                                                      int k, int hidden, uint16_t* __restrict__ out) {
+                                                      const uint16_t* residual, int k, int hidden,
+                                                      uint16_t* out) {  // out may alias residual
   const int t = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (h >= hidden) return;
@@ -378,6 +381,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     const float o = round_bf16(eo[p * hidden + h]);
     acc = round_bf16(acc + round_bf16(o * wj));
   }
+  if (residual != nullptr) acc = bf16_to_f32(residual[(int64_t)t * hidden + h]) + acc;
   out[(int64_t)t * hidden + h] = (uint16_t)f32_to_bf16_rne(acc);
 }
 
@@ -470,10 +474,11 @@ int launch_down(const void* const* w, const void* bias, const void* gated_split,
   return check_launch("moe_gemv_mfma_kernel<down>");
 }
 
-int launch_combine(const float* eo, const void* w, int64_t n_tok, int64_t k, int64_t hidden, void* out,
-                   hipStream_t stream) {
+int launch_combine(const float* eo, const void* w, const void* residual, int64_t n_tok, int64_t k, int64_t hidden,
+                   void* out, hipStream_t stream) {
   const dim3 grid((unsigned)((hidden + 255) / 256), (unsigned)n_tok);
-  combine_kernel<<<grid, 256, 0, stream>>>(eo, static_cast<const uint16_t*>(w), (int)k, (int)hidden,
+  combine_kernel<<<grid, 256, 0, stream>>>(eo, static_cast<const uint16_t*>(w),
+                                           static_cast<const uint16_t*>(residual), (int)k, (int)hidden,
                                            static_cast<uint16_t*>(out));
   return check_launch("combine_kernel");
 }
@@ -542,12 +547,12 @@ extern "C" int klc_moe_down(const void* const* w_down, const void* bias, const v
                      precision, expert_out, as_stream(stream));
 }
 
-extern "C" int klc_moe_combine(const float* expert_out, const void* weights, int64_t n_tokens, int64_t k,
-                               int64_t hidden, void* out, void* stream) {
+extern "C" int klc_moe_combine(const float* expert_out, const void* weights, const void* residual,
+                               int64_t n_tokens, int64_t k, int64_t hidden, void* out, void* stream) {
   KLC_REQUIRE(expert_out && weights && out, KLC_ERR_ARGUMENT, "klc_moe_combine: null pointer");
   KLC_REQUIRE(n_tokens > 0 && k > 0 && hidden > 0, KLC_ERR_ARGUMENT, "klc_moe_combine: bad sizes");
   KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "klc_moe_combine: n_tokens=%lld > 65535", (long long)n_tokens);
-  return launch_combine(expert_out, weights, n_tokens, k, hidden, out, as_stream(stream));
+  return launch_combine(expert_out, weights, residual, n_tokens, k, hidden, out, as_stream(stream));
 }
 
 extern "C" int klc_moe_bias_combine(const void* down_bias, const int32_t* ids, const void* weights, int64_t n_tokens,
@@ -584,7 +589,7 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
                              const void* gate_up_bias, const void* const* w_down, const void* down_bias,
                              int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
                              float swiglu_limit, int precision, void* workspace, int64_t workspace_bytes, void* out,
-                             int32_t* ids, void* weights, void* const* events, void* stream) {
+                             const void* residual, int32_t* ids, void* weights, void* const* events, void* stream) {
   KLC_REQUIRE(x && router_w && router_b && w_gate_up && gate_up_bias && w_down && down_bias && workspace && out,
               KLC_ERR_ARGUMENT, "klc_moe_layer: null pointer");
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
@@ -647,6 +652,6 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
                         precision, eo, st)))
     return rc;
   if ((rc = mark(5))) return rc;
-  if ((rc = launch_combine(eo, w_buf, n_tokens, k, hidden, out, st))) return rc;
+  if ((rc = launch_combine(eo, w_buf, residual, n_tokens, k, hidden, out, st))) return rc;
   return mark(6);
 }

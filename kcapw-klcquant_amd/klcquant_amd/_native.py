@@ -49,12 +49,13 @@ SIGNATURES: dict[str, tuple] = {
     "klc_moe_units_size": (_I64, [_I64, _I64]),
     "klc_moe_gate_up": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _F32, _I32, _P, _P, _P]),
     "klc_moe_down": (_I32, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I32, _P, _P]),
-    "klc_moe_combine": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P]),
+    "klc_moe_combine": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "klc_rms_norm": (_I32, [_P, _P, _P, _I64, _I64, _F32, _P]),
     "klc_moe_bias_combine": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_pair_norms": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "klc_moe_layer": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _P, _I64, _P,
-                             _P, _P, _P, _P]),
+                             _P, _P, _P, _P, _P]),
     "klc_synth_fill": (_I32, [_P, _I64, _U64, _I32, _I32, _I32, _P]),
 }
 

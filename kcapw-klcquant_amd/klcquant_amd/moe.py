@@ -159,8 +159,11 @@ class MoELayer:
         return ws
 
     def forward(self, x: torch.Tensor, out: torch.Tensor | None = None, ids: torch.Tensor | None = None,
-                weights: torch.Tensor | None = None, events: list | None = None) -> torch.Tensor:
+                weights: torch.Tensor | None = None, events: list | None = None,
+                residual: torch.Tensor | None = None) -> torch.Tensor:
         """Fused layer (klc_moe_layer); optional ``ids``/``weights`` receive the routing.
+
+        ``residual``: bf16 ``[B, H]`` added to the output (``out`` may be it).
 
         ``events``: optional list of ``KLC_LAYER_EVENTS`` recorded
         ``torch.cuda.Event`` objects, re-recorded around the six kernels.
@@ -169,6 +172,10 @@ class MoELayer:
         n_tok, hidden = x.shape
         if hidden != self.w.hidden:
             raise ValueError(f"hidden size {hidden} != layer hidden {self.w.hidden}")
+        if residual is not None:
+            ops._check_gpu("residual", residual, torch.bfloat16, 2)
+            if residual.shape != x.shape:
+                raise ValueError(f"residual shape {tuple(residual.shape)} != hidden shape {tuple(x.shape)}")
         if out is None:
             out = torch.empty_like(x)
         ws = self.workspace(n_tok)
@@ -181,7 +188,7 @@ class MoELayer:
         nat.call("klc_moe_layer", ops._ptr(x), ops._ptr(w.router_weight), ops._ptr(w.router_bias),
                  ops._ptr(w.gate_up_table), ops._ptr(w.gate_up_bias), ops._ptr(w.down_table), ops._ptr(w.down_bias),
                  n_tok, hidden, w.inter, w.n_experts, self.k, self.limit, ops.PRECISIONS[self.precision],
-                 ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(ids), ops._ptr(weights), ev,
+                 ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(residual), ops._ptr(ids), ops._ptr(weights), ev,
                  ops._stream(x.device))
         return out
 
@@ -213,3 +220,61 @@ class MoELayer:
                 "offsets": disp.offsets, "sorted_pairs": disp.sorted_pairs, "active": disp.active,
                 "n_active": disp.n_active, "units": disp.units, "gated": gated_raw, "gated_act": gated,
                 "expert_out": eo}
+
+
+def synthetic_norm_weight(workload: int, layer: int, hidden: int) -> np.ndarray:
+    """bf16 bit patterns of a layer's RMSNorm weight, 1 + N(0, 0.05)."""
+    return synth.random_normal_bf16(synth.tensor_seed(workload, "norm_weight", layer), hidden, 1.0, 0.05)
+
+
+class MoEStack:
+    """Stacked MoE decode: per layer ``h += moe(rms_norm(h))``.
+
+    The MoE-only view of the executor's layer loop
+    (streamed_transformer_executor.py:247-260): post-attention RMSNorm
+    (streamed_attention.py:27-28), the routed experts, and the residual add,
+    fused into the layer's combine.  All layers stay resident in HBM.
+    """
+
+    def __init__(self, layers: list[MoELayerWeights], norm_weights: list[torch.Tensor], experts_per_token: int = 4,
+                 swiglu_limit: float = 7.0, precision: str = "fp32", eps: float = 1e-5) -> None:
+        if len(layers) != len(norm_weights):
+            raise ValueError(f"{len(layers)} layers but {len(norm_weights)} norm weights")
+        self.layers = [MoELayer(w, experts_per_token, swiglu_limit, precision) for w in layers]
+        self.norm_weights = norm_weights
+        self.eps = float(eps)
+        self._normed: dict[tuple, torch.Tensor] = {}
+
+    def forward(self, hidden: torch.Tensor, out: torch.Tensor | None = None, trace: list | None = None,
+                ids: list | None = None) -> torch.Tensor:
+        """Runs every layer on bf16 ``hidden [B, H]``; returns the final hidden state.
+
+        ``trace``: if a list, receives a copy of the hidden state after each
+        layer.  ``ids``: if a list of int32 ``[B, k]`` tensors (one per layer),
+        they receive each layer's routing.
+        """
+        ops._check_gpu("hidden", hidden, torch.bfloat16, 2)
+        h = out if out is not None else torch.empty_like(hidden)
+        if h.data_ptr() != hidden.data_ptr():
+            h.copy_(hidden)
+        key = tuple(hidden.shape)
+        normed = self._normed.get(key)
+        if normed is None:
+            normed = self._normed[key] = torch.empty_like(hidden)
+        for i, (layer, nw) in enumerate(zip(self.layers, self.norm_weights)):
+            ops.rms_norm(h, nw, self.eps, out=normed)
+            layer.forward(normed, out=h, residual=h, ids=None if ids is None else ids[i])
+            if trace is not None:
+                trace.append(h.clone())
+        return h
+
+    __call__ = forward
+
+    @classmethod
+    def synthetic(cls, workload: int, n_layers: int, hidden: int, inter: int, n_experts: int,
+                  device: torch.device | str = "cuda", **kwargs) -> "MoEStack":
+        dev = torch.device(device)
+        layers = [MoELayerWeights.synthetic(workload, l, hidden, inter, n_experts, dev) for l in range(n_layers)]
+        norms = [torch.from_numpy(synthetic_norm_weight(workload, l, hidden).view(np.int16)).view(torch.bfloat16)
+                 .to(dev) for l in range(n_layers)]
+        return cls(layers, norms, **kwargs)

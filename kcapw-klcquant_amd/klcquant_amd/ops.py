@@ -222,13 +222,31 @@ def down(table: torch.Tensor, bias: torch.Tensor, gated_split: torch.Tensor, dis
     return eo
 
 
-def combine(expert_out: torch.Tensor, weights: torch.Tensor, n_tokens: int, k: int) -> torch.Tensor:
+def combine(expert_out: torch.Tensor, weights: torch.Tensor, n_tokens: int, k: int,
+            residual: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 weighted sum of the k expert outputs per token (+ ``residual`` if given)."""
     _check_gpu("expert_out", expert_out, torch.float32)
     _check_gpu("weights", weights, torch.bfloat16)
     hidden = expert_out.shape[-1]
+    if residual is not None:
+        _check_gpu("residual", residual, torch.bfloat16, 2)
+        if tuple(residual.shape) != (n_tokens, hidden):
+            raise ValueError(f"residual shape {tuple(residual.shape)} != ({n_tokens}, {hidden})")
     out = torch.empty((n_tokens, hidden), dtype=torch.bfloat16, device=expert_out.device)
-    nat.call("klc_moe_combine", _ptr(expert_out), _ptr(weights), n_tokens, k, hidden, _ptr(out),
+    nat.call("klc_moe_combine", _ptr(expert_out), _ptr(weights), _ptr(residual), n_tokens, k, hidden, _ptr(out),
              _stream(expert_out.device))
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5, out: torch.Tensor | None = None):
+    """bf16 ``x [B, H]`` -> ``x * rsqrt(mean(x^2) + eps).to(bf16) * weight`` (klc_rms_norm)."""
+    _check_gpu("x", x, torch.bfloat16, 2)
+    _check_gpu("weight", weight, torch.bfloat16, 1)
+    if weight.shape[0] != x.shape[1]:
+        raise ValueError(f"norm weight of {weight.shape[0]} for hidden {x.shape[1]}")
+    if out is None:
+        out = torch.empty_like(x)
+    nat.call("klc_rms_norm", _ptr(x), _ptr(weight), _ptr(out), x.shape[0], x.shape[1], float(eps), _stream(x.device))
     return out
 
 
