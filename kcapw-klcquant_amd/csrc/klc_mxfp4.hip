@@ -4,11 +4,13 @@
 // per value for bfloat16), so the kernel is built around coalesced traffic:
 // a workgroup owns a strip of 64 output columns (64 checkpoint rows, i.e. a
 // contiguous 64 x groups x 16-byte region) and walks the input dimension in
-// chunks of 4 groups.  Packed bytes are staged in LDS, then every thread
+// chunks of 16 groups.  Packed bytes are staged in LDS, then every thread
 // decodes a 4 (input rows) x 8 (output columns) block and writes four 16-byte
 // rows, so each wave-wide store covers full 128-byte lines of the transposed
-// [in, out] output.  Values are built with integer arithmetic
-// (mxfp4_f32_bits), which is exact for every (code, scale) pair.
+// [in, out] output.  Values come from gfx950's scaled E2M1 conversions
+// (v_cvt_scalef32_pk_{bf16,f16,f32}_fp4), exact for every scale byte below
+// 255; the MX NaN scale 255 takes an integer path (mxfp4_f32_bits) that
+// reproduces the reference's +-inf / NaN.
 #include "klc_common.h"
 
 namespace klc {
@@ -16,9 +18,9 @@ namespace {
 
 constexpr int kDqThreads = 256;
 constexpr int kDqCols = 64;      // output columns (= checkpoint rows) per workgroup
-constexpr int kDqGroups = 4;     // MX groups (32 inputs each) per chunk
-constexpr int kLdsStride = 17;   // dwords per staged row: 16 data + 1 pad (bank spread)
-constexpr int kSclStride = 5;    // dwords per staged scale row
+constexpr int kDqGroups = 16;    // MX groups (32 inputs each) per iteration
+constexpr int kLdsStride = kDqGroups * 4 + 1;  // dwords per staged row: data + 1 pad (bank spread)
+constexpr int kSclStride = kDqGroups + 1;      // dwords per staged scale row
 
 // Converts one exact float32 bit pattern to the output dtype's bits.
 template <int kDtype>
@@ -30,6 +32,30 @@ __device__ __forceinline__ uint32_t to_out_bits(uint32_t f32bits) {
   } else {
     return f32bits;
   }
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Byte `h` of `v16` (two E2M1 codes, low nibble first) times `scale`, as two
+// 16-bit values packed low-first (bfloat16 or float16 per kDtype).
+template <int kDtype>
+__device__ __forceinline__ uint32_t cvt_pair(uint32_t v16, float scale, int h) {
+  if constexpr (kDtype == KLC_DTYPE_F16) {
+    const f16x2_t v = h ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v16, scale, 1)
+                        : __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v16, scale, 0);
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    const bf16x2_t v = h ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v16, scale, 1)
+                         : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v16, scale, 0);
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+__device__ __forceinline__ f32x2_t cvt_pair_f32(uint32_t v16, float scale, int h) {
+  return h ? __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v16, scale, 1)
+           : __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(v16, scale, 0);
 }
 
 template <int kDtype, bool kPacked>
@@ -46,58 +72,92 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
   const int tid = threadIdx.x;
   const int in_dim = groups * 32;
 
-  // load mapping: one 16-byte chunk (row, gi) per thread
+  // load mapping: 16-byte chunks (row, 4 * i + gi), i = 0..3, per thread
   const int l_row = tid >> 2;
   const int l_gi = tid & 3;
-  // compute mapping: 4 input rows x 8 output columns per thread
+  // compute mapping: 4 input rows x 8 output columns per thread and sub-chunk
   const int c_oc = tid & 7;
-  const int c_iq = tid >> 3;          // 0..31 quads of input rows
-  const int c_gi = c_iq >> 3;         // group within the chunk
+  const int c_iq = tid >> 3;          // 0..31 quads of input rows in a 4-group sub-chunk
+  const int c_gi = c_iq >> 3;         // group within the sub-chunk
   const int c_q4 = c_iq & 7;          // quad within the group
   const int col = col0 + c_oc * 8;
 
   const uint8_t* mat = blocks;
   if constexpr (kPacked) mat = blocks + (int64_t)m * packed_stride;
 
+  // Each iteration moves 16 groups: all of a thread's loads are issued
+  // together, and the load -> LDS -> compute -> store round trip (whose waits
+  // cover the stores too: loads and stores share one counter) is paid once
+  // per 16 groups.
   for (int g0 = 0; g0 < groups; g0 += kDqGroups) {
-    const int ng = min(kDqGroups, groups - g0);
     {
       const int r = col0 + l_row;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      uint32_t e = 127u;
-      if (r < rows && l_gi < ng) {
-        const int g = g0 + l_gi;
-        if constexpr (kPacked) {
-          const uint8_t* src = mat + ((int64_t)(r / kTileRows) * groups + g) * 1024 + (r % kTileRows) * 16;
-          v = *reinterpret_cast<const uint4*>(src);
-          e = mat[packed_scale_offset(rows, groups, r, g)];
-        } else {
-          const int64_t chunk = ((int64_t)m * rows + r) * groups + g;
-          v = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
-          e = scales[chunk];
+      uint4 v[4];
+      uint32_t e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int g = g0 + 4 * i + l_gi;
+        v[i] = make_uint4(0u, 0u, 0u, 0u);
+        e[i] = 127u;
+        if (r < rows && g < groups) {
+          if constexpr (kPacked) {
+            const uint8_t* src = mat + ((int64_t)(r / kTileRows) * groups + g) * 1024 + (r % kTileRows) * 16;
+            v[i] = *reinterpret_cast<const uint4*>(src);
+            e[i] = mat[packed_scale_offset(rows, groups, r, g)];
+          } else {
+            const int64_t chunk = ((int64_t)m * rows + r) * groups + g;
+            v[i] = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
+            e[i] = scales[chunk];
+          }
         }
       }
-      uint32_t* dst = s_blk + l_row * kLdsStride + l_gi * 4;
-      dst[0] = v.x;
-      dst[1] = v.y;
-      dst[2] = v.z;
-      dst[3] = v.w;
-      s_scl[l_row * kSclStride + l_gi] = e;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t* dst = s_blk + l_row * kLdsStride + (4 * i + l_gi) * 4;
+        dst[0] = v[i].x;
+        dst[1] = v[i].y;
+        dst[2] = v[i].z;
+        dst[3] = v[i].w;
+        s_scl[l_row * kSclStride + 4 * i + l_gi] = e[i];
+      }
     }
     __syncthreads();
 
-    if (c_gi < ng) {
+#pragma unroll 1
+    for (int sc = 0; sc < kDqGroups / 4; ++sc) {
+      const int gl = 4 * sc + c_gi;  // group within the iteration
+      if (g0 + gl >= groups) break;  // uniform per 8-lane group; no barrier inside
       uint32_t bits[4][8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int lr = c_oc * 8 + j;
-        const uint32_t word = s_blk[lr * kLdsStride + c_gi * 4 + (c_q4 >> 1)];
+        const uint32_t word = s_blk[lr * kLdsStride + gl * 4 + (c_q4 >> 1)];
         const uint32_t v16 = (word >> ((c_q4 & 1) * 16)) & 0xffffu;
-        const uint32_t e = s_scl[lr * kSclStride + c_gi];
+        const uint32_t e = s_scl[lr * kSclStride + gl];
+        if (e != 255u) {
+          // hardware E2M1 x 2^(e-127) conversion, exact for e < 255 (e = 0:
+          // the float32 subnormal 2^-127 as scale)
+          const float scale = __uint_as_float(e == 0u ? 0x00400000u : (e << 23));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bits[r][j] = to_out_bits<kDtype>(mxfp4_f32_bits((v16 >> (4 * r)) & 0xfu, e));
+          for (int h = 0; h < 2; ++h) {  // rows 2h and 2h + 1
+            if constexpr (kDtype == KLC_DTYPE_F32) {
+              const f32x2_t cv = cvt_pair_f32(v16, scale, h);
+              bits[2 * h][j] = __float_as_uint(cv.x);
+              bits[2 * h + 1][j] = __float_as_uint(cv.y);
+            } else {
+              const uint32_t pair = cvt_pair<kDtype>(v16, scale, h);
+              bits[2 * h][j] = pair & 0xffffu;
+              bits[2 * h + 1][j] = pair >> 16;
+            }
+          }
+        } else {
+          // E8M0 255 (the MX NaN scale): the reference's fp32 ldexp gives +-inf,
+          // and NaN for the zero codes
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bits[r][j] = to_out_bits<kDtype>(mxfp4_f32_bits((v16 >> (4 * r)) & 0xfu, e));
+        }
       }
-      const int i0 = (g0 + c_gi) * 32 + c_q4 * 4;
+      const int i0 = (g0 + gl) * 32 + c_q4 * 4;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t row_off = ((int64_t)m * in_dim + i0 + r) * rows;
