@@ -108,13 +108,13 @@ int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens
  * token per call, streamed_moe_router.py:499).  Pairs p = t*k + j are
  * counting-sorted by expert, ties by p: offsets[n_experts+1],
  * sorted_pairs[n_pairs], active[n_experts] (experts with >= 1 pair,
- * ascending, then -1 padding) and *n_active.  Also writes the GEMV work
- * units, int32 units[klc_moe_units_size(n_pairs, n_experts)]:
- *   units[0] = number of gate_up units, units[1] = number of down units,
- *   then the gate_up list (capacity C8), then the down list (capacity C4),
- *   C_m = (n_pairs + (m - 1) * min(n_pairs, n_experts)) / m.
+ * ascending, then -1 padding) and *n_active.  Also writes the work units of
+ * the expert kernels, int32 units[klc_moe_units_size(n_pairs, n_experts)]:
+ *   units[0..2] = number of decode gate_up (m = 8), decode down (m = 4) and
+ *   prefill GEMM (m = 128) units, units[3] = 0, then the three lists in that
+ *   order, with capacities C_m = (n_pairs + (m - 1) * min(n_pairs, n_experts)) / m.
  * A unit is expert | (pass << 10) and covers the pass-th run of m tokens of
- * that expert (m = 8 for gate_up, 4 for down); experts ascending, then passes.
+ * that expert; experts ascending, then passes.
  * n_experts <= 256, n_pairs < 65536 and ceil(n_pairs / 64) * n_experts <= 65536. */
 int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
                      int32_t* sorted_pairs, int32_t* active, int32_t* n_active, int32_t* units, void* stream);
@@ -169,6 +169,20 @@ int klc_moe_bias_combine(const void* down_bias, const int32_t* ids, const void* 
 int klc_moe_pair_norms(const float* gated, const float* expert_out, int64_t n_pairs, int64_t inter,
                        int64_t hidden, float* norms, void* stream);
 
+/* ---- Prefill: expert-grouped GEMM ---------------------------------------------
+ * The same expert math as klc_moe_gate_up / klc_moe_down (same arguments,
+ * outputs and tolerance) for batches that give experts many tokens: the
+ * dispatch's 128-token GEMM units x 256-row tiles, weights decoded in
+ * registers into v_mfma_f32_16x16x32_bf16, activations staged in LDS. */
+int klc_moe_gemm_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens, int64_t k,
+                         int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* units,
+                         int64_t hidden, int64_t inter, float swiglu_limit, int precision, void* gated_split,
+                         float* gated_raw, void* stream);
+
+int klc_moe_gemm_down(const void* const* w_down, const void* bias, const void* gated_split, int64_t n_pairs,
+                      int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* units,
+                      int64_t hidden, int64_t inter, int precision, float* expert_out, void* stream);
+
 /* ---- One MoE layer --------------------------------------------------------- */
 
 /* Scratch bytes klc_moe_layer needs for n_tokens tokens.  The workspace must
@@ -189,10 +203,16 @@ int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter,
  * KLC_LAYER_EVENTS hipEvent_t handles recorded on `stream` before each of the
  * six kernels and after the last (NULL: no events). */
 #define KLC_LAYER_EVENTS 7
+/* Expert path of klc_moe_layer: AUTO picks the grouped GEMM once the batch
+ * gives experts 8 or more tokens on average (n_tokens * k >= 8 * n_experts),
+ * the decode GEMVs below that. */
+#define KLC_PATH_AUTO 0
+#define KLC_PATH_GEMV 1
+#define KLC_PATH_GEMM 2
 int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
                   const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
-                  void* workspace, int64_t workspace_bytes, void* out, const void* residual, int32_t* ids,
+                  int path, void* workspace, int64_t workspace_bytes, void* out, const void* residual, int32_t* ids,
                   void* weights, void* const* events, void* stream);
 
 /* ---- RMSNorm (stacked decode) -------------------------------------------------

@@ -51,18 +51,21 @@ __host__ __device__ __forceinline__ int64_t packed_scale_offset(int rows, int gr
          ((int64_t)row * 4 + (group & 3)) * rec + (group >> 2);
 }
 
-// Work units of the expert GEMVs.  A unit is one pass of one active expert
-// over up to kUnitTokens[kernel] of its tokens (gate_up stages 8 activation
-// rows per pass, down 4: it stages hi and lo rows per token); an expert with
-// more tokens gets several units, which run as separate workgroups.  The
-// dispatch writes both lists into one int32 array:
-//   [0] gate_up unit count, [1] down unit count,
-//   [2, 2 + cap(8))            gate_up units,
-//   [2 + cap(8), ... + cap(4)) down units,
+// Work units of the expert kernels.  A unit is one pass of one active expert
+// over up to kUnitTokens* of its tokens: the decode GEMVs stage 8 (gate_up)
+// or 4 (down: hi and lo rows per token) activation rows per pass, the
+// prefill grouped GEMM 128 tokens per tile.  An expert with more tokens gets
+// several units, which run as separate workgroups.  The dispatch writes all
+// three lists into one int32 array:
+//   [0] gate_up unit count, [1] down unit count, [2] GEMM unit count, [3] 0,
+//   then the gate_up list (capacity cap(8)), the down list (cap(4)) and the
+//   GEMM list (cap(128)),
 // a unit being expert | (pass << 10) (experts < 1024), experts ascending,
 // passes ascending.
 constexpr int kUnitTokensGateUp = 8;
 constexpr int kUnitTokensDown = 4;
+constexpr int kUnitTokensGemm = 128;
+constexpr int kUnitHeader = 4;
 __host__ __device__ __forceinline__ int32_t make_unit(int expert, int pass) { return expert | (pass << 10); }
 __host__ __device__ __forceinline__ int unit_expert(int32_t u) { return u & 1023; }
 __host__ __device__ __forceinline__ int unit_pass(int32_t u) { return (int)((uint32_t)u >> 10); }
@@ -72,8 +75,14 @@ __host__ __device__ inline int64_t units_capacity(int64_t n_pairs, int64_t n_exp
   const int64_t active = n_pairs < n_exp ? n_pairs : n_exp;
   return (n_pairs + (per - 1) * active) / per;
 }
+__host__ __device__ inline int64_t units_offset_down(int64_t n_pairs, int64_t n_exp) {
+  return kUnitHeader + units_capacity(n_pairs, n_exp, kUnitTokensGateUp);
+}
+__host__ __device__ inline int64_t units_offset_gemm(int64_t n_pairs, int64_t n_exp) {
+  return units_offset_down(n_pairs, n_exp) + units_capacity(n_pairs, n_exp, kUnitTokensDown);
+}
 __host__ __device__ inline int64_t units_size(int64_t n_pairs, int64_t n_exp) {
-  return 2 + units_capacity(n_pairs, n_exp, kUnitTokensGateUp) + units_capacity(n_pairs, n_exp, kUnitTokensDown);
+  return units_offset_gemm(n_pairs, n_exp) + units_capacity(n_pairs, n_exp, kUnitTokensGemm);
 }
 
 // ---- device side -----------------------------------------------------------
@@ -122,6 +131,27 @@ __device__ __forceinline__ float2 fp4x2_to_f32(uint32_t word) {
   typedef float f2v __attribute__((ext_vector_type(2)));
   f2v v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(word, 1.0f, kSel);
   return make_float2(v.x, v.y);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
+__device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {
+  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
+  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
+  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
+  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
+  return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3),
+                                 __builtin_shufflevector(p2, p3, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// E8M0 byte as the float32 scale operand of the scaled E2M1 conversions:
+// 2^(e-127) (e = 0: the float32 subnormal 2^-127), or 0 for a lane that has
+// no group (E2M1 values times 0 are +-0).
+__device__ __forceinline__ float cvt_scale_operand(uint32_t e, bool live) {
+  const uint32_t bits = e == 0u ? 0x00400000u : (e << 23);
+  return __uint_as_float(live ? bits : 0u);
 }
 
 }  // namespace klc

@@ -30,6 +30,13 @@ int launch_router_fused(const void* x, const void* w, const void* b, void* logit
                         int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* done,
                         hipStream_t stream);
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp);
+int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k,
+                        int64_t n_exp, const int32_t* offsets, const int32_t* pairs, const int32_t* units,
+                        int64_t hidden, int64_t inter, float limit, int precision, void* gated_split,
+                        float* gated_raw, hipStream_t stream);
+int launch_gemm_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs, int64_t n_exp,
+                     const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
+                     int precision, float* eo, hipStream_t stream);
 int check_topk_args(int64_t n_tok, int64_t n_exp, int64_t k);
 int check_dispatch_args(int64_t n_pairs, int64_t n_exp);
 
@@ -40,8 +47,6 @@ constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kVRows = 8;                     // activation rows (MFMA N columns) staged per unit
 constexpr int kMaxSteps = 24;                 // 4-group steps per row (inputs <= 3072)
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -53,15 +58,6 @@ constexpr int kBufferWord3 = 0x00020000;
 // sum cannot wrap (matrices are far below 1 GiB).
 constexpr uint32_t kOutOfRange = 0x40000000u;
 
-// Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
-__device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {
-  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);
-  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 1);
-  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 2);
-  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 3);
-  return __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3),
-                                 __builtin_shufflevector(p2, p3, 0, 1, 2, 3), 0, 1, 2, 3, 4, 5, 6, 7);
-}
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
   // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp
@@ -426,6 +422,8 @@ __global__ __launch_bounds__(256) void pair_norms_kernel(const float* __restrict
   }
 }
 
+}  // namespace
+
 int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t n_pairs, int64_t n_exp) {
   KLC_REQUIRE(hidden > 0 && inter > 0 && n_pairs > 0 && n_exp > 0, KLC_ERR_ARGUMENT,
               "experts: bad sizes hidden=%lld inter=%lld n_pairs=%lld n_experts=%lld", (long long)hidden,
@@ -442,6 +440,8 @@ int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t n_pairs, int64_t n_
   return KLC_OK;
 }
 
+namespace {
+
 int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k, int64_t n_exp,
                    const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
                    float limit, int precision, void* gated_split, float* gated_raw, hipStream_t stream) {
@@ -453,7 +453,8 @@ int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_
   gemv_kernel_for<false>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(x), 0, nullptr, static_cast<uint16_t*>(gated_split), n_tok * k * inter,
-      gated_raw, offsets, pairs, units + 2, units, (int)(2 * inter), (int)(hidden / 32), (int)k, limit, precision,
+      gated_raw, offsets, pairs, units + kUnitHeader, units, (int)(2 * inter), (int)(hidden / 32), (int)k, limit,
+      precision,
       tpw);
   return check_launch("moe_gemv_mfma_kernel<gate_up>");
 }
@@ -465,7 +466,7 @@ int launch_down(const void* const* w, const void* bias, const void* gated_split,
   const int64_t cap = units_capacity(n_pairs, n_exp, kUnitTokensDown);
   const int tpw = tiles_per_workgroup(tiles, cap);
   const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)cap);
-  const int32_t* list = units + 2 + units_capacity(n_pairs, n_exp, kUnitTokensGateUp);
+  const int32_t* list = units + units_offset_down(n_pairs, n_exp);
   const int steps = gemv_steps((int)(inter / 32));
   gemv_kernel_for<true>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
@@ -486,6 +487,11 @@ int launch_combine(const float* eo, const void* w, const void* residual, int64_t
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 constexpr int64_t kFusedRouterTokens = 2;  // batches up to this size use the one-launch router
+
+// The grouped GEMM pays off once experts see several MFMA column blocks of
+// tokens; below about 8 tokens per expert the GEMV streams the same weights
+// with less overhead.
+bool use_gemm_path(int64_t n_pairs, int64_t n_exp) { return n_pairs >= 8 * n_exp; }
 
 struct LayerScratch {
   int64_t counters, logits, ids, values, weights, offsets, sorted, active, n_active, units, gated, eo, total;
@@ -588,12 +594,15 @@ extern "C" int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int
 extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
                              const void* gate_up_bias, const void* const* w_down, const void* down_bias,
                              int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
-                             float swiglu_limit, int precision, void* workspace, int64_t workspace_bytes, void* out,
-                             const void* residual, int32_t* ids, void* weights, void* const* events, void* stream) {
+                             float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
+                             void* out, const void* residual, int32_t* ids, void* weights, void* const* events,
+                             void* stream) {
   KLC_REQUIRE(x && router_w && router_b && w_gate_up && gate_up_bias && w_down && down_bias && workspace && out,
               KLC_ERR_ARGUMENT, "klc_moe_layer: null pointer");
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "klc_moe_layer: unknown precision %d", precision);
+  KLC_REQUIRE(path == KLC_PATH_AUTO || path == KLC_PATH_GEMV || path == KLC_PATH_GEMM, KLC_ERR_ARGUMENT,
+              "klc_moe_layer: unknown path %d", path);
   int rc = check_router_args(n_tokens, hidden, n_experts);
   if (rc) return rc;
   rc = check_topk_args(n_tokens, n_experts, k);
@@ -644,13 +653,24 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
       return rc;
   }
   if ((rc = mark(3))) return rc;
-  if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden, inter,
-                           swiglu_limit, precision, gated, nullptr, st)))
-    return rc;
-  if ((rc = mark(4))) return rc;
-  if ((rc = launch_down(w_down, down_bias, gated, n_tokens * k, n_experts, offsets, sorted, units, hidden, inter,
-                        precision, eo, st)))
-    return rc;
+  const bool gemm = path == KLC_PATH_GEMM || (path == KLC_PATH_AUTO && use_gemm_path(n_tokens * k, n_experts));
+  if (gemm) {
+    if ((rc = launch_gemm_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden,
+                                  inter, swiglu_limit, precision, gated, nullptr, st)))
+      return rc;
+    if ((rc = mark(4))) return rc;
+    if ((rc = launch_gemm_down(w_down, down_bias, gated, n_tokens * k, n_experts, offsets, sorted, units, hidden,
+                               inter, precision, eo, st)))
+      return rc;
+  } else {
+    if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden,
+                             inter, swiglu_limit, precision, gated, nullptr, st)))
+      return rc;
+    if ((rc = mark(4))) return rc;
+    if ((rc = launch_down(w_down, down_bias, gated, n_tokens * k, n_experts, offsets, sorted, units, hidden, inter,
+                          precision, eo, st)))
+      return rc;
+  }
   if ((rc = mark(5))) return rc;
   if ((rc = launch_combine(eo, w_buf, residual, n_tokens, k, hidden, out, st))) return rc;
   return mark(6);

@@ -260,7 +260,7 @@ __host__ __device__ constexpr int dispatch_chunks(int n_pairs) { return (n_pairs
 // LDS bytes block_dispatch needs for n_pairs pairs over n_exp experts.
 __host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int n_exp) {
   return ((size_t)dispatch_chunks(n_pairs) * n_exp * sizeof(uint16_t) + 15) / 16 * 16 +
-         4 * kDispatchMaxExperts * sizeof(int32_t) + 4 * sizeof(int32_t);
+         5 * kDispatchMaxExperts * sizeof(int32_t) + 8 * sizeof(int32_t);
 }
 
 // Lanes of the wave holding the same key (key < 512): the lanes that agree
@@ -293,7 +293,8 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
   int32_t* flags = total + kDispatchMaxExperts;
   int32_t* ugu = flags + kDispatchMaxExperts;  // units per expert, then their prefix (gate_up)
   int32_t* udn = ugu + kDispatchMaxExperts;    // same for down
-  int32_t* sums = udn + kDispatchMaxExperts;
+  int32_t* ugm = udn + kDispatchMaxExperts;    // same for the GEMM
+  int32_t* sums = ugm + kDispatchMaxExperts;
   const uint64_t below = (1ull << lane) - 1ull;
 
   for (int i = tid; i < nchunk * n_exp; i += kDispatchThreads) hist[i] = 0;
@@ -319,6 +320,7 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
     flags[e] = run > 0 ? 1 : 0;
     ugu[e] = (run + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
     udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
+    ugm[e] = (run + kUnitTokensGemm - 1) / kUnitTokensGemm;
   }
   __syncthreads();
   // total[] becomes the expert offsets, flags[] the active-list positions,
@@ -331,6 +333,8 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
   __syncthreads();
   block_exclusive_scan_256(udn, n_exp, &sums[3]);
   __syncthreads();
+  block_exclusive_scan_256(ugm, n_exp, &sums[4]);
+  __syncthreads();
   // 3. scatter: position = expert offset + pairs of e in earlier chunks + rank in this chunk
   for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
     const int p = c * kDispatchChunk + lane;
@@ -340,16 +344,20 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
     if (valid) sorted[total[e] + hist[c * n_exp + e] + __popcll(peers & below)] = p;
   }
   {
-    int32_t* gu_list = units + 2;
-    int32_t* dn_list = gu_list + units_capacity(n_pairs, n_exp, kUnitTokensGateUp);
+    int32_t* gu_list = units + kUnitHeader;
+    int32_t* dn_list = units + units_offset_down(n_pairs, n_exp);
+    int32_t* gm_list = units + units_offset_gemm(n_pairs, n_exp);
     for (int e = tid; e < n_exp; e += kDispatchThreads) {
       const int c = (e + 1 < n_exp ? total[e + 1] : sums[0]) - total[e];
       for (int j = 0; j * kUnitTokensGateUp < c; ++j) gu_list[ugu[e] + j] = make_unit(e, j);
       for (int j = 0; j * kUnitTokensDown < c; ++j) dn_list[udn[e] + j] = make_unit(e, j);
+      for (int j = 0; j * kUnitTokensGemm < c; ++j) gm_list[ugm[e] + j] = make_unit(e, j);
     }
     if (tid == 0) {
       units[0] = sums[2];
       units[1] = sums[3];
+      units[2] = sums[4];
+      units[3] = 0;
     }
   }
   for (int e = tid; e < n_exp; e += kDispatchThreads) {

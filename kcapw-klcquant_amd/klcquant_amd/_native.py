@@ -27,6 +27,7 @@ PRECISION_FP32 = 0
 PRECISION_BF16 = 1
 
 LAYER_EVENTS = 7  # KLC_LAYER_EVENTS
+PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2  # KLC_PATH_*
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -49,13 +50,15 @@ SIGNATURES: dict[str, tuple] = {
     "klc_moe_units_size": (_I64, [_I64, _I64]),
     "klc_moe_gate_up": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _F32, _I32, _P, _P, _P]),
     "klc_moe_down": (_I32, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "klc_moe_gemm_gate_up": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _F32, _I32, _P, _P, _P]),
+    "klc_moe_gemm_down": (_I32, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I32, _P, _P]),
     "klc_moe_combine": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_rms_norm": (_I32, [_P, _P, _P, _I64, _I64, _F32, _P]),
     "klc_moe_bias_combine": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_pair_norms": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
-    "klc_moe_layer": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _P, _I64, _P,
-                             _P, _P, _P, _P, _P]),
+    "klc_moe_layer": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
+                             _P, _P, _P, _P, _P, _P]),
     "klc_synth_fill": (_I32, [_P, _I64, _U64, _I32, _I32, _I32, _P]),
 }
 

@@ -139,14 +139,19 @@ def synthetic_hidden(workload: int, n_tokens: int, hidden: int, step: int = 0) -
 class MoELayer:
     """Runs one MoE layer on batches of tokens (bf16 ``[B, H]`` in, bf16 ``[B, H]`` out)."""
 
+    PATHS = {"auto": nat.PATH_AUTO, "gemv": nat.PATH_GEMV, "gemm": nat.PATH_GEMM}
+
     def __init__(self, weights: MoELayerWeights, experts_per_token: int = 4, swiglu_limit: float = 7.0,
-                 precision: str = "fp32") -> None:
+                 precision: str = "fp32", path: str = "auto") -> None:
         if precision not in ops.PRECISIONS:
             raise ValueError(f"unknown matmul precision {precision!r}")
+        if path not in self.PATHS:
+            raise ValueError(f"unknown expert path {path!r} (auto, gemv or gemm)")
         self.w = weights
         self.k = min(int(experts_per_token), weights.n_experts)
         self.limit = float(swiglu_limit)
         self.precision = precision
+        self.path = path
         self._ws: dict[int, torch.Tensor] = {}
 
     def workspace(self, n_tokens: int) -> torch.Tensor:
@@ -188,11 +193,17 @@ class MoELayer:
         nat.call("klc_moe_layer", ops._ptr(x), ops._ptr(w.router_weight), ops._ptr(w.router_bias),
                  ops._ptr(w.gate_up_table), ops._ptr(w.gate_up_bias), ops._ptr(w.down_table), ops._ptr(w.down_bias),
                  n_tok, hidden, w.inter, w.n_experts, self.k, self.limit, ops.PRECISIONS[self.precision],
-                 ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(residual), ops._ptr(ids), ops._ptr(weights), ev,
-                 ops._stream(x.device))
+                 self.PATHS[self.path], ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(residual), ops._ptr(ids),
+                 ops._ptr(weights), ev, ops._stream(x.device))
         return out
 
     __call__ = forward
+
+    def uses_gemm(self, n_tokens: int) -> bool:
+        """Whether :meth:`forward` runs the grouped GEMM for ``n_tokens`` tokens (the library's rule)."""
+        if self.path != "auto":
+            return self.path == "gemm"
+        return n_tokens * self.k >= 8 * self.w.n_experts
 
     def forward_detailed(self, x: torch.Tensor, routing: tuple[torch.Tensor, torch.Tensor] | None = None) -> dict:
         """Step-by-step path exposing every intermediate (same kernels as :meth:`forward`).
@@ -212,9 +223,10 @@ class MoELayer:
             ops._check_gpu("weights", weights, torch.bfloat16, 2)
         k = ids.shape[1]
         disp = ops.dispatch(ids, w.n_experts)
+        gemm = self.uses_gemm(x.shape[0])
         gated, gated_raw = ops.gate_up(w.gate_up_table, w.gate_up_bias, x, k, disp, w.hidden, w.inter, self.limit,
-                                       self.precision, want_raw=True)
-        eo = ops.down(w.down_table, w.down_bias, gated, disp, w.hidden, w.inter, self.precision)
+                                       self.precision, want_raw=True, gemm=gemm)
+        eo = ops.down(w.down_table, w.down_bias, gated, disp, w.hidden, w.inter, self.precision, gemm=gemm)
         out = ops.combine(eo, weights, x.shape[0], k)
         return {"out": out, "logits": logits, "ids": ids, "values": values, "weights": weights,
                 "offsets": disp.offsets, "sorted_pairs": disp.sorted_pairs, "active": disp.active,

@@ -197,28 +197,32 @@ def pointer_table(mats: list[torch.Tensor] | torch.Tensor, device: torch.device)
 
 
 def gate_up(table: torch.Tensor, bias: torch.Tensor, x: torch.Tensor, k: int, disp: Dispatch, hidden: int,
-            inter: int, limit: float = 7.0, precision: str = "fp32", want_raw: bool = False):
-    """Returns the down input as bf16 hi/lo planes ``[2, B * k, I]`` (and the float32 SwiGLU output)."""
+            inter: int, limit: float = 7.0, precision: str = "fp32", want_raw: bool = False, gemm: bool = False):
+    """Returns the down input as bf16 hi/lo planes ``[2, B * k, I]`` (and the float32 SwiGLU output).
+
+    ``gemm`` selects the grouped GEMM (klc_moe_gemm_gate_up) instead of the GEMV.
+    """
     _check_gpu("hidden", x, torch.bfloat16, 2)
     dev = x.device
     n_tok = x.shape[0]
     split = torch.empty((2, n_tok * k, inter), dtype=torch.bfloat16, device=dev)
     raw = torch.empty((n_tok * k, inter), dtype=torch.float32, device=dev) if want_raw else None
-    nat.call("klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), n_tok, k, disp.n_experts, _ptr(disp.offsets),
-             _ptr(disp.sorted_pairs), _ptr(disp.units), hidden, inter, float(limit), PRECISIONS[precision],
-             _ptr(split), _ptr(raw), _stream(dev))
+    nat.call("klc_moe_gemm_gate_up" if gemm else "klc_moe_gate_up", _ptr(table), _ptr(bias), _ptr(x), n_tok, k,
+             disp.n_experts, _ptr(disp.offsets), _ptr(disp.sorted_pairs), _ptr(disp.units), hidden, inter,
+             float(limit), PRECISIONS[precision], _ptr(split), _ptr(raw), _stream(dev))
     return (split, raw) if want_raw else split
 
 
 def down(table: torch.Tensor, bias: torch.Tensor, gated_split: torch.Tensor, disp: Dispatch, hidden: int, inter: int,
-         precision: str = "fp32") -> torch.Tensor:
+         precision: str = "fp32", gemm: bool = False) -> torch.Tensor:
+    """float32 expert outputs ``[P, H]`` (``gemm``: klc_moe_gemm_down instead of the GEMV)."""
     _check_gpu("gated_split", gated_split, torch.bfloat16, 3)
     dev = gated_split.device
     n_pairs = gated_split.shape[1]
     eo = torch.empty((n_pairs, hidden), dtype=torch.float32, device=dev)
-    nat.call("klc_moe_down", _ptr(table), _ptr(bias), _ptr(gated_split), n_pairs, disp.n_experts, _ptr(disp.offsets),
-             _ptr(disp.sorted_pairs), _ptr(disp.units), hidden, inter, PRECISIONS[precision], _ptr(eo),
-             _stream(dev))
+    nat.call("klc_moe_gemm_down" if gemm else "klc_moe_down", _ptr(table), _ptr(bias), _ptr(gated_split), n_pairs,
+             disp.n_experts, _ptr(disp.offsets), _ptr(disp.sorted_pairs), _ptr(disp.units), hidden, inter,
+             PRECISIONS[precision], _ptr(eo), _stream(dev))
     return eo
 
 

@@ -83,13 +83,14 @@ def test_dispatch_matches_stable_counting_sort(gpu, n_tok, k, n_exp):
     # work units: every (expert, run of 8 / 4 tokens) once, experts ascending (the ABI's documented layout)
     u = disp.units.cpu().numpy()
     n_pairs = n_tok * k
-    cap8 = (n_pairs + 7 * min(n_pairs, n_exp)) // 8
-    cap4 = (n_pairs + 3 * min(n_pairs, n_exp)) // 4
-    assert u.size == 2 + cap8 + cap4
-    for per, start, n in [(8, 2, int(u[0])), (4, 2 + cap8, int(u[1]))]:
+    caps = {m: (n_pairs + (m - 1) * min(n_pairs, n_exp)) // m for m in (8, 4, 128)}
+    assert u.size == 4 + caps[8] + caps[4] + caps[128]
+    starts = {8: 4, 4: 4 + caps[8], 128: 4 + caps[8] + caps[4]}
+    for slot, per in enumerate((8, 4, 128)):
+        n = int(u[slot])
         want = [e | (j << 10) for e in range(n_exp) for j in range(-(-int(counts[e]) // per))]
-        assert u[start:start + n].tolist() == want
-        assert n <= (cap8 if per == 8 else cap4)
+        assert u[starts[per]:starts[per] + n].tolist() == want
+        assert n <= caps[per]
 
 
 def test_router_rejects_bad_shapes(gpu):
