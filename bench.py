@@ -12,8 +12,10 @@ from a cache left warm by the previous step.
 Prints one JSON line.  ``value`` is microseconds per token at the headline
 batch (64); ``per_batch`` holds B = 1, 8, 64.  ``stack`` is the 36-layer
 MoE-only decode (RMSNorm -> MoE -> residual per layer, 60.9 GB of experts
-resident, 64 sequences x 32 steps) and ``dequant`` the standalone MXFP4 ->
-bf16 dequant of 128 down_proj experts; both are extra lines of the same run.  ``roofline`` is for the
+resident, 64 sequences x 32 steps), ``prefill`` one layer over 2048 tokens
+with Zipf(1.1)-skewed routing (grouped GEMM), and ``dequant`` the standalone
+MXFP4 -> bf16 dequant of 128 down_proj experts; all are extra lines of the
+same run.  ``roofline`` is for the
 dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
 experts the batch touches + activations in + SwiGLU output) over its average
 duration measured with HIP events recorded by the library between its
@@ -62,6 +64,7 @@ def parse_args():
     ap.add_argument("--cpu-tokens", type=int, default=6, help="tokens in the CPU baseline sample (0 = skip)")
     ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16"])
     ap.add_argument("--skip-dequant", action="store_true", help="skip the standalone dequant measurement")
+    ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of the prefill measurement (0 = skip)")
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
     ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -177,6 +180,93 @@ def stack_bench(torch, dev, n_layers: int, n_seqs: int, n_steps: int, precision:
             "us_per_layer": round(dt * 1e6 / n_steps / n_layers, 2), "hbm_gbps": round(moved / dt / 1e9, 1),
             "frac_of_peak": round(moved / dt / 1e9 / HBM_PEAK_GBPS, 4), "resident_gb": round(resident / 1e9, 2),
             "unique_experts_mean": round(float(np.mean(uniq)), 2), "build_s": round(build_s, 1)}
+
+
+def zipf_router_bias(host_x, host_w, k: int, s: float, seed: int):
+    """bf16 router bias making expert popularity ~ Zipf(s) over a seeded permutation of the experts.
+
+    Target pair counts are n_pairs * r^-s / H(E, s) for expert rank r; the bias is fitted on the
+    host (float32 logits of the actual inputs) by 300 multiplicative steps on log(count / target),
+    keeping the best fit in L1."""
+    import numpy as np
+
+    from klcquant_amd import synth
+    from oracle.numerics import bf16_to_f32, f32_to_bf16
+
+    n_exp = host_w.shape[0]
+    perm = np.argsort(synth.random_ints(seed, n_exp, 0, 1 << 30), kind="stable")
+    rank = np.empty(n_exp, dtype=np.int64)
+    rank[perm] = np.arange(1, n_exp + 1)
+    p = rank.astype(np.float64) ** -s
+    p /= p.sum()
+    logits = bf16_to_f32(host_x) @ bf16_to_f32(host_w).T
+    target = p * logits.shape[0] * k
+
+    def counts_for(b_bits):
+        top = np.argpartition(-(logits + bf16_to_f32(b_bits)), k - 1, axis=1)[:, :k]
+        return np.bincount(top.ravel(), minlength=n_exp)
+
+    b = (-s * np.log(rank)).astype(np.float64)
+    best, best_err = None, None
+    for _ in range(300):
+        bits = f32_to_bf16(b.astype(np.float32))
+        c = counts_for(bits)
+        err = float(np.abs(c - target).sum())
+        if best_err is None or err < best_err:
+            best, best_err = bits, err
+        b += 0.25 * (np.log(target + 0.5) - np.log(c + 0.5))
+    return best, float(p.max())
+
+
+def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
+    """One 120B-shape MoE layer over a prefill chunk of n_tok tokens with Zipf(1.1)-skewed routing."""
+    import numpy as np
+
+    from klcquant_amd import moe
+
+    workload = 3
+    host = moe.synthetic_host_layer(workload, 0, HIDDEN, INTER, EXPERTS)
+    x_host = moe.synthetic_hidden(workload, n_tok, HIDDEN)
+    bias, target = zipf_router_bias(x_host, host["router_weight"], TOPK, 1.1, 1000 * workload + 11)
+    del host
+    layers = [moe.MoELayer(moe.MoELayerWeights.synthetic(workload, l, HIDDEN, INTER, EXPERTS, dev, bias), TOPK, 7.0,
+                           precision) for l in range(2)]
+    x = torch.from_numpy(x_host.view(np.int16)).view(torch.bfloat16).to(dev)
+    out = torch.empty_like(x)
+    ids = torch.empty((n_tok, TOPK), dtype=torch.int32, device=dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(reps)]
+    for row in evs:  # torch creates the HIP event on its first record
+        for ev in row:
+            ev.record()
+    for r in range(2):
+        layers[r % 2].forward(x, out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(reps):
+        layers[r % 2].forward(x, out=out, ids=ids if r == 0 else None, events=evs[r])
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    kern = np.array([[evs[r][i].elapsed_time(evs[r][i + 1]) for i in range(6)] for r in range(reps)]).mean(axis=0)
+    counts = np.bincount(ids.cpu().numpy().ravel(), minlength=EXPERTS)
+    flop = n_tok * TOPK * (2 * 2 * INTER * HIDDEN + 2 * HIDDEN * INTER) + 2 * n_tok * HIDDEN * EXPERTS
+    weights = int(np.count_nonzero(counts)) * (GATE_UP_EXPERT_BYTES + DOWN_EXPERT_BYTES)
+    expert_ms = float(kern[3] + kern[4])
+    bf16_peak = 2.5e15
+    del layers
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"gpt-oss-120B-shape MoE layer, prefill of {n_tok} tokens, top-4 of 128, Zipf(1.1) router bias",
+        "us_per_layer": round(dt * 1e6, 1), "tokens_per_s": round(n_tok / dt, 1),
+        "kernel_us_mean": {k: round(float(v) * 1e3, 2) for k, v in zip(KERNELS, kern)},
+        "flop": flop, "tflops": round(flop / dt / 1e12, 1),
+        "mfma_util_bf16": round(flop / (expert_ms * 1e-3) / bf16_peak, 4),
+        "weight_gbps": round(weights / (expert_ms * 1e-3) / 1e9, 1),
+        "expert_load": {"max": int(counts.max()), "mean": round(float(counts.mean()), 2),
+                        "min": int(counts.min()), "max_over_mean": round(float(counts.max() / counts.mean()), 2),
+                        "hottest_share": round(float(counts.max() / counts.sum()), 4),
+                        "zipf_target_share": round(target, 4), "experts_touched": int(np.count_nonzero(counts)),
+                        "top8": sorted((int(c) for c in counts), reverse=True)[:8]},
+    }
 
 
 def cpu_baseline(n_tokens: int) -> dict:
@@ -320,6 +410,9 @@ def main() -> int:
             "algorithmic_bytes_per_launch": round(head["gate_up_bytes_per_launch"]),
         },
     }
+    if args.prefill_tokens > 0:
+        result["prefill"] = prefill_bench(torch, dev, args.prefill_tokens, 10, args.precision)
+        print(f"[bench] prefill: {result['prefill']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del layers
         torch.cuda.empty_cache()

@@ -111,7 +111,7 @@ int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens
  * ascending, then -1 padding) and *n_active.  Also writes the work units of
  * the expert kernels, int32 units[klc_moe_units_size(n_pairs, n_experts)]:
  *   units[0..2] = number of decode gate_up (m = 8), decode down (m = 4) and
- *   prefill GEMM (m = 128) units, units[3] = 0, then the three lists in that
+ *   prefill GEMM (m = 64) units, units[3] = 0, then the three lists in that
  *   order, with capacities C_m = (n_pairs + (m - 1) * min(n_pairs, n_experts)) / m.
  * A unit is expert | (pass << 10) and covers the pass-th run of m tokens of
  * that expert; experts ascending, then passes.
@@ -172,7 +172,7 @@ int klc_moe_pair_norms(const float* gated, const float* expert_out, int64_t n_pa
 /* ---- Prefill: expert-grouped GEMM ---------------------------------------------
  * The same expert math as klc_moe_gate_up / klc_moe_down (same arguments,
  * outputs and tolerance) for batches that give experts many tokens: the
- * dispatch's 128-token GEMM units x 256-row tiles, weights decoded in
+ * dispatch's 64-token GEMM units x 256-row tiles, weights decoded in
  * registers into v_mfma_f32_16x16x32_bf16, activations staged in LDS. */
 int klc_moe_gemm_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens, int64_t k,
                          int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* units,

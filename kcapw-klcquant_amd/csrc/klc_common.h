@@ -54,17 +54,17 @@ __host__ __device__ __forceinline__ int64_t packed_scale_offset(int rows, int gr
 // Work units of the expert kernels.  A unit is one pass of one active expert
 // over up to kUnitTokens* of its tokens: the decode GEMVs stage 8 (gate_up)
 // or 4 (down: hi and lo rows per token) activation rows per pass, the
-// prefill grouped GEMM 128 tokens per tile.  An expert with more tokens gets
+// prefill grouped GEMM 64 tokens per tile.  An expert with more tokens gets
 // several units, which run as separate workgroups.  The dispatch writes all
 // three lists into one int32 array:
 //   [0] gate_up unit count, [1] down unit count, [2] GEMM unit count, [3] 0,
 //   then the gate_up list (capacity cap(8)), the down list (cap(4)) and the
-//   GEMM list (cap(128)),
+//   GEMM list (cap(64)),
 // a unit being expert | (pass << 10) (experts < 1024), experts ascending,
 // passes ascending.
 constexpr int kUnitTokensGateUp = 8;
 constexpr int kUnitTokensDown = 4;
-constexpr int kUnitTokensGemm = 128;
+constexpr int kUnitTokensGemm = 64;
 constexpr int kUnitHeader = 4;
 __host__ __device__ __forceinline__ int32_t make_unit(int expert, int pass) { return expert | (pass << 10); }
 __host__ __device__ __forceinline__ int unit_expert(int32_t u) { return u & 1023; }

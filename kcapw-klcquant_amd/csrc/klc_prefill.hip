@@ -1,14 +1,14 @@
 // Prefill path: expert-grouped GEMM on MFMA (gfx950).
 //
 // For batches that give experts many tokens, each expert's weights are read
-// once per 128-token unit and multiplied into all of the unit's tokens:
-// a workgroup owns one GEMM unit (up to 128 tokens of one expert, from the
+// once per 64-token unit and multiplied into all of the unit's tokens:
+// a workgroup owns one GEMM unit (up to 64 tokens of one expert, from the
 // dispatch) and 256 output rows (4 waves, each one 64-row packed tile, i.e.
 // 4 row blocks of 16).  Per 128-deep k step every wave decodes its A chunks
 // (MXFP4 -> bfloat16 with v_cvt_scalef32_pk_bf16_fp4, exact) and multiplies
 // them with v_mfma_f32_16x16x32_bf16 into each 16-token column block of B,
-// which the workgroup stages in LDS (double buffered) from the token rows.
-// A chunks stream from HBM two steps ahead.  The products are exact and the
+// which the workgroup stages in LDS (double buffered; global loads issued two
+// steps ahead) from the token rows.  A chunks stream from HBM two steps ahead.  The products are exact and the
 // sums run in float32, like the decode GEMVs, so both paths meet the same
 // tolerance; gate_up reads the bfloat16 hidden state as is, down reads the
 // float32 SwiGLU output as hi + lo bfloat16 planes (relative residual 2^-17).
@@ -39,6 +39,7 @@ constexpr int kGemmRows = kGemmWaves * kTileRows;   // 256 output rows per workg
 constexpr int kGemmCb = kUnitTokensGemm / 16;       // 8 column blocks of 16 tokens
 constexpr int kRowBytes = 128 * 2 + 16;             // one token's 128 bfloat16 of a step, padded (bank spread)
 constexpr int kPlaneBytes = kUnitTokensGemm * kRowBytes;
+constexpr int kPieces = kUnitTokensGemm * 16 / kGemmThreads;  // 16-byte pieces per thread per plane and step
 constexpr int kBufferWord3 = 0x00020000;
 constexpr uint32_t kOutOfRange = 0x40000000u;
 
@@ -86,9 +87,9 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
 
   // ---- staging: thread moves pieces (plane, token c = (tid >> 4) + 16 i, 8 values at 8 o), o = tid & 15 ----
   const int so = tid & 15;
-  int64_t src_row[8];
+  int64_t src_row[kPieces];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kPieces; ++i) {
     const int c = min((tid >> 4) + 16 * i, nt - 1);
     const int p = pairs[pb + tc + c];
     src_row[i] = (int64_t)(kDown ? p : p / k_top) * in_dim;
@@ -96,17 +97,17 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
   auto stage_load = [&](int s, u32x4_t* pv) {
     const int kc = min(s * 128 + so * 8, in_dim - 8);
 #pragma unroll
-    for (int i = 0; i < 8 * kPlanes; ++i)
-      pv[i] = *reinterpret_cast<const u32x4_t*>(act + (i >> 3) * act_plane + src_row[i & 7] + kc);
+    for (int i = 0; i < kPieces * kPlanes; ++i)
+      pv[i] = *reinterpret_cast<const u32x4_t*>(act + (i / kPieces) * act_plane + src_row[i % kPieces] + kc);
   };
   auto stage_store = [&](int s, int buf, const u32x4_t* pv) {
     uint8_t* base = stage + buf * kStage;
     const bool k_ok = s * 128 + so * 8 < in_dim;
 #pragma unroll
-    for (int i = 0; i < 8 * kPlanes; ++i) {
-      const int c = (tid >> 4) + 16 * (i & 7);
+    for (int i = 0; i < kPieces * kPlanes; ++i) {
+      const int c = (tid >> 4) + 16 * (i % kPieces);
       const u32x4_t z = {0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4_t*>(base + (i >> 3) * kPlaneBytes + c * kRowBytes + so * 16) =
+      *reinterpret_cast<u32x4_t*>(base + (i / kPieces) * kPlaneBytes + c * kRowBytes + so * 16) =
           (k_ok && c < nt) ? pv[i] : z;
     }
   };
@@ -135,45 +136,48 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
 #pragma unroll
     for (int cb = 0; cb < kGemmCb; ++cb) acc[rb][cb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  u32x4_t pv[8 * kPlanes];
+  // activation staging: two register sets, loads issued two steps ahead;
+  // LDS double buffered
+  u32x4_t pva[kPieces * kPlanes], pvb[kPieces * kPlanes];
   u32x4_t a_cur[4], a_nxt[4];
   uint32_t s_cur[4], s_nxt[4];
-  stage_load(0, pv);
+  stage_load(0, pva);
   a_load(0, a_cur, s_cur);
   if (steps > 1) a_load(1, a_nxt, s_nxt);
-  stage_store(0, 0, pv);
+  if (steps > 1) stage_load(1, pvb);
+  stage_store(0, 0, pva);
   __syncthreads();
 
-  for (int s = 0; s < steps; ++s) {
+  // one k step: stage s + 2 is loaded into `ld` (free since stage s was
+  // stored), stage s + 1 (loaded a step ago, in `st`) goes to LDS
+  auto step = [&](int s, u32x4_t* ld, const u32x4_t* st) {
     const int buf = s & 1;
-    if (s + 1 < steps) stage_load(s + 1, pv);
+    if (s + 2 < steps) stage_load(s + 2, ld);
     if (wave_live) {
-      // decode the 4 row blocks' A operands (16 bf16x8 per lane)
-      bf16x8_t a[4][4];
+      // per quarter j of the step: decode the 4 row blocks' A operands, then
+      // multiply them into every column block (row blocks innermost, so
+      // consecutive MFMAs update different accumulators)
       const bool live = 4 * s + lq < groups;
+      float scale[4];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        const float scale = cvt_scale_operand((s_cur[rb] >> (8 * (s & 3))) & 0xffu, live);
-        a[rb][0] = decode8(a_cur[rb].x, scale);
-        a[rb][1] = decode8(a_cur[rb].y, scale);
-        a[rb][2] = decode8(a_cur[rb].z, scale);
-        a[rb][3] = decode8(a_cur[rb].w, scale);
-      }
+      for (int rb = 0; rb < 4; ++rb) scale[rb] = cvt_scale_operand((s_cur[rb] >> (8 * (s & 3))) & 0xffu, live);
       const uint8_t* base = stage + buf * kStage + lr * kRowBytes + lq * 64;
 #pragma unroll
-      for (int cb = 0; cb < kGemmCb; ++cb) {
-        if (cb < ncb) {
+      for (int j = 0; j < 4; ++j) {
+        bf16x8_t a[4];
 #pragma unroll
-          for (int pl = 0; pl < kPlanes; ++pl) {
-            const uint8_t* bp = base + pl * kPlaneBytes + cb * 16 * kRowBytes;
-            bf16x8_t b[4];
+        for (int rb = 0; rb < 4; ++rb) a[rb] = decode8(a_cur[rb][j], scale[rb]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const bf16x8_t*>(bp + j * 16);
+        for (int cb = 0; cb < kGemmCb; ++cb) {
+          if (cb < ncb) {
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
+            for (int pl = 0; pl < kPlanes; ++pl) {
+              const bf16x8_t b =
+                  *reinterpret_cast<const bf16x8_t*>(base + pl * kPlaneBytes + cb * 16 * kRowBytes + j * 16);
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb][j], b[j], acc[rb][cb], 0, 0, 0);
+              for (int rb = 0; rb < 4; ++rb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], b, acc[rb][cb], 0, 0, 0);
+            }
           }
         }
       }
@@ -184,8 +188,12 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
       s_cur[rb] = s_nxt[rb];
     }
     if (s + 2 < steps) a_load(s + 2, a_nxt, s_nxt);
-    if (s + 1 < steps) stage_store(s + 1, buf ^ 1, pv);
+    if (s + 1 < steps) stage_store(s + 1, buf ^ 1, st);
     __syncthreads();
+  };
+  for (int s = 0; s < steps; s += 2) {
+    step(s, pva, pvb);
+    if (s + 1 < steps) step(s + 1, pvb, pva);
   }
 
   if (!wave_live) return;

@@ -258,8 +258,11 @@ constexpr int64_t kDispatchMaxHistBytes = 128 * 1024;
 __host__ __device__ constexpr int dispatch_chunks(int n_pairs) { return (n_pairs + kDispatchChunk - 1) / kDispatchChunk; }
 
 // LDS bytes block_dispatch needs for n_pairs pairs over n_exp experts.
+__host__ __device__ constexpr size_t dispatch_hist_bytes(int n_pairs, int n_exp) {
+  return ((size_t)dispatch_chunks(n_pairs) * n_exp * sizeof(uint16_t) + 15) / 16 * 16;
+}
 __host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int n_exp) {
-  return ((size_t)dispatch_chunks(n_pairs) * n_exp * sizeof(uint16_t) + 15) / 16 * 16 +
+  return dispatch_hist_bytes(n_pairs, n_exp) + ((size_t)n_pairs * sizeof(uint16_t) + 15) / 16 * 16 +
          5 * kDispatchMaxExperts * sizeof(int32_t) + 8 * sizeof(int32_t);
 }
 
@@ -289,7 +292,10 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
   const int lane = tid & 63;
   const int nchunk = dispatch_chunks(n_pairs);
   uint16_t* hist = reinterpret_cast<uint16_t*>(lds);
-  int32_t* total = reinterpret_cast<int32_t*>(lds + ((size_t)nchunk * n_exp * sizeof(uint16_t) + 15) / 16 * 16);
+  // the pairs' experts staged once in LDS (all loads in flight together), 0xffff = skip
+  uint16_t* sid = reinterpret_cast<uint16_t*>(lds + dispatch_hist_bytes(n_pairs, n_exp));
+  int32_t* total =
+      reinterpret_cast<int32_t*>(reinterpret_cast<char*>(sid) + ((size_t)n_pairs * sizeof(uint16_t) + 15) / 16 * 16);
   int32_t* flags = total + kDispatchMaxExperts;
   int32_t* ugu = flags + kDispatchMaxExperts;  // units per expert, then their prefix (gate_up)
   int32_t* udn = ugu + kDispatchMaxExperts;    // same for down
@@ -298,12 +304,22 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
   const uint64_t below = (1ull << lane) - 1ull;
 
   for (int i = tid; i < nchunk * n_exp; i += kDispatchThreads) hist[i] = 0;
+  for (int p0 = 0; p0 < n_pairs; p0 += 8 * kDispatchThreads) {
+    int32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ids[min(p0 + j * kDispatchThreads + tid, n_pairs - 1)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int p = p0 + j * kDispatchThreads + tid;
+      if (p < n_pairs) sid[p] = (v[j] >= 0 && v[j] < n_exp) ? (uint16_t)v[j] : (uint16_t)0xffffu;
+    }
+  }
   __syncthreads();
   // 1. per-chunk counts: the lowest lane of each expert's peer group writes them
   for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
     const int p = c * kDispatchChunk + lane;
-    const int e = p < n_pairs ? ids[p] : -1;
-    const bool valid = e >= 0 && e < n_exp;
+    const int e = p < n_pairs ? (int)sid[p] : 0xffff;
+    const bool valid = e < n_exp;
     const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
     if (valid && (peers & below) == 0ull) hist[c * n_exp + e] = (uint16_t)__popcll(peers);
   }
@@ -338,8 +354,8 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
   // 3. scatter: position = expert offset + pairs of e in earlier chunks + rank in this chunk
   for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
     const int p = c * kDispatchChunk + lane;
-    const int e = p < n_pairs ? ids[p] : -1;
-    const bool valid = e >= 0 && e < n_exp;
+    const int e = p < n_pairs ? (int)sid[p] : 0xffff;
+    const bool valid = e < n_exp;
     const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
     if (valid) sorted[total[e] + hist[c * n_exp + e] + __popcll(peers & below)] = p;
   }
@@ -492,6 +508,9 @@ int check_dispatch_args(int64_t n_pairs, int64_t n_exp) {
   KLC_REQUIRE(n_pairs < 65536 && (int64_t)dispatch_chunks((int)n_pairs) * n_exp * 2 <= kDispatchMaxHistBytes,
               KLC_ERR_UNSUPPORTED, "dispatch: n_pairs=%lld too large for %lld experts (ceil(n_pairs / 64) * "
               "n_experts <= 65536, n_pairs < 65536)", (long long)n_pairs, (long long)n_exp);
+  KLC_REQUIRE(dispatch_lds_bytes((int)n_pairs, (int)n_exp) <= 160 * 1024, KLC_ERR_UNSUPPORTED,
+              "dispatch: n_pairs=%lld with %lld experts needs more than 160 KiB of LDS", (long long)n_pairs,
+              (long long)n_exp);
   return KLC_OK;
 }
 

@@ -83,8 +83,8 @@ def test_argument_errors_before_any_launch():
 def test_units_size():
     lib = nat.load()
     # 256 pairs over 128 experts: gate_up (256 + 7 * 128) // 8 = 144, down (256 + 3 * 128) // 4 = 160,
-    # GEMM (256 + 127 * 128) // 128 = 129
-    assert lib.klc_moe_units_size(256, 128) == 4 + 144 + 160 + 129
+    # GEMM (256 + 63 * 128) // 64 = 130
+    assert lib.klc_moe_units_size(256, 128) == 4 + 144 + 160 + 130
     assert lib.klc_moe_units_size(4, 128) == 4 + 4 + 4 + 4
     assert lib.klc_moe_units_size(16, 300) == nat.KLC_ERR_UNSUPPORTED
 

@@ -40,7 +40,7 @@ def test_gemm_layer_matches_oracle(gpu, n_tok, k, n_exp, precision):
 
 
 def test_gemm_units_span_hot_experts(gpu):
-    """Router bias sends every token to the same 4 experts: 300 tokens per expert = 3 GEMM units each."""
+    """Router bias sends every token to the same 4 experts: 300 tokens per expert = 5 GEMM units each."""
     n_exp, n_tok = 8, 300
     bias = np.full(n_exp, 0xC2C8, dtype=np.uint16)  # -100.0
     bias[[0, 2, 5, 7]] = 0x42C8  # +100.0
@@ -50,7 +50,7 @@ def test_gemm_units_span_hot_experts(gpu):
     torch.cuda.synchronize()
     ref = oracle_layer(host, x, 4)
     assert set(np.unique(ref["ids"])) == {0, 2, 5, 7}
-    assert int(det["units"][2]) == 4 * 3
+    assert int(det["units"][2]) == 4 * 5
     assert_close(det["expert_out"].cpu().numpy().reshape(n_tok, 4, -1), ref["expert_out"], "expert output")
     assert_final_close(bf16_bits(det["out"]), ref)
 

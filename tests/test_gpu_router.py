@@ -83,10 +83,10 @@ def test_dispatch_matches_stable_counting_sort(gpu, n_tok, k, n_exp):
     # work units: every (expert, run of 8 / 4 tokens) once, experts ascending (the ABI's documented layout)
     u = disp.units.cpu().numpy()
     n_pairs = n_tok * k
-    caps = {m: (n_pairs + (m - 1) * min(n_pairs, n_exp)) // m for m in (8, 4, 128)}
-    assert u.size == 4 + caps[8] + caps[4] + caps[128]
-    starts = {8: 4, 4: 4 + caps[8], 128: 4 + caps[8] + caps[4]}
-    for slot, per in enumerate((8, 4, 128)):
+    caps = {m: (n_pairs + (m - 1) * min(n_pairs, n_exp)) // m for m in (8, 4, 64)}
+    assert u.size == 4 + caps[8] + caps[4] + caps[64]
+    starts = {8: 4, 4: 4 + caps[8], 64: 4 + caps[8] + caps[4]}
+    for slot, per in enumerate((8, 4, 64)):
         n = int(u[slot])
         want = [e | (j << 10) for e in range(n_exp) for j in range(-(-int(counts[e]) // per))]
         assert u[starts[per]:starts[per] + n].tolist() == want
