@@ -41,6 +41,7 @@ constexpr int kRowBytes = 128 * 2 + 16;             // one token's 128 bfloat16 
 constexpr int kPlaneBytes = kUnitTokensGemm * kRowBytes;
 constexpr int kPieces = kUnitTokensGemm * 16 / kGemmThreads;  // 16-byte pieces per thread per plane and step
 constexpr int kBufferWord3 = 0x00020000;
+constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
 constexpr uint32_t kOutOfRange = 0x40000000u;
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
@@ -61,13 +62,19 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
-    float limit, int precision) {
+    float limit, int precision, int row_wgs, int units_per_xcd) {
   constexpr int kPlanes = kDown ? 2 : 1;
   constexpr int kStage = kPlanes * kPlaneBytes;
   extern __shared__ __align__(16) uint8_t stage[];  // 2 x kStage
 
-  const int u = blockIdx.y;
-  if (u >= *n_units) return;
+  // XCD-aware order: workgroups are handed to the 8 XCDs round-robin, so XCD
+  // x = blockIdx.x % 8 runs units x, x + 8, ...; all row tiles of a unit run on
+  // one XCD, which reads the unit's activation rows into its own L2 once.
+  const int xcd = blockIdx.x % kXcds;
+  const int j = blockIdx.x / kXcds;
+  const int u = xcd + kXcds * (j / row_wgs);
+  const int row_wg = j % row_wgs;
+  if (j >= units_per_xcd * row_wgs || u >= *n_units) return;
   const int32_t unit = units[u];
   const int e = unit_expert(unit);
   const int pb = offsets[e];
@@ -80,7 +87,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
   const int lr = lane & 15;
   const int lq = lane >> 4;
   const int tiles = rows / kTileRows;
-  const int tile = blockIdx.x * kGemmWaves + wave;
+  const int tile = row_wg * kGemmWaves + wave;
   const bool wave_live = tile < tiles;
   const int in_dim = groups * 32;
   const int steps = (groups + 3) >> 2;
@@ -248,24 +255,28 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
                         float* gated_raw, hipStream_t stream) {
   const int64_t n_pairs = n_tok * k;
   const int64_t rows = 2 * inter;
-  const dim3 grid((unsigned)((rows + kGemmRows - 1) / kGemmRows),
-                  (unsigned)units_capacity(n_pairs, n_exp, kUnitTokensGemm));
+  const int row_wgs = (int)((rows + kGemmRows - 1) / kGemmRows);
+  const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
+  const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   moe_gemm_kernel<false><<<grid, kGemmThreads, 2 * kPlaneBytes, stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
       0, nullptr, static_cast<uint16_t*>(gated_split), n_pairs * inter, gated_raw, offsets, pairs,
-      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, (int)(hidden / 32), (int)k, limit, precision);
+      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, (int)(hidden / 32), (int)k, limit, precision,
+      row_wgs, per_xcd);
   return check_launch("moe_gemm_kernel<gate_up>");
 }
 
 int launch_gemm_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs, int64_t n_exp,
                      const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
                      int precision, float* eo, hipStream_t stream) {
-  const dim3 grid((unsigned)((hidden + kGemmRows - 1) / kGemmRows),
-                  (unsigned)units_capacity(n_pairs, n_exp, kUnitTokensGemm));
+  const int row_wgs = (int)((hidden + kGemmRows - 1) / kGemmRows);
+  const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
+  const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   moe_gemm_kernel<true><<<grid, kGemmThreads, 2 * 2 * kPlaneBytes, stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs,
-      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, (int)(inter / 32), 1, 0.0f, precision);
+      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, (int)(inter / 32), 1, 0.0f, precision,
+      row_wgs, per_xcd);
   return check_launch("moe_gemm_kernel<down>");
 }
 

@@ -115,13 +115,92 @@ __device__ void router_logits_tile(const uint16_t* __restrict__ x, const uint16_
   }
 }
 
-__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
-                                                            const uint16_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ b,
-                                                            uint16_t* __restrict__ logits, float* __restrict__ x_f32,
-                                                            int n_tok, int hidden, int n_exp) {
-  extern __shared__ uint16_t rxs[];
-  router_logits_tile(x, w, b, logits, x_f32, n_tok, hidden, n_exp, rxs);
+// Logits on the float64 matrix cores: one workgroup per tile of 16 experts x
+// 16 tokens, its 4 waves splitting the hidden dimension into quarters.  Per
+// 32-deep chunk lane l loads 8 consecutive weights of expert row l % 16 and
+// 8 hidden values of token l % 16 (k = 32 c + 8 (l / 16) + i), converts them
+// to float64 (bfloat16 products are exact in float64) and issues 8
+// v_mfma_f64_16x16x4_f64 (A lane l = row l % 16, k = l / 16; B lane l =
+// column l % 16, same k; D lane l register i = row l / 16 + 4 i, column
+// l % 16), alternating two accumulators.  The quarters are summed through LDS
+// in wave order, then rounded like F.linear in bfloat16: bf16(f32(sum) + b).
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+constexpr int kRouterMfmaRows = 16;
+
+__device__ void router_logits_mfma_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                        const uint16_t* __restrict__ b, uint16_t* logits, float* __restrict__ x_f32,
+                                        int n_tok, int hidden, int n_exp, int e0, int t0,
+                                        double* red /* LDS [3][64][4] */) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int nchunk = (hidden + 31) >> 5;
+  const int per = (nchunk + 3) >> 2;
+  const int c0 = wave * per;
+  const int c1 = min(c0 + per, nchunk);
+  const uint16_t* wrow = w + (int64_t)min(e0 + r, n_exp - 1) * hidden;
+  const int tok = t0 + r;
+  const uint16_t* xrow = x + (int64_t)min(tok, n_tok - 1) * hidden;
+  f64x4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+  for (int c = c0; c < c1; ++c) {
+    const int k = c * 32 + g * 8;
+    const bool ok = k < hidden;  // hidden % 8 == 0: a lane's 8 values are all in or all out
+    const int kc = ok ? k : 0;
+    uint4 wv = *reinterpret_cast<const uint4*>(wrow + kc);
+    uint4 xv = *reinterpret_cast<const uint4*>(xrow + kc);
+    if (!ok) {
+      wv = make_uint4(0u, 0u, 0u, 0u);
+      xv = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (x_f32 != nullptr && e0 == 0 && ok && tok < n_tok) {
+      float4* dst = reinterpret_cast<float4*>(x_f32 + (int64_t)tok * hidden + k);
+      dst[0] = make_float4(__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
+                           __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u));
+      dst[1] = make_float4(__uint_as_float(xv.z << 16), __uint_as_float(xv.z & 0xffff0000u),
+                           __uint_as_float(xv.w << 16), __uint_as_float(xv.w & 0xffff0000u));
+    }
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)__uint_as_float(ww[q] << 16),
+                                                   (double)__uint_as_float(xw[q] << 16), acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)__uint_as_float(ww[q] & 0xffff0000u),
+                                                   (double)__uint_as_float(xw[q] & 0xffff0000u), acc1, 0, 0, 0);
+    }
+  }
+  f64x4_t acc = acc0 + acc1;
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[((wave - 1) * 64 + lane) * 4 + i] = acc[i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += red[(q * 64 + lane) * 4 + i];
+    if (tok < n_tok) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = e0 + g + 4 * i;
+        if (e < n_exp)
+          logits[(int64_t)tok * n_exp + e] = (uint16_t)f32_to_bf16_rne((float)acc[i] + bf16_to_f32(b[e]));
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 const uint16_t* __restrict__ b,
+                                                                 uint16_t* __restrict__ logits,
+                                                                 float* __restrict__ x_f32, int n_tok, int hidden,
+                                                                 int n_exp) {
+  __shared__ double red[3 * 64 * 4];
+  router_logits_mfma_tile(x, w, b, logits, x_f32, n_tok, hidden, n_exp, blockIdx.x * kRouterMfmaRows,
+                          blockIdx.y * kRouterMfmaRows, red);
 }
 
 // Orderable key: larger key = larger logit; NaN is the largest value; -0 == +0;
@@ -249,7 +328,7 @@ __device__ void block_exclusive_scan_256(int32_t* v, int n, int32_t* total) {
   }
 }
 
-// Pairs are taken in chunks of 64 (one wave-wide pass); hist[c][e] counts the
+// Pairs are taken in chunks of 64 (one wave-wide pass); hist[e][c] counts the
 // pairs of expert e in chunk c (then, after the scan over chunks, the pairs
 // of e in chunks before c).
 constexpr int kDispatchChunk = kWave;
@@ -321,22 +400,32 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
     const int e = p < n_pairs ? (int)sid[p] : 0xffff;
     const bool valid = e < n_exp;
     const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
-    if (valid && (peers & below) == 0ull) hist[c * n_exp + e] = (uint16_t)__popcll(peers);
+    if (valid && (peers & below) == 0ull) hist[e * nchunk + c] = (uint16_t)__popcll(peers);
   }
   __syncthreads();
-  // 2. per expert: exclusive prefix over chunks, totals, unit counts
-  for (int e = tid; e < n_exp; e += kDispatchThreads) {
+  // 2. per expert (one wave each): exclusive prefix over its chunks, 64 at a
+  //    time with a wave scan; totals and unit counts
+  for (int e = wave; e < n_exp; e += kDispatchThreads / kWave) {
     int32_t run = 0;
-    for (int c = 0; c < nchunk; ++c) {
-      const int32_t v = hist[c * n_exp + e];
-      hist[c * n_exp + e] = (uint16_t)run;
-      run += v;
+    for (int base = 0; base < nchunk; base += kWave) {
+      const int c = base + lane;
+      const int32_t v = c < nchunk ? (int32_t)hist[e * nchunk + c] : 0;
+      int32_t incl = v;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int32_t o = __shfl_up(incl, off);
+        if (lane >= off) incl += o;
+      }
+      if (c < nchunk) hist[e * nchunk + c] = (uint16_t)(run + incl - v);
+      run += __shfl(incl, kWave - 1);
     }
-    total[e] = run;
-    flags[e] = run > 0 ? 1 : 0;
-    ugu[e] = (run + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
-    udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
-    ugm[e] = (run + kUnitTokensGemm - 1) / kUnitTokensGemm;
+    if (lane == 0) {
+      total[e] = run;
+      flags[e] = run > 0 ? 1 : 0;
+      ugu[e] = (run + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
+      udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
+      ugm[e] = (run + kUnitTokensGemm - 1) / kUnitTokensGemm;
+    }
   }
   __syncthreads();
   // total[] becomes the expert offsets, flags[] the active-list positions,
@@ -357,17 +446,25 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
     const int e = p < n_pairs ? (int)sid[p] : 0xffff;
     const bool valid = e < n_exp;
     const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
-    if (valid) sorted[total[e] + hist[c * n_exp + e] + __popcll(peers & below)] = p;
+    if (valid) sorted[total[e] + hist[e * nchunk + c] + __popcll(peers & below)] = p;
   }
   {
-    int32_t* gu_list = units + kUnitHeader;
-    int32_t* dn_list = units + units_offset_down(n_pairs, n_exp);
-    int32_t* gm_list = units + units_offset_gemm(n_pairs, n_exp);
-    for (int e = tid; e < n_exp; e += kDispatchThreads) {
-      const int c = (e + 1 < n_exp ? total[e + 1] : sums[0]) - total[e];
-      for (int j = 0; j * kUnitTokensGateUp < c; ++j) gu_list[ugu[e] + j] = make_unit(e, j);
-      for (int j = 0; j * kUnitTokensDown < c; ++j) dn_list[udn[e] + j] = make_unit(e, j);
-      for (int j = 0; j * kUnitTokensGemm < c; ++j) gm_list[ugm[e] + j] = make_unit(e, j);
+    // unit lists, one thread per unit: its expert is the last one whose first
+    // unit is <= it (experts without units share the next one's first unit)
+    const int32_t* firsts[3] = {ugu, udn, ugm};
+    int32_t* lists[3] = {units + kUnitHeader, units + units_offset_down(n_pairs, n_exp),
+                         units + units_offset_gemm(n_pairs, n_exp)};
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+      const int32_t* first = firsts[l];
+      for (int u = tid; u < sums[2 + l]; u += kDispatchThreads) {
+        int lo = 0, hi = n_exp;  // first[lo] <= u < first[hi] (first[n_exp] taken as +inf)
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (first[mid] <= u) lo = mid; else hi = mid;
+        }
+        lists[l][u] = make_unit(lo, u - first[lo]);
+      }
     }
     if (tid == 0) {
       units[0] = sums[2];
@@ -441,12 +538,12 @@ __global__ __launch_bounds__(256) void router_fused_kernel(const uint16_t* __res
 
 int launch_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32, int64_t n_tok,
                          int64_t hidden, int64_t n_exp, hipStream_t stream) {
-  const dim3 grid((unsigned)((n_exp + 3) / 4), (unsigned)((n_tok + kRouterTok - 1) / kRouterTok));
-  const size_t lds = (size_t)kRouterTok * hidden * sizeof(uint16_t);
-  router_logits_kernel<<<grid, 256, lds, stream>>>(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
-                                                 static_cast<const uint16_t*>(b), static_cast<uint16_t*>(logits),
-                                                 x_f32, (int)n_tok, (int)hidden, (int)n_exp);
-  return check_launch("router_logits_kernel");
+  const dim3 grid((unsigned)((n_exp + kRouterMfmaRows - 1) / kRouterMfmaRows),
+                  (unsigned)((n_tok + kRouterMfmaRows - 1) / kRouterMfmaRows));
+  router_logits_mfma_kernel<<<grid, 256, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
+      static_cast<uint16_t*>(logits), x_f32, (int)n_tok, (int)hidden, (int)n_exp);
+  return check_launch("router_logits_mfma_kernel");
 }
 
 int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
