@@ -115,7 +115,8 @@ int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens
  *   order, with capacities C_m = (n_pairs + (m - 1) * min(n_pairs, n_experts)) / m.
  * A unit is expert | (pass << 10) and covers the pass-th run of m tokens of
  * that expert; experts ascending, then passes.
- * n_experts <= 256, n_pairs < 65536 and ceil(n_pairs / 64) * n_experts <= 65536. */
+ * n_experts <= 256 and n_pairs <= 38648 (one workgroup stages every pair's
+ * expert and rank in LDS). */
 int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
                      int32_t* sorted_pairs, int32_t* active, int32_t* n_active, int32_t* units, void* stream);
 

@@ -298,83 +298,91 @@ __global__ __launch_bounds__(256) void softmax_weights_kernel(const float* __res
 constexpr int kDispatchThreads = 256;
 constexpr int kDispatchMaxExperts = 256;
 
-// Exclusive prefix sum of LDS array `v[n]` (n <= 256) by the whole block;
-// total written to *total.  Uses one wave, 4 entries per lane.
-__device__ void block_exclusive_scan_256(int32_t* v, int n, int32_t* total) {
-  if (threadIdx.x < kWave) {
-    const int lane = threadIdx.x;
-    int32_t local[4];
-    int32_t s = 0;
+// Exclusive prefix sum of LDS array `v[n]` (n <= 256) by the calling wave;
+// total written to *total.  4 entries per lane.
+__device__ void wave_exclusive_scan_256(int32_t* v, int n, int32_t* total, int lane) {
+  int32_t local[4];
+  int32_t s = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = lane * 4 + i;
-      local[i] = idx < n ? v[idx] : 0;
-      s += local[i];
-    }
-    int32_t incl = s;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int32_t o = __shfl_up(incl, off);
-      if (lane >= off) incl += o;
-    }
-    int32_t run = incl - s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = lane * 4 + i;
-      if (idx < n) v[idx] = run;
-      run += local[i];
-    }
-    if (lane == kWave - 1) *total = incl;
+  for (int i = 0; i < 4; ++i) {
+    const int idx = lane * 4 + i;
+    local[i] = idx < n ? v[idx] : 0;
+    s += local[i];
   }
+  int32_t incl = s;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int32_t o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  int32_t run = incl - s;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = lane * 4 + i;
+    if (idx < n) v[idx] = run;
+    run += local[i];
+  }
+  if (lane == kWave - 1) *total = incl;
 }
 
-// Pairs are taken in chunks of 64 (one wave-wide pass); hist[e][c] counts the
-// pairs of expert e in chunk c (then, after the scan over chunks, the pairs
-// of e in chunks before c).
+// Pairs are taken in chunks of 64 (one wave-wide pass); wave w owns the
+// contiguous chunks [w * cpw, (w + 1) * cpw), cpw = ceil(chunks / 4), and
+// ranks its pairs among the wave's earlier pairs of the same expert.  A wave
+// takes 4 chunks at a time so that their ballots overlap.
 constexpr int kDispatchChunk = kWave;
-constexpr int64_t kDispatchMaxHistBytes = 128 * 1024;
+constexpr int kDispatchGroup = 4;
+constexpr int kDispatchWaves = kDispatchThreads / kWave;
 
 __host__ __device__ constexpr int dispatch_chunks(int n_pairs) { return (n_pairs + kDispatchChunk - 1) / kDispatchChunk; }
 
-// LDS bytes block_dispatch needs for n_pairs pairs over n_exp experts.
-__host__ __device__ constexpr size_t dispatch_hist_bytes(int n_pairs, int n_exp) {
-  return ((size_t)dispatch_chunks(n_pairs) * n_exp * sizeof(uint16_t) + 15) / 16 * 16;
-}
-__host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int n_exp) {
-  return dispatch_hist_bytes(n_pairs, n_exp) + ((size_t)n_pairs * sizeof(uint16_t) + 15) / 16 * 16 +
-         5 * kDispatchMaxExperts * sizeof(int32_t) + 8 * sizeof(int32_t);
+// LDS bytes block_dispatch needs for n_pairs pairs: the pairs' experts and
+// ranks (uint16 each), per-wave counts and five per-expert arrays.
+__host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int /*n_exp*/) {
+  return 2 * (((size_t)n_pairs * sizeof(uint16_t) + 15) / 16 * 16) +
+         (kDispatchWaves + 5) * kDispatchMaxExperts * sizeof(int32_t) + 8 * sizeof(int32_t);
 }
 
-// Lanes of the wave holding the same key (key < 512): the lanes that agree
-// with this lane on each of the 9 key bits.
-__device__ __forceinline__ uint64_t wave_peers(uint32_t key) {
-  uint64_t peers = ~0ull;
+// Largest n_pairs whose staging fits in 160 KiB of LDS.
+constexpr int kDispatchMaxPairs = 38648;
+static_assert(dispatch_lds_bytes(kDispatchMaxPairs, kDispatchMaxExperts) <= 160 * 1024, "dispatch LDS");
+static_assert(dispatch_lds_bytes(kDispatchMaxPairs + 8, kDispatchMaxExperts) > 160 * 1024, "dispatch LDS");
+
+// For each of N keys (key < 512) held by this lane: the lanes of the wave
+// holding the same key, from one ballot per key bit.
+template <int N>
+__device__ __forceinline__ void wave_peers(const uint32_t (&key)[N], uint64_t (&peers)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) peers[i] = ~0ull;
 #pragma unroll
   for (int b = 0; b < 9; ++b) {
-    const bool bit = (key >> b) & 1u;
-    const uint64_t m = __ballot(bit);
-    peers &= bit ? m : ~m;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const bool bit = (key[i] >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      peers[i] &= bit ? m : ~m;
+    }
   }
-  return peers;
 }
 
 // Stable counting sort of the pairs by expert, by one 256-thread block, and
-// the GEMV work-unit lists (klc_common.h).  Chunk c of 64 pairs is handled by
-// wave c % 4: a lane's rank among the chunk's pairs of its expert comes from
-// ballots, so no step is serial over pairs.  lds holds
+// the work-unit lists (klc_common.h).  A pair's position is its expert's
+// offset + the pairs of that expert in earlier waves' chunks + its rank in
+// its wave's chunks (ballots within a chunk, a per-wave running count across
+// chunks), so no step is serial over pairs.  lds holds
 // dispatch_lds_bytes(n_pairs, n_exp) bytes.
 __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
                                int32_t* __restrict__ sorted, int32_t* __restrict__ active,
                                int32_t* __restrict__ n_active, int32_t* __restrict__ units, char* lds) {
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int nchunk = dispatch_chunks(n_pairs);
-  uint16_t* hist = reinterpret_cast<uint16_t*>(lds);
-  // the pairs' experts staged once in LDS (all loads in flight together), 0xffff = skip
-  uint16_t* sid = reinterpret_cast<uint16_t*>(lds + dispatch_hist_bytes(n_pairs, n_exp));
-  int32_t* total =
-      reinterpret_cast<int32_t*>(reinterpret_cast<char*>(sid) + ((size_t)n_pairs * sizeof(uint16_t) + 15) / 16 * 16);
+  const int cpw = (nchunk + kDispatchWaves - 1) / kDispatchWaves;
+  const size_t pair_bytes = ((size_t)n_pairs * sizeof(uint16_t) + 15) / 16 * 16;
+  uint16_t* sid = reinterpret_cast<uint16_t*>(lds);  // expert of each pair, 0xffff = skip
+  uint16_t* rank = reinterpret_cast<uint16_t*>(lds + pair_bytes);
+  int32_t* cnt = reinterpret_cast<int32_t*>(lds + 2 * pair_bytes);  // [wave][expert]
+  int32_t* total = cnt + kDispatchWaves * kDispatchMaxExperts;
   int32_t* flags = total + kDispatchMaxExperts;
   int32_t* ugu = flags + kDispatchMaxExperts;  // units per expert, then their prefix (gate_up)
   int32_t* udn = ugu + kDispatchMaxExperts;    // same for down
@@ -382,7 +390,7 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
   int32_t* sums = ugm + kDispatchMaxExperts;
   const uint64_t below = (1ull << lane) - 1ull;
 
-  for (int i = tid; i < nchunk * n_exp; i += kDispatchThreads) hist[i] = 0;
+  for (int i = tid; i < kDispatchWaves * kDispatchMaxExperts; i += kDispatchThreads) cnt[i] = 0;
   for (int p0 = 0; p0 < n_pairs; p0 += 8 * kDispatchThreads) {
     int32_t v[8];
 #pragma unroll
@@ -394,76 +402,106 @@ __device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32
     }
   }
   __syncthreads();
-  // 1. per-chunk counts: the lowest lane of each expert's peer group writes them
-  for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
-    const int p = c * kDispatchChunk + lane;
-    const int e = p < n_pairs ? (int)sid[p] : 0xffff;
-    const bool valid = e < n_exp;
-    const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
-    if (valid && (peers & below) == 0ull) hist[e * nchunk + c] = (uint16_t)__popcll(peers);
+  // 1. ranks: within a chunk from the ballots, plus the wave's running count
+  //    of the expert (read by all its lanes, then advanced by the lowest one;
+  //    a wave's LDS accesses complete in program order)
+  {
+    int32_t* wcnt = cnt + wave * kDispatchMaxExperts;
+    const int cend = min((wave + 1) * cpw, nchunk);
+    for (int c0 = wave * cpw; c0 < cend; c0 += kDispatchGroup) {
+      uint32_t key[kDispatchGroup];
+      uint64_t peers[kDispatchGroup];
+#pragma unroll
+      for (int i = 0; i < kDispatchGroup; ++i) {
+        const int p = (c0 + i) * kDispatchChunk + lane;
+        const uint32_t e = (c0 + i < cend && p < n_pairs) ? (uint32_t)sid[p] : 0xffffu;
+        key[i] = e < (uint32_t)n_exp ? e : 511u;
+      }
+      wave_peers(key, peers);
+#pragma unroll
+      for (int i = 0; i < kDispatchGroup; ++i) {
+        if (key[i] != 511u) {
+          const int32_t before = wcnt[key[i]];
+          rank[(c0 + i) * kDispatchChunk + lane] = (uint16_t)(before + __popcll(peers[i] & below));
+          if ((peers[i] & below) == 0ull) wcnt[key[i]] = before + __popcll(peers[i]);
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
   }
   __syncthreads();
-  // 2. per expert (one wave each): exclusive prefix over its chunks, 64 at a
-  //    time with a wave scan; totals and unit counts
-  for (int e = wave; e < n_exp; e += kDispatchThreads / kWave) {
+  // 2. per expert: the waves' counts become their exclusive prefix; totals
+  //    and unit counts
+  for (int e = tid; e < n_exp; e += kDispatchThreads) {
     int32_t run = 0;
-    for (int base = 0; base < nchunk; base += kWave) {
-      const int c = base + lane;
-      const int32_t v = c < nchunk ? (int32_t)hist[e * nchunk + c] : 0;
-      int32_t incl = v;
 #pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int32_t o = __shfl_up(incl, off);
-        if (lane >= off) incl += o;
-      }
-      if (c < nchunk) hist[e * nchunk + c] = (uint16_t)(run + incl - v);
-      run += __shfl(incl, kWave - 1);
+    for (int w = 0; w < kDispatchWaves; ++w) {
+      const int32_t v = cnt[w * kDispatchMaxExperts + e];
+      cnt[w * kDispatchMaxExperts + e] = run;
+      run += v;
     }
-    if (lane == 0) {
-      total[e] = run;
-      flags[e] = run > 0 ? 1 : 0;
-      ugu[e] = (run + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
-      udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
-      ugm[e] = (run + kUnitTokensGemm - 1) / kUnitTokensGemm;
-    }
+    total[e] = run;
+    flags[e] = run > 0 ? 1 : 0;
+    ugu[e] = (run + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
+    udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
+    ugm[e] = (run + kUnitTokensGemm - 1) / kUnitTokensGemm;
   }
   __syncthreads();
   // total[] becomes the expert offsets, flags[] the active-list positions,
-  // ugu[]/udn[] the first unit of each expert
-  block_exclusive_scan_256(total, n_exp, &sums[0]);
-  __syncthreads();
-  block_exclusive_scan_256(flags, n_exp, &sums[1]);
-  __syncthreads();
-  block_exclusive_scan_256(ugu, n_exp, &sums[2]);
-  __syncthreads();
-  block_exclusive_scan_256(udn, n_exp, &sums[3]);
-  __syncthreads();
-  block_exclusive_scan_256(ugm, n_exp, &sums[4]);
-  __syncthreads();
-  // 3. scatter: position = expert offset + pairs of e in earlier chunks + rank in this chunk
-  for (int c = wave; c < nchunk; c += kDispatchThreads / kWave) {
-    const int p = c * kDispatchChunk + lane;
-    const int e = p < n_pairs ? (int)sid[p] : 0xffff;
-    const bool valid = e < n_exp;
-    const uint64_t peers = wave_peers(valid ? (uint32_t)e : 511u);
-    if (valid) sorted[total[e] + hist[e * nchunk + c] + __popcll(peers & below)] = p;
+  // ugu[]/udn[]/ugm[] the first unit of each expert: one wave per array
+  if (wave == 0) {
+    wave_exclusive_scan_256(total, n_exp, &sums[0], lane);
+    wave_exclusive_scan_256(ugm, n_exp, &sums[4], lane);
+  } else if (wave == 1) {
+    wave_exclusive_scan_256(flags, n_exp, &sums[1], lane);
+  } else if (wave == 2) {
+    wave_exclusive_scan_256(ugu, n_exp, &sums[2], lane);
+  } else {
+    wave_exclusive_scan_256(udn, n_exp, &sums[3], lane);
   }
+  __syncthreads();
+  // 3. scatter
+  for (int p = tid; p < n_pairs; p += kDispatchThreads) {
+    const uint32_t e = sid[p];
+    if (e < (uint32_t)n_exp) {
+      const int w = (p / kDispatchChunk) / cpw;
+      sorted[total[e] + cnt[w * kDispatchMaxExperts + e] + rank[p]] = p;
+    }
+  }
+  // 4. unit lists, all three as one index space, 4 units per thread at a
+  //    time: a unit's expert is the last one whose first unit is <= the
+  //    unit (experts without units share the next one's first unit), found
+  //    by 8 bisection steps run in lockstep
   {
-    // unit lists, one thread per unit: its expert is the last one whose first
-    // unit is <= it (experts without units share the next one's first unit)
-    const int32_t* firsts[3] = {ugu, udn, ugm};
-    int32_t* lists[3] = {units + kUnitHeader, units + units_offset_down(n_pairs, n_exp),
-                         units + units_offset_gemm(n_pairs, n_exp)};
+    const int n_gu = sums[2], n_dn = sums[3], n_all = sums[2] + sums[3] + sums[4];
+    int32_t* const gu_list = units + kUnitHeader;
+    int32_t* const dn_list = units + units_offset_down(n_pairs, n_exp);
+    int32_t* const gm_list = units + units_offset_gemm(n_pairs, n_exp);
+    for (int u0 = tid; u0 < n_all; u0 += 4 * kDispatchThreads) {
+      int lo[4], uu[4], base[4];
+      int32_t* dst[4];
 #pragma unroll
-    for (int l = 0; l < 3; ++l) {
-      const int32_t* first = firsts[l];
-      for (int u = tid; u < sums[2 + l]; u += kDispatchThreads) {
-        int lo = 0, hi = n_exp;  // first[lo] <= u < first[hi] (first[n_exp] taken as +inf)
-        while (hi - lo > 1) {
-          const int mid = (lo + hi) >> 1;
-          if (first[mid] <= u) lo = mid; else hi = mid;
+      for (int i = 0; i < 4; ++i) {
+        const int u = u0 + i * kDispatchThreads;
+        const int l = u < n_gu ? 0 : (u < n_gu + n_dn ? 1 : 2);
+        uu[i] = u - (l == 0 ? 0 : (l == 1 ? n_gu : n_gu + n_dn));
+        base[i] = l * kDispatchMaxExperts;  // ugu, udn, ugm are consecutive
+        dst[i] = l == 0 ? gu_list : (l == 1 ? dn_list : gm_list);
+        lo[i] = 0;
+      }
+#pragma unroll
+      for (int step = kDispatchMaxExperts / 2; step >= 1; step >>= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int cand = lo[i] + step;
+          const int32_t f = ugu[base[i] + min(cand, n_exp - 1)];
+          if (cand < n_exp && f <= uu[i]) lo[i] = cand;
         }
-        lists[l][u] = make_unit(lo, u - first[lo]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int u = u0 + i * kDispatchThreads;
+        if (u < n_all) dst[i][uu[i]] = make_unit(lo[i], uu[i] - ugu[base[i] + lo[i]]);
       }
     }
     if (tid == 0) {
@@ -602,12 +640,9 @@ int check_dispatch_args(int64_t n_pairs, int64_t n_exp) {
               (long long)n_pairs, (long long)n_exp);
   KLC_REQUIRE(n_exp <= kDispatchMaxExperts, KLC_ERR_UNSUPPORTED, "dispatch: n_experts=%lld > %d", (long long)n_exp,
               kDispatchMaxExperts);
-  KLC_REQUIRE(n_pairs < 65536 && (int64_t)dispatch_chunks((int)n_pairs) * n_exp * 2 <= kDispatchMaxHistBytes,
-              KLC_ERR_UNSUPPORTED, "dispatch: n_pairs=%lld too large for %lld experts (ceil(n_pairs / 64) * "
-              "n_experts <= 65536, n_pairs < 65536)", (long long)n_pairs, (long long)n_exp);
-  KLC_REQUIRE(dispatch_lds_bytes((int)n_pairs, (int)n_exp) <= 160 * 1024, KLC_ERR_UNSUPPORTED,
-              "dispatch: n_pairs=%lld with %lld experts needs more than 160 KiB of LDS", (long long)n_pairs,
-              (long long)n_exp);
+  KLC_REQUIRE(n_pairs <= kDispatchMaxPairs, KLC_ERR_UNSUPPORTED,
+              "dispatch: n_pairs=%lld > %d (the pairs' experts and ranks are staged in 160 KiB of LDS)",
+              (long long)n_pairs, kDispatchMaxPairs);
   return KLC_OK;
 }
 

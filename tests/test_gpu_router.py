@@ -93,6 +93,41 @@ def test_dispatch_matches_stable_counting_sort(gpu, n_tok, k, n_exp):
         assert n <= caps[per]
 
 
+def check_dispatch(gpu, ids, n_exp):
+    disp = ops.dispatch(torch.from_numpy(ids).to(gpu), n_exp)
+    torch.cuda.synchronize()
+    counts, w_off, w_order, w_active = orr.dispatch(ids, n_exp)
+    assert np.array_equal(disp.offsets.cpu().numpy(), w_off)
+    assert np.array_equal(disp.sorted_pairs.cpu().numpy(), w_order)
+    assert int(disp.n_active.item()) == len(w_active)
+    u = disp.units.cpu().numpy()
+    n_pairs = ids.size
+    caps = {m: (n_pairs + (m - 1) * min(n_pairs, n_exp)) // m for m in (8, 4, 64)}
+    starts = {8: 4, 4: 4 + caps[8], 64: 4 + caps[8] + caps[4]}
+    for slot, per in enumerate((8, 4, 64)):
+        want = np.concatenate([e | (np.arange(-(-int(counts[e]) // per), dtype=np.int64) << 10)
+                               for e in range(n_exp)])
+        assert int(u[slot]) == want.size
+        assert np.array_equal(u[starts[per]:starts[per] + want.size], want)
+
+
+@pytest.mark.parametrize("n_tok,n_exp", [(2048, 128), (9662, 128), (4001, 256), (5000, 3)])
+def test_dispatch_skewed_loads(gpu, n_tok, n_exp):
+    """Hot experts take most pairs (one expert > 64 pairs per chunk, runs across the waves' chunk ranges);
+    9662 x 4 = 38648 pairs is the largest dispatch the LDS staging holds."""
+    rng = np.random.default_rng(n_tok)
+    hot = rng.random((n_tok, 4))
+    ids = np.where(hot < 0.3, 7 % n_exp, np.where(hot < 0.45, (n_exp - 1), rng.integers(0, n_exp, (n_tok, 4))))
+    check_dispatch(gpu, ids.astype(np.int32), n_exp)
+
+
+def test_dispatch_rejects_too_many_pairs(gpu):
+    from klcquant_amd._native import KlcError
+    ids = torch.zeros((38649,), dtype=torch.int32, device=gpu)
+    with pytest.raises(KlcError, match="n_pairs"):
+        ops.dispatch(ids.view(-1, 1), 128)
+
+
 def test_router_rejects_bad_shapes(gpu):
     x = torch.zeros((2, 64), dtype=torch.bfloat16, device=gpu)
     w = torch.zeros((8, 32), dtype=torch.bfloat16, device=gpu)
