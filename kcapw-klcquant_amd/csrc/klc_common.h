@@ -135,6 +135,16 @@ __device__ __forceinline__ float2 fp4x2_to_f32(uint32_t word) {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Raw buffer descriptor word 3 for gfx9-family buffer loads (32-bit data, no swizzle).
+constexpr int kBufferWord3 = 0x00020000;
+// A per-lane buffer offset (VGPR voffset) past every buffer: such raw-buffer
+// loads are out of range, return 0 and touch no memory, without a branch.
+// Only voffset is ever set to it; the uniform soffset always stays a valid
+// in-buffer offset, so the sum cannot wrap (buffers are far below 1 GiB).
+constexpr uint32_t kOutOfRange = 0x40000000u;
 
 // Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
 __device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {

@@ -25,10 +25,12 @@ int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, 
                 int64_t k, hipStream_t stream);
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
                     int32_t* active, int32_t* n_active, int32_t* units, hipStream_t stream);
-int launch_router_fused(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
-                        int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
-                        int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* done,
-                        hipStream_t stream);
+int launch_router_decode(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
+                         int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
+                         int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* counters,
+                         double* partials, hipStream_t stream);
+int64_t decode_router_counters(int64_t n_tok, int64_t n_exp);
+int64_t decode_router_partial_bytes(int64_t n_tok, int64_t hidden, int64_t n_exp);
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp);
 int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k,
                         int64_t n_exp, const int32_t* offsets, const int32_t* pairs, const int32_t* units,
@@ -48,15 +50,6 @@ constexpr int kVRows = 8;                     // activation rows (MFMA N columns
 constexpr int kMaxSteps = 24;                 // 4-group steps per row (inputs <= 3072)
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-// Raw buffer descriptor word 3 for gfx9-family buffer loads (32-bit data, no swizzle).
-constexpr int kBufferWord3 = 0x00020000;
-// A per-lane buffer offset (VGPR voffset) past every matrix: such raw-buffer
-// loads are out of range, return 0 and touch no memory.  Only voffset is ever
-// set to it; the uniform soffset always stays a valid in-matrix offset, so the
-// sum cannot wrap (matrices are far below 1 GiB).
-constexpr uint32_t kOutOfRange = 0x40000000u;
 
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
@@ -137,7 +130,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   const int g4 = (groups + 3) >> 2;
   const uint32_t voff = (uint32_t)(lq * 1024 + trow * 16);
   const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;  // step g4 - 1
-  auto chunk = [&](uint32_t tile_off, int t, bool valid) -> u32x4 {
+  auto chunk = [&](uint32_t tile_off, int t, bool valid) -> u32x4_t {
     const uint32_t v = !valid || t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
     return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, 0);
   };
@@ -158,7 +151,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
         src[r] = pairs[pb + tc + rr] / k_top;
       }
     }
-    u32x4 xv[kLoads];
+    u32x4_t xv[kLoads];
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int id = min((int)threadIdx.x + i * kGemvThreads, nrows * cpr - 1);
@@ -168,7 +161,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
 #pragma unroll
       for (int q = 1; q < kVRows; ++q) srow = r == q ? src[q] : srow;
       const uint16_t* p = act + (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim + c * 8;
-      xv[i] = *reinterpret_cast<const u32x4*>(p);
+      xv[i] = *reinterpret_cast<const u32x4_t*>(p);
     }
 
     // ---- 2. scale record of the first tile, then the ring prologue ----
@@ -178,7 +171,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       const uint32_t soff = scale_base + (uint32_t)(tile * kTileRows * 4 * rec);
 #pragma unroll
       for (int i = 0; i < kRecWords / 2; ++i) {
-        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, rec_voff + 8u * min(i, rec / 8 - 1), soff, 0);
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, rec_voff + 8u * min(i, rec / 8 - 1), soff, 0);
         dst[2 * i] = v.x;
         dst[2 * i + 1] = v.y;
       }
@@ -186,7 +179,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
     uint32_t sc[kRecWords], sc_next[kRecWords];
     load_rec(tile0, sc);
     uint32_t tb = (uint32_t)tile0 * tile_bytes;
-    u32x4 ring[kR];
+    u32x4_t ring[kR];
 #pragma unroll
     for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
 
@@ -198,7 +191,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       const int c = id - r * cpr;
       // ids past the staged rows land in row 0's spare 16-byte slot, which nothing reads
       const int dst = id < nrows * cpr ? r * row_stride + c * 8 : row_stride - 8;
-      *reinterpret_cast<u32x4*>(xs + dst) = xv[i];
+      *reinterpret_cast<u32x4_t*>(xs + dst) = xv[i];
     }
     {
       const int pad = kSteps * 128 - in_dim;  // zero: its A operand is zero, keep 0 * pad finite
@@ -239,7 +232,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
         // here, so decoded operands (16 registers per step) are never
         // computed early and kept live across steps
         asm volatile("" : "+v"(ring[s % kR]));
-        const u32x4 w = ring[s % kR];
+        const u32x4_t w = ring[s % kR];
         {
           const int t = s + kR;  // refill: kR steps ahead
           ring[s % kR] = t < kSteps ? chunk(tb, t, true) : chunk(nb, t - kSteps, has_next);
@@ -486,7 +479,10 @@ int launch_combine(const float* eo, const void* w, const void* residual, int64_t
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
-constexpr int64_t kFusedRouterTokens = 2;  // batches up to this size use the one-launch router
+// Batches up to this size route in one launch (router_decode_kernel); its
+// completion counters live in the workspace's first kCounterBytes.
+constexpr int64_t kDecodeRouterTokens = 128;
+constexpr int64_t kCounterBytes = 1024;
 
 // The grouped GEMM pays off once experts see several MFMA column blocks of
 // tokens; below about 8 tokens per expert the GEMV streams the same weights
@@ -494,14 +490,15 @@ constexpr int64_t kFusedRouterTokens = 2;  // batches up to this size use the on
 bool use_gemm_path(int64_t n_pairs, int64_t n_exp) { return n_pairs >= 8 * n_exp; }
 
 struct LayerScratch {
-  int64_t counters, logits, ids, values, weights, offsets, sorted, active, n_active, units, gated, eo, total;
+  int64_t counters, partials, logits, ids, values, weights, offsets, sorted, active, n_active, units, gated, eo, total;
 };
 
 LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k) {
   LayerScratch s{};
   const int64_t pairs = n_tok * k;
   int64_t off = 0;
-  s.counters = off; off += 256;  // self-resetting completion counters (zero before first use)
+  s.counters = off; off += kCounterBytes;  // self-resetting completion counters (zero before first use)
+  s.partials = off; off += align256(n_tok <= kDecodeRouterTokens ? decode_router_partial_bytes(n_tok, hidden, n_exp) : 0);
   s.logits = off;   off += align256(n_tok * n_exp * 2);
   s.ids = off;      off += align256(pairs * 4);
   s.values = off;   off += align256(pairs * 4);
@@ -636,10 +633,14 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   };
 
   if ((rc = mark(0))) return rc;
-  if (n_tokens <= kFusedRouterTokens) {
+  if (n_tokens <= kDecodeRouterTokens) {
     // decode batches: logits, top-k and dispatch in one launch
-    if ((rc = launch_router_fused(x, router_w, router_b, logits, n_tokens, hidden, n_experts, k, ids_buf, values,
-                                  w_buf, offsets, sorted, active, n_active, units, counters, st)))
+    KLC_REQUIRE(decode_router_counters(n_tokens, n_experts) * 4 <= kCounterBytes, KLC_ERR_UNSUPPORTED,
+                "klc_moe_layer: %lld experts need more completion counters than the workspace holds",
+                (long long)n_experts);
+    if ((rc = launch_router_decode(x, router_w, router_b, logits, n_tokens, hidden, n_experts, k, ids_buf, values,
+                                   w_buf, offsets, sorted, active, n_active, units, counters,
+                                   reinterpret_cast<double*>(ws + s.partials), st)))
       return rc;
     if ((rc = mark(1))) return rc;
     if ((rc = mark(2))) return rc;

@@ -30,7 +30,6 @@
 namespace klc {
 namespace {
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmThreads = 256;
@@ -40,9 +39,7 @@ constexpr int kGemmCb = kUnitTokensGemm / 16;       // 8 column blocks of 16 tok
 constexpr int kRowBytes = 128 * 2 + 16;             // one token's 128 bfloat16 of a step, padded (bank spread)
 constexpr int kPlaneBytes = kUnitTokensGemm * kRowBytes;
 constexpr int kPieces = kUnitTokensGemm * 16 / kGemmThreads;  // 16-byte pieces per thread per plane and step
-constexpr int kBufferWord3 = 0x00020000;
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
-constexpr uint32_t kOutOfRange = 0x40000000u;
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
   // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp

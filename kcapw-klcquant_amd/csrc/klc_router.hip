@@ -1,10 +1,9 @@
 // Router logits, top-k + softmax, and expert-sorted dispatch (gfx950).
 //
-// Logits: one wave per (expert, block of 8 tokens).  Lanes stride the hidden
-// dimension with 16-byte loads; each bfloat16 product is exact in float32 and
-// is accumulated in float64, so the only roundings are the reference's own:
-// float32 of the dot product, float32 bias add, bfloat16 result
-// (streamed_moe_router.py:269).
+// Logits: float64 MFMA tiles of 16 experts x 16 tokens.  Each bfloat16
+// product is exact in float64 and the sums are float64, so the only roundings
+// are the reference's own: float32 of the dot product, float32 bias add,
+// bfloat16 result (streamed_moe_router.py:269).
 //
 // Top-k: one wave per token.  Each logit becomes a 64-bit key (ordered value
 // bits, then inverted expert index), so a wave-wide max picks the largest
@@ -13,161 +12,97 @@
 // float64 and rounded to float32, then to bfloat16.
 //
 // Dispatch: one workgroup performs a stable counting sort of the (token, slot)
-// pairs by expert: per-64-pair-chunk histograms from wave ballots, an
-// exclusive scan over chunks and experts, then an in-order scatter.
+// pairs by expert: ranks from wave ballots and per-wave running counts, a
+// per-expert prefix over the waves, then a scatter.
+//
+// Decode batches run all three in one launch (router_decode_kernel): the
+// logits tiles are split along the hidden dimension over many workgroups and
+// the last workgroup to finish each step (counted in self-resetting
+// counters) goes on to the next one.
+#include <algorithm>
+
 #include "klc_common.h"
 
 namespace klc {
 namespace {
 
-constexpr int kRouterTok = 8;     // tokens per workgroup
-constexpr int kRouterChunks = 8;  // 16-byte weight chunks per lane: hidden <= 64 * 8 * 8 = 4096
-
-// One wave per (expert, block of up to 8 tokens).  The workgroup stages the
-// block's hidden rows in LDS; every lane first issues all of its weight-row
-// loads, then accumulates float64 sums of exact float32 products per token.
-__device__ void router_logits_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                   const uint16_t* __restrict__ b, uint16_t* logits, float* __restrict__ x_f32,
-                                   int n_tok, int hidden, int n_exp, uint16_t* xs /* LDS [kRouterTok][hidden] */) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int t0 = blockIdx.y * kRouterTok;
-  const int nt = min(kRouterTok, n_tok - t0);
-  const int e = blockIdx.x * 4 + wave;
-  const int nchunk = hidden >> 3;  // hidden % 8 == 0 (checked on the host)
-
-  // every load is unconditional (indices clamped into range, surplus values
-  // discarded) so all of a lane's loads are in flight together
-  uint4 wv[kRouterChunks];
-  {
-    const uint16_t* wr = w + (int64_t)min(e, n_exp - 1) * hidden;
-#pragma unroll
-    for (int i = 0; i < kRouterChunks; ++i) {
-      const int c = lane + i * kWave;
-      const uint4 v = *reinterpret_cast<const uint4*>(wr + min(c, nchunk - 1) * 8);
-      wv[i] = c < nchunk ? v : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-  const int64_t base = (int64_t)t0 * hidden;
-  const int n_stage = nt * nchunk;
-  constexpr int kStage = kRouterTok * kWave * kRouterChunks / 256;  // chunks per thread (blockDim.x == 256)
-  uint4 xv[kStage];
-#pragma unroll
-  for (int j = 0; j < kStage; ++j) {
-    const int i = min((int)threadIdx.x + j * 256, n_stage - 1);
-    xv[j] = *reinterpret_cast<const uint4*>(x + base + (int64_t)i * 8);
-  }
-#pragma unroll
-  for (int j = 0; j < kStage; ++j) {
-    const int i = (int)threadIdx.x + j * 256;
-    if (i < n_stage) {
-      const uint4 v = xv[j];
-      *reinterpret_cast<uint4*>(xs + i * 8) = v;
-      if (x_f32 != nullptr && blockIdx.x == 0) {
-        const uint32_t words[4] = {v.x, v.y, v.z, v.w};
-        float4* dst = reinterpret_cast<float4*>(x_f32 + base + (int64_t)i * 8);
-        dst[0] = make_float4(__uint_as_float(words[0] << 16), __uint_as_float(words[0] & 0xffff0000u),
-                             __uint_as_float(words[1] << 16), __uint_as_float(words[1] & 0xffff0000u));
-        dst[1] = make_float4(__uint_as_float(words[2] << 16), __uint_as_float(words[2] & 0xffff0000u),
-                             __uint_as_float(words[3] << 16), __uint_as_float(words[3] & 0xffff0000u));
-      }
-    }
-  }
-  __syncthreads();
-  if (e >= n_exp) return;  // the caller synchronises the block only after this function
-
-  double acc[kRouterTok];
-#pragma unroll
-  for (int j = 0; j < kRouterTok; ++j) {
-    acc[j] = 0.0;
-    if (j < nt) {
-      double s = 0.0;
-#pragma unroll
-      for (int i = 0; i < kRouterChunks; ++i) {
-        const int c = lane + i * kWave;
-        if (c < nchunk) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(xs + j * hidden + c * 8);
-          const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-          const uint32_t ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            s += (double)(__uint_as_float(xw[q] << 16) * __uint_as_float(ww[q] << 16));
-            s += (double)(__uint_as_float(xw[q] & 0xffff0000u) * __uint_as_float(ww[q] & 0xffff0000u));
-          }
-        }
-      }
-      acc[j] = s;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < kRouterTok; ++j) {
-    if (j < nt) {
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) acc[j] += __shfl_xor(acc[j], off);
-    }
-  }
-  if (lane < nt) {
-    double mine = 0.0;
-#pragma unroll
-    for (int j = 0; j < kRouterTok; ++j)
-      if (j == lane) mine = acc[j];
-    logits[(int64_t)(t0 + lane) * n_exp + e] = (uint16_t)f32_to_bf16_rne((float)mine + bf16_to_f32(b[e]));
-  }
-}
-
-// Logits on the float64 matrix cores: one workgroup per tile of 16 experts x
-// 16 tokens, its 4 waves splitting the hidden dimension into quarters.  Per
-// 32-deep chunk lane l loads 8 consecutive weights of expert row l % 16 and
-// 8 hidden values of token l % 16 (k = 32 c + 8 (l / 16) + i), converts them
-// to float64 (bfloat16 products are exact in float64) and issues 8
-// v_mfma_f64_16x16x4_f64 (A lane l = row l % 16, k = l / 16; B lane l =
-// column l % 16, same k; D lane l register i = row l / 16 + 4 i, column
-// l % 16), alternating two accumulators.  The quarters are summed through LDS
-// in wave order, then rounded like F.linear in bfloat16: bf16(f32(sum) + b).
+constexpr int kRouterTile = 16;    // experts and tokens per logits tile
+constexpr int kRouterDepth = 4;    // 32-deep chunks per lane in flight
+constexpr int kRouterMaxSlices = 8;  // hidden-dimension slices of the decode router
+#ifndef KLC_DECODE_ROUTER_WORKGROUPS
+#define KLC_DECODE_ROUTER_WORKGROUPS 128
+#endif
+constexpr int kDecodeRouterWorkgroups = KLC_DECODE_ROUTER_WORKGROUPS;  // target grid size of the decode router
 typedef double f64x4_t __attribute__((ext_vector_type(4)));
-constexpr int kRouterMfmaRows = 16;
 
-__device__ void router_logits_mfma_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                        const uint16_t* __restrict__ b, uint16_t* logits, float* __restrict__ x_f32,
-                                        int n_tok, int hidden, int n_exp, int e0, int t0,
-                                        double* red /* LDS [3][64][4] */) {
+// Partial logits of the tile (experts e0.., tokens t0..) over the 32-deep
+// hidden chunks [c_begin, c_end), by the 4 waves of the workgroup, each on a
+// quarter of the range.  Per chunk lane l holds 8 consecutive weights of
+// expert row l % 16 and 8 hidden values of token l % 16 (k = 32 c + 8 (l / 16)
+// + i), converted to float64, and issues 8 v_mfma_f64_16x16x4_f64 (A lane l
+// = row l % 16, k = l / 16; B lane l = column l % 16, same k; D lane l
+// register i = row l / 16 + 4 i, column l % 16) on two accumulators.  The
+// rows are read as raw buffers (the tile's rows, the chunk in the uniform
+// offset): chunks or rows outside the matrices load zeros without a branch,
+// so the loads of the next kRouterDepth chunks stay in flight while the
+// current ones multiply.  The waves' sums are added through LDS in wave
+// order; the result is valid in wave 0.  x_f32, when given, receives the
+// float32 copy of the hidden rows the tile reads.
+__device__ f64x4_t router_block_dot(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int n_tok,
+                                    int hidden, int n_exp, int e0, int t0, int c_begin, int c_end,
+                                    float* __restrict__ x_f32, double* red /* LDS [3][64][4] */) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int nchunk = (hidden + 31) >> 5;
-  const int per = (nchunk + 3) >> 2;
-  const int c0 = wave * per;
-  const int c1 = min(c0 + per, nchunk);
-  const uint16_t* wrow = w + (int64_t)min(e0 + r, n_exp - 1) * hidden;
+  const int per = (c_end - c_begin + 3) >> 2;
+  const int c0 = min(c_begin + wave * per, c_end);
+  const int c1 = min(c0 + per, c_end);
   const int tok = t0 + r;
-  const uint16_t* xrow = x + (int64_t)min(tok, n_tok - 1) * hidden;
+  const int row_bytes = hidden * 2;
+  const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + (int64_t)e0 * hidden), (short)0, min(kRouterTile, n_exp - e0) * row_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t xbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(x + (int64_t)t0 * hidden), (short)0, min(kRouterTile, n_tok - t0) * row_bytes, kBufferWord3);
+  const uint32_t lane_off = (uint32_t)(r * row_bytes + g * 16);
+  const bool w_ok = e0 + r < n_exp;
+  const bool x_ok = tok < n_tok;
   f64x4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
-  for (int c = c0; c < c1; ++c) {
-    const int k = c * 32 + g * 8;
-    const bool ok = k < hidden;  // hidden % 8 == 0: a lane's 8 values are all in or all out
-    const int kc = ok ? k : 0;
-    uint4 wv = *reinterpret_cast<const uint4*>(wrow + kc);
-    uint4 xv = *reinterpret_cast<const uint4*>(xrow + kc);
-    if (!ok) {
-      wv = make_uint4(0u, 0u, 0u, 0u);
-      xv = make_uint4(0u, 0u, 0u, 0u);
-    }
-    if (x_f32 != nullptr && e0 == 0 && ok && tok < n_tok) {
-      float4* dst = reinterpret_cast<float4*>(x_f32 + (int64_t)tok * hidden + k);
-      dst[0] = make_float4(__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
-                           __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u));
-      dst[1] = make_float4(__uint_as_float(xv.z << 16), __uint_as_float(xv.z & 0xffff0000u),
-                           __uint_as_float(xv.w << 16), __uint_as_float(xv.w & 0xffff0000u));
-    }
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+  auto load = [&](int c, u32x4_t (&wv)[kRouterDepth], u32x4_t (&xv)[kRouterDepth]) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)__uint_as_float(ww[q] << 16),
-                                                   (double)__uint_as_float(xw[q] << 16), acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)__uint_as_float(ww[q] & 0xffff0000u),
-                                                   (double)__uint_as_float(xw[q] & 0xffff0000u), acc1, 0, 0, 0);
+    for (int i = 0; i < kRouterDepth; ++i) {
+      // hidden % 8 == 0: a lane's 8 values are all inside the row or all past it
+      const bool ok = c + i < c1 && (c + i) * 32 + g * 8 < hidden;
+      wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, ok && w_ok ? lane_off : kOutOfRange, (c + i) * 64, 0);
+      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xbuf, ok && x_ok ? lane_off : kOutOfRange, (c + i) * 64, 0);
+    }
+  };
+  u32x4_t wa[kRouterDepth], xa[kRouterDepth];
+  load(c0, wa, xa);
+  for (int c = c0; c < c1; c += kRouterDepth) {
+    u32x4_t wb[kRouterDepth], xb[kRouterDepth];
+    load(c + kRouterDepth, wb, xb);
+#pragma unroll
+    for (int i = 0; i < kRouterDepth; ++i) {
+      if (x_f32 != nullptr && x_ok && c + i < c1 && (c + i) * 32 + g * 8 < hidden) {
+        float4* dst = reinterpret_cast<float4*>(x_f32 + (int64_t)tok * hidden + (c + i) * 32 + g * 8);
+        dst[0] = make_float4(__uint_as_float(xa[i].x << 16), __uint_as_float(xa[i].x & 0xffff0000u),
+                             __uint_as_float(xa[i].y << 16), __uint_as_float(xa[i].y & 0xffff0000u));
+        dst[1] = make_float4(__uint_as_float(xa[i].z << 16), __uint_as_float(xa[i].z & 0xffff0000u),
+                             __uint_as_float(xa[i].w << 16), __uint_as_float(xa[i].w & 0xffff0000u));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)__uint_as_float(wa[i][q] << 16),
+                                                     (double)__uint_as_float(xa[i][q] << 16), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)__uint_as_float(wa[i][q] & 0xffff0000u),
+                                                     (double)__uint_as_float(xa[i][q] & 0xffff0000u), acc1, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRouterDepth; ++i) {
+      wa[i] = wb[i];
+      xa[i] = xb[i];
     }
   }
   f64x4_t acc = acc0 + acc1;
@@ -181,13 +116,25 @@ __device__ void router_logits_mfma_tile(const uint16_t* __restrict__ x, const ui
     for (int q = 0; q < 3; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] += red[(q * 64 + lane) * 4 + i];
-    if (tok < n_tok) {
+  }
+  return acc;
+}
+
+// The calling wave rounds a tile's sums (its lanes holding them in the MFMA
+// D layout) like F.linear in bfloat16: bf16(f32(sum) + b).  Optionally also
+// into an LDS copy [16 tokens][n_exp] of the token tile's logits.
+__device__ void router_tile_store(f64x4_t acc, const uint16_t* __restrict__ b, uint16_t* logits, int n_tok,
+                                  int n_exp, int e0, int t0, uint16_t* lds_rows = nullptr) {
+  const int lane = threadIdx.x & 63;
+  const int tok = t0 + (lane & 15);
+  if (tok >= n_tok) return;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = e0 + g + 4 * i;
-        if (e < n_exp)
-          logits[(int64_t)tok * n_exp + e] = (uint16_t)f32_to_bf16_rne((float)acc[i] + bf16_to_f32(b[e]));
-      }
+  for (int i = 0; i < 4; ++i) {
+    const int e = e0 + (lane >> 4) + 4 * i;
+    if (e < n_exp) {
+      const uint16_t v = (uint16_t)f32_to_bf16_rne((float)acc[i] + bf16_to_f32(b[e]));
+      logits[(int64_t)tok * n_exp + e] = v;
+      if (lds_rows != nullptr) lds_rows[(lane & 15) * n_exp + e] = v;
     }
   }
 }
@@ -199,8 +146,11 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t*
                                                                  float* __restrict__ x_f32, int n_tok, int hidden,
                                                                  int n_exp) {
   __shared__ double red[3 * 64 * 4];
-  router_logits_mfma_tile(x, w, b, logits, x_f32, n_tok, hidden, n_exp, blockIdx.x * kRouterMfmaRows,
-                          blockIdx.y * kRouterMfmaRows, red);
+  const int e0 = blockIdx.x * kRouterTile;
+  const int t0 = blockIdx.y * kRouterTile;
+  const f64x4_t acc = router_block_dot(x, w, n_tok, hidden, n_exp, e0, t0, 0, (hidden + 31) >> 5,
+                                       blockIdx.x == 0 ? x_f32 : nullptr, red);
+  if (threadIdx.x < kWave) router_tile_store(acc, b, logits, n_tok, n_exp, e0, t0);
 }
 
 // Orderable key: larger key = larger logit; NaN is the largest value; -0 == +0;
@@ -219,52 +169,93 @@ __device__ __forceinline__ uint64_t logit_key(uint32_t bf16bits, int idx) {
 
 constexpr int kTopkMaxPerLane = 16;  // n_experts <= 1024
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t o = __shfl_xor(v, off);
-    v = o > v ? o : v;
-  }
-  return v;
+// Cross-lane steps on the DPP network (VALU, no LDS round trip).  Lanes whose
+// source is outside the row or masked off keep `old`.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, kCtrl, kRowMask, 0xf, false);
+}
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint64_t dpp_max_step(uint64_t v) {
+  const uint32_t lo = dpp_u32<kCtrl, kRowMask>((uint32_t)v, (uint32_t)v);
+  const uint32_t hi = dpp_u32<kCtrl, kRowMask>((uint32_t)(v >> 32), (uint32_t)(v >> 32));
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o > v ? o : v;
 }
 
-// Top-k + softmax of one token's logits row by one wave.
-__device__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t, int32_t* __restrict__ ids,
-                                 float* __restrict__ values, uint16_t* __restrict__ weights) {
+// Wave-wide maximum of a 64-bit key, returned to every lane: quad swaps,
+// half-row and row mirrors make every row hold its maximum, two row
+// broadcasts carry it into row 3, and lane 63 is read back.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = dpp_max_step<0xB1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_max_step<0x4E, 0xf>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_max_step<0x140, 0xf>(v);  // row_mirror
+  v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Top-k + softmax of one token's logits row by one wave, kSlots keys per lane.
+template <int kSlots>
+__device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_exp, int k, int64_t t,
+                                                   int32_t* __restrict__ ids, float* __restrict__ values,
+                                                   uint16_t* __restrict__ weights) {
   const int lane = threadIdx.x & 63;
-  uint64_t keys[kTopkMaxPerLane];
+  uint64_t keys[kSlots];
 #pragma unroll
-  for (int s = 0; s < kTopkMaxPerLane; ++s) {
+  for (int s = 0; s < kSlots; ++s) {
     const int idx = lane + s * kWave;
-    keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;
+    keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
   }
   // lane r keeps the r-th selection
   int my_id = 0;
   float my_val = 0.0f;
   for (int r = 0; r < k; ++r) {
-    uint64_t best = 0ull;
+    uint64_t best = keys[0];
 #pragma unroll
-    for (int s = 0; s < kTopkMaxPerLane; ++s) best = keys[s] > best ? keys[s] : best;
+    for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
     best = wave_max_u64(best);
 #pragma unroll
-    for (int s = 0; s < kTopkMaxPerLane; ++s)
+    for (int s = 0; s < kSlots; ++s)
       if (keys[s] == best) keys[s] = 0ull;
     if (lane == r) {
       my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
       my_val = bf16_to_f32(row[my_id]);
     }
   }
-  // softmax over the k values: max is the first selection (NaN propagates),
-  // exponentials summed in selection order, all in float64
-  const double mx = (double)__shfl(my_val, 0);
+  // softmax over the k values: max is the first selection (NaN propagates);
+  // lane r evaluates exp(v_r - max) in float64, the sum runs in selection order
+  const double mx = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), 0));
+  const double ex = lane < k ? exp((double)my_val - mx) : 0.0;
   double sum = 0.0;
-  for (int r = 0; r < k; ++r) sum += exp((double)__shfl(my_val, r) - mx);
+  for (int r = 0; r < k; ++r) sum += readlane_f64(ex, r);
   if (lane < k) {
     const int64_t o = t * k + lane;
     ids[o] = my_id;
     if (values) values[o] = my_val;
-    weights[o] = (uint16_t)f32_to_bf16_rne((float)(exp((double)my_val - mx) / sum));
+    weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
   }
+}
+
+__device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t,
+                                                 int32_t* __restrict__ ids, float* __restrict__ values,
+                                                 uint16_t* __restrict__ weights) {
+  const int slots = (n_exp + kWave - 1) / kWave;  // <= kTopkMaxPerLane (checked on the host)
+  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, ids, values, weights);
+  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, ids, values, weights);
+  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, ids, values, weights);
+  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, ids, values, weights);
+  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights);
 }
 
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
@@ -298,9 +289,22 @@ __global__ __launch_bounds__(256) void softmax_weights_kernel(const float* __res
 constexpr int kDispatchThreads = 256;
 constexpr int kDispatchMaxExperts = 256;
 
+// Inclusive prefix sum over the wave on the DPP network: shifts by 1, 2, 4
+// and 8 within each 16-lane row, then two row broadcasts.
+__device__ __forceinline__ int32_t wave_inclusive_scan(int32_t v) {
+  uint32_t s = (uint32_t)v;
+  s += dpp_u32<0x111, 0xf>(0u, s);  // row_shr:1
+  s += dpp_u32<0x112, 0xf>(0u, s);  // row_shr:2
+  s += dpp_u32<0x114, 0xf>(0u, s);  // row_shr:4
+  s += dpp_u32<0x118, 0xf>(0u, s);  // row_shr:8
+  s += dpp_u32<0x142, 0xa>(0u, s);  // row_bcast:15 into rows 1 and 3
+  s += dpp_u32<0x143, 0xc>(0u, s);  // row_bcast:31 into rows 2 and 3
+  return (int32_t)s;
+}
+
 // Exclusive prefix sum of LDS array `v[n]` (n <= 256) by the calling wave;
 // total written to *total.  4 entries per lane.
-__device__ void wave_exclusive_scan_256(int32_t* v, int n, int32_t* total, int lane) {
+__device__ __forceinline__ void wave_exclusive_scan_256(int32_t* v, int n, int32_t* total, int lane) {
   int32_t local[4];
   int32_t s = 0;
 #pragma unroll
@@ -309,12 +313,7 @@ __device__ void wave_exclusive_scan_256(int32_t* v, int n, int32_t* total, int l
     local[i] = idx < n ? v[idx] : 0;
     s += local[i];
   }
-  int32_t incl = s;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int32_t o = __shfl_up(incl, off);
-    if (lane >= off) incl += o;
-  }
+  const int32_t incl = wave_inclusive_scan(s);
   int32_t run = incl - s;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -370,7 +369,7 @@ __device__ __forceinline__ void wave_peers(const uint32_t (&key)[N], uint64_t (&
 // its wave's chunks (ballots within a chunk, a per-wave running count across
 // chunks), so no step is serial over pairs.  lds holds
 // dispatch_lds_bytes(n_pairs, n_exp) bytes.
-__device__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
+__device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
                                int32_t* __restrict__ sorted, int32_t* __restrict__ active,
                                int32_t* __restrict__ n_active, int32_t* __restrict__ units, char* lds) {
   const int tid = threadIdx.x;
@@ -533,51 +532,105 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
   block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
 }
 
-// Router for decode batches in one launch: every workgroup computes its
-// (4 experts x 8 tokens) logits tile; the last workgroup to finish (counted
-// in *done, which it resets to 0) then selects the top-k of every token and
-// builds the expert-sorted dispatch.  Release/acquire fences at agent scope
-// make the other workgroups' logits visible across XCDs.
-__global__ __launch_bounds__(256) void router_fused_kernel(const uint16_t* __restrict__ x,
-                                                           const uint16_t* __restrict__ w,
-                                                           const uint16_t* __restrict__ b, uint16_t* logits,
-                                                           int n_tok, int hidden, int n_exp, int k, int32_t* ids,
-                                                           float* __restrict__ values, uint16_t* __restrict__ weights,
-                                                           int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
-                                                           int32_t* __restrict__ active,
-                                                           int32_t* __restrict__ n_active, int32_t* __restrict__ units,
-                                                           uint32_t* done) {
-  extern __shared__ char flds[];
-  router_logits_tile(x, w, b, logits, nullptr, n_tok, hidden, n_exp, reinterpret_cast<uint16_t*>(flds));
-  __shared__ uint32_t last;
+// Last-arriver election among `expected` workgroups on *ctr.  Every wave
+// first waits for its own stores to reach L2; thread 0 then releases them at
+// device scope (L2 write-back), counts the arrival, and in the last workgroup
+// resets the counter (for the next launch) and acquires the others' writes
+// (L2 and L1 invalidation, shared by the workgroup's waves on this CU).
+// Returns the same value in every thread.
+__device__ bool arrive_last(uint32_t* ctr, uint32_t expected, uint32_t* flag) {
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     __threadfence();
-    const uint32_t n_blocks = gridDim.x * gridDim.y;
-    const uint32_t prev = atomicAdd(done, 1u);
-    last = prev == n_blocks - 1 ? 1u : 0u;
+    const uint32_t prev = atomicAdd(ctr, 1u);
+    const uint32_t last = prev == expected - 1u ? 1u : 0u;
     if (last) {
-      *done = 0u;  // ready for the next launch
+      atomicExch(ctr, 0u);
       __threadfence();
     }
+    *flag = last;
   }
   __syncthreads();
-  if (!last) return;
-  for (int t = threadIdx.x >> 6; t < n_tok; t += 4) {
-    const uint16_t* row = logits + (int64_t)t * n_exp;
-    topk_softmax_row(row, n_exp, k, t, ids, values, weights);
+  return *flag != 0u;
+}
+
+// Router of a decode batch in one launch.  Workgroup (et, tt, ks) computes
+// the partial logits of the tile (experts 16 et.., tokens 16 tt..) over the
+// ks-th of gridDim.z slices of the hidden dimension and stores them.  The
+// last of a token tile's workgroups to arrive (counted in a self-resetting
+// counter) sums every expert tile's slices in slice order (a fixed order, so
+// the result does not depend on which workgroup is last), rounds the logits,
+// and selects the top-k + softmax of the tile's tokens from an LDS copy.
+// With one token tile it then builds the expert-sorted dispatch itself;
+// otherwise the last token tile to finish does.
+// counters: [n_tt] token-tile counters and 1 final counter, zero before the
+// first launch and left zero by every launch.  partials: [n_tt][n_et]
+// [gridDim.z][256] float64.
+__global__ __launch_bounds__(256) void router_decode_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b, uint16_t* logits,
+    int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted, int32_t* __restrict__ active,
+    int32_t* __restrict__ n_active, int32_t* __restrict__ units, uint32_t* counters, double* partials) {
+  extern __shared__ char lds[];  // wave sums; then the token tile's logits; then the dispatch's staging
+  __shared__ uint32_t flag;
+  const int et = blockIdx.x, tt = blockIdx.y, ks = blockIdx.z;
+  const int n_et = gridDim.x, n_tt = gridDim.y, n_ks = gridDim.z;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int t0 = tt * kRouterTile;
+  const int nchunk = (hidden + 31) >> 5;
+  const int per_slice = (nchunk + n_ks - 1) / n_ks;
+  const int cb = min(ks * per_slice, nchunk);
+  const int ce = min(cb + per_slice, nchunk);
+  const f64x4_t part =
+      router_block_dot(x, w, n_tok, hidden, n_exp, et * kRouterTile, t0, cb, ce, nullptr, reinterpret_cast<double*>(lds));
+  double* tile_parts = partials + (int64_t)tt * n_et * n_ks * 256;  // [n_et][n_ks][256]
+  if (threadIdx.x < kWave) {
+    double* slot = tile_parts + ((int64_t)et * n_ks + ks) * 256 + lane * 4;
+    reinterpret_cast<double2*>(slot)[0] = make_double2(part[0], part[1]);
+    reinterpret_cast<double2*>(slot)[1] = make_double2(part[2], part[3]);
   }
-  __threadfence_block();
+  if (!arrive_last(counters + tt, (uint32_t)(n_et * n_ks), &flag)) return;
+  // sums: wave w takes expert tiles w, w + 4, ..., all slices' loads in flight
+  uint16_t* rows = reinterpret_cast<uint16_t*>(lds);  // [16][n_exp]
+  for (int e_t = wave; e_t < n_et; e_t += 4) {
+    const double* src = tile_parts + (int64_t)e_t * n_ks * 256 + lane * 4;
+    double2 v[2 * kRouterMaxSlices];
+#pragma unroll
+    for (int q = 0; q < kRouterMaxSlices; ++q) {
+      const int qq = min(q, n_ks - 1);
+      v[2 * q] = reinterpret_cast<const double2*>(src + qq * 256)[0];
+      v[2 * q + 1] = reinterpret_cast<const double2*>(src + qq * 256)[1];
+    }
+    f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int q = 0; q < kRouterMaxSlices; ++q) {
+      if (q < n_ks) {
+        acc[0] += v[2 * q].x;
+        acc[1] += v[2 * q].y;
+        acc[2] += v[2 * q + 1].x;
+        acc[3] += v[2 * q + 1].y;
+      }
+    }
+    router_tile_store(acc, b, logits, n_tok, n_exp, e_t * kRouterTile, t0, rows);
+  }
   __syncthreads();
-  block_dispatch(ids, n_tok * k, n_exp, offsets, sorted, active, n_active, units, flds);
+  for (int t = t0 + wave; t < min(t0 + kRouterTile, n_tok); t += 4)
+    topk_softmax_row(rows + (t - t0) * n_exp, n_exp, k, t, ids, values, weights);
+  if (n_tt > 1) {
+    if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;
+  } else {
+    __syncthreads();
+  }
+  block_dispatch(ids, n_tok * k, n_exp, offsets, sorted, active, n_active, units, lds);
 }
 
 }  // namespace
 
 int launch_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32, int64_t n_tok,
                          int64_t hidden, int64_t n_exp, hipStream_t stream) {
-  const dim3 grid((unsigned)((n_exp + kRouterMfmaRows - 1) / kRouterMfmaRows),
-                  (unsigned)((n_tok + kRouterMfmaRows - 1) / kRouterMfmaRows));
+  const dim3 grid((unsigned)((n_exp + kRouterTile - 1) / kRouterTile), (unsigned)((n_tok + kRouterTile - 1) / kRouterTile));
   router_logits_mfma_kernel<<<grid, 256, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
       static_cast<uint16_t*>(logits), x_f32, (int)n_tok, (int)hidden, (int)n_exp);
@@ -599,18 +652,39 @@ int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t*
   return check_launch("dispatch_kernel");
 }
 
-int launch_router_fused(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
-                        int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
-                        int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* done,
-                        hipStream_t stream) {
-  const dim3 grid((unsigned)((n_exp + 3) / 4), (unsigned)((n_tok + kRouterTok - 1) / kRouterTok));
-  const size_t lds_logits = (size_t)kRouterTok * hidden * sizeof(uint16_t);
-  const size_t lds_dispatch = dispatch_lds_bytes((int)(n_tok * k), (int)n_exp);
-  router_fused_kernel<<<grid, 256, lds_logits > lds_dispatch ? lds_logits : lds_dispatch, stream>>>(
+// Slices of the hidden dimension for the decode router: about 128
+// workgroups, at most kRouterMaxSlices slices (the last workgroup of a token
+// tile reads every slice of its expert tiles).
+int64_t decode_router_slices(int64_t n_tok, int64_t hidden, int64_t n_exp) {
+  const int64_t tiles = ((n_exp + kRouterTile - 1) / kRouterTile) * ((n_tok + kRouterTile - 1) / kRouterTile);
+  const int64_t nchunk = (hidden + 31) / 32;
+  int64_t ks = (kDecodeRouterWorkgroups + tiles - 1) / tiles;
+  ks = ks < kRouterMaxSlices ? ks : kRouterMaxSlices;
+  ks = ks < nchunk ? ks : nchunk;
+  return ks > 1 ? ks : 1;
+}
+
+int64_t decode_router_counters(int64_t n_tok, int64_t /*n_exp*/) { return (n_tok + kRouterTile - 1) / kRouterTile + 1; }
+
+int64_t decode_router_partial_bytes(int64_t n_tok, int64_t hidden, int64_t n_exp) {
+  const int64_t tiles = ((n_exp + kRouterTile - 1) / kRouterTile) * ((n_tok + kRouterTile - 1) / kRouterTile);
+  return tiles * decode_router_slices(n_tok, hidden, n_exp) * 256 * (int64_t)sizeof(double);
+}
+
+int launch_router_decode(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
+                         int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
+                         int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* counters,
+                         double* partials, hipStream_t stream) {
+  const dim3 grid((unsigned)((n_exp + kRouterTile - 1) / kRouterTile), (unsigned)((n_tok + kRouterTile - 1) / kRouterTile),
+                  (unsigned)decode_router_slices(n_tok, hidden, n_exp));
+  size_t lds = 3 * 64 * 4 * sizeof(double);
+  lds = std::max(lds, (size_t)kRouterTile * n_exp * sizeof(uint16_t));
+  lds = std::max(lds, dispatch_lds_bytes((int)(n_tok * k), (int)n_exp));
+  router_decode_kernel<<<grid, 256, lds, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
       static_cast<uint16_t*>(logits), (int)n_tok, (int)hidden, (int)n_exp, (int)k, ids, values,
-      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, units, done);
-  return check_launch("router_fused_kernel");
+      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, units, counters, partials);
+  return check_launch("router_decode_kernel");
 }
 
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp) {
@@ -618,10 +692,9 @@ int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp) {
               "router: bad sizes n_tokens=%lld hidden=%lld n_experts=%lld", (long long)n_tok, (long long)hidden,
               (long long)n_exp);
   KLC_REQUIRE(hidden % 8 == 0, KLC_ERR_SHAPE, "router: hidden=%lld must be a multiple of 8", (long long)hidden);
-  KLC_REQUIRE(n_tok <= (int64_t)65535 * kRouterTok && hidden <= 64 * 8 * kRouterChunks && n_exp <= 1024,
-              KLC_ERR_UNSUPPORTED,
-              "router: unsupported sizes n_tokens=%lld hidden=%lld n_experts=%lld (hidden <= %d, n_experts <= 1024)",
-              (long long)n_tok, (long long)hidden, (long long)n_exp, 64 * 8 * kRouterChunks);
+  KLC_REQUIRE(n_tok <= (int64_t)65535 * kRouterTile && hidden <= (1 << 20) && n_exp <= 1024, KLC_ERR_UNSUPPORTED,
+              "router: unsupported sizes n_tokens=%lld hidden=%lld n_experts=%lld (n_tokens <= %d, hidden <= "
+              "1048576, n_experts <= 1024)", (long long)n_tok, (long long)hidden, (long long)n_exp, 65535 * kRouterTile);
   return KLC_OK;
 }
 

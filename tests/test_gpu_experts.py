@@ -62,7 +62,9 @@ def check_layer(gpu, host, dev_w, x, k, precision):
     layer = moe.MoELayer(dev_w, experts_per_token=k, precision=precision)
     xt = bf16_tensor(x, gpu)
     det = layer.forward_detailed(xt)
-    fused = layer.forward(xt)
+    fused_ids = torch.empty((x.shape[0], k), dtype=torch.int32, device=gpu)
+    fused_w = torch.empty((x.shape[0], k), dtype=torch.bfloat16, device=gpu)
+    fused = layer.forward(xt, ids=fused_ids, weights=fused_w)
     torch.cuda.synchronize()
     ref = oracle_layer(host, x, k, precision)
 
@@ -70,6 +72,9 @@ def check_layer(gpu, host, dev_w, x, k, precision):
     assert np.array_equal(bf16_bits(det["logits"]), ref["logits"])
     assert np.array_equal(ids, ref["ids"])
     assert np.array_equal(bf16_bits(det["weights"]), ref["weights"])
+    # the single-call layer's own routing (one-launch router for decode batches)
+    assert np.array_equal(fused_ids.cpu().numpy(), ref["ids"])
+    assert np.array_equal(bf16_bits(fused_w), ref["weights"])
 
     n_tok = x.shape[0]
     gated = det["gated"].cpu().numpy().reshape(n_tok, k, -1)
@@ -99,7 +104,7 @@ def assert_final_close(out_bits, ref, precision="fp32"):
     assert (err <= ATOL + RTOL * np.abs(want) + slack).all(), f"final output worst error {err.max():.3e}"
 
 
-@pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 8), (16, 4, 8), (5, 2, 3), (33, 4, 16)])
+@pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 8), (16, 4, 8), (5, 2, 3), (33, 4, 16), (97, 2, 37), (128, 4, 256)])
 def test_small_layer_matches_oracle(gpu, n_tok, k, n_exp):
     host, dev_w, x = build(gpu, 50 + n_tok, 128, 64, n_exp, n_tok)
     check_layer(gpu, host, dev_w, x, k, "fp32")
