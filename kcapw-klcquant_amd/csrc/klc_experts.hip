@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;  // step g4 - 1
   auto chunk = [&](uint32_t tile_off, int t, bool valid) -> u32x4_t {
     const uint32_t v = !valid || t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
-    return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, kStreamPolicy);
   };
   const uint32_t rec_voff = (uint32_t)((trow * 4 + lq) * rec);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       const uint32_t soff = scale_base + (uint32_t)(tile * kTileRows * 4 * rec);
 #pragma unroll
       for (int i = 0; i < kRecWords / 2; ++i) {
-        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, rec_voff + 8u * min(i, rec / 8 - 1), soff, 0);
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, rec_voff + 8u * min(i, rec / 8 - 1), soff, kStreamPolicy);
         dst[2 * i] = v.x;
         dst[2 * i + 1] = v.y;
       }
