@@ -196,7 +196,7 @@ int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter,
  * path (streamed_moe_router.py:257-315, 483-522) for every row of x:
  * router logits -> top-k/softmax -> dispatch -> gate_up/SwiGLU -> down ->
  * combine, all enqueued on `stream` with no host synchronisation (batches of
- * up to 2 tokens run the router, top-k and dispatch as one launch).  Writes
+ * up to 128 tokens run the router, top-k and dispatch as one launch).  Writes
  * out[n_tokens][hidden] bfloat16, plus residual (bfloat16 [n_tokens][hidden])
  * when that is not NULL (streamed_transformer_executor.py:260; out may alias
  * residual); ids/weights (optional, may be NULL) receive the routing.  workspace must be 256-byte aligned, hold
