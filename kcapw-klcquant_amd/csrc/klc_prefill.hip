@@ -6,12 +6,20 @@
 // dispatch) and 256 output rows (4 waves, each one 64-row packed tile, i.e.
 // 4 row blocks of 16).  Per 128-deep k step every wave decodes its A chunks
 // (MXFP4 -> bfloat16 with v_cvt_scalef32_pk_bf16_fp4, exact) and multiplies
-// them with v_mfma_f32_16x16x32_bf16 into each 16-token column block of B,
-// which the workgroup stages in LDS (double buffered; global loads issued two
-// steps ahead) from the token rows.  A chunks stream from HBM two steps ahead.  The products are exact and the
-// sums run in float32, like the decode GEMVs, so both paths meet the same
-// tolerance; gate_up reads the bfloat16 hidden state as is, down reads the
-// float32 SwiGLU output as hi + lo bfloat16 planes (relative residual 2^-17).
+// them with v_mfma_f32_16x16x32_bf16 into each 16-token column block of B.
+//
+// Both operand streams run kRing - 1 steps ahead of the MFMAs: A (per wave)
+// in a register ring, B (shared by the 4 waves) in an LDS ring filled by
+// global_load_lds_dwordx4, which writes lane l's 16 bytes at the
+// instruction's LDS base + 16 l.  One instruction fills 4 token rows of 256
+// bytes; the 16-byte piece q of row r sits in slot q ^ (r % 16), so the B
+// reads of 16 consecutive rows at one piece hit 16 different slots (all 64
+// banks).  A step waits once for its own loads (vector memory operations
+// complete in order, so the later steps' loads stay in flight) and passes
+// one barrier.  The products are exact and the sums run in float32, like
+// the decode GEMVs, so both paths meet the same tolerance; gate_up reads the
+// bfloat16 hidden state as is, down reads the float32 SwiGLU output as hi +
+// lo bfloat16 planes (relative residual 2^-17).
 //
 // (The scaled FP4 MFMA, v_mfma_scale_f32_16x16x128_f8f6f4 with FP8 hi/lo
 // activations, takes the weights in their own format but forms its
@@ -24,7 +32,7 @@
 // row 4 (l / 16) + v, column l % 16.  A step of 4 MX groups is four MFMAs:
 // MFMA j takes dword j of every lane's 16-byte chunk (group 4s + l/16), so
 // its k set is {128 s + 32 q + 8 j + i}; the B lane (column n, q) reads those
-// 8 activations of its token.
+// 8 activations of its token, piece 4 q + j of its row.
 #include "klc_common.h"
 
 namespace klc {
@@ -36,10 +44,14 @@ constexpr int kGemmThreads = 256;
 constexpr int kGemmWaves = 4;
 constexpr int kGemmRows = kGemmWaves * kTileRows;   // 256 output rows per workgroup
 constexpr int kGemmCb = kUnitTokensGemm / 16;       // 8 column blocks of 16 tokens
-constexpr int kRowBytes = 128 * 2 + 16;             // one token's 128 bfloat16 of a step, padded (bank spread)
-constexpr int kPlaneBytes = kUnitTokensGemm * kRowBytes;
-constexpr int kPieces = kUnitTokensGemm * 16 / kGemmThreads;  // 16-byte pieces per thread per plane and step
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
+#ifndef KLC_GEMM_RING_UP
+#define KLC_GEMM_RING_UP 4
+#endif
+#ifndef KLC_GEMM_RING_DOWN
+#define KLC_GEMM_RING_DOWN 2
+#endif
+
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
   // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp
@@ -53,25 +65,54 @@ __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
 // [2][pairs][in_down] (and float32 SwiGLU output to out_raw if set).  down:
 // act = those planes (rows by pair); writes float32 expert outputs.
+// s_waitcnt immediate that waits until at most n vector memory operations
+// and no LDS operation are outstanding (gfx9 encoding; export counter free).
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70; }
+
+// Step barrier of the LDS ring.  Each wave first waits for its own step-s
+// loads (vmcnt) and its LDS reads (lgkmcnt 0); the barrier then orders every
+// wave's B rows before any wave's reads, and the acquire fence keeps the
+// compiler from moving LDS reads above it.  (__syncthreads' release fence
+// would wait for every outstanding LDS-DMA, i.e. for all later steps too.)
+template <int kOutstanding>
+__device__ __forceinline__ void ring_barrier() {
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kOutstanding));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 template <bool kDown>
-__global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
+__host__ __device__ constexpr int gemm_ring() { return kDown ? KLC_GEMM_RING_DOWN : KLC_GEMM_RING_UP; }
+template <bool kDown>
+__host__ __device__ constexpr int gemm_stage_bytes() { return (kDown ? 2 : 1) * kUnitTokensGemm * 256; }
+
+// One GEMM unit x one 256-row tile.  gate_up: act = bfloat16 hidden state
+// [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
+// [2][pairs][in_down] (and float32 SwiGLU output to out_raw if set).  down:
+// act = those planes (rows by pair); writes float32 expert outputs.
+template <bool kDown, int kFixedSteps>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_kernel(
     const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
     float limit, int precision, int row_wgs, int units_per_xcd) {
   constexpr int kPlanes = kDown ? 2 : 1;
-  constexpr int kStage = kPlanes * kPlaneBytes;
-  extern __shared__ __align__(16) uint8_t stage[];  // 2 x kStage
+  constexpr int kRing = gemm_ring<kDown>();
+  constexpr int kStage = gemm_stage_bytes<kDown>();  // one step: 64 token rows x 256 bytes per plane
+  constexpr int kPlaneStage = kStage / kPlanes;
+  // A: 4 chunks (+ 4 scale words unless preloaded); B: 4 rows of 4 per plane
+  constexpr int kLoadsPerStep = (kFixedSteps > 0 ? 4 : 8) + 4 * kPlanes;
+  extern __shared__ __align__(16) uint8_t stage[];    // kRing x kStage
 
   // XCD-aware order: workgroups are handed to the 8 XCDs round-robin, so XCD
   // x = blockIdx.x % 8 runs units x, x + 8, ...; all row tiles of a unit run on
   // one XCD, which reads the unit's activation rows into its own L2 once.
   const int xcd = blockIdx.x % kXcds;
-  const int j = blockIdx.x / kXcds;
-  const int u = xcd + kXcds * (j / row_wgs);
-  const int row_wg = j % row_wgs;
-  if (j >= units_per_xcd * row_wgs || u >= *n_units) return;
+  const int j0 = blockIdx.x / kXcds;
+  const int u = xcd + kXcds * (j0 / row_wgs);
+  const int row_wg = j0 % row_wgs;
+  if (j0 >= units_per_xcd * row_wgs || u >= *n_units) return;
   const int32_t unit = units[u];
   const int e = unit_expert(unit);
   const int pb = offsets[e];
@@ -89,48 +130,72 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
   const int in_dim = groups * 32;
   const int steps = (groups + 3) >> 2;
 
-  // ---- staging: thread moves pieces (plane, token c = (tid >> 4) + 16 i, 8 values at 8 o), o = tid & 15 ----
-  const int so = tid & 15;
-  int64_t src_row[kPieces];
+  // ---- B stream: wave w's LDS-DMA instruction i fills token rows 16 w + 4 i .. + 3;
+  // lane l brings piece (l % 16) ^ (r % 16) of row r = 16 w + 4 i + l / 16.
+  // Rows past the unit's tokens repeat its last token (their columns are
+  // discarded); k past the input repeats its last piece (A is zero there). ----
+  int64_t src_row[4];
+  int piece[4];
 #pragma unroll
-  for (int i = 0; i < kPieces; ++i) {
-    const int c = min((tid >> 4) + 16 * i, nt - 1);
-    const int p = pairs[pb + tc + c];
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * wave + 4 * i + lq;
+    const int p = pairs[pb + tc + min(r, nt - 1)];
     src_row[i] = (int64_t)(kDown ? p : p / k_top) * in_dim;
+    piece[i] = lr ^ (r & 15);
   }
-  auto stage_load = [&](int s, u32x4_t* pv) {
-    const int kc = min(s * 128 + so * 8, in_dim - 8);
+  auto b_dma = [&](int s, int slot) {
+    const int sc = min(s, steps - 1);
 #pragma unroll
-    for (int i = 0; i < kPieces * kPlanes; ++i)
-      pv[i] = *reinterpret_cast<const u32x4_t*>(act + (i / kPieces) * act_plane + src_row[i % kPieces] + kc);
-  };
-  auto stage_store = [&](int s, int buf, const u32x4_t* pv) {
-    uint8_t* base = stage + buf * kStage;
-    const bool k_ok = s * 128 + so * 8 < in_dim;
+    for (int pl = 0; pl < kPlanes; ++pl) {
 #pragma unroll
-    for (int i = 0; i < kPieces * kPlanes; ++i) {
-      const int c = (tid >> 4) + 16 * (i % kPieces);
-      const u32x4_t z = {0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4_t*>(base + (i / kPieces) * kPlaneBytes + c * kRowBytes + so * 16) =
-          (k_ok && c < nt) ? pv[i] : z;
+      for (int i = 0; i < 4; ++i) {
+        const int kc = min(sc * 128 + piece[i] * 8, in_dim - 8);
+        const uint16_t* g = act + pl * act_plane + src_row[i] + kc;
+        __attribute__((address_space(3))) uint8_t* dst =
+            (__attribute__((address_space(3))) uint8_t*)stage + slot * kStage + pl * kPlaneStage + (16 * wave + 4 * i) * 256;
+        __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
+      }
     }
   };
 
-  // ---- A stream: the wave's 64-row tile, 4 row blocks, two steps ahead ----
+  // ---- A stream: the wave's 64-row tile, 4 row blocks; steps past the end
+  // load out of range (zeros, no traffic, no branch) ----
   const int wtile = wave_live ? tile : 0;
   const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
       (void*)wptr[e], (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
   const uint32_t tile_off = (uint32_t)wtile * (uint32_t)groups * 1024u;
   const int rec = (int)packed_scale_record(groups);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
-  auto a_load = [&](int s, u32x4_t* a, uint32_t* sw) {
-    const bool ok = 4 * s + lq < groups;
+  // With the step loop unrolled, the lane's whole scale record (one byte per
+  // step, <= 24 steps) is loaded once up front: per-step scale words, one
+  // 4-byte load per lane at a 24-byte stride, cost more issue time in the
+  // texture unit than the weight chunks themselves.
+  constexpr bool kPreloadScales = kFixedSteps > 0;
+  static_assert(kFixedSteps <= 24, "scale records hold at most 24 steps");
+  u32x4_t srec_lo[4];
+  u32x2_t srec_hi[4];
+  if constexpr (kPreloadScales) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
+      srec_lo[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, r * (uint32_t)rec, scale_base, 0);
+      srec_hi[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, r * (uint32_t)rec + 16u, scale_base, 0);
+    }
+  }
+  auto a_load = [&](int s, u32x4_t (&a)[4], uint32_t (&sw)[4]) {
+    const bool ok = s < steps && 4 * s + lq < groups;
+    const int sc = min(s, steps - 1);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const uint32_t v = ok ? (uint32_t)(lq * 1024 + (rb * 16 + lr) * 16) : kOutOfRange;
-      a[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * s, 0);
-      const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
-      sw[rb] = __builtin_amdgcn_raw_buffer_load_b32(wbuf, r * (uint32_t)rec + (uint32_t)(s & ~3), scale_base, 0);
+      a[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * sc, 0);
+      if constexpr (!kPreloadScales) {
+        // the scale word is always in range (step clamped, lanes past the
+        // last group read record padding that `live` discards): a select
+        // here would make the compiler split the load and wait on all loads
+        const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
+        sw[rb] = __builtin_amdgcn_raw_buffer_load_b32(wbuf, r * (uint32_t)rec + (uint32_t)(sc & ~3), scale_base, 0);
+      }
     }
   };
 
@@ -140,65 +205,90 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
 #pragma unroll
     for (int cb = 0; cb < kGemmCb; ++cb) acc[rb][cb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // activation staging: two register sets, loads issued two steps ahead;
-  // LDS double buffered
-  u32x4_t pva[kPieces * kPlanes], pvb[kPieces * kPlanes];
-  u32x4_t a_cur[4], a_nxt[4];
-  uint32_t s_cur[4], s_nxt[4];
-  stage_load(0, pva);
-  a_load(0, a_cur, s_cur);
-  if (steps > 1) a_load(1, a_nxt, s_nxt);
-  if (steps > 1) stage_load(1, pvb);
-  stage_store(0, 0, pva);
-  __syncthreads();
+  // B read offsets: lane (lr, lq) reads piece 4 lq + j of row 16 cb + lr
+  int b_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b_off[j] = lr * 256 + (((4 * lq + j) ^ lr) << 4);
 
-  // one k step: stage s + 2 is loaded into `ld` (free since stage s was
-  // stored), stage s + 1 (loaded a step ago, in `st`) goes to LDS
-  auto step = [&](int s, u32x4_t* ld, const u32x4_t* st) {
-    const int buf = s & 1;
-    if (s + 2 < steps) stage_load(s + 2, ld);
-    if (wave_live) {
-      // per quarter j of the step: decode the 4 row blocks' A operands, then
-      // multiply them into every column block (row blocks innermost, so
-      // consecutive MFMAs update different accumulators)
-      const bool live = 4 * s + lq < groups;
-      float scale[4];
+  auto compute = [&](int s, int slot, const u32x4_t (&a_cur)[4], const uint32_t (&s_cur)[4]) {
+    const bool live = 4 * s + lq < groups;
+    float scale[4];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) scale[rb] = cvt_scale_operand((s_cur[rb] >> (8 * (s & 3))) & 0xffu, live);
-      const uint8_t* base = stage + buf * kStage + lr * kRowBytes + lq * 64;
+    for (int rb = 0; rb < 4; ++rb) {
+      uint32_t word;
+      if constexpr (kPreloadScales) {
+        // s is a compile-time constant here (fully unrolled loop)
+        const int d = min(s >> 2, 5);
+        word = d < 4 ? srec_lo[rb][d & 3] : srec_hi[rb][d & 1];
+      } else {
+        word = s_cur[rb];
+      }
+      scale[rb] = cvt_scale_operand((word >> (8 * (s & 3))) & 0xffu, live);
+    }
+    const uint8_t* base = stage + slot * kStage;
+    // the B operands of a quarter are read one quarter ahead of their MFMAs
+    // (unconditionally: the stage always holds 64 token rows)
+    bf16x8_t bq[2][kGemmCb][kPlanes];
+    auto load_b = [&](int j, bf16x8_t (&dst)[kGemmCb][kPlanes]) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bf16x8_t a[4];
+      for (int cb = 0; cb < kGemmCb; ++cb)
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) a[rb] = decode8(a_cur[rb][j], scale[rb]);
+        for (int pl = 0; pl < kPlanes; ++pl)
+          dst[cb][pl] = *reinterpret_cast<const bf16x8_t*>(base + pl * kPlaneStage + cb * 16 * 256 + b_off[j]);
+    };
+    load_b(0, bq[0]);
 #pragma unroll
-        for (int cb = 0; cb < kGemmCb; ++cb) {
-          if (cb < ncb) {
+    for (int j = 0; j < 4; ++j) {
+      if (j < 3) load_b(j + 1, bq[(j + 1) & 1]);
+      bf16x8_t a[4];
 #pragma unroll
-            for (int pl = 0; pl < kPlanes; ++pl) {
-              const bf16x8_t b =
-                  *reinterpret_cast<const bf16x8_t*>(base + pl * kPlaneBytes + cb * 16 * kRowBytes + j * 16);
+      for (int rb = 0; rb < 4; ++rb) a[rb] = decode8(a_cur[rb][j], scale[rb]);
 #pragma unroll
-              for (int rb = 0; rb < 4; ++rb)
-                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], b, acc[rb][cb], 0, 0, 0);
-            }
+      for (int cb = 0; cb < kGemmCb; ++cb) {
+        if (cb < ncb) {
+#pragma unroll
+          for (int pl = 0; pl < kPlanes; ++pl) {
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+              acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], bq[j & 1][cb][pl], acc[rb][cb], 0, 0, 0);
           }
         }
       }
     }
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      a_cur[rb] = a_nxt[rb];
-      s_cur[rb] = s_nxt[rb];
-    }
-    if (s + 2 < steps) a_load(s + 2, a_nxt, s_nxt);
-    if (s + 1 < steps) stage_store(s + 1, buf ^ 1, st);
-    __syncthreads();
   };
-  for (int s = 0; s < steps; s += 2) {
-    step(s, pva, pvb);
-    if (s + 1 < steps) step(s + 1, pvb, pva);
+
+  u32x4_t a_ring[kRing][4];
+  uint32_t s_ring[kRing][4];
+#pragma unroll
+  for (int i = 0; i < kRing - 1; ++i) {
+    a_load(i, a_ring[i], s_ring[i]);
+    b_dma(i, i);
   }
+  // step s: wait for its own loads (the kRing - 2 later steps' stay in
+  // flight), barrier (every wave's B rows of step s have landed and every
+  // wave is done with step s - 1), issue step s + kRing - 1 into the slots
+  // step s - 1 used, multiply.  Unrolled by kRing so slot indices are
+  // constants, and run to a multiple of kRing steps with no branch around a
+  // step (the steps past the end multiply zeros: A loads out of range and
+  // its scales are 0), so no register of an in-flight load is copied.
+  // With kFixedSteps (the padded step count of the launch's shape) the step
+  // loop is unrolled completely: the compiler's wait analysis is exact in
+  // straight-line code, whereas across a loop back edge it waits for every
+  // outstanding load before the first use of a ring slot.
+  const int steps_pad = kFixedSteps > 0 ? kFixedSteps : (steps + kRing - 1) / kRing * kRing;
+  constexpr int kOuterUnroll = kFixedSteps > 0 ? kFixedSteps / kRing : 1;
+#pragma unroll kOuterUnroll
+  for (int s0 = 0; s0 < (kFixedSteps > 0 ? kFixedSteps : steps_pad); s0 += kRing) {
+#pragma unroll
+    for (int uu = 0; uu < kRing; ++uu) {
+      const int s = s0 + uu;
+      ring_barrier<(kRing - 2) * kLoadsPerStep>();
+      a_load(s + kRing - 1, a_ring[(uu + kRing - 1) % kRing], s_ring[(uu + kRing - 1) % kRing]);
+      b_dma(s + kRing - 1, (uu + kRing - 1) % kRing);
+      if (wave_live) compute(s, uu, a_ring[uu], s_ring[uu]);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no LDS-DMA may outlive the workgroup
 
   if (!wave_live) return;
   // ---- epilogue: lane holds rows rb * 16 + 4 lq + v of the tile, token column cb * 16 + lr ----
@@ -244,6 +334,11 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(
   }
 }
 
+// Step count (128-deep) of a `groups`-group input, padded to the ring size.
+int padded_steps(int groups, int ring) { return ((groups + 3) / 4 + ring - 1) / ring * ring; }
+// Inputs of 2880 (gpt-oss): 23 steps, padded to 24, get the unrolled kernels.
+constexpr int kUnrolledSteps = 24;
+
 }  // namespace
 
 int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k,
@@ -255,10 +350,13 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
   const int row_wgs = (int)((rows + kGemmRows - 1) / kGemmRows);
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
-  moe_gemm_kernel<false><<<grid, kGemmThreads, 2 * kPlaneBytes, stream>>>(
+  const int groups = (int)(hidden / 32);
+  auto kernel = padded_steps(groups, gemm_ring<false>()) == kUnrolledSteps ? moe_gemm_kernel<false, kUnrolledSteps>
+                                                                              : moe_gemm_kernel<false, 0>;
+  kernel<<<grid, kGemmThreads, gemm_ring<false>() * gemm_stage_bytes<false>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
       0, nullptr, static_cast<uint16_t*>(gated_split), n_pairs * inter, gated_raw, offsets, pairs,
-      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, (int)(hidden / 32), (int)k, limit, precision,
+      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, groups, (int)k, limit, precision,
       row_wgs, per_xcd);
   return check_launch("moe_gemm_kernel<gate_up>");
 }
@@ -269,10 +367,13 @@ int launch_gemm_down(const void* const* w, const void* bias, const void* gated_s
   const int row_wgs = (int)((hidden + kGemmRows - 1) / kGemmRows);
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
-  moe_gemm_kernel<true><<<grid, kGemmThreads, 2 * 2 * kPlaneBytes, stream>>>(
+  const int groups = (int)(inter / 32);
+  auto kernel = padded_steps(groups, gemm_ring<true>()) == kUnrolledSteps ? moe_gemm_kernel<true, kUnrolledSteps>
+                                                                             : moe_gemm_kernel<true, 0>;
+  kernel<<<grid, kGemmThreads, gemm_ring<true>() * gemm_stage_bytes<true>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs,
-      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, (int)(inter / 32), 1, 0.0f, precision,
+      units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, groups, 1, 0.0f, precision,
       row_wgs, per_xcd);
   return check_launch("moe_gemm_kernel<down>");
 }
