@@ -54,10 +54,12 @@ constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with it
 
 
 __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
-  // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp
+  // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp.
+  // The sigmoid uses the hardware exp2 and reciprocal (a few ulp, far inside
+  // the expert-output tolerance).
   gate = gate > limit ? limit : gate;
   up = up > limit ? limit : (up < -limit ? -limit : up);
-  const float glu = gate * (1.0f / (1.0f + expf(-(gate * 1.702f))));
+  const float glu = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-(gate * 1.702f)));
   return (up + 1.0f) * glu;
 }
 
@@ -90,7 +92,7 @@ __host__ __device__ constexpr int gemm_stage_bytes() { return (kDown ? 2 : 1) * 
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
 // [2][pairs][in_down] (and float32 SwiGLU output to out_raw if set).  down:
 // act = those planes (rows by pair); writes float32 expert outputs.
-template <bool kDown, int kFixedSteps>
+template <bool kDown>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_kernel(
     const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
@@ -101,8 +103,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   constexpr int kRing = gemm_ring<kDown>();
   constexpr int kStage = gemm_stage_bytes<kDown>();  // one step: 64 token rows x 256 bytes per plane
   constexpr int kPlaneStage = kStage / kPlanes;
-  // A: 4 chunks (+ 4 scale words unless preloaded); B: 4 rows of 4 per plane
-  constexpr int kLoadsPerStep = (kFixedSteps > 0 ? 4 : 8) + 4 * kPlanes;
+  constexpr int kLoadsPerStep = 4 + 4 * kPlanes;  // A: 4 chunks; B: 4 rows of 4 per plane
   extern __shared__ __align__(16) uint8_t stage[];    // kRing x kStage
 
   // XCD-aware order: workgroups are handed to the 8 XCDs round-robin, so XCD
@@ -170,32 +171,26 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // step, <= 24 steps) is loaded once up front: per-step scale words, one
   // 4-byte load per lane at a 24-byte stride, cost more issue time in the
   // texture unit than the weight chunks themselves.
-  constexpr bool kPreloadScales = kFixedSteps > 0;
-  static_assert(kFixedSteps <= 24, "scale records hold at most 24 steps");
+  // The lane's whole scale record (one byte per step; inputs <= 3072 have
+  // <= 24 steps, so <= 24 bytes) is loaded once: per-step 4-byte scale loads
+  // at a 24-byte stride cost more issue time in the texture unit than the
+  // weight chunks themselves.  (Bytes past a shorter record belong to the
+  // next record or lie past the buffer, which loads zeros; neither is used.)
   u32x4_t srec_lo[4];
   u32x2_t srec_hi[4];
-  if constexpr (kPreloadScales) {
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
-      srec_lo[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, r * (uint32_t)rec, scale_base, 0);
-      srec_hi[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, r * (uint32_t)rec + 16u, scale_base, 0);
-    }
+  for (int rb = 0; rb < 4; ++rb) {
+    const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
+    srec_lo[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, r * (uint32_t)rec, scale_base, 0);
+    srec_hi[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, r * (uint32_t)rec + 16u, scale_base, 0);
   }
-  auto a_load = [&](int s, u32x4_t (&a)[4], uint32_t (&sw)[4]) {
+  auto a_load = [&](int s, u32x4_t (&a)[4]) {
     const bool ok = s < steps && 4 * s + lq < groups;
     const int sc = min(s, steps - 1);
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const uint32_t v = ok ? (uint32_t)(lq * 1024 + (rb * 16 + lr) * 16) : kOutOfRange;
       a[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * sc, 0);
-      if constexpr (!kPreloadScales) {
-        // the scale word is always in range (step clamped, lanes past the
-        // last group read record padding that `live` discards): a select
-        // here would make the compiler split the load and wait on all loads
-        const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
-        sw[rb] = __builtin_amdgcn_raw_buffer_load_b32(wbuf, r * (uint32_t)rec + (uint32_t)(sc & ~3), scale_base, 0);
-      }
     }
   };
 
@@ -210,19 +205,15 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
   for (int j = 0; j < 4; ++j) b_off[j] = lr * 256 + (((4 * lq + j) ^ lr) << 4);
 
-  auto compute = [&](int s, int slot, const u32x4_t (&a_cur)[4], const uint32_t (&s_cur)[4]) {
+  auto compute = [&](int s, int slot, const u32x4_t (&a_cur)[4]) {
     const bool live = 4 * s + lq < groups;
+    const int d = min(s >> 2, 5);  // dword of the scale record holding step s
     float scale[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      uint32_t word;
-      if constexpr (kPreloadScales) {
-        // s is a compile-time constant here (fully unrolled loop)
-        const int d = min(s >> 2, 5);
-        word = d < 4 ? srec_lo[rb][d & 3] : srec_hi[rb][d & 1];
-      } else {
-        word = s_cur[rb];
-      }
+      const uint32_t lo = (d & 2) ? ((d & 1) ? srec_lo[rb][3] : srec_lo[rb][2])
+                                  : ((d & 1) ? srec_lo[rb][1] : srec_lo[rb][0]);
+      const uint32_t word = d >= 4 ? ((d & 1) ? srec_hi[rb][1] : srec_hi[rb][0]) : lo;
       scale[rb] = cvt_scale_operand((word >> (8 * (s & 3))) & 0xffu, live);
     }
     const uint8_t* base = stage + slot * kStage;
@@ -258,10 +249,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   };
 
   u32x4_t a_ring[kRing][4];
-  uint32_t s_ring[kRing][4];
 #pragma unroll
   for (int i = 0; i < kRing - 1; ++i) {
-    a_load(i, a_ring[i], s_ring[i]);
+    a_load(i, a_ring[i]);
     b_dma(i, i);
   }
   // step s: wait for its own loads (the kRing - 2 later steps' stay in
@@ -271,57 +261,95 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // constants, and run to a multiple of kRing steps with no branch around a
   // step (the steps past the end multiply zeros: A loads out of range and
   // its scales are 0), so no register of an in-flight load is copied.
-  // With kFixedSteps (the padded step count of the launch's shape) the step
-  // loop is unrolled completely: the compiler's wait analysis is exact in
-  // straight-line code, whereas across a loop back edge it waits for every
-  // outstanding load before the first use of a ring slot.
-  const int steps_pad = kFixedSteps > 0 ? kFixedSteps : (steps + kRing - 1) / kRing * kRing;
-  constexpr int kOuterUnroll = kFixedSteps > 0 ? kFixedSteps / kRing : 1;
-#pragma unroll kOuterUnroll
-  for (int s0 = 0; s0 < (kFixedSteps > 0 ? kFixedSteps : steps_pad); s0 += kRing) {
+  const int steps_pad = (steps + kRing - 1) / kRing * kRing;
+  for (int s0 = 0; s0 < steps_pad; s0 += kRing) {
 #pragma unroll
     for (int uu = 0; uu < kRing; ++uu) {
       const int s = s0 + uu;
       ring_barrier<(kRing - 2) * kLoadsPerStep>();
-      a_load(s + kRing - 1, a_ring[(uu + kRing - 1) % kRing], s_ring[(uu + kRing - 1) % kRing]);
+      a_load(s + kRing - 1, a_ring[(uu + kRing - 1) % kRing]);
       b_dma(s + kRing - 1, (uu + kRing - 1) % kRing);
-      if (wave_live) compute(s, uu, a_ring[uu], s_ring[uu]);
+      if (wave_live) compute(s, uu, a_ring[uu]);
     }
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no LDS-DMA may outlive the workgroup
 
-  if (!wave_live) return;
-  // ---- epilogue: lane holds rows rb * 16 + 4 lq + v of the tile, token column cb * 16 + lr ----
+  // ---- epilogue: lane holds rows rb * 16 + 4 lq + v of its tile, token column cb * 16 + lr ----
+  if constexpr (!kDown) {
+    // SwiGLU outputs of the workgroup (128 columns x up to 64 tokens) go
+    // through LDS (the ring is idle now), so each token's 128 outputs leave
+    // as 16-byte stores instead of 2-byte ones scattered over 16 rows
+    constexpr int kYStride = 129;  // floats per token row (odd: spreads the banks)
+    static_assert(kUnitTokensGemm * kYStride * 4 <= kRing * kStage, "the output tile fits in the ring's LDS");
+    float* ytile = reinterpret_cast<float*>(stage);
+    __syncthreads();  // every wave is done reading the ring
+    if (wave_live) {
 #pragma unroll
-  for (int cb = 0; cb < kGemmCb; ++cb) {
-    if (cb >= ncb) continue;
-    const int c = cb * 16 + lr;
-    if (c >= nt) continue;
-    const int p = pairs[pb + tc + c];
+      for (int cb = 0; cb < kGemmCb; ++cb) {
+        if (cb >= ncb) continue;
+        const int c = cb * 16 + lr;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const int row0 = tile * kTileRows + rb * 16 + 4 * lq;
-      const f32x4_t v4 = acc[rb][cb];
-      if constexpr (!kDown) {
-        const int half = rows >> 1;
+        for (int rb = 0; rb < 4; ++rb) {
+          const int row0 = tile * kTileRows + rb * 16 + 4 * lq;
+          const f32x4_t v4 = acc[rb][cb];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float gate = v4[2 * h], up = v4[2 * h + 1];
-          if (precision == KLC_PRECISION_BF16) {
-            gate = round_bf16(gate);
-            up = round_bf16(up);
+          for (int h = 0; h < 2; ++h) {
+            float gate = v4[2 * h], up = v4[2 * h + 1];
+            if (precision == KLC_PRECISION_BF16) {
+              gate = round_bf16(gate);
+              up = round_bf16(up);
+            }
+            gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
+            up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
+            ytile[c * kYStride + wave * 32 + rb * 8 + 2 * lq + h] = swiglu(gate, up, limit);
           }
-          gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
-          up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
-          const float y = swiglu(gate, up, limit);
-          const int64_t idx = (int64_t)p * half + (row0 >> 1) + h;
-          if (out_raw) out_raw[idx] = y;
-          const uint32_t hi = f32_to_bf16_rne(y);
-          const uint32_t lo = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y - bf16_to_f32(hi));
-          out_split[idx] = (uint16_t)hi;
-          out_split[out_plane + idx] = (uint16_t)lo;
         }
-      } else {
+      }
+    }
+    __syncthreads();
+    const int half = rows >> 1;
+    const int col0 = row_wg * (kGemmRows / 2);
+    const int ncols = min(kGemmRows / 2, half - col0);
+    for (int i = tid; i < nt * 16; i += kGemmThreads) {  // (token, 8-column piece)
+      const int c = i >> 4;
+      const int ch = (i & 15) * 8;
+      if (ch >= ncols) continue;
+      const int p = pairs[pb + tc + c];
+      float y[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) y[q] = ytile[c * kYStride + ch + q];
+      uint32_t hi[4], lo[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t h2[2], l2[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          h2[t] = f32_to_bf16_rne(y[2 * q + t]);
+          l2[t] = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y[2 * q + t] - bf16_to_f32(h2[t]));
+        }
+        hi[q] = h2[0] | (h2[1] << 16);
+        lo[q] = l2[0] | (l2[1] << 16);
+      }
+      const int64_t idx = (int64_t)p * half + col0 + ch;  // half % 8 == 0: 16-byte aligned
+      *reinterpret_cast<u32x4_t*>(out_split + idx) = u32x4_t{hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<u32x4_t*>(out_split + out_plane + idx) = u32x4_t{lo[0], lo[1], lo[2], lo[3]};
+      if (out_raw) {
+        reinterpret_cast<float4*>(out_raw + idx)[0] = make_float4(y[0], y[1], y[2], y[3]);
+        reinterpret_cast<float4*>(out_raw + idx)[1] = make_float4(y[4], y[5], y[6], y[7]);
+      }
+    }
+  } else {
+    if (!wave_live) return;
+#pragma unroll
+    for (int cb = 0; cb < kGemmCb; ++cb) {
+      if (cb >= ncb) continue;
+      const int c = cb * 16 + lr;
+      if (c >= nt) continue;
+      const int p = pairs[pb + tc + c];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        const int row0 = tile * kTileRows + rb * 16 + 4 * lq;
+        const f32x4_t v4 = acc[rb][cb];
         float o[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -333,11 +361,6 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     }
   }
 }
-
-// Step count (128-deep) of a `groups`-group input, padded to the ring size.
-int padded_steps(int groups, int ring) { return ((groups + 3) / 4 + ring - 1) / ring * ring; }
-// Inputs of 2880 (gpt-oss): 23 steps, padded to 24, get the unrolled kernels.
-constexpr int kUnrolledSteps = 24;
 
 }  // namespace
 
@@ -351,9 +374,7 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(hidden / 32);
-  auto kernel = padded_steps(groups, gemm_ring<false>()) == kUnrolledSteps ? moe_gemm_kernel<false, kUnrolledSteps>
-                                                                              : moe_gemm_kernel<false, 0>;
-  kernel<<<grid, kGemmThreads, gemm_ring<false>() * gemm_stage_bytes<false>(), stream>>>(
+  moe_gemm_kernel<false><<<grid, kGemmThreads, gemm_ring<false>() * gemm_stage_bytes<false>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
       0, nullptr, static_cast<uint16_t*>(gated_split), n_pairs * inter, gated_raw, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, groups, (int)k, limit, precision,
@@ -368,9 +389,7 @@ int launch_gemm_down(const void* const* w, const void* bias, const void* gated_s
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(inter / 32);
-  auto kernel = padded_steps(groups, gemm_ring<true>()) == kUnrolledSteps ? moe_gemm_kernel<true, kUnrolledSteps>
-                                                                             : moe_gemm_kernel<true, 0>;
-  kernel<<<grid, kGemmThreads, gemm_ring<true>() * gemm_stage_bytes<true>(), stream>>>(
+  moe_gemm_kernel<true><<<grid, kGemmThreads, gemm_ring<true>() * gemm_stage_bytes<true>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, groups, 1, 0.0f, precision,
