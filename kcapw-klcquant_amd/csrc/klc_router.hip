@@ -258,13 +258,84 @@ __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp,
   else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights);
 }
 
+// Top-k + softmax of 4 tokens at once by one wave: the 16 lanes of row q
+// (lanes 16 q .. 16 q + 15) take token t0 + q, lane r of the row holding the
+// keys of experts r + 16 s.  Each round's maximum comes from the lane's own
+// keys and 4 DPP steps inside the row (quad swaps, half-row and row
+// mirrors), so the 4 tokens' selections run side by side.  Same selection
+// and softmax as topk_softmax_row (n_exp <= 16 kSlots, k <= 16).  rows(q)
+// gives token q's logits row (any valid row for q >= n_valid, whose results
+// are not written).
+template <int kSlots, typename RowFn>
+__device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n_exp, int k, int64_t t0,
+                                                  int32_t* __restrict__ ids, float* __restrict__ values,
+                                                  uint16_t* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4;
+  const int r = lane & 15;
+  const uint16_t* row = rows(min(q, n_valid - 1));
+  uint64_t keys[kSlots];
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {
+    const int idx = r + s * 16;
+    keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
+  }
+  int my_id = 0;
+  float my_val = 0.0f;
+  for (int rd = 0; rd < k; ++rd) {
+    uint64_t best = keys[0];
+#pragma unroll
+    for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
+    best = dpp_max_step<0xB1, 0xf>(best);   // quad_perm [1, 0, 3, 2]
+    best = dpp_max_step<0x4E, 0xf>(best);   // quad_perm [2, 3, 0, 1]
+    best = dpp_max_step<0x141, 0xf>(best);  // row_half_mirror
+    best = dpp_max_step<0x140, 0xf>(best);  // row_mirror: every lane of the row holds its maximum
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s)
+      if (keys[s] == best) keys[s] = 0ull;
+    if (r == rd) {
+      my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+      my_val = bf16_to_f32(row[my_id]);
+    }
+  }
+  // softmax over the row's k values: max is the first selection (NaN
+  // propagates); lane r evaluates exp(v_r - max) in float64, the sum runs in
+  // selection order
+  const double mx = (double)__shfl(my_val, q * 16);
+  const double ex = r < k ? exp((double)my_val - mx) : 0.0;
+  double sum = 0.0;
+  for (int rd = 0; rd < k; ++rd) sum += __shfl(ex, q * 16 + rd);
+  if (q < n_valid && r < k) {
+    const int64_t o = (t0 + q) * k + r;
+    ids[o] = my_id;
+    if (values) values[o] = my_val;
+    weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
+  }
+}
+
+// Top-k of tokens t0 .. t0 + n - 1 (n <= 4) by one wave: the row-parallel
+// form when the row fits (n_exp <= 256, k <= 16), else token by token.
+template <typename RowFn>
+__device__ __forceinline__ void topk_softmax_tokens(RowFn rows, int n, int n_exp, int k, int64_t t0,
+                                                    int32_t* __restrict__ ids, float* __restrict__ values,
+                                                    uint16_t* __restrict__ weights) {
+  if (k <= 16 && n_exp <= 256) {
+    if (n_exp <= 64) topk_softmax_quad<4>(rows, n, n_exp, k, t0, ids, values, weights);
+    else if (n_exp <= 128) topk_softmax_quad<8>(rows, n, n_exp, k, t0, ids, values, weights);
+    else topk_softmax_quad<16>(rows, n, n_exp, k, t0, ids, values, weights);
+  } else {
+    for (int q = 0; q < n; ++q) topk_softmax_row(rows(q), n_exp, k, t0 + q, ids, values, weights);
+  }
+}
+
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
                                                            int32_t* __restrict__ ids, float* __restrict__ values,
                                                            uint16_t* __restrict__ weights, int n_tok, int n_exp,
                                                            int k) {
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= n_tok) return;
-  topk_softmax_row(logits + (int64_t)t * n_exp, n_exp, k, t, ids, values, weights);
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;  // 4 tokens per wave
+  if (t0 >= n_tok) return;
+  topk_softmax_tokens([&](int q) { return logits + (int64_t)(t0 + q) * n_exp; }, min(4, n_tok - t0), n_exp, k, t0,
+                      ids, values, weights);
 }
 
 // Softmax of caller-chosen scores (one thread per token): the routing-locality
@@ -616,8 +687,12 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     router_tile_store(acc, b, logits, n_tok, n_exp, e_t * kRouterTile, t0, rows);
   }
   __syncthreads();
-  for (int t = t0 + wave; t < min(t0 + kRouterTile, n_tok); t += 4)
-    topk_softmax_row(rows + (t - t0) * n_exp, n_exp, k, t, ids, values, weights);
+  {
+    const int tw = t0 + 4 * wave;  // 4 tokens per wave
+    if (tw < n_tok)
+      topk_softmax_tokens([&](int q) { return rows + (tw - t0 + q) * n_exp; }, min(4, n_tok - tw), n_exp, k, tw, ids,
+                          values, weights);
+  }
   if (n_tt > 1) {
     if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;
   } else {
@@ -639,7 +714,7 @@ int launch_router_logits(const void* x, const void* w, const void* b, void* logi
 
 int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
                 int64_t k, hipStream_t stream) {
-  topk_softmax_kernel<<<(unsigned)((n_tok + 3) / 4), 256, 0, stream>>>(
+  topk_softmax_kernel<<<(unsigned)((n_tok + 15) / 16), 256, 0, stream>>>(
       static_cast<const uint16_t*>(logits), ids, values, static_cast<uint16_t*>(weights), (int)n_tok, (int)n_exp,
       (int)k);
   return check_launch("topk_softmax_kernel");
