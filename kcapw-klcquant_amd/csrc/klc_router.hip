@@ -401,6 +401,7 @@ __device__ __forceinline__ void wave_exclusive_scan_256(int32_t* v, int n, int32
 // takes 4 chunks at a time so that their ballots overlap.
 constexpr int kDispatchChunk = kWave;
 constexpr int kDispatchGroup = 4;
+constexpr int kDispatchDirectPairs = 1024;  // up to this many pairs each expert's thread writes its units
 constexpr int kDispatchWaves = kDispatchThreads / kWave;
 
 __host__ __device__ constexpr int dispatch_chunks(int n_pairs) { return (n_pairs + kDispatchChunk - 1) / kDispatchChunk; }
@@ -538,16 +539,26 @@ __device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, 
       sorted[total[e] + cnt[w * kDispatchMaxExperts + e] + rank[p]] = p;
     }
   }
-  // 4. unit lists, all three as one index space, 4 units per thread at a
-  //    time: a unit's expert is the last one whose first unit is <= the
-  //    unit (experts without units share the next one's first unit), found
-  //    by 8 bisection steps run in lockstep
+  // 4. unit lists
   {
     const int n_gu = sums[2], n_dn = sums[3], n_all = sums[2] + sums[3] + sums[4];
     int32_t* const gu_list = units + kUnitHeader;
     int32_t* const dn_list = units + units_offset_down(n_pairs, n_exp);
     int32_t* const gm_list = units + units_offset_gemm(n_pairs, n_exp);
-    for (int u0 = tid; u0 < n_all; u0 += 4 * kDispatchThreads) {
+    // small batches: each expert's thread writes its own units (a few each)
+    if (n_pairs <= kDispatchDirectPairs) {
+      for (int e = tid; e < n_exp; e += kDispatchThreads) {
+        const int cnt = (e + 1 < n_exp ? total[e + 1] : sums[0]) - total[e];
+        for (int j = 0; j * kUnitTokensGateUp < cnt; ++j) gu_list[ugu[e] + j] = make_unit(e, j);
+        for (int j = 0; j * kUnitTokensDown < cnt; ++j) dn_list[udn[e] + j] = make_unit(e, j);
+        for (int j = 0; j * kUnitTokensGemm < cnt; ++j) gm_list[ugm[e] + j] = make_unit(e, j);
+      }
+    }
+    // large batches: all three lists as one index space, 4 units per thread
+    // at a time: a unit's expert is the last one whose first unit is <= the
+    // unit (experts without units share the next one's first unit), found
+    // by 8 bisection steps run in lockstep
+    for (int u0 = tid; n_pairs > kDispatchDirectPairs && u0 < n_all; u0 += 4 * kDispatchThreads) {
       int lo[4], uu[4], base[4];
       int32_t* dst[4];
 #pragma unroll
