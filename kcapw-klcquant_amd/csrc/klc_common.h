@@ -29,11 +29,12 @@ constexpr int kWave = 64;
 // Packed ("row-tile") MXFP4 layout used by the expert GEMV kernels.  One
 // matrix of `rows` x `groups` MX blocks (rows a multiple of 64) is stored as
 //   blocks: [rows / 64][groups][64 rows][16 bytes]
-//   scales: [rows / 64][64 rows][4 quarters][S bytes],  S = round_up(ceil(groups / 4), 8)
+//   scales: [rows / 64][S / 8][64 rows][4 quarters][8 bytes],  S = round_up(ceil(groups / 4), 8)
 // so one wave-wide 16-byte load fetches group g of 64 consecutive rows as
-// 1 KiB of contiguous memory, and the scale of (row r, group g) is byte g / 4
-// of the record (r, g % 4): a GEMV lane that works on groups q, q + 4, ...
-// of one row finds all of its scales in one S-byte record.
+// 1 KiB of contiguous memory.  A lane that works on groups q, q + 4, ... of
+// one row (step s = group / 4) finds the scale of step s in byte s % 8 of
+// the 8-byte word (s / 8, row, q): a wave reading one such word for its 16
+// rows x 4 quarters reads 512 contiguous bytes.
 constexpr int kTileRows = 64;
 __host__ __device__ inline int64_t packed_steps(int64_t groups) { return (groups + 3) / 4; }
 __host__ __device__ inline int64_t packed_scale_record(int64_t groups) { return (packed_steps(groups) + 7) / 8 * 8; }
@@ -44,11 +45,16 @@ __host__ __device__ inline int64_t packed_scale_bytes(int64_t rows, int64_t grou
 __host__ __device__ inline int64_t packed_matrix_bytes(int64_t rows, int64_t groups) {
   return packed_block_bytes(rows, groups) + packed_scale_bytes(rows, groups);
 }
+// Byte offset, from the start of the scales, of the 8-byte scale word
+// (pair p of steps, row, quarter q).
+__host__ __device__ __forceinline__ int64_t packed_scale_word(int64_t groups, int row, int p, int q) {
+  const int64_t tile_bytes = (int64_t)kTileRows * 4 * packed_scale_record(groups);
+  return (row / kTileRows) * tile_bytes + (((int64_t)p * kTileRows + row % kTileRows) * 4 + q) * 8;
+}
 // Byte offset of the scale of (row, group) inside a packed matrix.
 __host__ __device__ __forceinline__ int64_t packed_scale_offset(int rows, int groups, int row, int group) {
-  const int64_t rec = ((groups + 3) / 4 + 7) / 8 * 8;
-  return (int64_t)(rows / kTileRows) * groups * 1024 +
-         ((int64_t)row * 4 + (group & 3)) * rec + (group >> 2);
+  const int s = group >> 2;
+  return packed_block_bytes(rows, groups) + packed_scale_word(groups, row, s >> 3, group & 3) + (s & 7);
 }
 
 // Work units of the expert kernels.  A unit is one pass of one active expert

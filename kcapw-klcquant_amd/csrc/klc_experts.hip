@@ -134,7 +134,6 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
     const uint32_t v = !valid || t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
     return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, kStreamPolicy);
   };
-  const uint32_t rec_voff = (uint32_t)((trow * 4 + lq) * rec);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
 
   {
@@ -165,13 +164,14 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
     }
 
     // ---- 2. scale record of the first tile, then the ring prologue ----
-    // scale record of (row, quarter) in a tile: byte s = scale of group 4s + lq
+    // the lane's scales of a tile: 8-byte word i holds steps 8i .. 8i + 7 of
+    // (row, quarter); a wave's load of word i is 512 contiguous bytes
     constexpr int kRecWords = (kSteps + 7) / 8 * 2;
     auto load_rec = [&](int tile, uint32_t* dst) {
-      const uint32_t soff = scale_base + (uint32_t)(tile * kTileRows * 4 * rec);
 #pragma unroll
       for (int i = 0; i < kRecWords / 2; ++i) {
-        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, rec_voff + 8u * min(i, rec / 8 - 1), soff, kStreamPolicy);
+        const uint32_t off = (uint32_t)packed_scale_word(groups, tile * kTileRows + trow, min(i, rec / 8 - 1), lq);
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, off, scale_base, kStreamPolicy);
         dst[2 * i] = v.x;
         dst[2 * i + 1] = v.y;
       }

@@ -212,20 +212,28 @@ __global__ __launch_bounds__(256) void pack_blocks_kernel(const uint8_t* __restr
 __global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ scales,
                                                           uint8_t* __restrict__ packed, int64_t n_mat, int rows,
                                                           int groups, int64_t packed_stride) {
+  // one thread per packed scale byte, in packed order: (matrix, tile, pair,
+  // row in tile, quarter, byte); padding bytes (steps past the last group) are 0
   const int rec = (int)packed_scale_record(groups);
   const int64_t total = n_mat * rows * 4 * rec;
   const int64_t scale_base = packed_block_bytes(rows, groups);
+  const int64_t per_mat = (int64_t)rows * 4 * rec;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int s = (int)(idx % rec);
-    int64_t rest = idx / rec;
-    const int q = (int)(rest % 4);
-    rest /= 4;
-    const int r = (int)(rest % rows);
-    const int64_t m = rest / rows;
-    const int g = 4 * s + q;
+    const int64_t m = idx / per_mat;
+    int64_t rest = idx - m * per_mat;
+    const int b = (int)(rest & 7);
+    rest >>= 3;
+    const int q = (int)(rest & 3);
+    rest >>= 2;
+    const int rr = (int)(rest % kTileRows);
+    rest /= kTileRows;
+    const int p = (int)(rest % (rec / 8));
+    const int tile = (int)(rest / (rec / 8));
+    const int r = tile * kTileRows + rr;
+    const int g = 4 * (8 * p + b) + q;
     const uint8_t e = g < groups ? scales[(m * rows + r) * groups + g] : (uint8_t)0;
-    packed[m * packed_stride + scale_base + ((int64_t)r * 4 + q) * rec + s] = e;
+    packed[m * packed_stride + scale_base + packed_scale_word(groups, r, p, q) + b] = e;
   }
 }
 

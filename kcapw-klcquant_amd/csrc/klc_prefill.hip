@@ -171,18 +171,21 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // step, <= 24 steps) is loaded once up front: per-step scale words, one
   // 4-byte load per lane at a 24-byte stride, cost more issue time in the
   // texture unit than the weight chunks themselves.
-  // The lane's whole scale record (one byte per step; inputs <= 3072 have
-  // <= 24 steps, so <= 24 bytes) is loaded once: per-step 4-byte scale loads
-  // at a 24-byte stride cost more issue time in the texture unit than the
-  // weight chunks themselves.  (Bytes past a shorter record belong to the
-  // next record or lie past the buffer, which loads zeros; neither is used.)
-  u32x4_t srec_lo[4];
-  u32x2_t srec_hi[4];
+  // The lane's scales for all steps (one byte per step; inputs <= 3072 have
+  // <= 24 steps: three 8-byte words) are loaded once: per-step 4-byte scale
+  // loads cost more issue time in the texture unit than the weight chunks
+  // themselves.  (Words past a shorter record repeat its last word.)
+  // (three separately named arrays: the per-step choice among them is a
+  // select, where one array indexed by a run-time word would go to scratch)
+  u32x2_t srec0[4], srec1[4], srec2[4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
-    const uint32_t r = (uint32_t)((wtile * kTileRows + rb * 16 + lr) * 4 + lq);
-    srec_lo[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, r * (uint32_t)rec, scale_base, 0);
-    srec_hi[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, r * (uint32_t)rec + 16u, scale_base, 0);
+    const int row = wtile * kTileRows + rb * 16 + lr;
+    srec0[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, (uint32_t)packed_scale_word(groups, row, 0, lq), scale_base, 0);
+    srec1[rb] = __builtin_amdgcn_raw_buffer_load_b64(
+        wbuf, (uint32_t)packed_scale_word(groups, row, min(1, rec / 8 - 1), lq), scale_base, 0);
+    srec2[rb] = __builtin_amdgcn_raw_buffer_load_b64(
+        wbuf, (uint32_t)packed_scale_word(groups, row, min(2, rec / 8 - 1), lq), scale_base, 0);
   }
   auto a_load = [&](int s, u32x4_t (&a)[4]) {
     const bool ok = s < steps && 4 * s + lq < groups;
@@ -207,13 +210,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 
   auto compute = [&](int s, int slot, const u32x4_t (&a_cur)[4]) {
     const bool live = 4 * s + lq < groups;
-    const int d = min(s >> 2, 5);  // dword of the scale record holding step s
+    const int d = min(s >> 2, 5);  // dword of the lane's scales holding step s
     float scale[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
-      const uint32_t lo = (d & 2) ? ((d & 1) ? srec_lo[rb][3] : srec_lo[rb][2])
-                                  : ((d & 1) ? srec_lo[rb][1] : srec_lo[rb][0]);
-      const uint32_t word = d >= 4 ? ((d & 1) ? srec_hi[rb][1] : srec_hi[rb][0]) : lo;
+      const u32x2_t pair = d >= 4 ? srec2[rb] : ((d & 2) ? srec1[rb] : srec0[rb]);
+      const uint32_t word = (d & 1) ? pair.y : pair.x;
       scale[rb] = cvt_scale_operand((word >> (8 * (s & 3))) & 0xffu, live);
     }
     const uint8_t* base = stage + slot * kStage;

@@ -93,26 +93,40 @@ def test_pack_roundtrip_through_packed_dequant(gpu, rows, groups):
     assert np.array_equal(d[~nan], p[~nan])
 
 
-def test_pack_layout_positions(gpu):
-    """Byte (row r, group g, byte j) lands at tile/g/row/j of the row-tile layout."""
-    rows, groups = 128, 5
+@pytest.mark.parametrize("groups", [5, 37])
+def test_pack_layout_positions(gpu, groups):
+    """Block byte (row r, group g, byte j) lands at tile/g/row/j; the scale of (r, g) at byte s % 8 of the
+    8-byte word (tile, s // 8, row in tile, g % 4), s = g // 4."""
+    rows = 128
     blocks, scales = synth.mxfp4_expert_tensors(31, 32, 1, rows, groups * 32, 0, 255)
     packed = ops.mxfp4_pack(torch.from_numpy(blocks).to(gpu), torch.from_numpy(scales).to(gpu)).cpu().numpy()[0]
-    rec = ((groups + 3) // 4 + 7) // 8 * 8  # scale record bytes per (row, group % 4)
+    rec = ((groups + 3) // 4 + 7) // 8 * 8  # scale bytes per (row, group % 4): one per 4-group step, padded to 8
     blk_bytes = rows // 64 * groups * 1024
     assert packed.size == blk_bytes + rows * 4 * rec
+
+    def word(r, p, q):
+        t, rr = divmod(r, 64)
+        return blk_bytes + t * 64 * 4 * rec + ((p * 64 + rr) * 4 + q) * 8
+
     for r in (0, 1, 63, 64, 127):
         for g in range(groups):
             t, rr = divmod(r, 64)
             off = (t * groups + g) * 1024 + rr * 16
             assert np.array_equal(packed[off:off + 16], blocks[0, r, g])
-            soff = blk_bytes + (r * 4 + g % 4) * rec + g // 4
-            assert packed[soff] == scales[0, r, g]
-        # record bytes beyond the last group are zero
+            s = g // 4
+            assert packed[word(r, s // 8, g % 4) + s % 8] == scales[0, r, g]
+        # bytes of steps past the last group are zero
         for q in range(4):
             for s in range(rec):
                 if 4 * s + q >= groups:
-                    assert packed[blk_bytes + (r * 4 + q) * rec + s] == 0
+                    assert packed[word(r, s // 8, q) + s % 8] == 0
+    # every scale byte is accounted for: the scale area is exactly the words above
+    seen = np.zeros(rows * 4 * rec, dtype=bool)
+    for r in range(rows):
+        for q in range(4):
+            for s in range(rec):
+                seen[word(r, s // 8, q) + s % 8 - blk_bytes] = True
+    assert seen.all()
 
 
 def test_synth_fill_matches_host_generator(gpu):
