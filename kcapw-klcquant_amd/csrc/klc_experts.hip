@@ -176,8 +176,19 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
         dst[2 * i + 1] = v.y;
       }
     };
+    // Epilogue operands are loaded ahead too: the lane's output pair (the same
+    // for every tile) and the bias of its 4 rows one tile ahead, next to the
+    // scale record.  A load issued in the epilogue itself would be the
+    // youngest in flight, and waiting for it would drain the weight ring.
+    const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
+    const int out_pair = pairs[pb + tc + min(out_col, nt - 1)];
+    auto load_bias = [&](int tile) -> u32x2_t {
+      const int64_t row = (int64_t)e * rows + tile * kTileRows + wave * 16 + 4 * lq;
+      return *reinterpret_cast<const u32x2_t*>(bias + row);
+    };
     uint32_t sc[kRecWords], sc_next[kRecWords];
     load_rec(tile0, sc);
+    u32x2_t bias_cur = load_bias(tile0), bias_next = bias_cur;
     uint32_t tb = (uint32_t)tile0 * tile_bytes;
     u32x4_t ring[kR];
 #pragma unroll
@@ -215,7 +226,10 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       // the next tile's scale record is issued before the first refill that
       // reads the next tile, so waiting for it never waits for a ring load
       const int next_tile = has_next ? tile + 1 : tile;
-      if constexpr (kSteps <= kR) load_rec(next_tile, sc_next);
+      if constexpr (kSteps <= kR) {
+        load_rec(next_tile, sc_next);
+        bias_next = load_bias(next_tile);
+      }
 
       f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
       // B operands are read one step ahead of their MFMAs (LDS latency)
@@ -226,7 +240,10 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       for (int s = 0; s < kSteps; ++s) {
         __builtin_amdgcn_sched_barrier(0);  // keep each step's decode next to its MFMAs
         if constexpr (kSteps > kR) {
-          if (s == kSteps - kR) load_rec(next_tile, sc_next);
+          if (s == kSteps - kR) {
+            load_rec(next_tile, sc_next);
+            bias_next = load_bias(next_tile);
+          }
         }
         // an empty asm "modifying" the chunk pins each step's decode right
         // here, so decoded operands (16 registers per step) are never
@@ -262,13 +279,17 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       tb = nb;
 #pragma unroll
       for (int i = 0; i < kRecWords; ++i) sc[i] = sc_next[i];
+      // bias of rows row0 .. row0 + 3 as bfloat16 bits, low half first
+      const float bias_row[4] = {bf16_to_f32(bias_cur.x & 0xffffu), bf16_to_f32(bias_cur.x >> 16),
+                                 bf16_to_f32(bias_cur.y & 0xffffu), bf16_to_f32(bias_cur.y >> 16)};
+      bias_cur = bias_next;
 
       // ---- epilogue: lane holds rows 4*lq + v (v = 0..3) of the wave's 16, column lr ----
       const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
       float v[4] = {acc[0], acc[1], acc[2], acc[3]};
       if constexpr (!kDown) {
         if (lr < nt) {
-          const int pair = pairs[pb + tc + lr];
+          const int pair = out_pair;
           const int half = rows >> 1;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -277,8 +298,8 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
               gate = round_bf16(gate);
               up = round_bf16(up);
             }
-            gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
-            up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
+            gate += bias_row[2 * h];
+            up += bias_row[2 * h + 1];
             const float y = swiglu(gate, up, limit);
             const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
             if (out_raw) out_raw[idx] = y;
@@ -294,12 +315,12 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
         if ((lr & 1) == 0 && (lr >> 1) < nt) {
-          const int pair = pairs[pb + tc + (lr >> 1)];
+          const int pair = out_pair;
           float o[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float t = precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i];
-            o[i] = t + bf16_to_f32(bias[(int64_t)e * rows + row0 + i]);
+            o[i] = t + bias_row[i];
           }
           *reinterpret_cast<float4*>(out + (int64_t)pair * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
         }
