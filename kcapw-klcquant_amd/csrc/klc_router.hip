@@ -610,7 +610,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
                                                                     int32_t* __restrict__ active,
                                                                     int32_t* __restrict__ n_active,
                                                                     int32_t* __restrict__ units) {
-  extern __shared__ char dlds[];
+  extern __shared__ __align__(16) char dlds[];
   block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
 }
 
@@ -654,7 +654,9 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
     int32_t* __restrict__ offsets, int32_t* __restrict__ sorted, int32_t* __restrict__ active,
     int32_t* __restrict__ n_active, int32_t* __restrict__ units, uint32_t* counters, double* partials) {
-  extern __shared__ char lds[];  // wave sums; then the token tile's logits; then the dispatch's staging
+  // wave sums (float64); then the token tile's logits; then the dispatch's
+  // staging.  16-byte aligned: the static flag below comes first in LDS.
+  extern __shared__ __align__(16) char lds[];
   __shared__ uint32_t flag;
   const int et = blockIdx.x, tt = blockIdx.y, ks = blockIdx.z;
   const int n_et = gridDim.x, n_tt = gridDim.y, n_ks = gridDim.z;

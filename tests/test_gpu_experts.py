@@ -58,8 +58,8 @@ def assert_close(got, want, what, precision="fp32"):
     assert bad.size == 0, f"{what}: {bad.shape[0]} elements out of tolerance, worst {err.max():.3e}"
 
 
-def check_layer(gpu, host, dev_w, x, k, precision):
-    layer = moe.MoELayer(dev_w, experts_per_token=k, precision=precision)
+def check_layer(gpu, host, dev_w, x, k, precision, path="auto"):
+    layer = moe.MoELayer(dev_w, experts_per_token=k, precision=precision, path=path)
     xt = bf16_tensor(x, gpu)
     det = layer.forward_detailed(xt)
     fused_ids = torch.empty((x.shape[0], k), dtype=torch.int32, device=gpu)
@@ -120,6 +120,14 @@ def test_gpt_oss_20b_shape_layer(gpu, precision):
 def test_gpt_oss_120b_shape_batch8(gpu):
     host, dev_w, x = build(gpu, 2, 2880, 2880, 128, 8)
     check_layer(gpu, host, dev_w, x, 4, "fp32")
+
+
+@pytest.mark.parametrize("n_tok", [64, 45])
+def test_gemv_layer_many_units_per_expert(gpu, n_tok):
+    """Decode GEMVs with 4-6 gate_up and 8-12 down units per expert (20B shape, 8 experts): in the one-call
+    layer every down workgroup waits for several gate_up workgroups of its expert."""
+    host, dev_w, x = build(gpu, 5, 2880, 2880, 8, n_tok)
+    check_layer(gpu, host, dev_w, x, 4, "fp32", path="gemv")
 
 
 def test_many_tokens_one_expert(gpu):
