@@ -241,7 +241,8 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
   for (int r = 0; r < k; ++r) sum += readlane_f64(ex, r);
   if (lane < k) {
     const int64_t o = t * k + lane;
-    ids[o] = my_id;
+    // agent scope: the decode router's final dispatch may run in another workgroup
+    __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (values) values[o] = my_val;
     weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
   }
@@ -307,7 +308,8 @@ __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n
   for (int rd = 0; rd < k; ++rd) sum += __shfl(ex, q * 16 + rd);
   if (q < n_valid && r < k) {
     const int64_t o = (t0 + q) * k + r;
-    ids[o] = my_id;
+    // agent scope: the decode router's final dispatch may run in another workgroup
+    __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (values) values[o] = my_val;
     weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
   }
@@ -465,7 +467,9 @@ __device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, 
   for (int p0 = 0; p0 < n_pairs; p0 += 8 * kDispatchThreads) {
     int32_t v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = ids[min(p0 + j * kDispatchThreads + tid, n_pairs - 1)];
+    for (int j = 0; j < 8; ++j)
+      v[j] = __hip_atomic_load(ids + min(p0 + j * kDispatchThreads + tid, n_pairs - 1), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int p = p0 + j * kDispatchThreads + tid;
@@ -614,28 +618,29 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
   block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
 }
 
-// Last-arriver election among `expected` workgroups on *ctr.  Every wave
-// first waits for its own stores to reach L2; thread 0 then releases them at
-// device scope (L2 write-back), counts the arrival, and in the last workgroup
-// resets the counter (for the next launch) and acquires the others' writes
-// (L2 and L1 invalidation, shared by the workgroup's waves on this CU).
-// Returns the same value in every thread.
+// Last-arriver election among `expected` workgroups on *ctr.  Everything
+// the workgroups hand over (partial logits, ids) is stored and loaded at
+// agent scope (sc1: stores write through the XCD's L2, loads miss in the
+// non-coherent caches), so no fence is needed: every wave waits for its own
+// stores to complete, then thread 0 counts the arrival, and the last
+// workgroup resets the counter for the next launch.  (An agent-scope fence
+// would write back and invalidate the whole L2.)  Returns the same value in
+// every thread.
 __device__ bool arrive_last(uint32_t* ctr, uint32_t expected, uint32_t* flag) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
-    const uint32_t prev = atomicAdd(ctr, 1u);
+    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t last = prev == expected - 1u ? 1u : 0u;
-    if (last) {
-      atomicExch(ctr, 0u);
-      __threadfence();
-    }
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = last;
   }
   __syncthreads();
   return *flag != 0u;
 }
+
+// Cache policy of the partial logits (agent scope, see arrive_last).
+constexpr int kAgentScope = 16;
 
 // Router of a decode batch in one launch.  Workgroup (et, tt, ks) computes
 // the partial logits of the tile (experts 16 et.., tokens 16 tt..) over the
@@ -669,32 +674,42 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   const int ce = min(cb + per_slice, nchunk);
   const f64x4_t part =
       router_block_dot(x, w, n_tok, hidden, n_exp, et * kRouterTile, t0, cb, ce, nullptr, reinterpret_cast<double*>(lds));
-  double* tile_parts = partials + (int64_t)tt * n_et * n_ks * 256;  // [n_et][n_ks][256]
-  if (threadIdx.x < kWave) {
-    double* slot = tile_parts + ((int64_t)et * n_ks + ks) * 256 + lane * 4;
-    reinterpret_cast<double2*>(slot)[0] = make_double2(part[0], part[1]);
-    reinterpret_cast<double2*>(slot)[1] = make_double2(part[2], part[3]);
+  // [n_et][n_ks][64 lanes][4] float64; lane l holds token t0 + l % 16, so
+  // only lanes of the tile's real tokens store and read their partials
+  double* tile_parts = partials + (int64_t)tt * n_et * n_ks * 256;
+  const __amdgpu_buffer_rsrc_t pbuf = __builtin_amdgcn_make_buffer_rsrc(
+      tile_parts, (short)0, (int)(n_et * n_ks * 256 * sizeof(double)), kBufferWord3);
+  const bool real_tok = t0 + (lane & 15) < n_tok;
+  if (threadIdx.x < kWave && real_tok) {
+    const uint32_t off = (uint32_t)(((et * n_ks + ks) * 256 + lane * 4) * sizeof(double));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, make_double2(part[0], part[1])), pbuf, off, 0,
+                                           kAgentScope);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, make_double2(part[2], part[3])), pbuf, off,
+                                           16, kAgentScope);
   }
   if (!arrive_last(counters + tt, (uint32_t)(n_et * n_ks), &flag)) return;
   // sums: wave w takes expert tiles w, w + 4, ..., all slices' loads in flight
   uint16_t* rows = reinterpret_cast<uint16_t*>(lds);  // [16][n_exp]
   for (int e_t = wave; e_t < n_et; e_t += 4) {
-    const double* src = tile_parts + (int64_t)e_t * n_ks * 256 + lane * 4;
-    double2 v[2 * kRouterMaxSlices];
+    if (!real_tok) continue;
+    u32x4_t v[2 * kRouterMaxSlices];
 #pragma unroll
     for (int q = 0; q < kRouterMaxSlices; ++q) {
       const int qq = min(q, n_ks - 1);
-      v[2 * q] = reinterpret_cast<const double2*>(src + qq * 256)[0];
-      v[2 * q + 1] = reinterpret_cast<const double2*>(src + qq * 256)[1];
+      const uint32_t off = (uint32_t)(((e_t * n_ks + qq) * 256 + lane * 4) * sizeof(double));
+      v[2 * q] = __builtin_amdgcn_raw_buffer_load_b128(pbuf, off, 0, kAgentScope);
+      v[2 * q + 1] = __builtin_amdgcn_raw_buffer_load_b128(pbuf, off, 16, kAgentScope);
     }
     f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int q = 0; q < kRouterMaxSlices; ++q) {
       if (q < n_ks) {
-        acc[0] += v[2 * q].x;
-        acc[1] += v[2 * q].y;
-        acc[2] += v[2 * q + 1].x;
-        acc[3] += v[2 * q + 1].y;
+        const double2 lo = __builtin_bit_cast(double2, v[2 * q]);
+        const double2 hi = __builtin_bit_cast(double2, v[2 * q + 1]);
+        acc[0] += lo.x;
+        acc[1] += lo.y;
+        acc[2] += hi.x;
+        acc[3] += hi.y;
       }
     }
     router_tile_store(acc, b, logits, n_tok, n_exp, e_t * kRouterTile, t0, rows);
