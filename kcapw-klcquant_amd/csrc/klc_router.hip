@@ -29,6 +29,7 @@ namespace {
 constexpr int kRouterTile = 16;    // experts and tokens per logits tile
 constexpr int kRouterDepth = 4;    // 32-deep chunks per lane in flight
 constexpr int kRouterMaxSlices = 8;  // hidden-dimension slices of the decode router
+constexpr int kRouterMaxK = 32;      // experts per token (checked on the host)
 #ifndef KLC_DECODE_ROUTER_WORKGROUPS
 #define KLC_DECODE_ROUTER_WORKGROUPS 128
 #endif
@@ -123,8 +124,8 @@ __device__ f64x4_t router_block_dot(const uint16_t* __restrict__ x, const uint16
 // The calling wave rounds a tile's sums (its lanes holding them in the MFMA
 // D layout) like F.linear in bfloat16: bf16(f32(sum) + b).  Optionally also
 // into an LDS copy [16 tokens][n_exp] of the token tile's logits.
-__device__ void router_tile_store(f64x4_t acc, const uint16_t* __restrict__ b, uint16_t* logits, int n_tok,
-                                  int n_exp, int e0, int t0, uint16_t* lds_rows = nullptr) {
+__device__ __forceinline__ void router_tile_store(f64x4_t acc, const float (&bias4)[4], uint16_t* logits, int n_tok,
+                                                  int n_exp, int e0, int t0, uint16_t* lds_rows = nullptr) {
   const int lane = threadIdx.x & 63;
   const int tok = t0 + (lane & 15);
   if (tok >= n_tok) return;
@@ -132,7 +133,7 @@ __device__ void router_tile_store(f64x4_t acc, const uint16_t* __restrict__ b, u
   for (int i = 0; i < 4; ++i) {
     const int e = e0 + (lane >> 4) + 4 * i;
     if (e < n_exp) {
-      const uint16_t v = (uint16_t)f32_to_bf16_rne((float)acc[i] + bf16_to_f32(b[e]));
+      const uint16_t v = (uint16_t)f32_to_bf16_rne((float)acc[i] + bias4[i]);
       logits[(int64_t)tok * n_exp + e] = v;
       if (lds_rows != nullptr) lds_rows[(lane & 15) * n_exp + e] = v;
     }
@@ -150,7 +151,15 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t*
   const int t0 = blockIdx.y * kRouterTile;
   const f64x4_t acc = router_block_dot(x, w, n_tok, hidden, n_exp, e0, t0, 0, (hidden + 31) >> 5,
                                        blockIdx.x == 0 ? x_f32 : nullptr, red);
-  if (threadIdx.x < kWave) router_tile_store(acc, b, logits, n_tok, n_exp, e0, t0);
+  if (threadIdx.x < kWave) {
+    float bias4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + ((threadIdx.x & 63) >> 4) + 4 * i;
+      bias4[i] = e < n_exp ? bf16_to_f32(b[e]) : 0.0f;
+    }
+    router_tile_store(acc, bias4, logits, n_tok, n_exp, e0, t0);
+  }
 }
 
 // Orderable key: larger key = larger logit; NaN is the largest value; -0 == +0;
@@ -209,7 +218,7 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
 template <int kSlots>
 __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_exp, int k, int64_t t,
                                                    int32_t* __restrict__ ids, float* __restrict__ values,
-                                                   uint16_t* __restrict__ weights) {
+                                                   uint16_t* __restrict__ weights, int32_t* lds_ids) {
   const int lane = threadIdx.x & 63;
   uint64_t keys[kSlots];
 #pragma unroll
@@ -243,6 +252,7 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
     const int64_t o = t * k + lane;
     // agent scope: the decode router's final dispatch may run in another workgroup
     __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lds_ids != nullptr) lds_ids[o] = my_id;
     if (values) values[o] = my_val;
     weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
   }
@@ -250,13 +260,13 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
 
 __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t,
                                                  int32_t* __restrict__ ids, float* __restrict__ values,
-                                                 uint16_t* __restrict__ weights) {
+                                                 uint16_t* __restrict__ weights, int32_t* lds_ids) {
   const int slots = (n_exp + kWave - 1) / kWave;  // <= kTopkMaxPerLane (checked on the host)
-  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, ids, values, weights);
-  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, ids, values, weights);
-  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, ids, values, weights);
-  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, ids, values, weights);
-  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights);
+  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, ids, values, weights, lds_ids);
+  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, ids, values, weights, lds_ids);
+  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, ids, values, weights, lds_ids);
+  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, ids, values, weights, lds_ids);
+  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights, lds_ids);
 }
 
 // Top-k + softmax of 4 tokens at once by one wave: the 16 lanes of row q
@@ -270,7 +280,7 @@ __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp,
 template <int kSlots, typename RowFn>
 __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n_exp, int k, int64_t t0,
                                                   int32_t* __restrict__ ids, float* __restrict__ values,
-                                                  uint16_t* __restrict__ weights) {
+                                                  uint16_t* __restrict__ weights, int32_t* lds_ids) {
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
   const int r = lane & 15;
@@ -310,6 +320,7 @@ __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n
     const int64_t o = (t0 + q) * k + r;
     // agent scope: the decode router's final dispatch may run in another workgroup
     __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lds_ids != nullptr) lds_ids[o] = my_id;
     if (values) values[o] = my_val;
     weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
   }
@@ -317,16 +328,17 @@ __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n
 
 // Top-k of tokens t0 .. t0 + n - 1 (n <= 4) by one wave: the row-parallel
 // form when the row fits (n_exp <= 256, k <= 16), else token by token.
+// lds_ids (optional): a second copy of the ids in LDS, same indices.
 template <typename RowFn>
 __device__ __forceinline__ void topk_softmax_tokens(RowFn rows, int n, int n_exp, int k, int64_t t0,
                                                     int32_t* __restrict__ ids, float* __restrict__ values,
-                                                    uint16_t* __restrict__ weights) {
+                                                    uint16_t* __restrict__ weights, int32_t* lds_ids = nullptr) {
   if (k <= 16 && n_exp <= 256) {
-    if (n_exp <= 64) topk_softmax_quad<4>(rows, n, n_exp, k, t0, ids, values, weights);
-    else if (n_exp <= 128) topk_softmax_quad<8>(rows, n, n_exp, k, t0, ids, values, weights);
-    else topk_softmax_quad<16>(rows, n, n_exp, k, t0, ids, values, weights);
+    if (n_exp <= 64) topk_softmax_quad<4>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids);
+    else if (n_exp <= 128) topk_softmax_quad<8>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids);
+    else topk_softmax_quad<16>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids);
   } else {
-    for (int q = 0; q < n; ++q) topk_softmax_row(rows(q), n_exp, k, t0 + q, ids, values, weights);
+    for (int q = 0; q < n; ++q) topk_softmax_row(rows(q), n_exp, k, t0 + q, ids, values, weights, lds_ids);
   }
 }
 
@@ -437,13 +449,24 @@ __device__ __forceinline__ void wave_peers(const uint32_t (&key)[N], uint64_t (&
   }
 }
 
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads it
+// does not wait for the workgroup's outstanding global stores.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Stable counting sort of the pairs by expert, by one 256-thread block, and
 // the work-unit lists (klc_common.h).  A pair's position is its expert's
 // offset + the pairs of that expert in earlier waves' chunks + its rank in
 // its wave's chunks (ballots within a chunk, a per-wave running count across
-// chunks), so no step is serial over pairs.  lds holds
-// dispatch_lds_bytes(n_pairs, n_exp) bytes.
-__device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
+// chunks), so no step is serial over pairs.  get_id(p) returns pair p's
+// expert id; lds holds dispatch_lds_bytes(n_pairs, n_exp) bytes.  The steps
+// hand over LDS only, so the barriers between them do not wait for earlier
+// global stores.
+template <typename IdFn>
+__device__ __forceinline__ void block_dispatch(IdFn get_id, int n_pairs, int n_exp, int32_t* __restrict__ offsets,
                                int32_t* __restrict__ sorted, int32_t* __restrict__ active,
                                int32_t* __restrict__ n_active, int32_t* __restrict__ units, char* lds) {
   const int tid = threadIdx.x;
@@ -467,16 +490,14 @@ __device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, 
   for (int p0 = 0; p0 < n_pairs; p0 += 8 * kDispatchThreads) {
     int32_t v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      v[j] = __hip_atomic_load(ids + min(p0 + j * kDispatchThreads + tid, n_pairs - 1), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    for (int j = 0; j < 8; ++j) v[j] = get_id(min(p0 + j * kDispatchThreads + tid, n_pairs - 1));
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int p = p0 + j * kDispatchThreads + tid;
       if (p < n_pairs) sid[p] = (v[j] >= 0 && v[j] < n_exp) ? (uint16_t)v[j] : (uint16_t)0xffffu;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // 1. ranks: within a chunk from the ballots, plus the wave's running count
   //    of the expert (read by all its lanes, then advanced by the lowest one;
   //    a wave's LDS accesses complete in program order)
@@ -504,7 +525,7 @@ __device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, 
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   // 2. per expert: the waves' counts become their exclusive prefix; totals
   //    and unit counts
   for (int e = tid; e < n_exp; e += kDispatchThreads) {
@@ -521,7 +542,7 @@ __device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, 
     udn[e] = (run + kUnitTokensDown - 1) / kUnitTokensDown;
     ugm[e] = (run + kUnitTokensGemm - 1) / kUnitTokensGemm;
   }
-  __syncthreads();
+  lds_barrier();
   // total[] becomes the expert offsets, flags[] the active-list positions,
   // ugu[]/udn[]/ugm[] the first unit of each expert: one wave per array
   if (wave == 0) {
@@ -534,7 +555,7 @@ __device__ __forceinline__ void block_dispatch(const int32_t* ids, int n_pairs, 
   } else {
     wave_exclusive_scan_256(udn, n_exp, &sums[3], lane);
   }
-  __syncthreads();
+  lds_barrier();
   // 3. scatter
   for (int p = tid; p < n_pairs; p += kDispatchThreads) {
     const uint32_t e = sid[p];
@@ -615,7 +636,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
                                                                     int32_t* __restrict__ n_active,
                                                                     int32_t* __restrict__ units) {
   extern __shared__ __align__(16) char dlds[];
-  block_dispatch(ids, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
+  block_dispatch([&](int p) { return ids[p]; }, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
 }
 
 // Last-arriver election among `expected` workgroups on *ctr.  Everything
@@ -663,6 +684,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   // staging.  16-byte aligned: the static flag below comes first in LDS.
   extern __shared__ __align__(16) char lds[];
   __shared__ uint32_t flag;
+  __shared__ int32_t tile_ids[kRouterTile * kRouterMaxK];  // one token tile's ids, for its own dispatch
   const int et = blockIdx.x, tt = blockIdx.y, ks = blockIdx.z;
   const int n_et = gridDim.x, n_tt = gridDim.y, n_ks = gridDim.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -692,6 +714,13 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   uint16_t* rows = reinterpret_cast<uint16_t*>(lds);  // [16][n_exp]
   for (int e_t = wave; e_t < n_et; e_t += 4) {
     if (!real_tok) continue;
+    // the bias loads go first: they are independent of the partials
+    float bias4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e_t * kRouterTile + (lane >> 4) + 4 * i;
+      bias4[i] = e < n_exp ? bf16_to_f32(b[e]) : 0.0f;
+    }
     u32x4_t v[2 * kRouterMaxSlices];
 #pragma unroll
     for (int q = 0; q < kRouterMaxSlices; ++q) {
@@ -712,21 +741,25 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
         acc[3] += hi.y;
       }
     }
-    router_tile_store(acc, b, logits, n_tok, n_exp, e_t * kRouterTile, t0, rows);
+    router_tile_store(acc, bias4, logits, n_tok, n_exp, e_t * kRouterTile, t0, rows);
   }
-  __syncthreads();
+  lds_barrier();  // the rows are in LDS; the logits' global stores need not have completed
   {
     const int tw = t0 + 4 * wave;  // 4 tokens per wave
     if (tw < n_tok)
       topk_softmax_tokens([&](int q) { return rows + (tw - t0 + q) * n_exp; }, min(4, n_tok - tw), n_exp, k, tw, ids,
-                          values, weights);
+                          values, weights, n_tt == 1 ? tile_ids : nullptr);
   }
   if (n_tt > 1) {
     if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;
+    block_dispatch([&](int p) { return __hip_atomic_load(ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
+                   n_tok * k, n_exp, offsets, sorted, active, n_active, units, lds);
   } else {
-    __syncthreads();
+    // one token tile: its ids are still in LDS
+    lds_barrier();
+    block_dispatch([&](int p) { return tile_ids[p]; }, n_tok * k, n_exp, offsets, sorted, active, n_active, units,
+                   lds);
   }
-  block_dispatch(ids, n_tok * k, n_exp, offsets, sorted, active, n_active, units, lds);
 }
 
 }  // namespace
