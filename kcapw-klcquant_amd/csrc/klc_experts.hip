@@ -91,20 +91,29 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
     float limit, int precision, int tpw) {
-  extern __shared__ uint16_t xs[];  // [kVRows][row_stride] bfloat16 bits
+  extern __shared__ __align__(16) uint16_t xs[];  // [kVRows][row_stride] bfloat16 bits
 
-  const int u = blockIdx.y;
-  if (u >= *n_units) return;
-  const int32_t unit = units[u];
-  const int e = unit_expert(unit);
-  const int pb = offsets[e];
-  const int tok_per_pass = kDown ? kUnitTokensDown : kUnitTokensGateUp;
-  const int tc = unit_pass(unit) * tok_per_pass;  // first token of this unit
-  const int nt = min(tok_per_pass, offsets[e + 1] - pb - tc);
+  // Start-up: each load is issued as soon as its address is known, so the
+  // weight stream starts after two dependent levels (unit count and unit;
+  // the expert's offsets and matrix pointer) instead of one per value.
   const int tiles = rows / kTileRows;
   const int tile0 = blockIdx.x * tpw;
   const int ntile = min(tpw, tiles - tile0);
   if (ntile <= 0) return;
+  const int u = blockIdx.y;
+  const int n_u = *n_units;
+  const int32_t unit = units[u];  // u < the unit capacity: always readable
+  // both loads are issued before the branch waits (the compiler would
+  // otherwise sink the unit's load below it)
+  asm volatile("" ::"s"(unit), "s"(n_u));
+  if (u >= n_u) return;
+  const int e = unit_expert(unit);
+  const int pb = offsets[e];
+  const int pe = offsets[e + 1];
+  const uint8_t* const wmat = wptr[e];
+  const int tok_per_pass = kDown ? kUnitTokensDown : kUnitTokensGateUp;
+  const int tc = unit_pass(unit) * tok_per_pass;  // first token of this unit
+  const int nt = min(tok_per_pass, pe - pb - tc);
   const int in_dim = groups * 32;
   const int cpr = groups * 4;                   // 16-byte activation chunks per row
   const int row_stride = kSteps * 128 + 8;      // bf16 elements per staged row (zero padded)
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   // the expert matrix as a buffer: weight chunks and scale records are read
   // with a per-lane VGPR offset and a uniform (SGPR) step offset
   const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)wptr[e], (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
+      (void*)wmat, (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
   // chunk of step t in a tile = tile offset + 4096 t + voff.  kSteps is a
   // multiple of the ring size and may exceed the real step count g4: lanes
   // whose group 4t + lq is past the last group read out of range (0, no
@@ -139,16 +148,53 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   {
     const int nrows = kDown ? 2 * nt : nt;
 
-    // ---- 1. activation-row loads (row sources are uniform: scalar loads) ----
-    int src[kVRows];
+    // ---- 1. the unit's pairs: one vector load, issued before the weight
+    //      stream so that waiting for it does not wait for any weight chunk.
+    //      Lane r < kVRows holds staged row r's pair; the lane's output pair
+    //      (the same for every tile) comes in the same round trip. ----
+    const int rr_l = min(lane & (kVRows - 1), nrows - 1);
+    const int pair_l = pairs[pb + tc + (kDown ? rr_l >> 1 : rr_l)];
+    const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
+    const int out_pair = pairs[pb + tc + min(out_col, nt - 1)];
+
+    // ---- 2. scale record of the first tile, the first tile's bias, then the
+    //      ring prologue ----
+    // the lane's scales of a tile: 8-byte word i holds steps 8i .. 8i + 7 of
+    // (row, quarter); a wave's load of word i is 512 contiguous bytes
+    constexpr int kRecWords = (kSteps + 7) / 8 * 2;
+    auto load_rec = [&](int tile, uint32_t* dst) {
 #pragma unroll
-    for (int r = 0; r < kVRows; ++r) {
-      const int rr = min(r, nrows - 1);
-      if constexpr (kDown) {
-        src[r] = pairs[pb + tc + (rr >> 1)];
-      } else {
-        src[r] = pairs[pb + tc + rr] / k_top;
+      for (int i = 0; i < kRecWords / 2; ++i) {
+        const uint32_t off = (uint32_t)packed_scale_word(groups, tile * kTileRows + trow, min(i, rec / 8 - 1), lq);
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, off, scale_base, kStreamPolicy);
+        dst[2 * i] = v.x;
+        dst[2 * i + 1] = v.y;
       }
+    };
+    // Epilogue operands are loaded ahead too: the bias of the lane's 4 rows
+    // one tile ahead, next to the scale record.  A load issued in the
+    // epilogue itself would be the youngest in flight, and waiting for it
+    // would drain the weight ring.
+    auto load_bias = [&](int tile) -> u32x2_t {
+      const int64_t row = (int64_t)e * rows + tile * kTileRows + wave * 16 + 4 * lq;
+      return *reinterpret_cast<const u32x2_t*>(bias + row);
+    };
+    uint32_t sc[kRecWords], sc_next[kRecWords];
+    load_rec(tile0, sc);
+    u32x2_t bias_cur = load_bias(tile0), bias_next = bias_cur;
+    uint32_t tb = (uint32_t)tile0 * tile_bytes;
+    u32x4_t ring[kR];
+    __builtin_amdgcn_sched_barrier(0);  // the ring goes out before the rows' loads
+#pragma unroll
+    for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. activation-row loads (row sources read back from the pairs) ----
+    int src[kVRows];
+    {
+      const int src_l = kDown ? pair_l : pair_l / k_top;
+#pragma unroll
+      for (int r = 0; r < kVRows; ++r) src[r] = __builtin_amdgcn_readlane(src_l, r);
     }
     u32x4_t xv[kLoads];
 #pragma unroll
@@ -163,38 +209,7 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
       xv[i] = *reinterpret_cast<const u32x4_t*>(p);
     }
 
-    // ---- 2. scale record of the first tile, then the ring prologue ----
-    // the lane's scales of a tile: 8-byte word i holds steps 8i .. 8i + 7 of
-    // (row, quarter); a wave's load of word i is 512 contiguous bytes
-    constexpr int kRecWords = (kSteps + 7) / 8 * 2;
-    auto load_rec = [&](int tile, uint32_t* dst) {
-#pragma unroll
-      for (int i = 0; i < kRecWords / 2; ++i) {
-        const uint32_t off = (uint32_t)packed_scale_word(groups, tile * kTileRows + trow, min(i, rec / 8 - 1), lq);
-        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, off, scale_base, kStreamPolicy);
-        dst[2 * i] = v.x;
-        dst[2 * i + 1] = v.y;
-      }
-    };
-    // Epilogue operands are loaded ahead too: the lane's output pair (the same
-    // for every tile) and the bias of its 4 rows one tile ahead, next to the
-    // scale record.  A load issued in the epilogue itself would be the
-    // youngest in flight, and waiting for it would drain the weight ring.
-    const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
-    const int out_pair = pairs[pb + tc + min(out_col, nt - 1)];
-    auto load_bias = [&](int tile) -> u32x2_t {
-      const int64_t row = (int64_t)e * rows + tile * kTileRows + wave * 16 + 4 * lq;
-      return *reinterpret_cast<const u32x2_t*>(bias + row);
-    };
-    uint32_t sc[kRecWords], sc_next[kRecWords];
-    load_rec(tile0, sc);
-    u32x2_t bias_cur = load_bias(tile0), bias_next = bias_cur;
-    uint32_t tb = (uint32_t)tile0 * tile_bytes;
-    u32x4_t ring[kR];
-#pragma unroll
-    for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
-
-    // ---- 3. activation rows into LDS (waits only for the oldest loads) ----
+    // ---- 4. activation rows into LDS ----
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int id = (int)threadIdx.x + i * kGemvThreads;
