@@ -377,13 +377,20 @@ GemvKernel<kDown> gemv_kernel_for(int steps) {
 
 size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * (steps * 128 + 8) * 2; }
 
-// Tiles each workgroup streams: about three rounds of workgroups over the
-// chip (3 resident per CU x 256 CUs each round), so workgroups that finish
-// early are replaced and the tail stays short; one tile per workgroup when
-// few units exist.  max_units is an upper bound of the units.
-int tiles_per_workgroup(int tiles, int64_t max_units) {
-  const int64_t target = 3 * 3 * 256;
+// Tiles each workgroup streams: the unit capacity's tiles spread over about
+// `target` workgroups (768 are resident at once: 3 per CU), so workgroups
+// that finish early are replaced and the tail stays short; one tile per
+// workgroup when few units exist.  max_units is an upper bound of the units.
+// Measured at batches 64 and 128 (120B shape): gate_up is fastest with 2
+// tiles per workgroup, down with 3 -- one tile per workgroup is much slower
+// for both, since every workgroup start stages 8 activation rows and waits
+// for a chain of index loads.
+constexpr int64_t kGemvWorkgroupsUp = 6144, kGemvMaxTilesUp = 2;
+constexpr int64_t kGemvWorkgroupsDown = 2304, kGemvMaxTilesDown = 3;
+
+int tiles_per_workgroup(int tiles, int64_t max_units, int64_t target, int64_t max_tpw) {
   int64_t tpw = (int64_t)tiles * max_units / target;
+  if (tpw > max_tpw) tpw = max_tpw;
   if (tpw < 1) tpw = 1;
   if (tpw > tiles) tpw = tiles;
   return (int)tpw;
@@ -476,7 +483,7 @@ int launch_gate_up(const void* const* w, const void* bias, const void* x, int64_
                    float limit, int precision, void* gated_split, float* gated_raw, hipStream_t stream) {
   const int tiles = (int)(2 * inter / kTileRows);
   const int64_t cap = units_capacity(n_tok * k, n_exp, kUnitTokensGateUp);
-  const int tpw = tiles_per_workgroup(tiles, cap);
+  const int tpw = tiles_per_workgroup(tiles, cap, kGemvWorkgroupsUp, kGemvMaxTilesUp);
   const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)cap);
   const int steps = gemv_steps((int)(hidden / 32));
   gemv_kernel_for<false>(steps)<<<grid, kGemvThreads, gemv_lds_bytes(steps), stream>>>(
@@ -493,7 +500,7 @@ int launch_down(const void* const* w, const void* bias, const void* gated_split,
                 int precision, float* eo, hipStream_t stream) {
   const int tiles = (int)(hidden / kTileRows);
   const int64_t cap = units_capacity(n_pairs, n_exp, kUnitTokensDown);
-  const int tpw = tiles_per_workgroup(tiles, cap);
+  const int tpw = tiles_per_workgroup(tiles, cap, kGemvWorkgroupsDown, kGemvMaxTilesDown);
   const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)cap);
   const int32_t* list = units + units_offset_down(n_pairs, n_exp);
   const int steps = gemv_steps((int)(inter / 32));
