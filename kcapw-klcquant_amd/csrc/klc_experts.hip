@@ -417,6 +417,49 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   out[(int64_t)t * hidden + h] = (uint16_t)f32_to_bf16_rne(acc);
 }
 
+// The same combine, 4 consecutive outputs per thread, for hidden % 4 == 0
+// and 16-byte aligned expert outputs (8-byte aligned out/residual): every
+// slot's 16-byte load is issued before the first is used, so a token costs
+// one memory round trip instead of one per slot.  Same operations, same
+// order, per output.
+constexpr int kCombineMaxK = 4;  // slots whose loads are in flight together (top-4)
+__global__ __launch_bounds__(256) void combine4_kernel(const float* __restrict__ eo, const uint16_t* __restrict__ w,
+                                                       const uint16_t* residual, int k, int hidden,
+                                                       uint16_t* out) {  // out may alias residual
+  const int t = blockIdx.y;
+  const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (h >= hidden) return;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j0 = 0; j0 < k; j0 += kCombineMaxK) {
+    float4 v[kCombineMaxK];
+    float wj[kCombineMaxK];
+#pragma unroll
+    for (int q = 0; q < kCombineMaxK; ++q) {
+      const int64_t p = (int64_t)t * k + min(j0 + q, k - 1);
+      wj[q] = bf16_to_f32(w[p]);
+      v[q] = *reinterpret_cast<const float4*>(eo + p * hidden + h);
+    }
+#pragma unroll
+    for (int q = 0; q < kCombineMaxK; ++q) {
+      if (j0 + q < k) {
+        const float o[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = round_bf16(acc[i] + round_bf16(round_bf16(o[i]) * wj[q]));
+      }
+    }
+  }
+  if (residual != nullptr) {
+    const uint2 r = *reinterpret_cast<const uint2*>(residual + (int64_t)t * hidden + h);
+    acc[0] = bf16_to_f32(r.x & 0xffffu) + acc[0];
+    acc[1] = bf16_to_f32(r.x >> 16) + acc[1];
+    acc[2] = bf16_to_f32(r.y & 0xffffu) + acc[2];
+    acc[3] = bf16_to_f32(r.y >> 16) + acc[3];
+  }
+  const uint2 o = make_uint2(f32_to_bf16_rne(acc[0]) | (f32_to_bf16_rne(acc[1]) << 16),
+                             f32_to_bf16_rne(acc[2]) | (f32_to_bf16_rne(acc[3]) << 16));
+  *reinterpret_cast<uint2*>(out + (int64_t)t * hidden + h) = o;
+}
+
 __global__ __launch_bounds__(256) void bias_combine_kernel(const uint16_t* __restrict__ bias,
                                                            const int32_t* __restrict__ ids,
                                                            const uint16_t* __restrict__ w, int k, int hidden,
@@ -513,6 +556,15 @@ int launch_down(const void* const* w, const void* bias, const void* gated_split,
 
 int launch_combine(const float* eo, const void* w, const void* residual, int64_t n_tok, int64_t k, int64_t hidden,
                    void* out, hipStream_t stream) {
+  const bool vec = hidden % 4 == 0 && ((uintptr_t)eo & 15) == 0 && ((uintptr_t)out & 7) == 0 &&
+                   ((uintptr_t)residual & 7) == 0;
+  if (vec) {
+    const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)n_tok);
+    combine4_kernel<<<grid, 256, 0, stream>>>(eo, static_cast<const uint16_t*>(w),
+                                              static_cast<const uint16_t*>(residual), (int)k, (int)hidden,
+                                              static_cast<uint16_t*>(out));
+    return check_launch("combine4_kernel");
+  }
   const dim3 grid((unsigned)((hidden + 255) / 256), (unsigned)n_tok);
   combine_kernel<<<grid, 256, 0, stream>>>(eo, static_cast<const uint16_t*>(w),
                                            static_cast<const uint16_t*>(residual), (int)k, (int)hidden,

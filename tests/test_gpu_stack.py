@@ -36,13 +36,24 @@ def test_rms_norm_bit_exact(gpu, n_tok, hidden):
     assert np.array_equal(bf16_bits(got), rms_norm(x, w))
 
 
-def test_combine_with_residual_bit_exact(gpu):
-    n_tok, k, hidden = 9, 4, 256
+@pytest.mark.parametrize("n_tok,k,hidden,misaligned", [
+    (9, 4, 256, False),   # 4 outputs per thread, all slots' loads in flight together
+    (5, 2, 256, False),
+    (7, 6, 2880, False),  # more slots than one batch of loads
+    (6, 4, 30, False),    # hidden % 4 != 0: one output per thread
+    (4, 3, 256, True),    # expert outputs not 16-byte aligned: one output per thread
+])
+def test_combine_with_residual_bit_exact(gpu, n_tok, k, hidden, misaligned):
     eo = synth.random_normal_f32(80, n_tok * k * hidden, 0.0, 50.0).reshape(n_tok * k, hidden)
     wts = f32_to_bf16(np.abs(synth.random_normal_f32(81, n_tok * k)).reshape(n_tok, k) / 4)
     res = synth.random_normal_bf16(82, n_tok * hidden, 0.0, 20.0).reshape(n_tok, hidden)
     res_t = bf16_tensor(res, gpu)
-    got = ops.combine(torch.from_numpy(eo).to(gpu), bf16_tensor(wts, gpu), n_tok, k, residual=res_t)
+    eo_t = torch.from_numpy(eo).to(gpu)
+    if misaligned:
+        buf = torch.empty(eo.size + 1, dtype=torch.float32, device=gpu)
+        buf[1:] = eo_t.reshape(-1)
+        eo_t = buf[1:].reshape(n_tok * k, hidden)
+    got = ops.combine(eo_t, bf16_tensor(wts, gpu), n_tok, k, residual=res_t)
     torch.cuda.synchronize()
     want = residual_add(res, oex.combine(eo.reshape(n_tok, k, hidden), wts))
     assert np.array_equal(bf16_bits(got), want)
