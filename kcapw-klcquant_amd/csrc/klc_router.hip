@@ -710,38 +710,48 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
                                            16, kAgentScope);
   }
   if (!arrive_last(counters + tt, (uint32_t)(n_et * n_ks), &flag)) return;
-  // sums: wave w takes expert tiles w, w + 4, ..., all slices' loads in flight
   uint16_t* rows = reinterpret_cast<uint16_t*>(lds);  // [16][n_exp]
-  for (int e_t = wave; e_t < n_et; e_t += 4) {
+  // sums: wave w takes expert tiles w, w + 4, w + 8, ..., two per pass with
+  // both tiles' loads in flight before the first is summed
+  for (int e_t = wave; e_t < n_et; e_t += 8) {
     if (!real_tok) continue;
+    const bool second = e_t + 4 < n_et;
     // the bias loads go first: they are independent of the partials
-    float bias4[4];
+    float bias4[2][4];
+    u32x4_t v[2][2 * kRouterMaxSlices];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = e_t * kRouterTile + (lane >> 4) + 4 * i;
-      bias4[i] = e < n_exp ? bf16_to_f32(b[e]) : 0.0f;
-    }
-    u32x4_t v[2 * kRouterMaxSlices];
+    for (int h = 0; h < 2; ++h) {
+      const int et_h = h == 1 && second ? e_t + 4 : e_t;  // a missing second tile reloads the first
 #pragma unroll
-    for (int q = 0; q < kRouterMaxSlices; ++q) {
-      const int qq = min(q, n_ks - 1);
-      const uint32_t off = (uint32_t)(((e_t * n_ks + qq) * 256 + lane * 4) * sizeof(double));
-      v[2 * q] = __builtin_amdgcn_raw_buffer_load_b128(pbuf, off, 0, kAgentScope);
-      v[2 * q + 1] = __builtin_amdgcn_raw_buffer_load_b128(pbuf, off, 16, kAgentScope);
-    }
-    f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
+      for (int i = 0; i < 4; ++i) {
+        const int e = et_h * kRouterTile + (lane >> 4) + 4 * i;
+        bias4[h][i] = e < n_exp ? bf16_to_f32(b[e]) : 0.0f;
+      }
 #pragma unroll
-    for (int q = 0; q < kRouterMaxSlices; ++q) {
-      if (q < n_ks) {
-        const double2 lo = __builtin_bit_cast(double2, v[2 * q]);
-        const double2 hi = __builtin_bit_cast(double2, v[2 * q + 1]);
-        acc[0] += lo.x;
-        acc[1] += lo.y;
-        acc[2] += hi.x;
-        acc[3] += hi.y;
+      for (int q = 0; q < kRouterMaxSlices; ++q) {
+        const int qq = min(q, n_ks - 1);
+        const uint32_t off = (uint32_t)(((et_h * n_ks + qq) * 256 + lane * 4) * sizeof(double));
+        v[h][2 * q] = __builtin_amdgcn_raw_buffer_load_b128(pbuf, off, 0, kAgentScope);
+        v[h][2 * q + 1] = __builtin_amdgcn_raw_buffer_load_b128(pbuf, off, 16, kAgentScope);
       }
     }
-    router_tile_store(acc, bias4, logits, n_tok, n_exp, e_t * kRouterTile, t0, rows);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && !second) break;
+      f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int q = 0; q < kRouterMaxSlices; ++q) {
+        if (q < n_ks) {
+          const double2 lo = __builtin_bit_cast(double2, v[h][2 * q]);
+          const double2 hi = __builtin_bit_cast(double2, v[h][2 * q + 1]);
+          acc[0] += lo.x;
+          acc[1] += lo.y;
+          acc[2] += hi.x;
+          acc[3] += hi.y;
+        }
+      }
+      router_tile_store(acc, bias4[h], logits, n_tok, n_exp, (e_t + 4 * h) * kRouterTile, t0, rows);
+    }
   }
   lds_barrier();  // the rows are in LDS; the logits' global stores need not have completed
   {
