@@ -14,8 +14,9 @@ batch (64); ``per_batch`` holds B = 1, 8, 64.  ``stack`` is the 36-layer
 MoE-only decode (RMSNorm -> MoE -> residual per layer, 60.9 GB of experts
 resident, 64 sequences x 32 steps), ``prefill`` one layer over 2048 tokens
 with Zipf(1.1)-skewed routing (grouped GEMM), and ``dequant`` the standalone
-MXFP4 -> bf16 dequant of 128 down_proj experts; all are extra lines of the
-same run.  ``roofline`` is for the
+MXFP4 -> bf16 dequant of 128 down_proj experts, and ``loader`` the expert
+store's misses (page-cache-warm shard -> packed experts in HBM) against the
+safe_open chain they replace; all are extra lines of the same run.  ``roofline`` is for the
 dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
 experts the batch touches + activations in + SwiGLU output) over its average
 duration measured with HIP events recorded by the library between its
@@ -67,6 +68,8 @@ def parse_args():
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of the prefill measurement (0 = skip)")
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
     ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
+    ap.add_argument("--loader-experts", type=int, default=16,
+                    help="experts of the expert-store miss measurement (0 = skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB -> 1 GiB float32 copy kernel 5 times (HBM counter calibration)")
     return ap.parse_args()
@@ -269,6 +272,104 @@ def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
     }
 
 
+def loader_bench(torch, dev, n_experts: int, rounds: int = 3) -> dict:
+    """Expert-store misses of 120B-shape experts from a page-cache-resident shard.
+
+    ``native``: Mxfp4ExpertStore.packed_expert (shard -> pinned staging ring ->
+    device copy on the side stream -> pack).  ``safe_open_chain``: the
+    per-miss chain the store replaces (safe_open slice -> pin_memory -> .to
+    -> the same pack kernel), on the same slices.  The shard is fsync'ed
+    before timing (no writeback under the reads); the two legs run in
+    alternating order over ``rounds`` rounds (a fresh store each round) and
+    the medians are reported.
+    Expert 0 of every round is untimed (shard open, staging, allocator), and
+    the packed matrices of the two legs are compared.
+    """
+    import statistics
+    import tempfile
+
+    import numpy as np
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+
+    from klcquant_amd import ops
+    from klcquant_amd.mxfp4_expert import Mxfp4ExpertStore
+
+    rng = np.random.default_rng(11)
+    prefix = "model.layers.0.mlp.experts"
+    shapes = {"gate_up_proj": (2 * INTER, HIDDEN // 32), "down_proj": (HIDDEN, INTER // 32)}
+    tensors = {}
+    for proj, (rows, groups) in shapes.items():
+        tensors[f"{prefix}.{proj}_blocks"] = torch.from_numpy(
+            rng.integers(0, 256, (n_experts, rows, groups, 16), dtype=np.uint8))
+        tensors[f"{prefix}.{proj}_scales"] = torch.from_numpy(
+            rng.integers(118, 125, (n_experts, rows, groups), dtype=np.uint8))
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "model-00001-of-00001.safetensors"
+        save_file(tensors, str(path))
+        with open(path, "rb+") as fh:
+            os.fsync(fh.fileno())
+        (Path(tmp) / "model.safetensors.index.json").write_text(
+            json.dumps({"weight_map": {name: path.name for name in tensors}}))
+        del tensors
+        side = torch.cuda.Stream(dev)
+
+        def reference_chain(e, proj):
+            with safe_open(str(path), framework="pt", device="cpu") as handle:
+                b = handle.get_slice(f"{prefix}.{proj}_blocks")[e]
+                s = handle.get_slice(f"{prefix}.{proj}_scales")[e]
+            with torch.cuda.stream(side):
+                b_dev = b.contiguous().pin_memory().to(dev, non_blocking=True)
+                s_dev = s.contiguous().pin_memory().to(dev, non_blocking=True)
+                packed = ops.mxfp4_pack(b_dev, s_dev)[0]
+            side.synchronize()
+            return packed
+
+        times = {"native": [], "safe_open_chain": [], "copy": []}
+        same = True
+        for r in range(rounds):
+            store = Mxfp4ExpertStore(tmp, tmp, dev, dtype=torch.bfloat16, cache_bytes=1 << 40)
+            got = {}
+            for label in (("native", "safe_open_chain") if r % 2 == 0 else ("safe_open_chain", "native")):
+                got[label] = {}
+                for e in range(n_experts):
+                    if e == 1:
+                        torch.cuda.synchronize()
+                        t0 = time.perf_counter()
+                    for proj in shapes:
+                        got[label][(e, proj)] = (store.packed_expert(0, e, proj) if label == "native"
+                                                 else reference_chain(e, proj))
+                torch.cuda.synchronize()
+                times[label].append(time.perf_counter() - t0)
+            same = same and all(torch.equal(got["native"][k], got["safe_open_chain"][k]) for k in got["native"])
+            # the shard -> device copy alone (gate_up blocks, 8.3 MB per expert)
+            name = f"{prefix}.gate_up_proj_blocks"
+            shard = store.index.shard(name)
+            shard.copy_rows_to_device(name, 0, 1, dev, side)
+            t0 = time.perf_counter()
+            for e in range(1, n_experts):
+                shard.copy_rows_to_device(name, e, 1, dev, side)
+            times["copy"].append(time.perf_counter() - t0)
+            del store, got, shard
+        torch.cuda.empty_cache()
+    med = {k: statistics.median(v) for k, v in times.items()}
+    bytes_loaded = (n_experts - 1) * (GATE_UP_EXPERT_BYTES + DOWN_EXPERT_BYTES)
+    copy_bytes = (n_experts - 1) * 2 * INTER * (HIDDEN // 32) * 16
+    return {
+        "experts_timed": n_experts - 1,
+        "rounds": rounds,
+        "bytes_per_expert": GATE_UP_EXPERT_BYTES + DOWN_EXPERT_BYTES,
+        "native_us_per_expert": round(med["native"] * 1e6 / (n_experts - 1), 1),
+        "native_gbps": round(bytes_loaded / med["native"] / 1e9, 2),
+        "safe_open_chain_us_per_expert": round(med["safe_open_chain"] * 1e6 / (n_experts - 1), 1),
+        "safe_open_chain_gbps": round(bytes_loaded / med["safe_open_chain"] / 1e9, 2),
+        "copy_rows_to_device_gbps": round(copy_bytes / med["copy"] / 1e9, 2),
+        "native_gbps_rounds": [round(bytes_loaded / t / 1e9, 2) for t in times["native"]],
+        "safe_open_chain_gbps_rounds": [round(bytes_loaded / t / 1e9, 2) for t in times["safe_open_chain"]],
+        "packed_equal": bool(same),
+    }
+
+
 def cpu_baseline(n_tokens: int) -> dict:
     """The oracle (numpy port of the reference path) on single-token route calls."""
     import numpy as np
@@ -418,6 +519,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         result["stack"] = stack_bench(torch, dev, args.stack_layers, 64, args.stack_steps, args.precision)
         print(f"[bench] stack: {result['stack']}", file=sys.stderr, flush=True)
+    if args.loader_experts > 1:
+        result["loader"] = loader_bench(torch, dev, args.loader_experts)
+        print(f"[bench] loader: {result['loader']}", file=sys.stderr, flush=True)
     if not args.skip_dequant:
         result["dequant"] = dequant_bench(torch, dev)
         print(f"[bench] dequant: {result['dequant']}", file=sys.stderr, flush=True)

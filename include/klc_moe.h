@@ -224,6 +224,51 @@ int klc_moe_layer(const void* x, const void* router_w, const void* router_b, con
 int klc_rms_norm(const void* x, const void* weight, void* out, int64_t n_tokens, int64_t hidden, float eps,
                  void* stream);
 
+/* ---- Safetensors shards (expert store misses) ----------------------------------
+ * Replace the per-miss safe_open(...).get_slice(name)[expert] -> pin_memory()
+ * -> .to(device) chain of Mxfp4ExpertStore._load_expert_tensor /
+ * _materialize_expert_matrix (mxfp4_expert.py:487-525) and the shard lookups of
+ * SafetensorIndex (streamed_loader.py:43-82).  A shard is opened and its
+ * header parsed once (klc_st_open; *handle is an opaque pointer, released by
+ * klc_st_close; lookups are read-only, so threads may share a handle).
+ * Rows [first, first + count) along dimension 0 of a tensor -- one expert of
+ * a [E, ...] tensor -- are one contiguous byte range.
+ * klc_st_tensor_info: dtype string (<= 15 chars, e.g. "U8", "BF16"), shape
+ * (up to 8 dims), absolute byte offset in the file and byte size.  Missing
+ * names give KLC_ERR_ARGUMENT; malformed headers KLC_ERR_SHAPE. */
+int klc_st_open(const char* path, void** handle);
+int klc_st_close(void* handle);
+int klc_st_tensor_info(void* handle, const char* name, char* dtype, int64_t* shape, int* ndim, int64_t* data_offset,
+                       int64_t* nbytes);
+/* rows [first, first + count) into host memory, read with pread by a pool of
+ * up to 8 threads */
+int klc_st_read_rows(void* handle, const char* name, int64_t first, int64_t count, void* dst);
+/* the same rows into device memory: read into a ring of pinned staging slots
+ * (at most 2 MiB each; staging_bytes >= 8 KiB) and copied with hipMemcpyAsync
+ * on `stream`; a slot is refilled once its previous copy has read it, so
+ * reads overlap PCIe copies.  Returns once the staging buffer is free again
+ * (every device copy is then complete). */
+int klc_st_copy_rows_to_device(void* handle, const char* name, int64_t first, int64_t count, void* staging,
+                               int64_t staging_bytes, void* dst, void* stream);
+/* n row ranges (names[i], firsts[i], counts[i]) -> dsts[i] through one ring
+ * and one final wait: an expert's blocks and scales in a single call */
+int klc_st_copy_rows_batch(void* handle, int n, const char* const* names, const int64_t* firsts,
+                           const int64_t* counts, void* const* dsts, void* staging, int64_t staging_bytes,
+                           void* stream);
+/* One expert's MXFP4 projection from the shard straight into the packed
+ * row-tile layout in device memory (what klc_mxfp4_pack makes): blocks
+ * [E, rows, G, 16] and scales [E, rows, G], both U8 in this shard, expert
+ * `expert`, rows a multiple of 64.  Chunks of whole 64-row tiles are read
+ * (pread by the pool) into slots of the pinned host staging buffer, and a
+ * pack kernel on `stream` reads each slot over PCIe and writes its tiles of
+ * `packed`; a slot is refilled once its previous pack has run.  staging must
+ * be pinned host memory (hipHostMalloc / torch pin_memory) of staging_bytes,
+ * at least two tiles (2 * 64 * G * 17 bytes); staging and packed are 16-byte
+ * aligned; packed holds klc_mxfp4_packed_bytes(rows, G).  Returns once packed
+ * is complete. */
+int klc_st_load_mxfp4_packed(void* handle, const char* blocks_name, const char* scales_name, int64_t expert,
+                             void* staging, int64_t staging_bytes, void* packed, void* stream);
+
 /* ---- Synthetic inputs -------------------------------------------------------
  * Counter-based SplitMix64 stream, identical to klcquant_amd/synth.py:
  * mode 0: n random bytes; mode 1: n bytes uniform in [lo, hi]. */

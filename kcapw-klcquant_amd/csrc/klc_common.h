@@ -16,6 +16,17 @@ namespace klc {
 int set_error(int code, const char* fmt, ...);
 // Converts the last HIP launch error (if any) into a status.
 int check_launch(const char* what);
+// Packs n_mat checkpoint-layout matrices (blocks [rows][groups][16], scales
+// [rows][groups], rows a multiple of 64) into the row-tile layout on `st`:
+// the block region of matrix m at out_blocks + m * mat_stride, its scale
+// region at out_scales + m * mat_stride.  Defined in klc_mxfp4.hip.
+int launch_pack(const uint8_t* blocks, const uint8_t* scales, uint8_t* out_blocks, uint8_t* out_scales, int64_t n_mat,
+                int rows, int groups, int64_t mat_stride, hipStream_t st);
+// The same for one matrix of `rows` rows (a multiple of 64) whose blocks and
+// scales are in pinned host memory (device-accessible addresses): the kernel
+// reads them over PCIe, in source order.  Defined in klc_mxfp4.hip.
+int launch_pack_from_host(const uint8_t* blocks, const uint8_t* scales, uint8_t* out_blocks, uint8_t* out_scales,
+                          int rows, int groups, hipStream_t st);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -11,6 +11,8 @@
 // (v_cvt_scalef32_pk_{bf16,f16,f32}_fp4), exact for every scale byte below
 // 255; the MX NaN scale 255 takes an integer path (mxfp4_f32_bits) that
 // reproduces the reference's +-inf / NaN.
+#include <algorithm>
+
 #include "klc_common.h"
 
 namespace klc {
@@ -188,10 +190,13 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
 }
 
 // Checkpoint layout -> row-tile layout: one thread per (matrix, tile, group,
-// row in tile) 16-byte chunk, writes coalesced; runs once per load.
+// row in tile) 16-byte chunk, writes coalesced; runs once per load.  The
+// block and scale regions of matrix m start at out_blocks / out_scales +
+// m * mat_stride, so a run of whole tiles can be packed into the middle of a
+// larger matrix.
 __global__ __launch_bounds__(256) void pack_blocks_kernel(const uint8_t* __restrict__ blocks,
-                                                          uint8_t* __restrict__ packed, int64_t n_mat, int rows,
-                                                          int groups, int64_t packed_stride) {
+                                                          uint8_t* __restrict__ out_blocks, int64_t n_mat, int rows,
+                                                          int groups, int64_t mat_stride) {
   const int tiles = rows / kTileRows;
   const int64_t total = n_mat * tiles * groups * kTileRows;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -204,19 +209,18 @@ __global__ __launch_bounds__(256) void pack_blocks_kernel(const uint8_t* __restr
     const int64_t m = rest / tiles;
     const int r = tile * kTileRows + rr;
     const uint4 v = *reinterpret_cast<const uint4*>(blocks + ((m * rows + r) * groups + g) * 16);
-    *reinterpret_cast<uint4*>(packed + m * packed_stride + ((int64_t)tile * groups + g) * 1024 + rr * 16) = v;
+    *reinterpret_cast<uint4*>(out_blocks + m * mat_stride + ((int64_t)tile * groups + g) * 1024 + rr * 16) = v;
   }
 }
 
 // Scale records: one thread per (matrix, row, quarter, step) byte, padding zero.
 __global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ scales,
-                                                          uint8_t* __restrict__ packed, int64_t n_mat, int rows,
-                                                          int groups, int64_t packed_stride) {
+                                                          uint8_t* __restrict__ out_scales, int64_t n_mat, int rows,
+                                                          int groups, int64_t mat_stride) {
   // one thread per packed scale byte, in packed order: (matrix, tile, pair,
   // row in tile, quarter, byte); padding bytes (steps past the last group) are 0
   const int rec = (int)packed_scale_record(groups);
   const int64_t total = n_mat * rows * 4 * rec;
-  const int64_t scale_base = packed_block_bytes(rows, groups);
   const int64_t per_mat = (int64_t)rows * 4 * rec;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
@@ -233,9 +237,95 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restr
     const int r = tile * kTileRows + rr;
     const int g = 4 * (8 * p + b) + q;
     const uint8_t e = g < groups ? scales[(m * rows + r) * groups + g] : (uint8_t)0;
-    packed[m * packed_stride + scale_base + packed_scale_word(groups, r, p, q) + b] = e;
+    out_scales[m * mat_stride + packed_scale_word(groups, r, p, q) + b] = e;
   }
 }
+
+// Packs one run of whole tiles read straight from pinned host memory (the
+// GPU reads it over PCIe, so every read is 16 bytes per lane in source order:
+// a wavefront reads 1 KiB of contiguous host memory).  Three grid-stride
+// passes: block chunks (four loads in flight per thread before the four
+// scattered 16-byte stores), scale bytes read 16 at a time and scattered
+// (a row's 32 consecutive groups land in 32 contiguous bytes), and the zero
+// bytes that pad each row's scale record.  rows * groups < 2^30.
+__global__ __launch_bounds__(256) void pack_host_kernel(const uint8_t* __restrict__ blocks,
+                                                        const uint8_t* __restrict__ scales,
+                                                        uint8_t* __restrict__ out_blocks,
+                                                        uint8_t* __restrict__ out_scales, int rows, int groups) {
+  const int n = rows * groups;  // block chunks = scale bytes
+  const int stride = (int)(gridDim.x * blockDim.x);
+  const int tid = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const uint4* src = reinterpret_cast<const uint4*>(blocks);
+  uint4* dst = reinterpret_cast<uint4*>(out_blocks);
+  for (int base = tid; base < n; base += 4 * stride) {
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (base + k * stride < n) v[k] = src[base + k * stride];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = base + k * stride;
+      if (i < n) {
+        const int r = i / groups, g = i - r * groups;
+        dst[((r / kTileRows) * groups + g) * kTileRows + (r % kTileRows)] = v[k];
+      }
+    }
+  }
+  const uint4* ssrc = reinterpret_cast<const uint4*>(scales);
+  for (int j = tid; j < n / 16; j += stride) {
+    const uint4 v = ssrc[j];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    int r = (16 * j) / groups, g = 16 * j - r * groups;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int step = g >> 2;
+      out_scales[packed_scale_word(groups, r, step >> 3, g & 3) + (step & 7)] = (uint8_t)(w[k >> 2] >> (8 * (k & 3)));
+      if (++g == groups) {
+        g = 0;
+        ++r;
+      }
+    }
+  }
+  const int pad = 4 * (int)packed_scale_record(groups) - groups;
+  for (int k = tid; k < rows * pad; k += stride) {
+    const int r = k / pad, g = groups + (k - r * pad);
+    const int step = g >> 2;
+    out_scales[packed_scale_word(groups, r, step >> 3, g & 3) + (step & 7)] = 0;
+  }
+}
+
+}  // namespace
+
+int launch_pack_from_host(const uint8_t* blocks, const uint8_t* scales, uint8_t* out_blocks, uint8_t* out_scales,
+                          int rows, int groups, hipStream_t st) {
+  if (rows == 0) return KLC_OK;
+  KLC_REQUIRE(rows % kTileRows == 0 && (int64_t)rows * groups < (int64_t)1 << 30 &&
+                  (int64_t)rows * 4 * packed_scale_record(groups) < (int64_t)1 << 31,
+              KLC_ERR_UNSUPPORTED, "pack_host_kernel: %d rows x %d groups in one run", rows, groups);
+  // PCIe reads: a few hundred wavefronts with four 1 KiB reads each keep
+  // enough bytes in flight; more workgroups only add contention (a plain
+  // host-to-device copy kernel measured 51.7 GB/s at 64 workgroups, 40 at 512)
+  const int64_t want = ((int64_t)rows * groups + 1023) / 1024;
+  pack_host_kernel<<<(unsigned)std::min<int64_t>(128, std::max<int64_t>(1, want)), 256, 0, st>>>(
+      blocks, scales, out_blocks, out_scales, rows, groups);
+  return check_launch("pack_host_kernel");
+}
+
+int launch_pack(const uint8_t* blocks, const uint8_t* scales, uint8_t* out_blocks, uint8_t* out_scales, int64_t n_mat,
+                int rows, int groups, int64_t mat_stride, hipStream_t st) {
+  if (n_mat == 0 || rows == 0) return KLC_OK;
+  const int64_t chunks = n_mat * rows * groups;
+  const unsigned grid_b = (unsigned)((chunks + 255) / 256 < 65536 ? (chunks + 255) / 256 : 65536);
+  pack_blocks_kernel<<<grid_b, 256, 0, st>>>(blocks, out_blocks, n_mat, rows, groups, mat_stride);
+  const int rc = check_launch("pack_blocks_kernel");
+  if (rc) return rc;
+  const int64_t bytes = n_mat * rows * 4 * packed_scale_record(groups);
+  const unsigned grid_s = (unsigned)((bytes + 255) / 256 < 65536 ? (bytes + 255) / 256 : 65536);
+  pack_scales_kernel<<<grid_s, 256, 0, st>>>(scales, out_scales, n_mat, rows, groups, mat_stride);
+  return check_launch("pack_scales_kernel");
+}
+
+namespace {
 
 template <bool kPacked>
 int launch_dequant(const void* blocks, const void* scales, void* out, int64_t n_mat, int64_t rows, int64_t groups,
@@ -294,19 +384,10 @@ extern "C" int klc_mxfp4_pack(const void* blocks, const void* scales, void* pack
   if (stride < 0) return (int)stride;
   KLC_REQUIRE(n_mat >= 0, KLC_ERR_ARGUMENT, "klc_mxfp4_pack: n_mat=%lld", (long long)n_mat);
   KLC_REQUIRE(out_dim < (1 << 30) && groups < (1 << 24), KLC_ERR_UNSUPPORTED, "klc_mxfp4_pack: matrix too large");
-  if (n_mat == 0) return KLC_OK;
-  hipStream_t st = as_stream(stream);
-  const int64_t chunks = n_mat * out_dim * groups;
-  const unsigned grid_b = (unsigned)((chunks + 255) / 256 < 65536 ? (chunks + 255) / 256 : 65536);
-  pack_blocks_kernel<<<grid_b, 256, 0, st>>>(static_cast<const uint8_t*>(blocks), static_cast<uint8_t*>(packed), n_mat,
-                                             (int)out_dim, (int)groups, stride);
-  const int rc = check_launch("pack_blocks_kernel");
-  if (rc) return rc;
-  const int64_t bytes = n_mat * out_dim * 4 * packed_scale_record(groups);
-  const unsigned grid_s = (unsigned)((bytes + 255) / 256 < 65536 ? (bytes + 255) / 256 : 65536);
-  pack_scales_kernel<<<grid_s, 256, 0, st>>>(static_cast<const uint8_t*>(scales), static_cast<uint8_t*>(packed),
-                                             n_mat, (int)out_dim, (int)groups, stride);
-  return check_launch("pack_scales_kernel");
+  uint8_t* out = static_cast<uint8_t*>(packed);
+  return launch_pack(static_cast<const uint8_t*>(blocks), static_cast<const uint8_t*>(scales), out,
+                     out + packed_block_bytes(out_dim, groups), n_mat, (int)out_dim, (int)groups, stride,
+                     as_stream(stream));
 }
 
 extern "C" int klc_mxfp4_dequant_packed(const void* packed, void* out, int64_t n_mat, int64_t out_dim,

@@ -59,6 +59,13 @@ SIGNATURES: dict[str, tuple] = {
     "klc_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "klc_moe_layer": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
                              _P, _P, _P, _P, _P, _P]),
+    "klc_st_open": (_I32, [ctypes.c_char_p, _P]),
+    "klc_st_close": (_I32, [_P]),
+    "klc_st_tensor_info": (_I32, [_P, ctypes.c_char_p, _P, _P, _P, _P, _P]),
+    "klc_st_read_rows": (_I32, [_P, ctypes.c_char_p, _I64, _I64, _P]),
+    "klc_st_copy_rows_to_device": (_I32, [_P, ctypes.c_char_p, _I64, _I64, _P, _I64, _P, _P]),
+    "klc_st_copy_rows_batch": (_I32, [_P, _I32, _P, _P, _P, _P, _P, _I64, _P]),
+    "klc_st_load_mxfp4_packed": (_I32, [_P, ctypes.c_char_p, ctypes.c_char_p, _I64, _P, _I64, _P, _P]),
     "klc_synth_fill": (_I32, [_P, _I64, _U64, _I32, _I32, _I32, _P]),
 }
 

@@ -13,8 +13,10 @@ it unchanged.  What differs underneath:
   instead of 49.8 MB dequantized, so the same ``cache_bytes`` budget holds
   3.76x more experts.  ``load_expert_matrix`` dequantizes from the packed copy
   on demand; the router's fused kernels read the packed copy directly.
-* a miss reads the checkpoint slice, copies it host-to-device on a side stream
-  and packs it there; there is no device-wide synchronisation.
+* a miss reads the expert's slice from the checkpoint shard straight into the
+  packed layout in HBM (klc_st_load_mxfp4_packed: pread into pinned staging,
+  copy, pack, chunk by chunk on a side stream); there is no device-wide
+  synchronisation.
 """
 
 from __future__ import annotations
@@ -30,6 +32,7 @@ from threading import RLock
 import torch
 
 from . import ops
+from .safetensors_shard import SafetensorShard
 
 # E2M1 code -> value (bit 3 is the sign); the same table as mxfp4_expert.py:17-34.
 FP4_VALUES = [
@@ -334,6 +337,18 @@ class SafetensorIndex:
         with self.index_path.open("r", encoding="utf-8") as f:
             self.index = json.load(f)
         self.weight_map: dict[str, str] = self.index["weight_map"]
+        self._shards: dict[str, SafetensorShard] = {}
+        self._shards_lock = RLock()
+
+    def shard(self, name: str) -> SafetensorShard:
+        """The open shard holding tensor ``name`` (opened once, then shared)."""
+        file = self.weight_map[name]
+        with self._shards_lock:
+            shard = self._shards.get(file)
+            if shard is None:
+                shard = SafetensorShard(self.model_dir / file)
+                self._shards[file] = shard
+            return shard
 
 
 class Mxfp4ExpertStore:
@@ -462,60 +477,102 @@ class Mxfp4ExpertStore:
                 self.pending.pop(key, None)
 
     def _materialize_expert_matrix(self, key: Key, prefetched: bool) -> torch.Tensor:
-        """Checkpoint slice -> pinned host -> device (side stream) -> packed layout.
+        """Checkpoint shard -> pinned staging -> device (side stream) -> packed layout.
 
-        The packed tensor is allocated on the compute stream, so the caching
-        allocator orders its reuse after the compute work that reads it; the
-        side stream first waits for the compute stream, then copies and packs,
-        and only the side stream is synchronised.
+        Blocks and scales in one shard (the checkpoint's layout) take the fused
+        path: klc_st_load_mxfp4_packed reads, copies and packs chunk by chunk
+        on the side stream without waiting for the compute stream.  Otherwise
+        (a quantized loader, or the two tensors in different shards) the slices
+        are copied first and packed after the side stream has waited for the
+        compute stream, into a tensor allocated on the compute stream.  Only
+        the side stream is synchronised.
         """
         layer_idx, expert_idx, proj = key
         start = time.perf_counter()
         base = f"model.layers.{layer_idx}.mlp.experts.{proj}"
-        blocks = self._load_expert_tensor(f"{base}_blocks", expert_idx)
-        scales = self._load_expert_tensor(f"{base}_scales", expert_idx)
-        if blocks.shape[:-1] != scales.shape or blocks.dim() != 3:
-            raise ValueError(f"MXFP4 block/scale shape mismatch: blocks.shape={blocks.shape} scales.shape={scales.shape}")
-        loaded = _nbytes(blocks) + _nbytes(scales)
+        names = (f"{base}_blocks", f"{base}_scales")
+        compute = torch.cuda.current_stream(self.device)
+        if not self._from_quant_loader(names[0]) and self.index.shard(names[0]) is self.index.shard(names[1]):
+            # shard -> pinned staging -> device staging -> packed, chunk by
+            # chunk on the side stream; the packed tensor is allocated there
+            # and marked as used by the compute stream, so its memory is
+            # reused only after the compute work that reads it
+            packed, rows, groups = self.index.shard(names[0]).load_mxfp4_packed(
+                names[0], names[1], expert_idx, self.device, self._side)
+            packed.record_stream(compute)
+            loaded = rows * groups * 17
+            self.cache.stats.transfer_time_s += time.perf_counter() - start
+        else:
+            if self._from_quant_loader(names[0]):
+                blocks, scales = (self._load_expert_tensor(n, expert_idx) for n in names)
+                self._check_pair(blocks.shape, scales.shape)
+                with torch.cuda.stream(self._side):
+                    b_dev = blocks.to(torch.uint8).contiguous().pin_memory().to(self.device, non_blocking=True)
+                    s_dev = scales.to(torch.uint8).contiguous().pin_memory().to(self.device, non_blocking=True)
+            else:
+                # blocks and scales in different shards: staged copies, then the pack
+                b_dev, s_dev = self._copy_expert_tensors(names, expert_idx)
+                self._check_pair(b_dev.shape, s_dev.shape)
+            copied = torch.cuda.Event()
+            copied.record(self._side)
+            loaded = _nbytes(b_dev) + _nbytes(s_dev)
+            rows, groups = int(b_dev.shape[0]), int(b_dev.shape[1])
+            packed = torch.empty(ops.packed_bytes(rows, groups), dtype=torch.uint8, device=self.device)
+            self._side.wait_stream(compute)
+            with torch.cuda.stream(self._side):
+                ops.mxfp4_pack(b_dev, s_dev, out=packed)
+                done = torch.cuda.Event()
+                done.record(self._side)
+            copied.synchronize()
+            self.cache.stats.transfer_time_s += time.perf_counter() - start
+            pack_start = time.perf_counter()
+            done.synchronize()
+            self.cache.stats.dequant_time_s += time.perf_counter() - pack_start
         self.cache.stats.loaded_bytes += loaded
         self.cache.stats.miss_loaded_bytes += loaded
         self.cache.layer_loaded_bytes[layer_idx] += loaded
-        rows, groups = int(blocks.shape[0]), int(blocks.shape[1])
-        compute = torch.cuda.current_stream(self.device)
-        packed = torch.empty(ops.packed_bytes(rows, groups), dtype=torch.uint8, device=self.device)
-        self._side.wait_stream(compute)
-        with torch.cuda.stream(self._side):
-            b_dev = blocks.to(torch.uint8).contiguous().pin_memory().to(self.device, non_blocking=True)
-            s_dev = scales.to(torch.uint8).contiguous().pin_memory().to(self.device, non_blocking=True)
-            copied = torch.cuda.Event()
-            copied.record(self._side)
-            ops.mxfp4_pack(b_dev, s_dev, out=packed)
-            done = torch.cuda.Event()
-            done.record(self._side)
-        copied.synchronize()
-        self.cache.stats.transfer_time_s += time.perf_counter() - start
-        pack_start = time.perf_counter()
-        done.synchronize()
-        self.cache.stats.dequant_time_s += time.perf_counter() - pack_start
         self.cache.stats.materialization_time_s += time.perf_counter() - start
         self.cache.stats.materializations += 1
         self._shapes[key] = (rows, groups)
         self.cache.put(key, packed, prefetched=prefetched)
         return packed
 
-    def _load_expert_tensor(self, name: str, expert_idx: int) -> torch.Tensor:
+    @staticmethod
+    def _check_pair(bshape, sshape) -> None:
+        if len(bshape) != 3 or tuple(bshape[:-1]) != tuple(sshape):
+            raise ValueError(f"MXFP4 block/scale shape mismatch: blocks.shape={tuple(bshape)} "
+                             f"scales.shape={tuple(sshape)}")
+
+    def _from_quant_loader(self, name: str) -> bool:
         loader = self.quant_loader
-        if loader is not None and name in getattr(loader, "tensor_index", {}):
-            full, meta = loader.load_tensor(name, dtype=self.dtype)
+        return loader is not None and name in getattr(loader, "tensor_index", {})
+
+    def _copy_expert_tensors(self, names: tuple[str, ...], expert_idx: int) -> list[torch.Tensor]:
+        """The expert's slices of ``names`` (U8), from their shards to the
+        device, one staged copy per shard."""
+        by_shard: dict[int, tuple[SafetensorShard, list[int]]] = {}
+        for i, name in enumerate(names):
+            shard = self.index.shard(name)
+            dtype = shard.info(name)[0]
+            if dtype != "U8":
+                raise ValueError(f"{name}: MXFP4 blocks and scales are U8 in the checkpoint, found {dtype}")
+            by_shard.setdefault(id(shard), (shard, []))[1].append(i)
+        out: list[torch.Tensor | None] = [None] * len(names)
+        for shard, idx in by_shard.values():
+            got = shard.copy_rows_batch([(names[i], expert_idx, 1) for i in idx], self.device, self._side)
+            for i, t in zip(idx, got):
+                out[i] = t[0]
+        return out
+
+    def _load_expert_tensor(self, name: str, expert_idx: int) -> torch.Tensor:
+        """The expert's slice as a host tensor (the quantized-loader path, or the shard reader)."""
+        if self._from_quant_loader(name):
+            full, meta = self.quant_loader.load_tensor(name, dtype=self.dtype)
             selected = full[expert_idx].detach().cpu()
             if getattr(meta, "dtype", None) == "torch.uint8":
                 return torch.clamp(torch.round(selected.float()), 0, 255).to(torch.uint8)
             return selected
-        from safetensors import safe_open
-
-        shard = self.index.weight_map[name]
-        with safe_open(self.index.model_dir / shard, framework="pt", device="cpu") as handle:
-            return handle.get_slice(name)[expert_idx]
+        return self.index.shard(name).read_rows(name, expert_idx, 1)[0]
 
 
 class ResidentExpertStore:

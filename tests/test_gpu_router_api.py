@@ -137,6 +137,27 @@ def test_store_load_expert_matrix_is_exact(gpu, setup, tmp_path):
     assert (0, 5, "down_proj") in store.cache.pinned
 
 
+def test_store_split_shards_take_the_copy_then_pack_path(gpu, setup, tmp_path):
+    """Blocks and scales in different shards: staged copies, then the pack."""
+    from safetensors.torch import save_file
+
+    host, _ = setup
+    prefix = "model.layers.0.mlp.experts"
+    blocks = {f"{prefix}.{p}_blocks": torch.from_numpy(host[f"{p[:-5]}_blocks"]) for p in ("gate_up_proj", "down_proj")}
+    scales = {f"{prefix}.{p}_scales": torch.from_numpy(host[f"{p[:-5]}_scales"]) for p in ("gate_up_proj", "down_proj")}
+    save_file(blocks, str(tmp_path / "model-00001.safetensors"))
+    save_file(scales, str(tmp_path / "model-00002.safetensors"))
+    wmap = {**{n: "model-00001.safetensors" for n in blocks}, **{n: "model-00002.safetensors" for n in scales}}
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wmap}))
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, dtype=torch.bfloat16, cache_bytes=1 << 30)
+    for e, proj in [(4, "gate_up_proj"), (9, "down_proj")]:
+        got = store.load_expert_matrix(0, e, proj)
+        want = omx.dequantize(host[f"{proj[:-5]}_blocks"][e], host[f"{proj[:-5]}_scales"][e], "bf16")
+        assert np.array_equal(bf16_bits(got), want)
+    assert store.cache.stats.miss_loaded_bytes == sum(
+        host[f"{p}_blocks"][0].nbytes + host[f"{p}_scales"][0].nbytes for p in ("gate_up", "down"))
+
+
 def test_store_prefetch_then_consume(gpu, setup, tmp_path):
     host, _ = setup
     write_checkpoint(tmp_path, host)
