@@ -276,7 +276,8 @@ def loader_bench(torch, dev, n_experts: int, rounds: int = 3) -> dict:
     """Expert-store misses of 120B-shape experts from a page-cache-resident shard.
 
     ``native``: Mxfp4ExpertStore.packed_expert (shard -> pinned staging ring ->
-    device copy on the side stream -> pack).  ``safe_open_chain``: the
+    pack kernel reading the staging over PCIe, asynchronous on the side
+    stream).  ``safe_open_chain``: the
     per-miss chain the store replaces (safe_open slice -> pin_memory -> .to
     -> the same pack kernel), on the same slices.  The shard is fsync'ed
     before timing (no writeback under the reads); the two legs run in

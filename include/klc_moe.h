@@ -227,7 +227,7 @@ int klc_rms_norm(const void* x, const void* weight, void* out, int64_t n_tokens,
 /* ---- Safetensors shards (expert store misses) ----------------------------------
  * Replace the per-miss safe_open(...).get_slice(name)[expert] -> pin_memory()
  * -> .to(device) chain of Mxfp4ExpertStore._load_expert_tensor /
- * _materialize_expert_matrix (mxfp4_expert.py:487-525) and the shard lookups of
+ * _materialize_expert_matrix (mxfp4_expert.py:478-525) and the shard lookups of
  * SafetensorIndex (streamed_loader.py:43-82).  A shard is opened and its
  * header parsed once (klc_st_open; *handle is an opaque pointer, released by
  * klc_st_close; lookups are read-only, so threads may share a handle).
@@ -259,15 +259,25 @@ int klc_st_copy_rows_batch(void* handle, int n, const char* const* names, const 
  * row-tile layout in device memory (what klc_mxfp4_pack makes): blocks
  * [E, rows, G, 16] and scales [E, rows, G], both U8 in this shard, expert
  * `expert`, rows a multiple of 64.  Chunks of whole 64-row tiles are read
- * (pread by the pool) into slots of the pinned host staging buffer, and a
- * pack kernel on `stream` reads each slot over PCIe and writes its tiles of
- * `packed`; a slot is refilled once its previous pack has run.  staging must
- * be pinned host memory (hipHostMalloc / torch pin_memory) of staging_bytes,
- * at least two tiles (2 * 64 * G * 17 bytes); staging and packed are 16-byte
- * aligned; packed holds klc_mxfp4_packed_bytes(rows, G).  Returns once packed
- * is complete. */
+ * (pread by the pool) into the slots of a ring in the pinned host staging
+ * buffer, and a pack kernel on `stream` reads each slot over PCIe and writes
+ * its tiles of `packed`.  Asynchronous: returns once every chunk is read and
+ * its pack enqueued; `packed` is complete when `stream` reaches the last
+ * pack.  The staging buffer stays in use until then: a later call with the
+ * same buffer waits for a slot's pack before refilling it (so consecutive
+ * loads overlap), klc_st_copy_rows_* wait for all of them, and
+ * klc_st_staging_wait / klc_st_staging_release must be called before the
+ * buffer is freed or used otherwise.  One thread fills a buffer at a time.
+ * staging: pinned host memory (hipHostMalloc / torch pin_memory) of
+ * staging_bytes, at least two tiles (2 * 64 * G * 17 bytes); staging and
+ * packed 16-byte aligned; packed holds klc_mxfp4_packed_bytes(rows, G). */
 int klc_st_load_mxfp4_packed(void* handle, const char* blocks_name, const char* scales_name, int64_t expert,
                              void* staging, int64_t staging_bytes, void* packed, void* stream);
+/* Waits (host) for every pack still reading the staging buffer. */
+int klc_st_staging_wait(const void* staging);
+/* klc_st_staging_wait, then forgets the buffer's ring (its events are
+ * destroyed); call before freeing a staging buffer. */
+int klc_st_staging_release(const void* staging);
 
 /* ---- Synthetic inputs -------------------------------------------------------
  * Counter-based SplitMix64 stream, identical to klcquant_amd/synth.py:

@@ -1,13 +1,21 @@
-// Safetensors shard reader for the expert store's misses: the shard's header
-// is parsed once at open; an expert's slice (a contiguous byte range along
-// dimension 0 of a [E, ...] tensor) is read with pread by a small pool of
-// threads, straight into pinned staging, and copied to the device with
-// hipMemcpyAsync through two staging halves, so filling one half overlaps the
-// PCIe copy of the other.  pread copies from the page cache in the kernel:
-// no page faults on a user mapping, and several threads share the copy.
+// Safetensors shard reader for the expert store's misses.  A shard's header
+// is parsed once at open; an expert's slice of a [E, ...] tensor is a
+// contiguous byte range along dimension 0.  Reads use pread from a small
+// pool of spinning threads (the page cache is copied by the kernel: no page
+// faults on a user mapping, several threads share the copy).
+//
+// klc_st_load_mxfp4_packed goes from the file to the packed row-tile layout
+// in HBM in one pass: chunks of 64-row tiles are read into the slots of a
+// ring in pinned host memory, and a pack kernel reads each slot over PCIe
+// and writes its tiles.  There is no SDMA copy: on MI355X an H2D copy
+// followed by a kernel on the same stream ran at 10 GB/s (the engine
+// hand-off), a kernel reading pinned memory at 52 GB/s.  The ring outlives
+// the call, so a load returns once its packs are enqueued and the next
+// load's reads overlap them.  klc_st_copy_rows_* stage plain byte ranges
+// through the same kind of ring with hipMemcpyAsync.
 //
 // Replaces the per-miss safe_open(...).get_slice(name)[expert] ->
-// .contiguous().pin_memory() -> .to(device) chain of mxfp4_expert.py:487-525
+// .contiguous().pin_memory() -> .to(device) chain of mxfp4_expert.py:478-525
 // (and streamed_loader.py:43-82's index use).  File format: 8-byte
 // little-endian header length N, N bytes of JSON mapping each tensor name to
 // {"dtype", "shape", "data_offsets": [begin, end]} (offsets relative to the
@@ -537,6 +545,86 @@ hipError_t slot_events(int n, hipEvent_t** out) {
   return hipSuccess;
 }
 
+// The slot ring of one pinned staging buffer on one device, kept across
+// calls of klc_st_load_mxfp4_packed: which slots still have a pack in flight
+// (used + ev) and where the next chunk goes.  A call with another slot
+// layout first waits for every slot.  The registry is global, so any thread
+// may wait for or release a buffer's ring; one buffer is filled by one
+// thread at a time.
+struct Ring {
+  int slots = 0;
+  int64_t slot_bytes = 0;
+  int next = 0;
+  bool used[kMaxSlots] = {};
+  hipEvent_t ev[kMaxSlots] = {};
+};
+std::mutex g_rings_m;
+std::map<std::pair<const void*, int>, Ring*> g_rings;
+
+Ring* ring_of(const void* staging, int device) {
+  std::lock_guard<std::mutex> g(g_rings_m);
+  Ring*& r = g_rings[{staging, device}];
+  if (r == nullptr) r = new Ring;
+  return r;
+}
+
+hipError_t ring_drain(Ring* r) {
+  hipError_t first = hipSuccess;
+  for (int b = 0; b < kMaxSlots; ++b) {
+    if (!r->used[b]) continue;
+    const hipError_t e = hipEventSynchronize(r->ev[b]);
+    if (e != hipSuccess && first == hipSuccess) first = e;
+    r->used[b] = false;
+  }
+  return first;
+}
+
+// Waits for the rings of `staging` on every device (all of them if NULL);
+// with `release` also destroys their events and forgets them.
+hipError_t rings_wait(const void* staging, bool release) {
+  std::lock_guard<std::mutex> g(g_rings_m);
+  hipError_t first = hipSuccess;
+  for (auto it = g_rings.begin(); it != g_rings.end();) {
+    if (staging != nullptr && it->first.first != staging) {
+      ++it;
+      continue;
+    }
+    const hipError_t e = ring_drain(it->second);
+    if (e != hipSuccess && first == hipSuccess) first = e;
+    if (!release) {
+      ++it;
+      continue;
+    }
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(it->first.second);
+    for (int b = 0; b < kMaxSlots; ++b)
+      if (it->second->ev[b] != nullptr) (void)hipEventDestroy(it->second->ev[b]);
+    if (prev >= 0) (void)hipSetDevice(prev);
+    delete it->second;
+    it = g_rings.erase(it);
+  }
+  return first;
+}
+
+// Sets the ring's layout, waiting for every slot first if it changes, and
+// creates the events it needs (on the current device).
+hipError_t ring_layout(Ring* r, int slots, int64_t slot_bytes) {
+  if (r->slots != slots || r->slot_bytes != slot_bytes) {
+    const hipError_t e = ring_drain(r);
+    if (e != hipSuccess) return e;
+    r->slots = slots;
+    r->slot_bytes = slot_bytes;
+    r->next = 0;
+  }
+  for (int b = 0; b < slots; ++b) {
+    if (r->ev[b] != nullptr) continue;
+    const hipError_t e = hipEventCreateWithFlags(&r->ev[b], hipEventDisableTiming);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 struct RowCopy {
   const char* name;
   int64_t src, bytes;
@@ -556,12 +644,12 @@ int staged_copy(StFile* f, const RowCopy* copies, int n, void* staging, int64_t 
               "%s: staging of %lld bytes (at least 8 KiB, two slots)", fn, (long long)staging_bytes);
   int slots = (int)std::min<int64_t>(kMaxSlots, std::max<int64_t>(2, staging_bytes / kSlotBytes));
   const int64_t slot = std::min<int64_t>(kSlotBytes, staging_bytes / slots / 4096 * 4096);
-  hipEvent_t* done = nullptr;
-  hipError_t herr = slot_events(slots, &done);
+  // packs of earlier klc_st_load_mxfp4_packed calls may still read the staging
+  hipError_t herr = rings_wait(staging, false);
   KLC_REQUIRE(herr == hipSuccess, KLC_ERR_HIP, "%s: %s", fn, hipGetErrorString(herr));
-  for (int i = 0; i < n; ++i)
-    if (copies[i].bytes > 0)
-      (void)posix_fadvise(f->fd, (off_t)copies[i].src, (off_t)copies[i].bytes, POSIX_FADV_WILLNEED);
+  hipEvent_t* done = nullptr;
+  herr = slot_events(slots, &done);
+  KLC_REQUIRE(herr == hipSuccess, KLC_ERR_HIP, "%s: %s", fn, hipGetErrorString(herr));
   bool used[kMaxSlots] = {};
   int rc = KLC_OK;
   int64_t k = 0;  // chunks issued so far
@@ -680,24 +768,31 @@ extern "C" int klc_st_load_mxfp4_packed(void* handle, const char* blocks_name, c
                      hipGetErrorString(herr));
   }
   hipStream_t st = as_stream(stream);
-  hipEvent_t* done = nullptr;
-  herr = slot_events(slots, &done);
+  int device = 0;
+  herr = hipGetDevice(&device);
   KLC_REQUIRE(herr == hipSuccess, KLC_ERR_HIP, "klc_st_load_mxfp4_packed: %s", hipGetErrorString(herr));
-  (void)posix_fadvise(f->fd, (off_t)blocks_src, (off_t)(rows * groups * 16), POSIX_FADV_WILLNEED);
-  (void)posix_fadvise(f->fd, (off_t)scales_src, (off_t)(rows * groups), POSIX_FADV_WILLNEED);
-  bool used[kMaxSlots] = {};
+  Ring* ring = ring_of(staging, device);
+  herr = ring_layout(ring, slots, slot_bytes);
+  KLC_REQUIRE(herr == hipSuccess, KLC_ERR_HIP, "klc_st_load_mxfp4_packed: %s", hipGetErrorString(herr));
+  bool idle = true;
+  for (int b = 0; b < slots; ++b) idle = idle && !ring->used[b];
   int rc = KLC_OK;
   for (int64_t t0 = 0, nt = 0, k = 0; t0 < tiles && rc == KLC_OK; t0 += nt, ++k) {
-    const int b = (int)(k % slots);
-    // the first chunk is a quarter slot: the first pack starts sooner
-    nt = std::min(k == 0 ? std::max<int64_t>(1, slot_tiles / 4) : slot_tiles, tiles - t0);
+    const int b = ring->next;
+    ring->next = (b + 1) % slots;
+    // with the ring idle, the first chunk is a quarter slot: the GPU starts sooner
+    nt = std::min(k == 0 && idle ? std::max<int64_t>(1, slot_tiles / 4) : slot_tiles, tiles - t0);
     const int64_t nb = nt * tile_blocks, ns = nt * tile_scales;
     uint8_t* host = static_cast<uint8_t*>(staging) + b * slot_bytes;
     const uint8_t* mapped = static_cast<const uint8_t*>(staging_dev) + b * slot_bytes;
-    // the slot's previous pack has read it
-    if (used[b] && (herr = hipEventSynchronize(done[b])) != hipSuccess) {
-      rc = set_error(KLC_ERR_HIP, "klc_st_load_mxfp4_packed: %s", hipGetErrorString(herr));
-      break;
+    // the slot's previous pack (of this call or an earlier one) has read it
+    if (ring->used[b]) {
+      herr = hipEventSynchronize(ring->ev[b]);
+      ring->used[b] = false;
+      if (herr != hipSuccess) {
+        rc = set_error(KLC_ERR_HIP, "klc_st_load_mxfp4_packed: %s", hipGetErrorString(herr));
+        break;
+      }
     }
     int rerr = parallel_read(f, host, nb, blocks_src + t0 * tile_blocks);
     if (rerr == 0) rerr = parallel_read(f, host + nb, ns, scales_src + t0 * tile_scales);
@@ -709,14 +804,30 @@ extern "C" int klc_st_load_mxfp4_packed(void* handle, const char* blocks_name, c
     rc = launch_pack_from_host(mapped, mapped + nb, out_blocks + t0 * groups * 1024, out_scales + t0 * scale_tile_bytes,
                                (int)(nt * kTileRows), (int)groups, st);
     if (rc != KLC_OK) break;
-    herr = hipEventRecord(done[b], st);
-    used[b] = true;
-    if (herr != hipSuccess) rc = set_error(KLC_ERR_HIP, "klc_st_load_mxfp4_packed: %s", hipGetErrorString(herr));
-  }
-  for (int b = 0; b < slots; ++b) {
-    if (used[b] && (herr = hipEventSynchronize(done[b])) != hipSuccess && rc == KLC_OK)
+    herr = hipEventRecord(ring->ev[b], st);
+    if (herr != hipSuccess) {
       rc = set_error(KLC_ERR_HIP, "klc_st_load_mxfp4_packed: %s", hipGetErrorString(herr));
+      break;
+    }
+    ring->used[b] = true;
   }
-  if (rc != KLC_OK) (void)hipStreamSynchronize(st);  // no pack may still read the staging
+  if (rc != KLC_OK) {  // no pack may still read the staging
+    (void)hipStreamSynchronize(st);
+    (void)ring_drain(ring);
+  }
   return rc;
+}
+
+extern "C" int klc_st_staging_wait(const void* staging) {
+  KLC_REQUIRE(staging, KLC_ERR_ARGUMENT, "klc_st_staging_wait: null staging");
+  const hipError_t e = rings_wait(staging, false);
+  KLC_REQUIRE(e == hipSuccess, KLC_ERR_HIP, "klc_st_staging_wait: %s", hipGetErrorString(e));
+  return KLC_OK;
+}
+
+extern "C" int klc_st_staging_release(const void* staging) {
+  KLC_REQUIRE(staging, KLC_ERR_ARGUMENT, "klc_st_staging_release: null staging");
+  const hipError_t e = rings_wait(staging, true);
+  KLC_REQUIRE(e == hipSuccess, KLC_ERR_HIP, "klc_st_staging_release: %s", hipGetErrorString(e));
+  return KLC_OK;
 }

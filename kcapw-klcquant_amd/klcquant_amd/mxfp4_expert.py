@@ -382,6 +382,10 @@ class Mxfp4ExpertStore:
         self.pending_lock = RLock()
         self._shapes: dict[Key, tuple[int, int]] = {}
         self._side = torch.cuda.Stream(self.device)
+        # side-stream events of packs enqueued without a host wait, per key,
+        # until one is seen complete
+        self._ready: dict[Key, torch.cuda.Event] = {}
+        self._ready_lock = RLock()
 
     # ---- reference API ---------------------------------------------------------
 
@@ -439,7 +443,21 @@ class Mxfp4ExpertStore:
         cached = self.cache.get(key)
         if cached is None:
             cached = self._materialize_expert_matrix(key, prefetched=False)
+        if self._ready:
+            self._order_after_load(key)
         return cached
+
+    def _order_after_load(self, key: Key) -> None:
+        """Makes the current stream wait (on the device) for the pack of
+        ``key`` if it may still be running on the side stream."""
+        with self._ready_lock:
+            ev = self._ready.get(key)
+            if ev is None:
+                return
+            if ev.query():
+                del self._ready[key]
+                return
+        torch.cuda.current_stream(self.device).wait_event(ev)
 
     def matrix_shape(self, layer_idx: int, expert_idx: int, proj: str) -> tuple[int, int]:
         """``(rows, groups)`` of a materialized projection."""
@@ -480,8 +498,11 @@ class Mxfp4ExpertStore:
         """Checkpoint shard -> pinned staging -> device (side stream) -> packed layout.
 
         Blocks and scales in one shard (the checkpoint's layout) take the fused
-        path: klc_st_load_mxfp4_packed reads, copies and packs chunk by chunk
-        on the side stream without waiting for the compute stream.  Otherwise
+        path: klc_st_load_mxfp4_packed reads and packs chunk by chunk on the
+        side stream without waiting for the compute stream, and returns once
+        the last pack is enqueued; ``packed_expert`` then makes the caller's
+        stream wait for an event after that pack, so no host wait is needed
+        and the next miss's reads overlap these packs.  Otherwise
         (a quantized loader, or the two tensors in different shards) the slices
         are copied first and packed after the side stream has waited for the
         compute stream, into a tensor allocated on the compute stream.  Only
@@ -493,13 +514,16 @@ class Mxfp4ExpertStore:
         names = (f"{base}_blocks", f"{base}_scales")
         compute = torch.cuda.current_stream(self.device)
         if not self._from_quant_loader(names[0]) and self.index.shard(names[0]) is self.index.shard(names[1]):
-            # shard -> pinned staging -> device staging -> packed, chunk by
-            # chunk on the side stream; the packed tensor is allocated there
-            # and marked as used by the compute stream, so its memory is
-            # reused only after the compute work that reads it
+            # shard -> pinned staging -> packed, chunk by chunk on the side
+            # stream; the packed tensor is allocated on the compute stream
+            # and marked as used by the side stream, so its memory is reused
+            # only after both the packs and the compute work that reads it
             packed, rows, groups = self.index.shard(names[0]).load_mxfp4_packed(
-                names[0], names[1], expert_idx, self.device, self._side)
-            packed.record_stream(compute)
+                names[0], names[1], expert_idx, self.device, self._side, wait=False)
+            ready = torch.cuda.Event()
+            ready.record(self._side)
+            with self._ready_lock:
+                self._ready[key] = ready
             loaded = rows * groups * 17
             self.cache.stats.transfer_time_s += time.perf_counter() - start
         else:

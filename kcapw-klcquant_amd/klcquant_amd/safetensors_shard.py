@@ -6,12 +6,13 @@ pread by a small thread pool into host memory (``read_rows``) or into a ring
 of pinned staging slots and from there to device memory
 (``copy_rows_to_device``, ``copy_rows_batch``).
 This replaces the per-miss ``safe_open(...).get_slice(name)[expert]`` ->
-``pin_memory()`` -> ``.to(device)`` chain of mxfp4_expert.py:487-525.
+``pin_memory()`` -> ``.to(device)`` chain of mxfp4_expert.py:478-525.
 """
 
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from pathlib import Path
 
@@ -30,15 +31,35 @@ _DTYPES = {
 #: slots from the page cache overlaps the PCIe transfers of earlier ones.
 STAGING_BYTES = 8 << 20
 
+@functools.lru_cache(maxsize=64)
+def _packed_bytes(rows: int, groups: int) -> int:
+    return ops.packed_bytes(rows, groups)
+
+
+class _Staging:
+    """A thread's pinned staging buffer.  Packs enqueued by asynchronous
+    loads may still read it, so it is released through the library (which
+    waits for them) before torch may reuse the memory."""
+
+    def __init__(self) -> None:
+        self.buf = torch.empty(STAGING_BYTES, dtype=torch.uint8, pin_memory=True)
+
+    def __del__(self) -> None:
+        try:
+            _native.call("klc_st_staging_release", ctypes.c_void_p(self.buf.data_ptr()))
+        except Exception:
+            pass
+
+
 _staging = threading.local()
 
 
 def _thread_staging() -> torch.Tensor:
-    buf = getattr(_staging, "buf", None)
-    if buf is None:
-        buf = torch.empty(STAGING_BYTES, dtype=torch.uint8, pin_memory=True)
-        _staging.buf = buf
-    return buf
+    owner = getattr(_staging, "owner", None)
+    if owner is None:
+        owner = _Staging()
+        _staging.owner = owner
+    return owner.buf
 
 
 class SafetensorShard:
@@ -133,14 +154,17 @@ class SafetensorShard:
         return outs
 
     def load_mxfp4_packed(self, blocks_name: str, scales_name: str, expert: int, device: torch.device,
-                          stream: torch.cuda.Stream | None = None) -> tuple[torch.Tensor, int, int]:
+                          stream: torch.cuda.Stream | None = None, wait: bool = True) -> tuple[torch.Tensor, int, int]:
         """One expert's MXFP4 projection, read from the shard straight into the
         packed row-tile layout on the device: ``(packed, rows, groups)``.
 
         Chunks of 64-row tiles are read into this thread's pinned staging and
         packed by a kernel on ``stream`` that reads the staging over PCIe (the
-        packed tensor is allocated on ``stream``).  Returns once the packed
-        matrix is complete.
+        packed tensor is allocated on the current stream and marked as used
+        by ``stream``).  With ``wait`` the call
+        returns once the packed matrix is complete; without it, once the last
+        pack is enqueued (work on ``stream`` then sees the finished matrix, and
+        the next load from this thread overlaps the packs still running).
         """
         device = torch.device(device)
         stream = stream if stream is not None else torch.cuda.current_stream(device)
@@ -151,9 +175,11 @@ class SafetensorShard:
                              f"scales.shape={s_shape[1:]} ({b_dtype}/{s_dtype})")
         rows, groups = int(b_shape[1]), int(b_shape[2])
         staging = _thread_staging()
-        with torch.cuda.stream(stream):
-            packed = torch.empty(ops.packed_bytes(rows, groups), dtype=torch.uint8, device=device)
+        packed = torch.empty(_packed_bytes(rows, groups), dtype=torch.uint8, device=device)
+        packed.record_stream(stream)
         _native.call("klc_st_load_mxfp4_packed", self._h(), blocks_name.encode(), scales_name.encode(), int(expert),
                      ctypes.c_void_p(staging.data_ptr()), staging.numel(), ctypes.c_void_p(packed.data_ptr()),
                      ctypes.c_void_p(stream.cuda_stream))
+        if wait:
+            _native.call("klc_st_staging_wait", ctypes.c_void_p(staging.data_ptr()))
         return packed, rows, groups

@@ -192,3 +192,41 @@ def test_load_mxfp4_packed_rejects_bad_inputs(gpu, mxfp4_shard):
         assert call(b"l.down_proj_blocks", b"l.down_proj_scales", 0, dst=out.data_ptr() + 8) == -1  # misaligned
         with pytest.raises(ValueError):
             shard.load_mxfp4_packed("l.down_proj_blocks", "l.gate_up_proj_scales", 0, gpu)
+
+
+def test_async_loads_share_one_ring(gpu, mxfp4_shard):
+    """Loads that return before their packs finish: the ring carries over
+    between calls (three experts through a 3-tile staging), a change of slot
+    layout (90 -> 22 groups) waits for the old slots, and a staged copy after
+    them waits for every pack before it reuses the buffer."""
+    from klcquant_amd import ops
+
+    path, tensors = mxfp4_shard
+    nbytes = 3 * 64 * 90 * 17
+    with SafetensorShard(path) as shard:
+        staging = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        side = torch.cuda.Stream(gpu)
+        h = ctypes.c_void_p(staging.data_ptr())
+        outs = []
+        for proj, e in [("gate_up_proj", 0), ("gate_up_proj", 1), ("gate_up_proj", 2), ("down_proj", 0),
+                        ("down_proj", 1)]:
+            rows, groups = tensors[f"l.{proj}_scales"].shape[1:]
+            out = torch.empty(ops.packed_bytes(rows, groups), dtype=torch.uint8, device=gpu)
+            _native.call("klc_st_load_mxfp4_packed", shard._h(), f"l.{proj}_blocks".encode(),
+                         f"l.{proj}_scales".encode(), e, h, nbytes, ctypes.c_void_p(out.data_ptr()),
+                         ctypes.c_void_p(side.cuda_stream))
+            outs.append((proj, e, out))
+        # a staged copy through the same buffer waits for the packs still reading it
+        got = shard.copy_rows_batch([("l.down_proj_blocks", 1, 1)], gpu, side)[0]
+        side.synchronize()
+        for proj, e, out in outs:
+            assert torch.equal(out, _expected_packed(tensors, proj, e, gpu)), (proj, e)
+        assert torch.equal(got.cpu(), tensors["l.down_proj_blocks"][1:2])
+        _native.call("klc_st_staging_wait", h)
+        _native.call("klc_st_staging_release", h)
+        _native.call("klc_st_staging_release", h)  # nothing left: still fine
+        # the Python wrapper without waiting, then an ordinary stream wait
+        packed, _, _ = shard.load_mxfp4_packed("l.gate_up_proj_blocks", "l.gate_up_proj_scales", 2, gpu, side,
+                                               wait=False)
+        torch.cuda.current_stream(gpu).wait_stream(side)
+        assert torch.equal(packed, _expected_packed(tensors, "gate_up_proj", 2, gpu))
