@@ -16,7 +16,8 @@ resident, 64 sequences x 32 steps), ``prefill`` one layer over 2048 tokens
 with Zipf(1.1)-skewed routing (grouped GEMM), and ``dequant`` the standalone
 MXFP4 -> bf16 dequant of 128 down_proj experts, and ``loader`` the expert
 store's misses (page-cache-warm shard -> packed experts in HBM) against the
-safe_open chain they replace; all are extra lines of the same run.  ``roofline`` is for the
+safe_open chain they replace, and ``lm_head`` the gpt-oss logits pass with
+the greedy token; all are extra lines of the same run.  ``roofline`` is for the
 dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
 experts the batch touches + activations in + SwiGLU output) over its average
 duration measured with HIP events recorded by the library between its
@@ -68,6 +69,7 @@ def parse_args():
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of the prefill measurement (0 = skip)")
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
     ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
+    ap.add_argument("--skip-lm-head", action="store_true", help="skip the lm_head logits measurement")
     ap.add_argument("--loader-experts", type=int, default=16,
                     help="experts of the expert-store miss measurement (0 = skip)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -371,6 +373,57 @@ def loader_bench(torch, dev, n_experts: int, rounds: int = 3) -> dict:
     }
 
 
+def lm_head_bench(torch, dev, reps: int = 50) -> dict:
+    """gpt-oss lm_head (201,088 x 2880 bf16, resident): one logits pass plus
+    the greedy token, against the executor's chunked float32 matmul with a
+    host copy per 4096-row chunk (streamed_transformer_executor.py:177-191)."""
+    from klcquant_amd.lm_head import LmHead
+
+    vocab = 201088
+    g = torch.Generator(device=dev).manual_seed(17)
+    w = (torch.randn((vocab, HIDDEN), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = torch.randn(HIDDEN, generator=g, device=dev)
+    head = LmHead(w)
+    out, token = head.logits_device(x)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        head.logits_device(x, out=out)
+    end.record()
+    end.synchronize()
+    us = start.elapsed_time(end) * 1e3 / reps
+    t0 = time.perf_counter()
+    for _ in range(5):
+        tok = head.greedy_token(x)
+    greedy_us = (time.perf_counter() - t0) * 1e6 / 5
+
+    def reference():
+        parts = []
+        for s in range(0, vocab, 4096):
+            parts.append(torch.matmul(w[s:s + 4096].float(), x.float()).detach().cpu())
+        logits = torch.cat(parts)
+        return int(torch.argmax(torch.nan_to_num(logits, nan=-1e9, posinf=1e9, neginf=-1e9)).item())
+
+    reference()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        ref_tok = reference()
+    ref_us = (time.perf_counter() - t0) * 1e6 / 3
+    nbytes = vocab * HIDDEN * 2
+    del w, head
+    torch.cuda.empty_cache()
+    return {
+        "workload": "gpt-oss lm_head 201088 x 2880 bf16 resident, logits + greedy token",
+        "us": round(us, 2),
+        "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "frac_of_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "greedy_token_us_host": round(greedy_us, 1),
+        "reference_chunked_us_host": round(ref_us, 1),
+        "same_token_as_reference": bool(tok == ref_tok),
+    }
+
+
 def cpu_baseline(n_tokens: int) -> dict:
     """The oracle (numpy port of the reference path) on single-token route calls."""
     import numpy as np
@@ -520,6 +573,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         result["stack"] = stack_bench(torch, dev, args.stack_layers, 64, args.stack_steps, args.precision)
         print(f"[bench] stack: {result['stack']}", file=sys.stderr, flush=True)
+    if not args.skip_lm_head:
+        result["lm_head"] = lm_head_bench(torch, dev)
+        print(f"[bench] lm_head: {result['lm_head']}", file=sys.stderr, flush=True)
     if args.loader_experts > 1:
         result["loader"] = loader_bench(torch, dev, args.loader_experts)
         print(f"[bench] loader: {result['loader']}", file=sys.stderr, flush=True)

@@ -279,6 +279,23 @@ int klc_st_staging_wait(const void* staging);
  * destroyed); call before freeing a staging buffer. */
 int klc_st_staging_release(const void* staging);
 
+/* ---- lm_head ---------------------------------------------------------------
+ * Replaces StreamedTransformerExecutor.logits (streamed_transformer_executor.py:177-209:
+ * float32 matmul of 4096-row chunks of the resident lm_head weight with the
+ * final hidden state, each chunk copied to the host) and the greedy pick of
+ * its callers (generation_runtime.py:118-122, inference_server.py:383-386:
+ * nan_to_num(nan=-1e9, posinf=1e9, neginf=-1e9), then argmax).
+ * w: bfloat16 [vocab][hidden]; x: float32 [hidden] (hidden.float()).
+ * logits[v] = f32(sum_h f64(w[v][h]) * f64(x[h])), the correctly rounded
+ * float32 dot product; *token = the first index of the largest
+ * nan_to_num(logits[v]), *token_logit (may be NULL) that value.
+ * hidden a multiple of 8, at most 4096; w, x, workspace 16-byte aligned;
+ * workspace of klc_lm_head_workspace_bytes(vocab) bytes (scratch, no
+ * initialisation needed). */
+int64_t klc_lm_head_workspace_bytes(int64_t vocab);
+int klc_lm_head_logits(const void* w, const float* x, float* logits, int64_t vocab, int64_t hidden, void* workspace,
+                       int64_t workspace_bytes, int32_t* token, float* token_logit, void* stream);
+
 /* ---- Synthetic inputs -------------------------------------------------------
  * Counter-based SplitMix64 stream, identical to klcquant_amd/synth.py:
  * mode 0: n random bytes; mode 1: n bytes uniform in [lo, hi]. */

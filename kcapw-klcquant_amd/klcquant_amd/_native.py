@@ -68,6 +68,8 @@ SIGNATURES: dict[str, tuple] = {
     "klc_st_load_mxfp4_packed": (_I32, [_P, ctypes.c_char_p, ctypes.c_char_p, _I64, _P, _I64, _P, _P]),
     "klc_st_staging_wait": (_I32, [_P]),
     "klc_st_staging_release": (_I32, [_P]),
+    "klc_lm_head_workspace_bytes": (_I64, [_I64]),
+    "klc_lm_head_logits": (_I32, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P]),
     "klc_synth_fill": (_I32, [_P, _I64, _U64, _I32, _I32, _I32, _P]),
 }
 
