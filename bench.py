@@ -16,8 +16,9 @@ resident, 64 sequences x 32 steps), ``prefill`` one layer over 2048 tokens
 with Zipf(1.1)-skewed routing (grouped GEMM), and ``dequant`` the standalone
 MXFP4 -> bf16 dequant of 128 down_proj experts, and ``loader`` the expert
 store's misses (page-cache-warm shard -> packed experts in HBM) against the
-safe_open chain they replace, and ``lm_head`` the gpt-oss logits pass with
-the greedy token; all are extra lines of the same run.  ``roofline`` is for the
+safe_open chain they replace, ``lm_head`` the gpt-oss logits pass with
+the greedy token, and ``attention`` the decode attention core on an fp16 KV
+ring; all are extra lines of the same run.  ``roofline`` is for the
 dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
 experts the batch touches + activations in + SwiGLU output) over its average
 duration measured with HIP events recorded by the library between its
@@ -70,6 +71,7 @@ def parse_args():
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
     ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
     ap.add_argument("--skip-lm-head", action="store_true", help="skip the lm_head logits measurement")
+    ap.add_argument("--skip-attention", action="store_true", help="skip the decode attention measurement")
     ap.add_argument("--loader-experts", type=int, default=16,
                     help="experts of the expert-store miss measurement (0 = skip)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -424,6 +426,81 @@ def lm_head_bench(torch, dev, reps: int = 50) -> dict:
     }
 
 
+def attention_bench(torch, dev, context: int = 4096, reps: int = 100) -> dict:
+    """gpt-oss decode attention core (64 query / 8 KV heads, head_dim 64, fp16
+    KV ring): RoPE + append + scores / softmax with sinks / value sum, at a
+    full-attention context and at the 128-token sliding window, against the
+    reference's per-step stack + repeat_interleave + einsum + softmax
+    (streamed_attention.py:120-141, kv_cache_manager.py:50-56) on the same
+    cache contents."""
+    import ctypes
+
+    from klcquant_amd import _native
+    from klcquant_amd.attention import AttentionConfig, rope_cos_sin
+
+    cfg = AttentionConfig(hidden_size=HIDDEN, num_heads=64, num_kv_heads=8, head_dim=64, rope_factor=32.0)
+    nh, nkv, d, cap = 64, 8, 64, 8192
+    g = torch.Generator(device=dev).manual_seed(23)
+    kc = torch.randn((cap, nkv, d), generator=g, device=dev).to(torch.float16)
+    vc = torch.randn((cap, nkv, d), generator=g, device=dev).to(torch.float16)
+    q = torch.randn((nh, d), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((nkv, d), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((nkv, d), generator=g, device=dev).to(torch.bfloat16)
+    sinks = torch.randn(nh, generator=g, device=dev).to(torch.bfloat16)
+    cos, sin = rope_cos_sin(cfg, context, dev, torch.bfloat16)
+    q_rot, k_rot = torch.empty_like(q), torch.empty_like(k)
+    ctx = torch.empty((nh, d), dtype=torch.bfloat16, device=dev)
+    P = ctypes.c_void_p
+    stream = P(torch.cuda.current_stream(dev).cuda_stream)
+    ws = torch.empty(_native.call("klc_attn_workspace_bytes", nh, d, cap), dtype=torch.uint8, device=dev)
+
+    def step(count):
+        _native.call("klc_rope_append", P(q.data_ptr()), P(k.data_ptr()), P(v.data_ptr()), P(cos.data_ptr()),
+                     P(sin.data_ptr()), P(q_rot.data_ptr()), P(k_rot.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()),
+                     count - 1, cap, nh, nkv, d, 1, stream)
+        _native.call("klc_attn_decode", P(q_rot.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()), P(sinks.data_ptr()),
+                     cap, 0, count, nh, nkv, d, 1, P(ws.data_ptr()), ws.numel(), P(ctx.data_ptr()), stream)
+
+    out = {"workload": f"gpt-oss decode attention core, 64/8 heads x 64, fp16 KV ring, sinks; context {context} and window 128"}
+    for label, count in (("full", context), ("window128", 128)):
+        step(count)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            step(count)
+        end.record()
+        end.synchronize()
+        us = start.elapsed_time(end) * 1e3 / reps
+        kv_bytes = 2 * count * nkv * d * 2
+        out[f"{label}_us"] = round(us, 2)
+        out[f"{label}_kv_gbps"] = round(kv_bytes / (us * 1e-6) / 1e9, 1)
+    # the reference's per-step work on the same cache: a list of per-token tensors stacked every step
+    keys = [kc[i] for i in range(context)]
+    values = [vc[i] for i in range(context)]
+
+    def reference():
+        kk, vv = torch.stack(keys, 0), torch.stack(values, 0)
+        kh = kk.repeat_interleave(nh // nkv, dim=1).transpose(0, 1)
+        vh = vv.repeat_interleave(nh // nkv, dim=1).transpose(0, 1)
+        scores = torch.einsum("hd,htd->ht", q.float(), kh.float()) / 8.0
+        comb = torch.cat([scores, sinks.float().reshape(-1, 1)], dim=-1)
+        comb = comb - comb.max(dim=-1, keepdim=True).values
+        probs = torch.softmax(comb, dim=-1)[..., :-1].to(vh.dtype)
+        return torch.einsum("ht,htd->hd", probs, vh.contiguous())
+
+    reference()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        reference()
+    torch.cuda.synchronize()
+    out["reference_full_us_host"] = round((time.perf_counter() - t0) * 1e6 / 10, 1)
+    del kc, vc, ws, keys, values
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(n_tokens: int) -> dict:
     """The oracle (numpy port of the reference path) on single-token route calls."""
     import numpy as np
@@ -573,6 +650,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         result["stack"] = stack_bench(torch, dev, args.stack_layers, 64, args.stack_steps, args.precision)
         print(f"[bench] stack: {result['stack']}", file=sys.stderr, flush=True)
+    if not args.skip_attention:
+        result["attention"] = attention_bench(torch, dev)
+        print(f"[bench] attention: {result['attention']}", file=sys.stderr, flush=True)
     if not args.skip_lm_head:
         result["lm_head"] = lm_head_bench(torch, dev)
         print(f"[bench] lm_head: {result['lm_head']}", file=sys.stderr, flush=True)

@@ -296,6 +296,33 @@ int64_t klc_lm_head_workspace_bytes(int64_t vocab);
 int klc_lm_head_logits(const void* w, const float* x, float* logits, int64_t vocab, int64_t hidden, void* workspace,
                        int64_t workspace_bytes, int32_t* token, float* token_logit, void* stream);
 
+/* ---- Decode attention ------------------------------------------------------
+ * One decode token of StreamedAttention.forward (streamed_attention.py:80-141)
+ * on a device-resident KV ring (kv_cache_manager.py:39-56 keeps a list and
+ * stacks it every step).  The ring of a layer holds k_cache and v_cache,
+ * [cap][n_kv][head_dim] of kv_dtype (KLC_DTYPE_F16, the reference's "fp16"
+ * default, or KLC_DTYPE_BF16); token n lives in slot n % cap.  q, k, v and
+ * the context are bfloat16. */
+/* apply_rope (:88-98) to q [n_heads][head_dim] -> q_out (may alias q) and to
+ * k [n_kv][head_dim] -> k_cache slot `slot` (and, if k_out is not NULL, the
+ * rotated bfloat16 key to k_out); v is stored to v_cache slot `slot`.  cos_half / sin_half: bfloat16 [head_dim / 2] of the position
+ * (rope_cos_sin, :81-85).  Every bfloat16 op rounds as torch's does. */
+int klc_rope_append(const void* q, const void* k, const void* v, const void* cos_half, const void* sin_half,
+                    void* q_out, void* k_out, void* k_cache, void* v_cache, int64_t slot, int64_t cap, int64_t n_heads,
+                    int64_t n_kv, int64_t head_dim, int kv_dtype, void* stream);
+/* Scratch bytes of klc_attn_decode for `count` keys. */
+int64_t klc_attn_workspace_bytes(int64_t n_heads, int64_t head_dim, int64_t count);
+/* context [n_heads][head_dim] bfloat16 from the `count` keys starting at ring
+ * slot `first` (in token order, wrapping at cap) -- the caller applies the
+ * sliding window by choosing them.  scores = f32(q . k) / sqrt(head_dim);
+ * softmax over [scores, sinks[h]] (sinks bfloat16 [n_heads], or NULL) with
+ * the maximum subtracted; probabilities rounded to kv_dtype; context =
+ * bf16(kv_dtype(sum p * v)).  head_dim a multiple of 8 up to 128; n_heads / n_kv <= 16;
+ * count <= 2^22; caches and workspace 16-byte aligned. */
+int klc_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* sinks, int64_t cap,
+                    int64_t first, int64_t count, int64_t n_heads, int64_t n_kv, int64_t head_dim, int kv_dtype,
+                    void* workspace, int64_t workspace_bytes, void* context, void* stream);
+
 /* ---- Synthetic inputs -------------------------------------------------------
  * Counter-based SplitMix64 stream, identical to klcquant_amd/synth.py:
  * mode 0: n random bytes; mode 1: n bytes uniform in [lo, hi]. */

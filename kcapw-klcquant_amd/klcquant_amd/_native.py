@@ -70,6 +70,9 @@ SIGNATURES: dict[str, tuple] = {
     "klc_st_staging_release": (_I32, [_P]),
     "klc_lm_head_workspace_bytes": (_I64, [_I64]),
     "klc_lm_head_logits": (_I32, [_P, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P]),
+    "klc_rope_append": (_I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P]),
+    "klc_attn_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "klc_attn_decode": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P, _I64, _P, _P]),
     "klc_synth_fill": (_I32, [_P, _I64, _U64, _I32, _I32, _I32, _P]),
 }
 
