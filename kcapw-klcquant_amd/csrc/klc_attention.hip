@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kAttnThreads) void rope_append_kernel(
     uint16_t* __restrict__ k_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t slot, int nh, int nkv, int d, bool f16) {
   const int half = d / 2;
   const int pairs = (nh + nkv) * half;
-  for (int i = threadIdx.x; i < pairs + nkv * d; i += blockDim.x) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < pairs + nkv * d; i += gridDim.x * blockDim.x) {
     if (i < pairs) {
       const int row = i / half, j = i - row * half;
       const bool is_q = row < nh;
@@ -97,35 +97,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
   }
 }
 
-// per query head: m = max(scores, sink), l = sum exp(x - m) over [scores, sink]
+// per query head: m = max(scores, sink), l = sum exp(x - m) over [scores, sink];
+// each reduction is a wave shuffle tree plus one exchange of the 4 waves' values
 __global__ __launch_bounds__(kAttnThreads) void attn_stats_kernel(const float* __restrict__ scores,
                                                                   const uint16_t* __restrict__ sinks, int count,
                                                                   float* __restrict__ stats) {
-  __shared__ float red[kAttnThreads];
-  __shared__ double redd[kAttnThreads];
-  const int h = blockIdx.x;
+  __shared__ float wm[kAttnThreads / kWave];
+  __shared__ double wl[kAttnThreads / kWave];
+  const int h = blockIdx.x, lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const float* s = scores + (int64_t)h * count;
   float m = sinks != nullptr ? bf(sinks[h]) : -INFINITY;
   for (int i = threadIdx.x; i < count; i += kAttnThreads) m = fmaxf(m, s[i]);
-  red[threadIdx.x] = m;
+  for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (lane == 0) wm[wave] = m;
   __syncthreads();
-  for (int w = kAttnThreads / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
-    __syncthreads();
-  }
-  m = red[0];
+  m = wm[0];
+  for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, wm[w]);
   double l = 0.0;
   for (int i = threadIdx.x; i < count; i += kAttnThreads) l += (double)expf(s[i] - m);
   if (threadIdx.x == 0 && sinks != nullptr) l += (double)expf(bf(sinks[h]) - m);
-  redd[threadIdx.x] = l;
+  for (int off = kWave / 2; off > 0; off >>= 1) l += __shfl_xor(l, off);
+  if (lane == 0) wl[wave] = l;
   __syncthreads();
-  for (int w = kAttnThreads / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) redd[threadIdx.x] += redd[threadIdx.x + w];
-    __syncthreads();
-  }
   if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < kAttnThreads / kWave; ++w) t += wl[w];
     stats[2 * h] = m;
-    stats[2 * h + 1] = (float)redd[0];
+    stats[2 * h + 1] = (float)t;
   }
 }
 
@@ -142,22 +140,36 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __re
   const float m = stats[2 * h], l = stats[2 * h + 1];
   for (int i = threadIdx.x; i < nk; i += kAttnThreads) p[i] = rkv(expf(scores[(int64_t)h * count + k0 + i] - m) / l, f16);
   __syncthreads();
-  // thread (slice, pair of dims): slices of keys, two dims per thread
-  const int pairs = d / 2, slices = kAttnThreads / pairs;
-  const int dp = threadIdx.x % pairs, sl = threadIdx.x / pairs;
-  float a0 = 0.f, a1 = 0.f;
+  // thread (slice, four dims): slices of keys; each thread issues the 8-byte
+  // loads of four keys before their multiply-adds, so L2 round trips overlap
+  const int quads = d / 4, slices = kAttnThreads / quads;
+  const int dq = threadIdx.x % quads, sl = threadIdx.x / quads;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  auto vrow = [&](int i) {
+    return *reinterpret_cast<const uint2*>(v_cache + (((first + k0 + i) % cap) * nkv + kvh) * d + 4 * dq);
+  };
+  auto add = [&](float pi, uint2 w) {
+    a[0] = fmaf(pi, kv_f((uint16_t)(w.x & 0xffffu), f16), a[0]);
+    a[1] = fmaf(pi, kv_f((uint16_t)(w.x >> 16), f16), a[1]);
+    a[2] = fmaf(pi, kv_f((uint16_t)(w.y & 0xffffu), f16), a[2]);
+    a[3] = fmaf(pi, kv_f((uint16_t)(w.y >> 16), f16), a[3]);
+  };
   if (sl < slices) {
-    for (int i = sl; i < nk; i += slices) {
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(v_cache + (((first + k0 + i) % cap) * nkv + kvh) * d + 2 * dp);
-      a0 = fmaf(p[i], kv_f((uint16_t)(w & 0xffffu), f16), a0);
-      a1 = fmaf(p[i], kv_f((uint16_t)(w >> 16), f16), a1);
+    int i = sl;
+    for (; i + 3 * slices < nk; i += 4 * slices) {
+      const uint2 w0 = vrow(i), w1 = vrow(i + slices), w2 = vrow(i + 2 * slices), w3 = vrow(i + 3 * slices);
+      add(p[i], w0);
+      add(p[i + slices], w1);
+      add(p[i + 2 * slices], w2);
+      add(p[i + 3 * slices], w3);
     }
+    for (; i < nk; i += slices) add(p[i], vrow(i));
   }
-  // sum the slices: slices <= kAttnThreads / 32 = 8 for d >= 64, more for small d
+  // sum the slices, kAttnThreads / 32 of them at a time through LDS
   for (int base = 0; base < slices; base += kAttnThreads / 32) {
     if (sl >= base && sl < base + kAttnThreads / 32) {
-      acc_s[sl - base][2 * dp] = a0;
-      acc_s[sl - base][2 * dp + 1] = a1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc_s[sl - base][4 * dq + e] = a[e];
     }
     __syncthreads();
     if ((int)threadIdx.x < d) {
@@ -204,7 +216,8 @@ extern "C" int klc_rope_append(const void* q, const void* k, const void* v, cons
               (long long)cap);
   KLC_REQUIRE(kv_dtype == KLC_DTYPE_BF16 || kv_dtype == KLC_DTYPE_F16, KLC_ERR_UNSUPPORTED,
               "klc_rope_append: kv_dtype %d (bfloat16 or float16)", kv_dtype);
-  rope_append_kernel<<<1, kAttnThreads, 0, as_stream(stream)>>>(
+  const int64_t items = (n_heads + n_kv) * (head_dim / 2) + n_kv * head_dim;  // one thread each
+  rope_append_kernel<<<(unsigned)((items + kAttnThreads - 1) / kAttnThreads), kAttnThreads, 0, as_stream(stream)>>>(
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
       static_cast<const uint16_t*>(cos_half), static_cast<const uint16_t*>(sin_half), static_cast<uint16_t*>(q_out),
       static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), slot, (int)n_heads, (int)n_kv,
