@@ -18,7 +18,8 @@
 //
 // Kernels per step: scores (workgroup = one KV head x 64 keys, its whole
 // query group), per-head max and sum, probabilities x values (workgroup =
-// one query head x 256 keys), and the sum of the splits.
+// one query head x 256 keys), and the sum of the splits; a window of at most
+// 256 keys takes the max, sum and context in the value workgroup itself.
 #include <math.h>
 
 #include "klc_common.h"
@@ -127,17 +128,48 @@ __global__ __launch_bounds__(kAttnThreads) void attn_stats_kernel(const float* _
   }
 }
 
-// partial[h][split][d] = sum over the split's keys of bf16(p) * v
+// partial[h][split][d] = sum over the split's keys of p * v, p rounded to the
+// cache type.  kWhole (count <= 256, one split): the workgroup also takes the
+// head's max and sum itself and writes the context, so the step needs
+// neither the stats nor the combine launch.
+template <bool kWhole>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __restrict__ scores,
                                                                const float* __restrict__ stats,
+                                                               const uint16_t* __restrict__ sinks,
                                                                const uint16_t* __restrict__ v_cache,
-                                                               float* __restrict__ partial, int64_t cap, int64_t first,
-                                                               int count, int nh, int nkv, int d, bool f16) {
+                                                               float* __restrict__ partial,
+                                                               uint16_t* __restrict__ context, int64_t cap,
+                                                               int64_t first, int count, int nh, int nkv, int d,
+                                                               bool f16) {
   __shared__ float p[kPvKeys];
   __shared__ float acc_s[kAttnThreads / 32][kMaxHeadDim];
   const int h = blockIdx.x, split = blockIdx.y, g = nh / nkv, kvh = h / g;
   const int k0 = split * kPvKeys, nk = min(kPvKeys, count - k0);
-  const float m = stats[2 * h], l = stats[2 * h + 1];
+  float m, l;
+  if constexpr (kWhole) {
+    __shared__ float wm[kAttnThreads / kWave];
+    __shared__ double wl[kAttnThreads / kWave];
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const float x = (int)threadIdx.x < nk ? scores[(int64_t)h * count + threadIdx.x] : -INFINITY;
+    m = sinks != nullptr ? bf(sinks[h]) : -INFINITY;
+    m = fmaxf(m, x);
+    for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) wm[wave] = m;
+    __syncthreads();
+    m = wm[0];
+    for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, wm[w]);
+    double e = (int)threadIdx.x < nk ? (double)expf(x - m) : 0.0;
+    if (threadIdx.x == 0 && sinks != nullptr) e += (double)expf(bf(sinks[h]) - m);
+    for (int off = kWave / 2; off > 0; off >>= 1) e += __shfl_xor(e, off);
+    if (lane == 0) wl[wave] = e;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < kAttnThreads / kWave; ++w) t += wl[w];
+    l = (float)t;
+  } else {
+    m = stats[2 * h];
+    l = stats[2 * h + 1];
+  }
   for (int i = threadIdx.x; i < nk; i += kAttnThreads) p[i] = rkv(expf(scores[(int64_t)h * count + k0 + i] - m) / l, f16);
   __syncthreads();
   // thread (slice, four dims): slices of keys; each thread issues the 8-byte
@@ -179,6 +211,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __re
       *out = base == 0 ? t : *out + t;
     }
     __syncthreads();
+  }
+  if constexpr (kWhole) {
+    if ((int)threadIdx.x < d) {
+      const float t = partial[((int64_t)h * gridDim.y + split) * d + threadIdx.x];
+      context[(int64_t)h * d + threadIdx.x] = to_bf(rkv(t, f16));
+    }
   }
 }
 
@@ -264,11 +302,17 @@ extern "C" int klc_attn_decode(const void* q, const void* k_cache, const void* v
       qb, kb, scores, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, sqrtf((float)head_dim), f16);
   int rc = check_launch("attn_scores_kernel");
   if (rc) return rc;
-  attn_stats_kernel<<<(unsigned)n_heads, kAttnThreads, 0, st>>>(scores, static_cast<const uint16_t*>(sinks),
-                                                                  (int)count, stats);
+  const uint16_t* sk = static_cast<const uint16_t*>(sinks);
+  uint16_t* ctx = static_cast<uint16_t*>(context);
+  if (splits == 1) {  // a window of at most 256 keys: one workgroup per head does the rest
+    attn_pv_kernel<true><<<dim3((unsigned)n_heads, 1u), kAttnThreads, 0, st>>>(
+        scores, stats, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
+    return check_launch("attn_pv_kernel");
+  }
+  attn_stats_kernel<<<(unsigned)n_heads, kAttnThreads, 0, st>>>(scores, sk, (int)count, stats);
   if ((rc = check_launch("attn_stats_kernel"))) return rc;
-  attn_pv_kernel<<<dim3((unsigned)n_heads, (unsigned)splits), kAttnThreads, 0, st>>>(
-      scores, stats, vb, partial, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
+  attn_pv_kernel<false><<<dim3((unsigned)n_heads, (unsigned)splits), kAttnThreads, 0, st>>>(
+      scores, stats, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
   if ((rc = check_launch("attn_pv_kernel"))) return rc;
   attn_combine_kernel<<<(unsigned)((n_heads * head_dim + kAttnThreads - 1) / kAttnThreads), kAttnThreads, 0, st>>>(
       partial, splits, (int)n_heads, (int)head_dim, static_cast<uint16_t*>(context), f16);
