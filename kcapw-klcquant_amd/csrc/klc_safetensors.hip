@@ -407,6 +407,8 @@ int row_range(StFile* f, const char* name, int64_t first, int64_t count, int64_t
   KLC_REQUIRE(it != f->tensors.end(), KLC_ERR_ARGUMENT, "safetensors: no tensor named '%s'", name);
   const StTensor& t = it->second;
   KLC_REQUIRE(!t.shape.empty(), KLC_ERR_SHAPE, "safetensors: '%s' is a scalar", name);
+  KLC_REQUIRE(dtype_bytes(t.dtype) > 0, KLC_ERR_UNSUPPORTED, "safetensors: '%s' has dtype %s, whose rows are not sliced",
+              name, t.dtype.c_str());
   const int64_t rows = t.shape[0];
   KLC_REQUIRE(first >= 0 && count >= 0 && first + count <= rows, KLC_ERR_SHAPE,
               "safetensors: rows [%lld, %lld) outside the %lld rows of '%s'", (long long)first,

@@ -10,6 +10,7 @@ bad row ranges must raise, not read out of bounds.
 
 from __future__ import annotations
 
+import ctypes
 import json
 import struct
 
@@ -147,6 +148,17 @@ def test_malformed_files_are_rejected(tmp_path, case):
             deep = {"x": deep}
         path = _handmade(tmp_path, {"__metadata__": deep, **ok}, data)
     assert _err(SafetensorShard, path).status == -2
+
+
+def test_unknown_dtype_rows_are_refused(tmp_path):
+    """A dtype whose element size the reader does not know (sub-byte or new
+    formats) is listed but never sliced by rows."""
+    path = _handmade(tmp_path, {"f4": {"dtype": "F4", "shape": [4, 2], "data_offsets": [0, 4]}}, bytes(4))
+    with SafetensorShard(path) as shard:
+        assert shard.info("f4") == ("F4", (4, 2), 8 + len(json.dumps({"f4": {"dtype": "F4", "shape": [4, 2],
+                                                                        "data_offsets": [0, 4]}}).encode()), 4)
+        buf = (ctypes.c_uint8 * 4)()
+        assert _err(_native.call, "klc_st_read_rows", shard._h(), b"f4", 0, 1, ctypes.addressof(buf)).status == -3
 
 
 def test_missing_file_is_an_argument_error(tmp_path):
