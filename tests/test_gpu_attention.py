@@ -1,6 +1,8 @@
 """Decode attention on the device KV ring against the oracle.
 
-RoPE and the stored keys/values are bit-exact (every bfloat16 op rounded as
+Cases cover the single-split path (at most 256 keys) and the split path
+with its statistics and combine launches (up to 4500 keys, 18 splits).  RoPE
+and the stored keys/values are bit-exact (every bfloat16 op rounded as
 torch rounds it, then the cache type's rounding); the context is within
 1e-2 + 2e-2 |ref| of the oracle (probabilities rounded to the cache type can
 land one unit apart when the softmax sum is taken in another order).
@@ -35,7 +37,8 @@ def dev(b: np.ndarray, gpu) -> torch.Tensor:
 
 @pytest.mark.parametrize("kv", ["fp16", "bf16"])
 @pytest.mark.parametrize("steps,cap,window,sinks", [(1, 64, None, True), (300, 512, None, True), (300, 512, 128, False),
-                                                    (700, 512, None, True), (1000, 1024, 128, True)])
+                                                    (700, 512, None, True), (1000, 1024, 128, True),
+                                                    (4500, 8192, None, True)])
 def test_rope_append_and_decode_match_oracle(gpu, kv, steps, cap, window, sinks):
     cfg = AttentionConfig(**CFG)
     nh, nkv, d = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
