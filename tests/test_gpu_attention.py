@@ -141,3 +141,65 @@ def test_device_kv_cache_api(gpu):
     assert g.get(0)[0].dtype == torch.float16 and g.get(0)[0][:, 0, 0].tolist() == [0.0, 1.0, 2.0, 3.0, 4.0]
     with pytest.raises(ValueError):
         DeviceKVCache(gpu, precision="q8")
+
+
+@pytest.mark.parametrize("nh,nkv,d", [(32, 2, 128), (8, 8, 8), (12, 4, 24)])
+@pytest.mark.parametrize("window", [None, 100])
+def test_other_head_shapes(gpu, nh, nkv, d, window):
+    """Group sizes 16, 1 and 3 and head dims 128, 8 and 24 (a value-slice
+    count that does not divide the workgroup), bf16 cache, 300 steps."""
+    cfg = AttentionConfig(hidden_size=nh * d, num_heads=nh, num_kv_heads=nkv, head_dim=d, rope_factor=8.0)
+    rng = np.random.default_rng(nh * 1000 + d + (window or 0))
+    cap, steps = 512, 300
+    kc = torch.empty((cap, nkv, d), dtype=torch.bfloat16, device=gpu)
+    vc = torch.empty((cap, nkv, d), dtype=torch.bfloat16, device=gpu)
+    stream = P(torch.cuda.current_stream(gpu).cuda_stream)
+    keys, vals = [], []
+    for pos in range(steps):
+        q = f32_to_bf16(rng.standard_normal((nh, d)).astype(np.float32))
+        k = f32_to_bf16(rng.standard_normal((nkv, d)).astype(np.float32))
+        v = f32_to_bf16(rng.standard_normal((nkv, d)).astype(np.float32))
+        cos, sin = rope_cos_sin(cfg, pos, gpu, torch.bfloat16)
+        qd, kd, vd = dev(q, gpu), dev(k, gpu), dev(v, gpu)
+        q_out = torch.empty_like(qd)
+        _native.call("klc_rope_append", P(qd.data_ptr()), P(kd.data_ptr()), P(vd.data_ptr()), P(cos.data_ptr()),
+                     P(sin.data_ptr()), P(q_out.data_ptr()), None, P(kc.data_ptr()), P(vc.data_ptr()), pos % cap,
+                     cap, nh, nkv, d, 0, stream)
+        keys.append(oat.rope_rotate(k, bits(cos), bits(sin)))
+        vals.append(v)
+    q_rot = oat.rope_rotate(q, bits(cos), bits(sin))
+    assert np.array_equal(bits(q_out), q_rot)
+    count = min(steps, window) if window else steps
+    sk = f32_to_bf16(rng.standard_normal(nh).astype(np.float32))
+    skd = dev(sk, gpu)
+    ws = torch.empty(_native.call("klc_attn_workspace_bytes", nh, d, count), dtype=torch.uint8, device=gpu)
+    ctx = torch.empty((nh, d), dtype=torch.bfloat16, device=gpu)
+    _native.call("klc_attn_decode", P(q_out.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()), P(skd.data_ptr()), cap,
+                 steps - count, count, nh, nkv, d, 0, P(ws.data_ptr()), ws.numel(), P(ctx.data_ptr()), stream)
+    want, _ = oat.decode_attention(q_rot, np.stack(keys[-count:]), np.stack(vals[-count:]), sk, kv="bf16")
+    got, ref = bf16_to_f32(bits(ctx)), bf16_to_f32(want)
+    assert np.all(np.abs(got - ref) <= 1e-2 + 2e-2 * np.abs(ref)), np.abs(got - ref).max()
+
+
+def test_attention_rejects_bad_shapes(gpu):
+    x = torch.zeros(4096, dtype=torch.bfloat16, device=gpu)
+    ws = torch.zeros(1 << 16, dtype=torch.uint8, device=gpu)
+    stream = P(torch.cuda.current_stream(gpu).cuda_stream)
+
+    def decode(nh, nkv, d, count=4, cap=8, first=0):
+        with pytest.raises(_native.KlcError) as exc:
+            _native.call("klc_attn_decode", P(x.data_ptr()), P(x.data_ptr()), P(x.data_ptr()), None, cap, first,
+                         count, nh, nkv, d, 0, P(ws.data_ptr()), ws.numel(), P(x.data_ptr()), stream)
+        return exc.value.status
+
+    assert decode(34, 2, 64) == -2      # group of 17 > 16
+    assert decode(8, 8, 136) == -2      # head_dim above 128
+    assert decode(8, 8, 12) == -2       # head_dim not a multiple of 8
+    assert decode(8, 3, 64) == -2       # heads not a multiple of KV heads
+    assert decode(8, 8, 64, count=9) == -1   # more keys than the ring holds
+    assert decode(8, 8, 64, first=8) == -1   # first slot outside the ring
+    with pytest.raises(_native.KlcError) as exc:
+        _native.call("klc_rope_append", P(x.data_ptr()), P(x.data_ptr()), P(x.data_ptr()), P(x.data_ptr()),
+                     P(x.data_ptr()), P(x.data_ptr()), None, P(x.data_ptr()), P(x.data_ptr()), 8, 8, 8, 8, 64, 0,
+                     stream)
+    assert exc.value.status == -1       # slot == cap
