@@ -22,6 +22,7 @@
 #include <algorithm>
 
 #include "klc_common.h"
+#include "klc_torch_order.h"
 
 namespace klc {
 namespace {
@@ -207,18 +208,135 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ double readlane_f64(double v, int lane) {
-  const uint64_t u = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
-  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+// Orders LDS accesses of the lanes of one wave (no instruction: a wave's
+// LDS operations complete in order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
-// Top-k + softmax of one token's logits row by one wave, kSlots keys per lane.
+// LDS bytes one wave needs for wave_torch_topk over n logits: the entries
+// and the two stop-position lists of a partition step.
+__host__ __device__ constexpr size_t topk_tie_scratch_bytes(int n) { return ((size_t)n * 8 + 15) / 16 * 16; }
+
+// LDS bytes of the decode router's bfloat16 logits rows of one token tile.
+__host__ __device__ constexpr size_t decode_rows_bytes(int n_exp) {
+  return ((size_t)kRouterTile * n_exp * sizeof(uint16_t) + 15) / 16 * 16;
+}
+
+// torch.topk(row.float(), k)'s CPU order (klc_torch_order.h) for one row of
+// n bfloat16 logits, by one wave; leaves the k results in a[0 .. k)
+// (entry = comparator key << 16 | expert).  scratch: topk_tie_scratch_bytes(n)
+// bytes of LDS owned by the wave.  libstdc++'s introselect is followed step
+// by step, but each __unguarded_partition runs as one wave step: with the
+// pivot P at `first`, the left scan stops at the positions L holding a value
+// not greater than P (ascending) and the right scan at the positions R
+// holding a value not less than P (descending, then `first` itself); the
+// i-th swap exchanges L[i] and R[i] while L[i] < R[i], and after m swaps the
+// scan returns L[0] (m = 0), min(L[m], R[m - 1]) or, with L used up,
+// R[m - 1].  Lane 0 runs the sequential pieces (median of three, insertion
+// sorts, heap select, the final std::sort of k - 1 entries).
+__device__ void wave_torch_topk(const uint16_t* row, int n, int k, uint32_t* scratch) {
+  const int lane = threadIdx.x & 63;
+  uint32_t* a = scratch;
+  uint16_t* lp = reinterpret_cast<uint16_t*>(scratch + n);
+  uint16_t* rp = lp + n;
+  for (int p = lane; p < n; p += kWave) a[p] = order_entry(row[p], p);
+  wave_lds_sync();
+  if (k * 64 <= n) {  // TopKImpl.h: std::partial_sort
+    if (lane == 0) stl_partial_sort(a, 0, k, n);
+    wave_lds_sync();
+    return;
+  }
+  const int nth = k - 1;
+  int first = 0, last = n;
+  int depth = floor_log2(n) * 2;
+  bool selected = false;
+  while (last - first > 3) {
+    if (depth == 0) {
+      if (lane == 0) {
+        stl_heap_select(a, first, nth + 1, last);
+        entry_swap(a, first, nth);
+      }
+      selected = true;
+      break;
+    }
+    --depth;
+    if (lane == 0) stl_move_median_to_first(a, first, first + 1, first + (last - first) / 2, last - 1);
+    wave_lds_sync();
+    const uint32_t pk = a[first] >> 16;
+    int cl = 0, cr = 0;
+    for (int c = first + 1; c < last; c += kWave) {
+      const int p = c + lane;
+      const uint32_t key = p < last ? a[p] >> 16 : 0u;
+      const bool fl = p < last && key <= pk;
+      const bool fr = p < last && key >= pk;
+      const uint64_t bl = __ballot(fl), br = __ballot(fr);
+      const uint64_t below = (1ull << lane) - 1ull;
+      if (fl) lp[cl + __popcll(bl & below)] = (uint16_t)p;
+      if (fr) rp[cr + __popcll(br & below)] = (uint16_t)p;
+      cl += __popcll(bl);
+      cr += __popcll(br);
+    }
+    wave_lds_sync();
+    // R descending: R[i] = rp[cr - 1 - i]; L[i] < R[i] holds for a prefix of i
+    const int lim = min(cl, cr);
+    int m = 0;
+    for (int c = 0; c < lim; c += kWave) {
+      const int i = c + lane;
+      m += __popcll(__ballot(i < lim && lp[i] < rp[cr - 1 - i]));
+    }
+    int cut;
+    if (m == 0) cut = lp[0];
+    else if (m < cl) cut = min((int)lp[m], (int)rp[cr - m]);
+    else cut = rp[cr - m];
+    for (int c = 0; c < m; c += kWave) {
+      const int i = c + lane;
+      if (i < m) {
+        const int x = lp[i], y = rp[cr - 1 - i];
+        const uint32_t vx = a[x], vy = a[y];
+        a[x] = vy;
+        a[y] = vx;
+      }
+    }
+    wave_lds_sync();
+    if (cut <= nth) first = cut;
+    else last = cut;
+  }
+  if (lane == 0) {
+    if (!selected) stl_insertion_sort(a, first, last);
+    stl_sort(a, 0, k - 1);
+  }
+  wave_lds_sync();
+}
+
+// torch's CPU softmax (klc_torch_order.h) of the k values held by lanes
+// base .. base + k - 1 (lane base + r holds slot r), evaluated by every
+// lane; returns the bfloat16 weight of the calling lane's slot.
+__device__ __forceinline__ uint32_t torch_softmax_bf16(float v, int base, int k) {
+#pragma clang fp contract(off)
+  float mx = __shfl(v, base);
+  for (int r = 1; r < k; ++r) mx = torch_vec_max(mx, __shfl(v, base + r));
+  const float e = sleef_expf_u10(v - mx);
+  float sum = __shfl(e, base);
+  for (int r = 1; r < k; ++r) sum = sum + __shfl(e, base + r);
+  const float inv = 1.0f / sum;
+  return f32_to_bf16_rne(e * inv);
+}
+
+// Top-k + softmax of one token's logits row by one wave, kSlots keys per
+// lane.  The keys order values (NaN largest, -0 == +0), then lower expert
+// index first; k + 1 rounds of wave maxima give the k largest and the next
+// value.  If no two of those k + 1 values are equal, torch's order is that
+// descending order; otherwise the wave replays torch's order
+// (wave_torch_topk, tie_scratch: topk_tie_scratch_bytes(n_exp) bytes of
+// the wave's LDS).
 template <int kSlots>
 __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_exp, int k, int64_t t,
                                                    int32_t* __restrict__ ids, float* __restrict__ values,
-                                                   uint16_t* __restrict__ weights, int32_t* lds_ids) {
+                                                   uint16_t* __restrict__ weights, int32_t* lds_ids,
+                                                   uint32_t* tie_scratch) {
   const int lane = threadIdx.x & 63;
   uint64_t keys[kSlots];
 #pragma unroll
@@ -228,8 +346,10 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
   }
   // lane r keeps the r-th selection
   int my_id = 0;
-  float my_val = 0.0f;
-  for (int r = 0; r < k; ++r) {
+  bool tie = false;
+  uint32_t prev = 0;
+  const int rounds = k < n_exp ? k + 1 : k;
+  for (int r = 0; r < rounds; ++r) {
     uint64_t best = keys[0];
 #pragma unroll
     for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
@@ -237,50 +357,54 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
 #pragma unroll
     for (int s = 0; s < kSlots; ++s)
       if (keys[s] == best) keys[s] = 0ull;
-    if (lane == r) {
-      my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
-      my_val = bf16_to_f32(row[my_id]);
-    }
+    const uint32_t value_key = (uint32_t)(best >> 32);
+    tie |= r > 0 && value_key == prev;
+    prev = value_key;
+    if (lane == r) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
   }
-  // softmax over the k values: max is the first selection (NaN propagates);
-  // lane r evaluates exp(v_r - max) in float64, the sum runs in selection order
-  const double mx = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), 0));
-  const double ex = lane < k ? exp((double)my_val - mx) : 0.0;
-  double sum = 0.0;
-  for (int r = 0; r < k; ++r) sum += readlane_f64(ex, r);
+  if (tie) {  // uniform: every lane saw the same maxima
+    wave_torch_topk(row, n_exp, k, tie_scratch);
+    if (lane < k) my_id = (int)(tie_scratch[lane] & 0xffffu);
+    wave_lds_sync();
+  }
+  const float my_val = bf16_to_f32(row[lane < k ? my_id : 0]);
+  const uint32_t w = torch_softmax_bf16(my_val, 0, k);
   if (lane < k) {
     const int64_t o = t * k + lane;
     // agent scope: the decode router's final dispatch may run in another workgroup
     __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (lds_ids != nullptr) lds_ids[o] = my_id;
     if (values) values[o] = my_val;
-    weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
+    weights[o] = (uint16_t)w;
   }
 }
 
 __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t,
                                                  int32_t* __restrict__ ids, float* __restrict__ values,
-                                                 uint16_t* __restrict__ weights, int32_t* lds_ids) {
+                                                 uint16_t* __restrict__ weights, int32_t* lds_ids,
+                                                 uint32_t* tie_scratch) {
   const int slots = (n_exp + kWave - 1) / kWave;  // <= kTopkMaxPerLane (checked on the host)
-  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, ids, values, weights, lds_ids);
-  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, ids, values, weights, lds_ids);
-  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, ids, values, weights, lds_ids);
-  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, ids, values, weights, lds_ids);
-  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights, lds_ids);
+  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
+  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
+  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
+  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
+  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
 }
 
 // Top-k + softmax of 4 tokens at once by one wave: the 16 lanes of row q
 // (lanes 16 q .. 16 q + 15) take token t0 + q, lane r of the row holding the
 // keys of experts r + 16 s.  Each round's maximum comes from the lane's own
 // keys and 4 DPP steps inside the row (quad swaps, half-row and row
-// mirrors), so the 4 tokens' selections run side by side.  Same selection
-// and softmax as topk_softmax_row (n_exp <= 16 kSlots, k <= 16).  rows(q)
-// gives token q's logits row (any valid row for q >= n_valid, whose results
-// are not written).
+// mirrors), so the 4 tokens' selections run side by side.  Same selection,
+// tie handling and softmax as topk_softmax_row (n_exp <= 16 kSlots,
+// k <= 16); a row with ties is replayed by the whole wave.  rows(q) gives
+// token q's logits row (any valid row for q >= n_valid, whose results are
+// not written).
 template <int kSlots, typename RowFn>
 __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n_exp, int k, int64_t t0,
                                                   int32_t* __restrict__ ids, float* __restrict__ values,
-                                                  uint16_t* __restrict__ weights, int32_t* lds_ids) {
+                                                  uint16_t* __restrict__ weights, int32_t* lds_ids,
+                                                  uint32_t* tie_scratch) {
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
   const int r = lane & 15;
@@ -292,8 +416,10 @@ __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n
     keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
   }
   int my_id = 0;
-  float my_val = 0.0f;
-  for (int rd = 0; rd < k; ++rd) {
+  bool tie = false;
+  uint32_t prev = 0;
+  const int rounds = k < n_exp ? k + 1 : k;
+  for (int rd = 0; rd < rounds; ++rd) {
     uint64_t best = keys[0];
 #pragma unroll
     for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
@@ -304,41 +430,49 @@ __device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n
 #pragma unroll
     for (int s = 0; s < kSlots; ++s)
       if (keys[s] == best) keys[s] = 0ull;
-    if (r == rd) {
-      my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
-      my_val = bf16_to_f32(row[my_id]);
+    const uint32_t value_key = (uint32_t)(best >> 32);
+    tie |= rd > 0 && value_key == prev;
+    prev = value_key;
+    if (r == rd) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+  }
+  // rows whose k + 1 largest values include equal ones take torch's order
+  const uint64_t tie_rows = __ballot(tie && q < n_valid);
+  if (tie_rows != 0ull) {
+    for (int qq = 0; qq < 4; ++qq) {
+      if (((tie_rows >> (16 * qq)) & 1ull) == 0ull) continue;
+      wave_torch_topk(rows(qq), n_exp, k, tie_scratch);
+      if (q == qq && r < k) my_id = (int)(tie_scratch[r] & 0xffffu);
+      wave_lds_sync();
     }
   }
-  // softmax over the row's k values: max is the first selection (NaN
-  // propagates); lane r evaluates exp(v_r - max) in float64, the sum runs in
-  // selection order
-  const double mx = (double)__shfl(my_val, q * 16);
-  const double ex = r < k ? exp((double)my_val - mx) : 0.0;
-  double sum = 0.0;
-  for (int rd = 0; rd < k; ++rd) sum += __shfl(ex, q * 16 + rd);
+  const float my_val = bf16_to_f32(row[r < k ? my_id : 0]);
+  const uint32_t w = torch_softmax_bf16(my_val, q * 16, k);
   if (q < n_valid && r < k) {
     const int64_t o = (t0 + q) * k + r;
     // agent scope: the decode router's final dispatch may run in another workgroup
     __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (lds_ids != nullptr) lds_ids[o] = my_id;
     if (values) values[o] = my_val;
-    weights[o] = (uint16_t)f32_to_bf16_rne((float)(ex / sum));
+    weights[o] = (uint16_t)w;
   }
 }
 
 // Top-k of tokens t0 .. t0 + n - 1 (n <= 4) by one wave: the row-parallel
 // form when the row fits (n_exp <= 256, k <= 16), else token by token.
 // lds_ids (optional): a second copy of the ids in LDS, same indices.
+// tie_scratch: topk_tie_scratch_bytes(n_exp) bytes of LDS for this wave.
 template <typename RowFn>
 __device__ __forceinline__ void topk_softmax_tokens(RowFn rows, int n, int n_exp, int k, int64_t t0,
                                                     int32_t* __restrict__ ids, float* __restrict__ values,
-                                                    uint16_t* __restrict__ weights, int32_t* lds_ids = nullptr) {
+                                                    uint16_t* __restrict__ weights, int32_t* lds_ids,
+                                                    uint32_t* tie_scratch) {
   if (k <= 16 && n_exp <= 256) {
-    if (n_exp <= 64) topk_softmax_quad<4>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids);
-    else if (n_exp <= 128) topk_softmax_quad<8>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids);
-    else topk_softmax_quad<16>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids);
+    if (n_exp <= 64) topk_softmax_quad<4>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids, tie_scratch);
+    else if (n_exp <= 128) topk_softmax_quad<8>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids, tie_scratch);
+    else topk_softmax_quad<16>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids, tie_scratch);
   } else {
-    for (int q = 0; q < n; ++q) topk_softmax_row(rows(q), n_exp, k, t0 + q, ids, values, weights, lds_ids);
+    for (int q = 0; q < n; ++q)
+      topk_softmax_row(rows(q), n_exp, k, t0 + q, ids, values, weights, lds_ids, tie_scratch);
   }
 }
 
@@ -346,29 +480,31 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __res
                                                            int32_t* __restrict__ ids, float* __restrict__ values,
                                                            uint16_t* __restrict__ weights, int n_tok, int n_exp,
                                                            int k) {
-  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;  // 4 tokens per wave
+  extern __shared__ __align__(16) char lds[];  // topk_tie_scratch_bytes(n_exp) per wave
+  const int wave = threadIdx.x >> 6;
+  const int t0 = (blockIdx.x * 4 + wave) * 4;  // 4 tokens per wave
   if (t0 >= n_tok) return;
+  uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + wave * topk_tie_scratch_bytes(n_exp));
   topk_softmax_tokens([&](int q) { return logits + (int64_t)(t0 + q) * n_exp; }, min(4, n_tok - t0), n_exp, k, t0,
-                      ids, values, weights);
+                      ids, values, weights, nullptr, tie_scratch);
 }
 
-// Softmax of caller-chosen scores (one thread per token): the routing-locality
-// path picks the experts on the host and hands over their fp32 scores.  The
-// maximum propagates NaN; exponentials are summed in slot order in float64.
+// Softmax of caller-chosen scores (one thread per token), as torch's CPU
+// softmax computes it (klc_torch_order.h): the routing-locality path picks
+// the experts on the host and hands over their float32 scores in slot order.
 __global__ __launch_bounds__(256) void softmax_weights_kernel(const float* __restrict__ values,
                                                               uint16_t* __restrict__ weights, int n_tok, int k) {
+#pragma clang fp contract(off)
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_tok) return;
   const float* v = values + (int64_t)t * k;
-  double mx = (double)v[0];
-  for (int r = 1; r < k; ++r) {
-    const double x = (double)v[r];
-    mx = (x != x || x > mx) ? x : mx;
-  }
-  double sum = 0.0;
-  for (int r = 0; r < k; ++r) sum += exp((double)v[r] - mx);
+  float mx = v[0];
+  for (int r = 1; r < k; ++r) mx = torch_vec_max(mx, v[r]);
+  float sum = sleef_expf_u10(v[0] - mx);
+  for (int r = 1; r < k; ++r) sum = sum + sleef_expf_u10(v[r] - mx);
+  const float inv = 1.0f / sum;
   for (int r = 0; r < k; ++r)
-    weights[(int64_t)t * k + r] = (uint16_t)f32_to_bf16_rne((float)(exp((double)v[r] - mx) / sum));
+    weights[(int64_t)t * k + r] = (uint16_t)f32_to_bf16_rne(sleef_expf_u10(v[r] - mx) * inv);
 }
 
 constexpr int kDispatchThreads = 256;
@@ -756,9 +892,12 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   lds_barrier();  // the rows are in LDS; the logits' global stores need not have completed
   {
     const int tw = t0 + 4 * wave;  // 4 tokens per wave
+    // each wave's tie scratch follows the 16 logits rows
+    uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp) +
+                                                        wave * topk_tie_scratch_bytes(n_exp));
     if (tw < n_tok)
       topk_softmax_tokens([&](int q) { return rows + (tw - t0 + q) * n_exp; }, min(4, n_tok - tw), n_exp, k, tw, ids,
-                          values, weights, n_tt == 1 ? tile_ids : nullptr);
+                          values, weights, n_tt == 1 ? tile_ids : nullptr, tie_scratch);
   }
   if (n_tt > 1) {
     if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;
@@ -785,7 +924,7 @@ int launch_router_logits(const void* x, const void* w, const void* b, void* logi
 
 int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
                 int64_t k, hipStream_t stream) {
-  topk_softmax_kernel<<<(unsigned)((n_tok + 15) / 16), 256, 0, stream>>>(
+  topk_softmax_kernel<<<(unsigned)((n_tok + 15) / 16), 256, 4 * topk_tie_scratch_bytes((int)n_exp), stream>>>(
       static_cast<const uint16_t*>(logits), ids, values, static_cast<uint16_t*>(weights), (int)n_tok, (int)n_exp,
       (int)k);
   return check_launch("topk_softmax_kernel");
@@ -824,7 +963,7 @@ int launch_router_decode(const void* x, const void* w, const void* b, void* logi
   const dim3 grid((unsigned)((n_exp + kRouterTile - 1) / kRouterTile), (unsigned)((n_tok + kRouterTile - 1) / kRouterTile),
                   (unsigned)decode_router_slices(n_tok, hidden, n_exp));
   size_t lds = 3 * 64 * 4 * sizeof(double);
-  lds = std::max(lds, (size_t)kRouterTile * n_exp * sizeof(uint16_t));
+  lds = std::max(lds, decode_rows_bytes((int)n_exp) + 4 * topk_tie_scratch_bytes((int)n_exp));
   lds = std::max(lds, dispatch_lds_bytes((int)(n_tok * k), (int)n_exp));
   router_decode_kernel<<<grid, 256, lds, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),

@@ -14,8 +14,10 @@ Differences a caller can see:
 * ``hidden`` may also be ``[B, H]`` (a batch of tokens routed independently);
   the route dict then holds one list per token.  ``position`` may be a list of
   per-row positions.
-* top-k ties between equal bf16 logits go to the lower expert index (torch's
-  order on ties is unspecified).
+* none in the selection: equal logits come out in torch's CPU ``topk`` order
+  (the GPU replays libstdc++'s nth_element + sort on rows with ties).  The
+  logits themselves are correctly rounded, where torch's float32 F.linear
+  differs by one bf16 ulp on about 1 token in 60 at E = 128.
 * all tensors must be bf16 (the dtype the executor feeds,
   streamed_transformer_executor.py:354-355) and on the GPU.
 
@@ -216,11 +218,13 @@ class RouterStats:
 
 
 def _topk_order(values: np.ndarray, k: int) -> list[int]:
-    """Indices of the k largest float32 values: descending, NaN first, ties to the lower index."""
-    keyed = np.where(np.isnan(values), np.inf, values)
-    nan_first = ~np.isnan(values)
-    order = np.lexsort((np.arange(values.size), -keyed, nan_first))
-    return [int(i) for i in order[:k]]
+    """``torch.topk(values, k).indices`` of float32 host values (streamed_moe_router.py:271-273).
+
+    The routing-locality path selects on the host, row by row, as the
+    reference does; torch's own CPU top-k gives its order of equal values.
+    """
+    t = torch.from_numpy(np.ascontiguousarray(values, dtype=np.float32))
+    return [int(i) for i in torch.topk(t, int(k)).indices.tolist()]
 
 
 class StreamedMoERouter:

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import numpy as np
 
+from . import torch_cpu
 from .numerics import bf16_to_f32, f32_to_bf16
 
 
@@ -28,30 +29,29 @@ def router_logits(x_bits: np.ndarray, w_bits: np.ndarray, b_bits: np.ndarray) ->
 
 
 def topk(logits_bits: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
-    """``torch.topk(logits.float(), k)`` per row (streamed_moe_router.py:270-278).
+    """``torch.topk(logits.float(), k)`` per row on CPU (streamed_moe_router.py:270-278).
 
-    ``k = min(experts_per_token, E)`` (:442-451).  Values descend; equal values
-    are ordered by lower expert index first (the tie rule of this
-    implementation; torch leaves it implementation defined).
+    ``k = min(experts_per_token, E)`` (:442-451).  Values descend with NaN the
+    largest; equal values come in the order torch's CPU kernel leaves them
+    (libstdc++ ``nth_element`` + ``sort``, or ``partial_sort`` when
+    ``k * 64 <= E``), restated in ``torch_cpu.topk_order``.
     """
-    vals = bf16_to_f32(np.atleast_2d(logits_bits))
+    bits = np.atleast_2d(np.asarray(logits_bits, dtype=np.uint16))
+    vals = bf16_to_f32(bits)
     k = min(int(k), vals.shape[1])
-    # NaN sorts first, as in torch.topk (NaN is treated as the largest value).
-    key = np.where(np.isnan(vals), -np.inf, -vals)
-    order = np.argsort(key, axis=1, kind="stable")[:, :k]
-    return order.astype(np.int64), np.take_along_axis(vals, order, axis=1)
+    keys = torch_cpu.order_key_bf16(bits)
+    order = np.array([torch_cpu.topk_order(keys[r], k) for r in range(bits.shape[0])], dtype=np.int64)
+    order = order.reshape(bits.shape[0], k)
+    return order, np.take_along_axis(vals, order, axis=1)
 
 
 def softmax_weights(values: np.ndarray) -> np.ndarray:
-    """``torch.softmax(fp32 scores).to(bf16)`` (streamed_moe_router.py:281-282).
+    """``torch.softmax(fp32 scores, dim=-1).to(bf16)`` (streamed_moe_router.py:281-282).
 
-    Computed in float64 and rounded to float32, then to bfloat16.
+    The float32 softmax is torch's CPU kernel step for step
+    (``torch_cpu.softmax_f32``), then rounded to bfloat16.
     """
-    v = np.asarray(values, dtype=np.float32).astype(np.float64)
-    m = v.max(axis=-1, keepdims=True)
-    e = np.exp(v - m)
-    w = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
-    return f32_to_bf16(w)
+    return f32_to_bf16(torch_cpu.softmax_f32(values))
 
 
 def dispatch(ids: np.ndarray, num_experts: int):

@@ -56,7 +56,8 @@ def test_topk_ties_nan_and_signed_zero(gpu):
     bits = f32_to_bf16(f)
     ids, values, weights = ops.topk_softmax(bf16_tensor(bits, gpu), 3)
     torch.cuda.synchronize()
-    assert ids.cpu().numpy().tolist() == [[5, 1, 3], [0, 1, 2], [1, 9, 2], [9, 0, 1]]
+    # torch.topk's CPU order of these rows (torch 2.10)
+    assert ids.cpu().numpy().tolist() == [[5, 4, 1], [1, 0, 3], [1, 9, 3], [9, 6, 5]]
     want_ids, want_vals = orr.topk(bits, 3)
     assert np.array_equal(ids.cpu().numpy(), want_ids)
     w = bf16_bits(weights)
@@ -64,6 +65,51 @@ def test_topk_ties_nan_and_signed_zero(gpu):
     gn = (w & 0x7FFF) > 0x7F80
     assert np.array_equal(gn, (ow & 0x7FFF) > 0x7F80)
     assert np.array_equal(w[~gn], ow[~gn])
+
+
+def tie_heavy_logits(seed, n_tok, n_exp):
+    """bf16 logits with few distinct values per row (ties everywhere), some NaN and signed zeros."""
+    rng = np.random.default_rng(seed)
+    levels = rng.integers(1, 9, size=(n_tok, 1))
+    f = (rng.integers(0, 1 << 20, size=(n_tok, n_exp)) % levels).astype(np.float32) - 2.0
+    nan_rows = rng.random(n_tok) < 0.1
+    f[nan_rows, rng.integers(0, n_exp, int(nan_rows.sum()))] = np.nan
+    zero_rows = rng.random(n_tok) < 0.2
+    f[zero_rows, rng.integers(0, n_exp, int(zero_rows.sum()))] = -0.0
+    return f32_to_bf16(f)
+
+
+@pytest.mark.parametrize("n_exp,k", [(5, 3), (32, 4), (64, 4), (128, 4), (128, 16), (200, 7), (256, 4), (256, 16),
+                                     (300, 4), (1024, 4), (1024, 16), (1024, 32), (100, 32), (128, 1)])
+def test_topk_torch_order_on_tie_heavy_rows(gpu, n_exp, k):
+    """Rows full of equal values take the replay of torch's libstdc++ order (nth_element + sort, or
+    partial_sort when k * 64 <= n_exp), in the 4-tokens-per-wave and the wave-per-token kernels."""
+    n_tok = 203
+    bits = tie_heavy_logits(n_exp * 100 + k, n_tok, n_exp)
+    ids, values, weights = ops.topk_softmax(bf16_tensor(bits, gpu), k)
+    torch.cuda.synchronize()
+    want_ids, want_vals = orr.topk(bits, k)
+    assert np.array_equal(ids.cpu().numpy(), want_ids)
+    w = bf16_bits(weights)
+    ow = orr.softmax_weights(want_vals)
+    nan = (ow & 0x7FFF) > 0x7F80
+    assert np.array_equal((w & 0x7FFF) > 0x7F80, nan)
+    assert np.array_equal(w[~nan], ow[~nan])
+
+
+def test_topk_torch_order_past_the_introselect_depth_limit(gpu):
+    """Adversarial rows (McIlroy's adversary against median-of-three) drive libstdc++'s introselect
+    to its heap-select fallback; the kernel replays that branch too."""
+    from test_oracle_torch_cpu import _mcilroy_killer
+
+    rows = []
+    for n in (128,):
+        for coarse in (1, 2, 3):
+            rows.append(f32_to_bf16(np.floor(_mcilroy_killer(n, 3) / coarse)))
+    bits = np.stack(rows)
+    ids, _, _ = ops.topk_softmax(bf16_tensor(bits, gpu), 4)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), orr.topk(bits, 4)[0])
 
 
 @pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 128), (64, 4, 128), (2048, 4, 128), (7, 3, 5), (300, 2, 256),

@@ -52,9 +52,14 @@ def test_logits_at_full_width_match_fsum():
 def test_topk_tie_rule_and_order():
     bits = f32_to_bf16(np.array([[0, 2, 1, 2, 2, 3, 2]], dtype=np.float32))
     ids, vals = router.topk(bits, 3)
-    # value-descending, equal values by lower expert index (torch leaves ties implementation defined)
-    assert ids.tolist() == [[5, 1, 3]]
+    # value-descending; equal values in the order torch's CPU topk leaves them
+    # (measured with torch 2.10: topk([0, 2, 1, 2, 2, 3, 2], 3) -> [5, 4, 3])
+    assert ids.tolist() == [[5, 4, 3]]
     assert vals.tolist() == [[3.0, 2.0, 2.0]]
+    # four equal maxima at 5, 17, 40, 99 of 128 zeros (measured: [17, 99, 5, 40])
+    v = np.zeros((1, 128), np.float32)
+    v[0, [5, 17, 40, 99]] = 1.0
+    assert router.topk(f32_to_bf16(v), 4)[0].tolist() == [[17, 99, 5, 40]]
 
 
 def test_topk_matches_brute_force_without_ties():
