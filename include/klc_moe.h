@@ -216,6 +216,26 @@ int klc_moe_layer(const void* x, const void* router_w, const void* router_b, con
                   int path, void* workspace, int64_t workspace_bytes, void* out, const void* residual, int32_t* ids,
                   void* weights, void* const* events, void* stream);
 
+/* The same layer as klc_moe_layer without a workspace argument: it has no
+ * counterpart in the reference and is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  It calls no hipMalloc, hipFree or allocating routine.
+ * Its scratch is a static device array of KLC_STATIC_SCRATCH_BYTES in the
+ * library, one per GPU, held until the process ends; a call needing more
+ * (klc_moe_workspace_bytes(n_tokens, ...) > KLC_STATIC_SCRATCH_BYTES: at
+ * gpt-oss-120B shape, more than about 360 tokens) fails with
+ * KLC_ERR_UNSUPPORTED.  Every call on one GPU shares that GPU's array, so
+ * calls that overlap on one GPU (different streams, or threads without
+ * ordering) race: order them on one stream.  The first call on a device
+ * looks the array up and clears its counters with a kernel on `stream`.
+ * Arguments and results as klc_moe_layer. */
+#define KLC_STATIC_SCRATCH_BYTES (32 * 1024 * 1024)
+int klc_moe_layer_static_scratch(const void* x, const void* router_w, const void* router_b,
+                                 const void* const* w_gate_up, const void* gate_up_bias, const void* const* w_down,
+                                 const void* down_bias, int64_t n_tokens, int64_t hidden, int64_t inter,
+                                 int64_t n_experts, int64_t k, float swiglu_limit, int precision, int path, void* out,
+                                 const void* residual, int32_t* ids, void* weights, void* const* events, void* stream);
+
 /* ---- RMSNorm (stacked decode) -------------------------------------------------
  * rms_norm(x, weight, eps) of streamed_attention.py:27-28 for bfloat16
  * x[n_tokens][hidden] and weight[hidden]: x * rsqrt(mean(x.float()^2) + eps)

@@ -15,6 +15,8 @@
 // klc_common.h).  gate_up applies bias and the
 // clamped SwiGLU on interleaved row pairs in registers and writes the down
 // input; down applies bias and writes float32 expert outputs.
+#include <mutex>
+
 #include "klc_common.h"
 
 namespace klc {
@@ -683,31 +685,40 @@ extern "C" int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int
   return layer_scratch(n_tokens, hidden, inter, n_experts, k).total;
 }
 
-extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
-                             const void* gate_up_bias, const void* const* w_down, const void* down_bias,
-                             int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
-                             float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
-                             void* out, const void* residual, int32_t* ids, void* weights, void* const* events,
-                             void* stream) {
-  KLC_REQUIRE(x && router_w && router_b && w_gate_up && gate_up_bias && w_down && down_bias && workspace && out,
-              KLC_ERR_ARGUMENT, "klc_moe_layer: null pointer");
+namespace klc {
+namespace {
+
+// Argument checks shared by klc_moe_layer and klc_moe_layer_static_scratch
+// (everything but the scratch memory); `fn` names the entry point.
+int check_layer_args(const char* fn, const void* x, const void* router_w, const void* router_b,
+                     const void* const* w_gate_up, const void* gate_up_bias, const void* const* w_down,
+                     const void* down_bias, const void* out, int64_t n_tokens, int64_t hidden, int64_t inter,
+                     int64_t n_experts, int64_t k, int precision, int path) {
+  KLC_REQUIRE(x && router_w && router_b && w_gate_up && gate_up_bias && w_down && down_bias && out,
+              KLC_ERR_ARGUMENT, "%s: null pointer", fn);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
-              "klc_moe_layer: unknown precision %d", precision);
+              "%s: unknown precision %d", fn, precision);
   KLC_REQUIRE(path == KLC_PATH_AUTO || path == KLC_PATH_GEMV || path == KLC_PATH_GEMM, KLC_ERR_ARGUMENT,
-              "klc_moe_layer: unknown path %d", path);
+              "%s: unknown path %d", fn, path);
   int rc = check_router_args(n_tokens, hidden, n_experts);
   if (rc) return rc;
   rc = check_topk_args(n_tokens, n_experts, k);
   if (rc) return rc;
   rc = check_gemv_shapes(hidden, inter, n_tokens * k, n_experts);
   if (rc) return rc;
-  KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "klc_moe_layer: n_tokens=%lld > 65535", (long long)n_tokens);
-  const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
-  KLC_REQUIRE(workspace_bytes >= s.total, KLC_ERR_ARGUMENT, "klc_moe_layer: workspace of %lld bytes < %lld needed",
-              (long long)workspace_bytes, (long long)s.total);
-  KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "klc_moe_layer: workspace must be 256-byte aligned");
+  KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "%s: n_tokens=%lld > 65535", fn, (long long)n_tokens);
+  return KLC_OK;
+}
 
-  char* ws = static_cast<char*>(workspace);
+// The layer's launches on scratch memory `ws` (layer_scratch layout, counters
+// zero on entry and left zero).
+int run_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                  const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
+                  int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
+                  int path, char* ws, void* out, const void* residual, int32_t* ids, void* weights,
+                  void* const* events, void* stream) {
+  int rc = KLC_OK;
+  const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
   void* logits = ws + s.logits;
   int32_t* ids_buf = ids ? ids : reinterpret_cast<int32_t*>(ws + s.ids);
   float* values = reinterpret_cast<float*>(ws + s.values);
@@ -770,4 +781,89 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   if ((rc = mark(5))) return rc;
   if ((rc = launch_combine(eo, w_buf, residual, n_tokens, k, hidden, out, st))) return rc;
   return mark(6);
+}
+
+__global__ __launch_bounds__(256) void clear_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Scratch memory of klc_moe_layer_static_scratch: one array per GPU, held by
+// the process from the library's load on.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a host-side stand-in): the
+// device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[KLC_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's `scratch`, looked up (and its
+// completion counters cleared on `stream`) on the first call on that device.
+int static_scratch_address(const char* fn, hipStream_t stream, char** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  KLC_REQUIRE(err == hipSuccess, KLC_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(err));
+  KLC_REQUIRE(dev >= 0 && dev < kMaxDevices, KLC_ERR_UNSUPPORTED, "%s: device %d >= %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    KLC_REQUIRE(err == hipSuccess && ptr != nullptr, KLC_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", fn,
+                hipGetErrorString(err));
+    // the array starts zeroed; the counters are cleared once more, by a kernel
+    // (not a memset, so that a caller capturing this call in a graph records
+    // no memset node), and every launch leaves them zero
+    clear_words_kernel<<<(kCounterBytes / 4 + 255) / 256, 256, 0, stream>>>(static_cast<uint32_t*>(ptr),
+                                                                             (int)(kCounterBytes / 4));
+    const int rc = check_launch("clear_words_kernel");
+    if (rc) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<char*>(g_scratch_ptr[dev]);
+  return KLC_OK;
+}
+
+}  // namespace
+}  // namespace klc
+
+extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                             const void* gate_up_bias, const void* const* w_down, const void* down_bias,
+                             int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                             float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
+                             void* out, const void* residual, int32_t* ids, void* weights, void* const* events,
+                             void* stream) {
+  int rc = check_layer_args("klc_moe_layer", x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, out,
+                            n_tokens, hidden, inter, n_experts, k, precision, path);
+  if (rc) return rc;
+  KLC_REQUIRE(workspace != nullptr, KLC_ERR_ARGUMENT, "klc_moe_layer: null pointer");
+  const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
+  KLC_REQUIRE(workspace_bytes >= s.total, KLC_ERR_ARGUMENT, "klc_moe_layer: workspace of %lld bytes < %lld needed",
+              (long long)workspace_bytes, (long long)s.total);
+  KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "klc_moe_layer: workspace must be 256-byte aligned");
+  return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
+                       n_experts, k, swiglu_limit, precision, path, static_cast<char*>(workspace), out, residual, ids,
+                       weights, events, stream);
+}
+
+extern "C" int klc_moe_layer_static_scratch(const void* x, const void* router_w, const void* router_b,
+                                            const void* const* w_gate_up, const void* gate_up_bias,
+                                            const void* const* w_down, const void* down_bias, int64_t n_tokens,
+                                            int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                                            float swiglu_limit, int precision, int path, void* out,
+                                            const void* residual, int32_t* ids, void* weights, void* const* events,
+                                            void* stream) {
+  const char* fn = "klc_moe_layer_static_scratch";
+  int rc = check_layer_args(fn, x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, out, n_tokens,
+                            hidden, inter, n_experts, k, precision, path);
+  if (rc) return rc;
+  const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
+  KLC_REQUIRE(s.total <= (int64_t)KLC_STATIC_SCRATCH_BYTES, KLC_ERR_UNSUPPORTED,
+              "%s: the layer needs %lld bytes of scratch for n_tokens=%lld, more than the %lld bytes of the "
+              "library's static scratch (use klc_moe_layer with a workspace)", fn, (long long)s.total,
+              (long long)n_tokens, (long long)KLC_STATIC_SCRATCH_BYTES);
+  char* ws = nullptr;
+  if ((rc = static_scratch_address(fn, as_stream(stream), &ws))) return rc;
+  return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
+                       n_experts, k, swiglu_limit, precision, path, ws, out, residual, ids, weights, events, stream);
 }

@@ -199,6 +199,33 @@ class MoELayer:
 
     __call__ = forward
 
+    def forward_static_scratch(self, x: torch.Tensor, out: torch.Tensor | None = None,
+                               ids: torch.Tensor | None = None, weights: torch.Tensor | None = None,
+                               residual: torch.Tensor | None = None) -> torch.Tensor:
+        """:meth:`forward` without a workspace (klc_moe_layer_static_scratch).
+
+        The library's static per-GPU scratch is used instead of a workspace
+        tensor, so nothing is allocated when ``out`` is given: for callers
+        that cannot allocate (HIP graph capture, serving loops).  Calls on one
+        GPU share that scratch and must be ordered on one stream.
+        """
+        ops._check_gpu("hidden", x, torch.bfloat16, 2)
+        if x.shape[1] != self.w.hidden:
+            raise ValueError(f"hidden size {x.shape[1]} != layer hidden {self.w.hidden}")
+        if residual is not None:
+            ops._check_gpu("residual", residual, torch.bfloat16, 2)
+            if residual.shape != x.shape:
+                raise ValueError(f"residual shape {tuple(residual.shape)} != hidden shape {tuple(x.shape)}")
+        if out is None:
+            out = torch.empty_like(x)
+        w = self.w
+        nat.call("klc_moe_layer_static_scratch", ops._ptr(x), ops._ptr(w.router_weight), ops._ptr(w.router_bias),
+                 ops._ptr(w.gate_up_table), ops._ptr(w.gate_up_bias), ops._ptr(w.down_table), ops._ptr(w.down_bias),
+                 x.shape[0], w.hidden, w.inter, w.n_experts, self.k, self.limit, ops.PRECISIONS[self.precision],
+                 self.PATHS[self.path], ops._ptr(out), ops._ptr(residual), ops._ptr(ids), ops._ptr(weights), None,
+                 ops._stream(x.device))
+        return out
+
     def uses_gemm(self, n_tokens: int) -> bool:
         """Whether :meth:`forward` runs the grouped GEMM for ``n_tokens`` tokens (the library's rule)."""
         if self.path != "auto":
