@@ -92,16 +92,19 @@ int klc_moe_router_logits(const void* x, const void* w, const void* b, void* log
 
 /* Top-k selection and routing weights (streamed_moe_router.py:270-284,
  * 442-451, with routing locality disabled): per token, ids[t][j] (int32) of
- * the k largest logits in descending order (NaN largest; equal values: lower
- * expert index first), their float32 values, and weights = softmax over the
- * k values rounded to bfloat16.  k <= 32, n_experts <= 1024. */
+ * the k largest logits in descending order (NaN largest), equal values in
+ * the order torch.topk leaves them on the CPU (libstdc++ nth_element + sort,
+ * or partial_sort when k * 64 <= n_experts), their float32 values, and
+ * weights = torch's float32 CPU softmax over the k values rounded to
+ * bfloat16.  k <= 32, n_experts <= 1024. */
 int klc_moe_topk_softmax(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tokens,
                          int64_t n_experts, int64_t k, void* stream);
 
 /* Routing weights for experts chosen on the host (streamed_moe_router.py:281-282
  * when routing locality is enabled and the selection of :331-394 is made by
- * the caller): weights[t][j] = bf16(softmax(values[t][:])[j]) with the maximum
- * propagating NaN and the sum taken in slot order in float64.  k <= 1024. */
+ * the caller): weights[t][j] = bf16(softmax(values[t][:])[j]) as torch's
+ * CPU softmax computes it in float32 (maximum propagating NaN, SLEEF expf,
+ * sum in slot order, one reciprocal).  k <= 1024. */
 int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens, int64_t k, void* stream);
 
 /* Expert-sorted dispatch (no reference counterpart: the reference routes one

@@ -19,7 +19,12 @@ Modules and what pins them (tests/test_oracle_*.py):
 * ``router``    — router logits, top-k, softmax, dispatch
   (streamed_moe_router.py:268-284, 365-375).  Pinned by exact rational
   dot products (``fractions``), brute-force selection and closed-form
-  softmax cases.
+  softmax cases, and against torch's own CPU results on the golden vectors
+  of tests/golden/ (ids, tie order, bf16 weights, combine bits).
+* ``torch_cpu`` — the torch CPU kernels the router calls: top-k's libstdc++
+  order of equal values and the float32 softmax with SLEEF's expf.  Pinned
+  directly against ``torch.topk`` / ``torch.softmax`` (tie-heavy rows, the
+  partial-sort regime, adversarial rows past the introselect depth limit).
 * ``experts``   — gate_up / clamped SwiGLU / down / weighted combine
   (streamed_moe_router.py:483-529) and the bias-only fallback (:317-322).
   Pinned by clamp special cases, exact rational GEMVs on tiny shapes and
