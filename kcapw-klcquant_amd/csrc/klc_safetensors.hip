@@ -82,8 +82,10 @@ bool pread_all(int fd, void* dst, int64_t n, int64_t off) {
 // the process).  run(n, fn) calls fn(0..n-1) on the workers and the caller
 // and returns when all have finished; concurrent callers take turns.  A job
 // is published through one 64-bit ticket, (generation << 32) | next slice:
-// a slice is claimed by a compare-exchange that also checks the generation,
-// so a worker holding a finished job's generation claims nothing.  Between
+// a slice is claimed by a compare-exchange that also checks the generation.
+// Before the next job is written the finished one's ticket is retired (slice
+// index past any count), so a worker holding a finished job's generation
+// claims nothing.  Between
 // jobs a worker spins for kSpinNs before it sleeps, so the chunks of one
 // load, tens of microseconds apart, find it awake.  In a forked child the
 // workers do not exist, so the caller runs every slice.
@@ -101,10 +103,16 @@ class ReadPool {
       return;
     }
     std::lock_guard<std::mutex> turn(run_m_);
+    // Retire the finished job first: its ticket's slice index becomes
+    // kRetired, above any slice count, so a worker still holding that
+    // generation claims nothing, whatever n_ it reads while the new job is
+    // written (a stale compare-exchange fails on the changed ticket).
+    const uint64_t old_gen = ticket_.load(std::memory_order_relaxed) >> 32;
+    ticket_.store((old_gen << 32) | kRetired, std::memory_order_seq_cst);
     job_ = &fn;
     n_.store(n, std::memory_order_relaxed);
     unfinished_.store(n, std::memory_order_relaxed);
-    const uint64_t gen = (ticket_.load(std::memory_order_relaxed) >> 32) + 1;
+    const uint64_t gen = old_gen + 1;
     ticket_.store(gen << 32, std::memory_order_seq_cst);
     if (sleepers_.load(std::memory_order_seq_cst) > 0) {
       std::lock_guard<std::mutex> g(m_);
@@ -118,6 +126,7 @@ class ReadPool {
  private:
   static constexpr unsigned kMaxReaders = 16;
   static constexpr int64_t kSpinNs = 200000;
+  static constexpr uint64_t kRetired = 0xffffffffu;
 
   explicit ReadPool(int threads) : pid_(getpid()), workers_(threads - 1) {
     for (unsigned i = 0; i < workers_; ++i) std::thread([this] { loop(); }).detach();

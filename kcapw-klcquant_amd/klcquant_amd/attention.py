@@ -97,14 +97,20 @@ def apply_rope(q: torch.Tensor, k: torch.Tensor, position: int, config: Attentio
 
 class DeviceKVCache:
     """KVCacheManager (kv_cache_manager.py:18-113) for the "fp16" and "bf16"
-    precisions, kept as one ring per layer in device memory."""
+    precisions, kept as one ring per layer in device memory.
+
+    ``offload_to_cpu`` is accepted (the executor passes its
+    ``offload_kv_cache`` setting, streamed_transformer_executor.py) but the
+    ring stays in HBM: the attention kernels read it in place, and a gpt-oss
+    cache of 4,096 tokens is about 8 MB per layer of the 288 GB.  ``get``
+    returns tensors on the compute device either way, as the reference's does.
+    """
 
     def __init__(self, device: torch.device, offload_to_cpu: bool = False, max_tokens: int | None = None,
                  precision: str = "fp16", capacity: int = 4096) -> None:
         if precision not in _KV_DTYPES:
             raise ValueError(f"unsupported KV cache precision for the device cache: {precision}")
-        if offload_to_cpu:
-            raise ValueError("DeviceKVCache keeps the cache in GPU memory (offload_to_cpu=False)")
+        self.offload_to_cpu = bool(offload_to_cpu)  # recorded; the ring stays on the device
         self.device = torch.device(device)
         self.compute_device = self.device
         self.max_tokens = max_tokens

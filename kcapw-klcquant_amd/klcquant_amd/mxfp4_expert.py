@@ -22,9 +22,10 @@ it unchanged.  What differs underneath:
 from __future__ import annotations
 
 import json
+import queue
+import threading
 import time
-from collections import Counter
-from concurrent.futures import Future, ThreadPoolExecutor
+from collections import Counter, OrderedDict, deque
 from dataclasses import dataclass
 from pathlib import Path
 from threading import RLock
@@ -83,219 +84,272 @@ def _nbytes(t: torch.Tensor) -> int:
     return t.numel() * t.element_size()
 
 
-class ExpertWeightCache:
-    """Byte-bounded cache of expert matrices keyed ``(layer, expert, proj)``.
+@dataclass
+class _Entry:
+    """One cached packed matrix and what the eviction policy knows about it."""
 
-    Eviction follows mxfp4_expert.py:183-245: among unpinned entries (and, with
-    layer-aware quotas, the most over-quota layer's entries first), prefer those
-    whose protection window has passed, then evict the lowest
-    ``(future_score, frequency, last_access)``.  ``max_bytes <= 0`` disables
-    insertion.  Thread safe.
+    value: torch.Tensor
+    nbytes: int
+    born: int  # clock value at insertion
+    uses: int = 0  # lookups that found it
+    hold_until: int = 0  # clock value up to which a protect/prefetch hint holds it
+    pinned: bool = False
+    prefetched: bool = False  # brought in by a prefetch and not looked up since
+
+
+class ExpertWeightCache:
+    """Byte-budgeted cache of packed expert matrices, keyed ``(layer, expert, proj)``.
+
+    The reference's cache holds dequantized matrices (mxfp4_expert.py:68-354);
+    this one holds the packed MXFP4 form the expert kernels stream, 3.76x
+    smaller, with its own policy:
+
+    * **Recency order.**  Entries sit in least-recently-used order; a lookup
+      that finds an entry moves it to the back.  The clock advances by one per
+      lookup and per insertion.
+    * **Holds.**  ``hold(keys, window)`` (the store's protect / prefetch hints,
+      also reachable as ``set_future_scores``) protects those matrices for the
+      next ``window`` clock ticks, whether or not they are resident yet.
+    * **Eviction.**  While the resident bytes exceed ``max_bytes``, the victim
+      is the least recently used entry that is neither pinned nor held; if
+      every unpinned candidate is held, the least recently used held one goes
+      (counted in ``protected_eviction_skips``).  Pinned entries never go.
+    * **Layer quotas** (``layer_aware`` with ``layer_count > 0``): each layer's
+      quota is ``max_bytes / layer_count``; while some layer is over its quota,
+      victims come from the layer with the largest bytes-to-quota ratio first.
+      With ``adaptive_layer_quota``, a layer with at least 32 lookups gets the
+      quota scaled by ``max(0.25, 1 + strength * (its hit rate - the mean hit
+      rate of such layers))``: layers that reuse their experts keep more.
+    * ``max_bytes <= 0`` stores nothing.
+
+    Counters and telemetry keep the reference's names (``ExpertCacheStats``,
+    ``to_json`` keys), since the router and the executor's runtime stats read
+    them.  Thread safe (one re-entrant lock).
     """
+
+    HOLD_ADAPT_MIN_LOOKUPS = 32
 
     def __init__(self, max_bytes: int, layer_count: int = 0, layer_aware: bool = False,
                  adaptive_layer_quota: bool = False, adaptive_layer_quota_strength: float = 1.5) -> None:
-        self.max_bytes = max_bytes
+        self.max_bytes = int(max_bytes)
         self.layer_count = max(int(layer_count), 0)
-        self.layer_aware = layer_aware
-        self.adaptive_layer_quota = adaptive_layer_quota
+        self.layer_aware = bool(layer_aware)
+        self.adaptive_layer_quota = bool(adaptive_layer_quota)
         self.adaptive_layer_quota_strength = max(float(adaptive_layer_quota_strength), 0.0)
-        self.current_bytes = 0
-        self.items: dict[Key, torch.Tensor] = {}
-        self.item_bytes: dict[Key, int] = {}
-        self.layer_bytes: Counter[int] = Counter()
-        self.frequency: dict[Key, int] = {}
-        self.last_access: dict[Key, int] = {}
-        self.birth_access: dict[Key, int] = {}
-        self.future_score: dict[Key, float] = {}
-        self.protected_until: dict[Key, int] = {}
-        self.prefetched: set[Key] = set()
-        self.evicted_lifetimes: list[int] = []
-        self.eviction_reasons: Counter[str] = Counter()
-        self.layer_hits: Counter[int] = Counter()
-        self.layer_misses: Counter[int] = Counter()
-        self.layer_evictions: Counter[int] = Counter()
-        self.layer_hit_bytes: Counter[int] = Counter()
-        self.layer_loaded_bytes: Counter[int] = Counter()
-        self.pinned: set[Key] = set()
-        self.access_index = 0
         self.stats = ExpertCacheStats()
         self.lock = RLock()
+        self.clock = 0
+        self.current_bytes = 0
+        self._entries: OrderedDict[Key, _Entry] = OrderedDict()
+        self._held: dict[Key, int] = {}  # holds of keys that are not resident (yet)
+        self._layer_bytes: Counter[int] = Counter()
+        self._lookups: Counter[int] = Counter()  # per layer
+        self._found: Counter[int] = Counter()  # per layer
+        self._layer_found_bytes: Counter[int] = Counter()
+        self._layer_evicted: Counter[int] = Counter()
+        self.layer_loaded_bytes: Counter[int] = Counter()  # the store books miss traffic here
+        self._lifetimes: list[int] = []
+        self._reasons: Counter[str] = Counter()
+        self.eviction_log: deque[Key] = deque(maxlen=4096)  # the most recent victims, oldest first
+
+    # ---- lookups and insertions -------------------------------------------------------
 
     def get(self, key: Key) -> torch.Tensor | None:
         with self.lock:
-            self.access_index += 1
+            self.clock += 1
             self.stats.lifetime_accesses += 1
-            value = self.items.get(key)
-            if value is None:
+            layer = key[0]
+            self._lookups[layer] += 1
+            entry = self._entries.get(key)
+            if entry is None:
                 self.stats.misses += 1
-                self.layer_misses[key[0]] += 1
                 return None
-            size = _nbytes(value)
+            self._entries.move_to_end(key)
+            entry.uses += 1
+            self._found[layer] += 1
+            self._layer_found_bytes[layer] += entry.nbytes
             self.stats.hits += 1
-            self.stats.hit_bytes += size
-            self.layer_hits[key[0]] += 1
-            self.layer_hit_bytes[key[0]] += size
-            self.frequency[key] = self.frequency.get(key, 0) + 1
-            self.last_access[key] = self.access_index
-            self.future_score[key] = self.future_score.get(key, 0.0) * 0.80
-            if key in self.pinned:
-                self.stats.pinned_hits += 1
-            if key in self.prefetched:
-                self.prefetched.discard(key)
+            self.stats.hit_bytes += entry.nbytes
+            self.stats.pinned_hits += entry.pinned
+            if entry.prefetched:
+                entry.prefetched = False
                 self.stats.prefetch_used += 1
-            return value
+            return entry.value
 
     def put(self, key: Key, value: torch.Tensor, pin: bool = False, prefetched: bool = False) -> None:
-        size = _nbytes(value)
         if self.max_bytes <= 0:
             return
+        nbytes = _nbytes(value)
         with self.lock:
-            if key in self.items:
-                old = self.item_bytes.get(key, _nbytes(self.items[key]))
-                self.current_bytes -= old
-                self.layer_bytes[key[0]] -= old
-            else:
-                self.birth_access[key] = self.access_index
-            self.items[key] = value
-            self.item_bytes[key] = size
-            self.access_index += 1
-            self.frequency[key] = self.frequency.get(key, 0) + 1
-            self.last_access[key] = self.access_index
-            if prefetched:
-                self.prefetched.add(key)
-            if pin:
-                self.pinned.add(key)
-            self.current_bytes += size
-            self.layer_bytes[key[0]] += size
-            self.stats.dequantized_bytes += size
-            self._evict_to_budget()
+            self.clock += 1
+            old = self._entries.pop(key, None)
+            if old is not None:
+                self._account(key, -old.nbytes)
+            entry = _Entry(value, nbytes, born=self.clock, pinned=pin or (old is not None and old.pinned),
+                           prefetched=prefetched, hold_until=self._held.pop(key, 0))
+            if old is not None:
+                entry.hold_until = max(entry.hold_until, old.hold_until)
+            self._entries[key] = entry
+            self._account(key, nbytes)
+            self.stats.dequantized_bytes += nbytes
+            self._shrink_to_budget()
+
+    def count_hits(self, layer: int, n: int) -> None:
+        """Books ``n`` lookups served outside the cache (always-resident matrices) as hits."""
+        with self.lock:
+            self.clock += n
+            self.stats.lifetime_accesses += n
+            self.stats.hits += n
+            self._lookups[layer] += n
+            self._found[layer] += n
 
     def pin(self, key: Key) -> None:
         with self.lock:
-            if key in self.items:
-                self.pinned.add(key)
+            entry = self._entries.get(key)
+            if entry is not None:
+                entry.pinned = True
+
+    @property
+    def pinned(self) -> set[Key]:
+        with self.lock:
+            return {k for k, e in self._entries.items() if e.pinned}
 
     def contains(self, key: Key) -> bool:
         with self.lock:
-            return key in self.items
+            return key in self._entries
 
     def resident_experts(self, layer_idx: int) -> set[int]:
         with self.lock:
-            return {expert for layer, expert, _ in self.items if layer == layer_idx}
+            return {expert for layer, expert, _ in self._entries if layer == layer_idx}
 
-    def set_future_scores(self, keys: list[Key], scores: dict[Key, float] | None = None,
-                          protect_window: int = 64) -> None:
+    def hold(self, keys, window: int = 64) -> None:
+        """Protects ``keys`` from eviction for the next ``window`` clock ticks."""
         with self.lock:
-            for key in list(self.future_score):
-                decayed = self.future_score[key] * 0.85
-                if decayed < 1e-4:
-                    del self.future_score[key]
-                else:
-                    self.future_score[key] = decayed
-            horizon = self.access_index + max(int(protect_window), 1)
+            until = self.clock + max(int(window), 1)
             for key in keys:
-                score = float(scores.get(key, 1.0)) if scores else 1.0
-                self.future_score[key] = max(self.future_score.get(key, 0.0), score)
-                self.protected_until[key] = max(self.protected_until.get(key, 0), horizon)
+                entry = self._entries.get(key)
+                if entry is not None:
+                    entry.hold_until = max(entry.hold_until, until)
+                else:
+                    self._held[key] = max(self._held.get(key, 0), until)
+            # forget holds of keys that never arrived once they have run out
+            if len(self._held) > 4096:
+                self._held = {k: t for k, t in self._held.items() if t > self.clock}
 
-    def _evict_to_budget(self) -> None:
-        while self.current_bytes > self.max_bytes and self.items:
-            candidates, reason = self._eviction_candidates()
-            if not candidates:
-                break
-            free = [k for k in candidates if self.protected_until.get(k, 0) <= self.access_index]
-            if free:
-                candidates = free
-            else:
-                self.stats.protected_eviction_skips += 1
-            victim = min(candidates, key=lambda k: (self.future_score.get(k, 0.0), self.frequency.get(k, 0),
-                                                     self.last_access.get(k, 0)))
-            old = self.items.pop(victim)
-            size = self.item_bytes.pop(victim, _nbytes(old))
-            born = self.birth_access.pop(victim, self.access_index)
-            self.evicted_lifetimes.append(max(self.access_index - born, 0))
-            for table in (self.frequency, self.last_access, self.future_score, self.protected_until):
-                table.pop(victim, None)
-            self.prefetched.discard(victim)
-            self.current_bytes -= size
-            self.layer_bytes[victim[0]] -= size
-            if self.layer_bytes[victim[0]] <= 0:
-                self.layer_bytes.pop(victim[0], None)
-            self.eviction_reasons[reason] += 1
-            self.layer_evictions[victim[0]] += 1
-            self.stats.evictions += 1
+    def set_future_scores(self, keys, scores=None, protect_window: int = 64) -> None:
+        """The reference's name for a hint (mxfp4_expert.py:166-181): a hold of ``protect_window``."""
+        self.hold(keys, protect_window)
 
-    def _eviction_candidates(self) -> tuple[list[Key], str]:
-        candidates = [k for k in self.items if k not in self.pinned]
-        if not candidates or not self.layer_aware or self.layer_count <= 0:
-            return candidates, "global_pressure"
+    # ---- eviction -----------------------------------------------------------------------
+
+    def _account(self, key: Key, delta: int) -> None:
+        self.current_bytes += delta
+        self._layer_bytes[key[0]] += delta
+        if self._layer_bytes[key[0]] <= 0:
+            del self._layer_bytes[key[0]]
+
+    def layer_quota(self, layer: int) -> float:
+        """Bytes layer ``layer`` may hold before its entries are evicted first."""
         base = self.max_bytes / max(self.layer_count, 1)
-        over = [layer for layer, size in self.layer_bytes.items()
-                if size > self._layer_quota(layer, base)
-                and any(k[0] == layer and k not in self.pinned for k in self.items)]
-        if not over:
-            return candidates, "global_pressure"
-        worst = max(over, key=lambda layer: self.layer_bytes[layer] / max(self._layer_quota(layer, base), 1.0))
-        in_layer = [k for k in candidates if k[0] == worst]
-        reason = "adaptive_layer_quota_pressure" if self.adaptive_layer_quota else "layer_quota_pressure"
-        return in_layer or candidates, reason
-
-    def _layer_quota(self, layer: int, base_quota: float) -> float:
         if not self.adaptive_layer_quota:
-            return base_quota
-        hits = self.layer_hits.get(layer, 0)
-        total = hits + self.layer_misses.get(layer, 0)
-        if total < 32:
-            return base_quota
-        weight = 0.5 + self.adaptive_layer_quota_strength * (hits / max(total, 1))
-        return base_quota * max(weight, 0.25)
+            return base
+        rates = {l: self._found[l] / n for l, n in self._lookups.items() if n >= self.HOLD_ADAPT_MIN_LOOKUPS}
+        if layer not in rates:
+            return base
+        mean = sum(rates.values()) / len(rates)
+        return base * max(0.25, 1.0 + self.adaptive_layer_quota_strength * (rates[layer] - mean))
+
+    def _pressured_layer(self) -> int | None:
+        if not (self.layer_aware and self.layer_count > 0):
+            return None
+        worst, worst_ratio = None, 1.0
+        for layer, nbytes in self._layer_bytes.items():
+            ratio = nbytes / max(self.layer_quota(layer), 1.0)
+            if ratio > worst_ratio and any(k[0] == layer and not e.pinned for k, e in self._entries.items()):
+                worst, worst_ratio = layer, ratio
+        return worst
+
+    def _oldest_evictable(self, layer: int | None) -> Key | None:
+        """Least recently used unpinned entry (of ``layer``, if given), preferring unheld ones."""
+        first_held = None
+        for key, entry in self._entries.items():  # least recently used first
+            if entry.pinned or (layer is not None and key[0] != layer):
+                continue
+            if entry.hold_until <= self.clock:
+                return key
+            if first_held is None:
+                first_held = key
+        if first_held is not None:
+            self.stats.protected_eviction_skips += 1
+        return first_held
+
+    def _pick_victim(self) -> tuple[Key | None, str]:
+        layer = self._pressured_layer()
+        if layer is not None:
+            victim = self._oldest_evictable(layer)
+            if victim is not None:
+                return victim, ("adaptive_layer_quota_pressure" if self.adaptive_layer_quota
+                                else "layer_quota_pressure")
+        return self._oldest_evictable(None), "global_pressure"
+
+    def _shrink_to_budget(self) -> None:
+        while self.current_bytes > self.max_bytes:
+            victim, reason = self._pick_victim()
+            if victim is None:
+                return  # everything left is pinned
+            entry = self._entries.pop(victim)
+            self._account(victim, -entry.nbytes)
+            self._lifetimes.append(self.clock - entry.born)
+            self._reasons[reason] += 1
+            self._layer_evicted[victim[0]] += 1
+            self.stats.evictions += 1
+            self.eviction_log.append(victim)
+
+    @property
+    def eviction_reasons(self) -> Counter[str]:
+        return self._reasons
+
+    # ---- telemetry (keys of mxfp4_expert.py:310-354) --------------------------------------
 
     def to_json(self) -> dict:
-        """Telemetry with the keys of mxfp4_expert.py:310-354."""
         with self.lock:
             st = self.stats
-            hot = sorted(
-                ({"layer": k[0], "expert": k[1], "proj": k[2], "frequency": self.frequency.get(k, 0),
-                  "future_score": round(self.future_score.get(k, 0.0), 6),
-                  "age_accesses": self.access_index - self.birth_access.get(k, self.access_index),
-                  "pinned": k in self.pinned, "prefetched": k in self.prefetched} for k in self.items),
-                key=lambda row: (row["future_score"], row["frequency"], row["pinned"]), reverse=True)
-            life = sorted(self.evicted_lifetimes)
-
-            def pct(q):
-                return life[int(q * (len(life) - 1))] if life else None
-
-            mats = max(st.materializations, 1)
+            mib = 2 ** 20
+            per_item = [{"layer": k[0], "expert": k[1], "proj": k[2], "frequency": e.uses,
+                         "future_score": float(max(e.hold_until - self.clock, 0)),
+                         "age_accesses": self.clock - e.born, "pinned": e.pinned, "prefetched": e.prefetched}
+                        for k, e in self._entries.items()]
+            per_item.sort(key=lambda r: (r["future_score"], r["frequency"], r["pinned"]), reverse=True)
+            life = sorted(self._lifetimes)
+            n_mat = max(st.materializations, 1)
             finished = st.prefetch_completed + st.prefetch_failed
-            residency = [{"layer": int(layer), "resident_mb": round(size / 2**20, 6),
-                          "resident_items": sum(1 for k in self.items if k[0] == layer),
-                          "resident_experts": len({k[1] for k in self.items if k[0] == layer})}
-                         for layer, size in sorted(self.layer_bytes.items())]
-            layers = sorted(set(self.layer_hits) | set(self.layer_misses) | set(self.layer_evictions)
-                            | set(self.layer_loaded_bytes) | set(self.layer_hit_bytes))
-            activity = []
-            for layer in layers:
-                h, m = int(self.layer_hits.get(layer, 0)), int(self.layer_misses.get(layer, 0))
-                activity.append({"layer": int(layer), "hits": h, "misses": m, "hit_rate": h / max(h + m, 1),
-                                 "evictions": int(self.layer_evictions.get(layer, 0)),
-                                 "loaded_mb": round(int(self.layer_loaded_bytes.get(layer, 0)) / 2**20, 6),
-                                 "hit_mb": round(int(self.layer_hit_bytes.get(layer, 0)) / 2**20, 6)})
+            by_layer: dict[int, list[Key]] = {}
+            for k in self._entries:
+                by_layer.setdefault(k[0], []).append(k)
+            residency = [{"layer": int(l), "resident_mb": round(self._layer_bytes[l] / mib, 6),
+                          "resident_items": len(keys), "resident_experts": len({k[1] for k in keys})}
+                         for l, keys in sorted(by_layer.items())]
+            activity = [{"layer": int(l), "hits": int(self._found[l]), "misses": int(self._lookups[l] - self._found[l]),
+                         "hit_rate": self._found[l] / max(self._lookups[l], 1),
+                         "evictions": int(self._layer_evicted[l]),
+                         "loaded_mb": round(self.layer_loaded_bytes[l] / mib, 6),
+                         "hit_mb": round(self._layer_found_bytes[l] / mib, 6)}
+                        for l in sorted(set(self._lookups) | set(self._layer_evicted) | set(self.layer_loaded_bytes))]
             return {
                 "hits": st.hits, "misses": st.misses, "hit_rate": st.hit_rate, "pinned_hits": st.pinned_hits,
                 "evictions": st.evictions, "resident_bytes": self.current_bytes,
-                "resident_mb": round(self.current_bytes / 2**20, 6), "resident_items": len(self.items),
-                "pinned_items": len(self.pinned), "loaded_bytes": st.loaded_bytes,
-                "loaded_mb": round(st.loaded_bytes / 2**20, 6), "dequantized_bytes": st.dequantized_bytes,
-                "dequantized_mb": round(st.dequantized_bytes / 2**20, 6), "hit_bytes": st.hit_bytes,
-                "hit_mb": round(st.hit_bytes / 2**20, 6), "miss_loaded_bytes": st.miss_loaded_bytes,
-                "miss_loaded_mb": round(st.miss_loaded_bytes / 2**20, 6),
+                "resident_mb": round(self.current_bytes / mib, 6), "resident_items": len(self._entries),
+                "pinned_items": sum(e.pinned for e in self._entries.values()), "loaded_bytes": st.loaded_bytes,
+                "loaded_mb": round(st.loaded_bytes / mib, 6), "dequantized_bytes": st.dequantized_bytes,
+                "dequantized_mb": round(st.dequantized_bytes / mib, 6), "hit_bytes": st.hit_bytes,
+                "hit_mb": round(st.hit_bytes / mib, 6), "miss_loaded_bytes": st.miss_loaded_bytes,
+                "miss_loaded_mb": round(st.miss_loaded_bytes / mib, 6),
                 "effective_useful_bandwidth": st.hit_bytes / max(st.loaded_bytes, 1),
                 "materializations": st.materializations,
                 "materialization_time_s": round(st.materialization_time_s, 6),
-                "avg_materialization_time_ms": round(1000.0 * st.materialization_time_s / mats, 6),
+                "avg_materialization_time_ms": round(1e3 * st.materialization_time_s / n_mat, 6),
                 "transfer_time_s": round(st.transfer_time_s, 6), "dequant_time_s": round(st.dequant_time_s, 6),
-                "avg_dequant_time_ms": round(1000.0 * st.dequant_time_s / mats, 6),
+                "avg_dequant_time_ms": round(1e3 * st.dequant_time_s / n_mat, 6),
                 "blocked_on_prefetch_s": round(st.blocked_on_prefetch_s, 6), "futures_waited": st.futures_waited,
                 "prefetch_submitted": st.prefetch_submitted, "prefetch_completed": st.prefetch_completed,
                 "prefetch_failed": st.prefetch_failed, "prefetch_used": st.prefetch_used,
@@ -304,13 +358,13 @@ class ExpertWeightCache:
                 "prefetch_skipped_pending": st.prefetch_skipped_pending,
                 "protected_eviction_skips": st.protected_eviction_skips,
                 "evicted_lifetime": {"count": len(life), "mean_accesses": sum(life) / len(life) if life else None,
-                                     "p50_accesses": pct(0.50), "p90_accesses": pct(0.90)},
+                                     "p50_accesses": life[(len(life) - 1) // 2] if life else None,
+                                     "p90_accesses": life[int(0.9 * (len(life) - 1))] if life else None},
                 "layer_aware": self.layer_aware, "adaptive_layer_quota": self.adaptive_layer_quota,
                 "layer_count": self.layer_count,
-                "layer_quota_mb": round((self.max_bytes / max(self.layer_count, 1)) / 2**20, 6)
-                if self.layer_count else None,
+                "layer_quota_mb": round(self.max_bytes / max(self.layer_count, 1) / mib, 6) if self.layer_count else None,
                 "layer_residency": residency, "layer_activity": activity,
-                "eviction_reasons": dict(self.eviction_reasons), "hot_items": hot[:50],
+                "eviction_reasons": dict(self._reasons), "hot_items": per_item[:50],
             }
 
 
@@ -351,13 +405,33 @@ class SafetensorIndex:
             return shard
 
 
+class _Inflight:
+    """A miss being brought in by a background loader: done when ``event`` is set."""
+
+    __slots__ = ("event", "error")
+
+    def __init__(self) -> None:
+        self.event = threading.Event()
+        self.error: BaseException | None = None
+
+
 class Mxfp4ExpertStore:
     """Expert store with the constructor and methods of mxfp4_expert.py:382-531.
 
-    Cached values are packed matrices (uint8, row-tile layout).  Misses are
-    read from the checkpoint (``model.layers.{L}.mlp.experts.{proj}_{blocks,scales}``
-    sliced at the expert), copied to the device on a side stream and packed
-    there; the compute stream waits on an event, never on the device.
+    Cached values are packed matrices (uint8, row-tile layout).  A miss reads
+    the expert's slice of ``model.layers.{L}.mlp.experts.{proj}_{blocks,scales}``
+    from the checkpoint shard into pinned staging and packs it into HBM on a
+    side stream; the stream that then uses the matrix waits on an event, never
+    on the device.
+
+    Prefetch (``async_prefetch=True``): ``max_prefetch_workers`` daemon loader
+    threads take keys from one queue and bring them in; a key is "in flight"
+    from its submission until its loader finishes.  A lookup of an in-flight
+    key waits (host) for its loader and re-raises the loader's exception, as
+    the reference does when it consumes a failed prefetch (mxfp4_expert.py:454-462).
+    Packed tensors are allocated on the side stream and recorded on every
+    stream they are handed to, so the caching allocator reuses their memory
+    only after the work that reads them.
     """
 
     def __init__(self, model_dir: str | Path, support_dir: str | Path, device: torch.device,
@@ -376,16 +450,21 @@ class Mxfp4ExpertStore:
         self.quant_loader = quant_loader
         self.async_prefetch = async_prefetch
         self.default_protect_window = max(int(default_protect_window), 1)
-        self.executor = (ThreadPoolExecutor(max_workers=max_prefetch_workers)
-                         if async_prefetch and max_prefetch_workers > 0 else None)
-        self.pending: dict[Key, Future] = {}
-        self.pending_lock = RLock()
-        self._shapes: dict[Key, tuple[int, int]] = {}
         self._side = torch.cuda.Stream(self.device)
-        # side-stream events of packs enqueued without a host wait, per key,
-        # until one is seen complete
+        self._shapes: dict[Key, tuple[int, int]] = {}
+        # side-stream events of packs not yet seen complete, per key
         self._ready: dict[Key, torch.cuda.Event] = {}
         self._ready_lock = RLock()
+        self._inflight: dict[Key, _Inflight] = {}
+        self._inflight_lock = RLock()
+        self._queue: queue.SimpleQueue | None = None
+        self._loaders: list[threading.Thread] = []
+        if async_prefetch and max_prefetch_workers > 0:
+            self._queue = queue.SimpleQueue()
+            for i in range(int(max_prefetch_workers)):
+                t = threading.Thread(target=self._loader_loop, name=f"expert-loader-{i}", daemon=True)
+                t.start()
+                self._loaders.append(t)
 
     # ---- reference API ---------------------------------------------------------
 
@@ -397,25 +476,27 @@ class Mxfp4ExpertStore:
         return ops.mxfp4_dequant_packed(packed, rows, groups, self.dtype)
 
     def protect_experts(self, layer_idx: int, expert_ids: list[int], protect_window: int | None = None) -> None:
-        self.cache.set_future_scores(self._matrix_keys(layer_idx, expert_ids),
-                                     protect_window=protect_window or self.default_protect_window)
+        self.cache.hold(self._matrix_keys(layer_idx, expert_ids), protect_window or self.default_protect_window)
 
     def prefetch_experts(self, layer_idx: int, expert_ids: list[int], protect_window: int | None = None) -> None:
         if not expert_ids:
             return
         keys = self._matrix_keys(layer_idx, expert_ids)
-        self.cache.set_future_scores(keys, protect_window=protect_window or self.default_protect_window)
-        if self.executor is None:
+        self.cache.hold(keys, protect_window or self.default_protect_window)
+        if self._queue is None:
             return
-        with self.pending_lock:
-            for key in keys:
-                if self.cache.contains(key):
-                    self.cache.stats.prefetch_skipped_resident += 1
-                elif key in self.pending:
-                    self.cache.stats.prefetch_skipped_pending += 1
-                else:
-                    self.pending[key] = self.executor.submit(self._prefetch_worker, key)
-                    self.cache.stats.prefetch_submitted += 1
+        st = self.cache.stats
+        for key in keys:
+            if self.cache.contains(key):
+                st.prefetch_skipped_resident += 1
+                continue
+            with self._inflight_lock:
+                if key in self._inflight:
+                    st.prefetch_skipped_pending += 1
+                    continue
+                self._inflight[key] = _Inflight()
+            st.prefetch_submitted += 1
+            self._queue.put(key)
 
     def resident_experts(self, layer_idx: int) -> set[int]:
         return self.cache.resident_experts(layer_idx)
@@ -427,37 +508,37 @@ class Mxfp4ExpertStore:
 
     def to_json(self) -> dict:
         payload = self.cache.to_json()
-        with self.pending_lock:
-            payload["pending_prefetches"] = len(self.pending)
+        with self._inflight_lock:
+            payload["pending_prefetches"] = len(self._inflight)
         return payload
+
+    def close(self) -> None:
+        """Stops the loader threads after the keys already queued (idempotent)."""
+        if self._queue is None:
+            return
+        for _ in self._loaders:
+            self._queue.put(None)
+        for t in self._loaders:
+            t.join()
+        self._loaders, self._queue = [], None
 
     # ---- packed access (the fused router path) ---------------------------------
 
     def packed_expert(self, layer_idx: int, expert_idx: int, proj: str) -> torch.Tensor:
         """Packed matrix of one expert projection, usable on the current stream.
 
-        Counts one cache access, like ``load_expert_matrix`` in the reference.
+        Counts one cache lookup, like ``load_expert_matrix`` in the reference.
         """
         key = (int(layer_idx), int(expert_idx), proj)
-        self._consume_pending_if_needed(key)
-        cached = self.cache.get(key)
-        if cached is None:
-            cached = self._materialize_expert_matrix(key, prefetched=False)
-        if self._ready:
-            self._order_after_load(key)
-        return cached
-
-    def _order_after_load(self, key: Key) -> None:
-        """Makes the current stream wait (on the device) for the pack of
-        ``key`` if it may still be running on the side stream."""
-        with self._ready_lock:
-            ev = self._ready.get(key)
-            if ev is None:
-                return
-            if ev.query():
-                del self._ready[key]
-                return
-        torch.cuda.current_stream(self.device).wait_event(ev)
+        self._wait_inflight(key)
+        packed = self.cache.get(key)
+        if packed is None:
+            packed = self._materialize_expert_matrix(key, prefetched=False)
+        stream = torch.cuda.current_stream(self.device)
+        self._order_after_load(key, stream)
+        if stream != self._side:
+            packed.record_stream(stream)
+        return packed
 
     def matrix_shape(self, layer_idx: int, expert_idx: int, proj: str) -> tuple[int, int]:
         """``(rows, groups)`` of a materialized projection."""
@@ -467,57 +548,71 @@ class Mxfp4ExpertStore:
 
     @staticmethod
     def _matrix_keys(layer_idx: int, expert_ids: list[int]) -> list[Key]:
-        return [(int(layer_idx), int(e), "gate_up_proj") for e in expert_ids] + \
-               [(int(layer_idx), int(e), "down_proj") for e in expert_ids]
+        # the order the router uses them: every gate_up, then every down
+        return [(int(layer_idx), int(e), proj) for proj in PROJECTIONS for e in expert_ids]
 
-    def _consume_pending_if_needed(self, key: Key) -> None:
-        with self.pending_lock:
-            future = self.pending.pop(key, None)
-        if future is None:
+    def _order_after_load(self, key: Key, stream: torch.cuda.Stream) -> None:
+        """``stream`` waits (on the device) for the pack of ``key`` if it may still run."""
+        with self._ready_lock:
+            ev = self._ready.get(key)
+            if ev is None:
+                return
+            if ev.query():
+                del self._ready[key]
+                return
+        stream.wait_event(ev)
+
+    def _wait_inflight(self, key: Key) -> None:
+        with self._inflight_lock:
+            job = self._inflight.get(key)
+        if job is None:
             return
         start = time.perf_counter()
         self.cache.stats.futures_waited += 1
-        try:
-            future.result()
-        finally:
-            self.cache.stats.blocked_on_prefetch_s += time.perf_counter() - start
+        job.event.wait()
+        self.cache.stats.blocked_on_prefetch_s += time.perf_counter() - start
+        if job.error is not None:
+            raise job.error
 
-    def _prefetch_worker(self, key: Key) -> None:
-        try:
-            if not self.cache.contains(key):
-                self._materialize_expert_matrix(key, prefetched=True)
-            self.cache.stats.prefetch_completed += 1
-        except Exception:
-            self.cache.stats.prefetch_failed += 1
-            raise
-        finally:
-            with self.pending_lock:
-                self.pending.pop(key, None)
+    def _loader_loop(self) -> None:
+        while True:
+            key = self._queue.get() if self._queue is not None else None
+            if key is None:
+                return
+            with self._inflight_lock:
+                job = self._inflight.get(key)
+            try:
+                if not self.cache.contains(key):
+                    self._materialize_expert_matrix(key, prefetched=True)
+                self.cache.stats.prefetch_completed += 1
+            except BaseException as exc:  # handed to whoever looks the key up
+                self.cache.stats.prefetch_failed += 1
+                if job is not None:
+                    job.error = exc
+            finally:
+                with self._inflight_lock:
+                    self._inflight.pop(key, None)
+                if job is not None:
+                    job.event.set()
 
     def _materialize_expert_matrix(self, key: Key, prefetched: bool) -> torch.Tensor:
-        """Checkpoint shard -> pinned staging -> device (side stream) -> packed layout.
+        """Checkpoint shard -> pinned staging -> packed layout in HBM, on the side stream.
 
         Blocks and scales in one shard (the checkpoint's layout) take the fused
-        path: klc_st_load_mxfp4_packed reads and packs chunk by chunk on the
-        side stream without waiting for the compute stream, and returns once
-        the last pack is enqueued; ``packed_expert`` then makes the caller's
-        stream wait for an event after that pack, so no host wait is needed
-        and the next miss's reads overlap these packs.  Otherwise
-        (a quantized loader, or the two tensors in different shards) the slices
-        are copied first and packed after the side stream has waited for the
-        compute stream, into a tensor allocated on the compute stream.  Only
-        the side stream is synchronised.
+        path: klc_st_load_mxfp4_packed reads and packs chunk by chunk and
+        returns once the last pack is enqueued; an event after that pack is
+        what a consuming stream waits on (``_order_after_load``), so the next
+        miss's reads overlap these packs.  Otherwise (a quantized loader, or
+        the two tensors in different shards) the slices are copied to the
+        device and packed, and the side stream is synchronised.  The packed
+        tensor is always allocated on the side stream.
         """
         layer_idx, expert_idx, proj = key
         start = time.perf_counter()
         base = f"model.layers.{layer_idx}.mlp.experts.{proj}"
         names = (f"{base}_blocks", f"{base}_scales")
-        compute = torch.cuda.current_stream(self.device)
+        st = self.cache.stats
         if not self._from_quant_loader(names[0]) and self.index.shard(names[0]) is self.index.shard(names[1]):
-            # shard -> pinned staging -> packed, chunk by chunk on the side
-            # stream; the packed tensor is allocated on the compute stream
-            # and marked as used by the side stream, so its memory is reused
-            # only after both the packs and the compute work that reads it
             packed, rows, groups = self.index.shard(names[0]).load_mxfp4_packed(
                 names[0], names[1], expert_idx, self.device, self._side, wait=False)
             ready = torch.cuda.Event()
@@ -525,7 +620,7 @@ class Mxfp4ExpertStore:
             with self._ready_lock:
                 self._ready[key] = ready
             loaded = rows * groups * 17
-            self.cache.stats.transfer_time_s += time.perf_counter() - start
+            st.transfer_time_s += time.perf_counter() - start
         else:
             if self._from_quant_loader(names[0]):
                 blocks, scales = (self._load_expert_tensor(n, expert_idx) for n in names)
@@ -534,29 +629,27 @@ class Mxfp4ExpertStore:
                     b_dev = blocks.to(torch.uint8).contiguous().pin_memory().to(self.device, non_blocking=True)
                     s_dev = scales.to(torch.uint8).contiguous().pin_memory().to(self.device, non_blocking=True)
             else:
-                # blocks and scales in different shards: staged copies, then the pack
                 b_dev, s_dev = self._copy_expert_tensors(names, expert_idx)
                 self._check_pair(b_dev.shape, s_dev.shape)
-            copied = torch.cuda.Event()
-            copied.record(self._side)
             loaded = _nbytes(b_dev) + _nbytes(s_dev)
             rows, groups = int(b_dev.shape[0]), int(b_dev.shape[1])
-            packed = torch.empty(ops.packed_bytes(rows, groups), dtype=torch.uint8, device=self.device)
-            self._side.wait_stream(compute)
             with torch.cuda.stream(self._side):
+                copied = torch.cuda.Event()
+                copied.record(self._side)
+                packed = torch.empty(ops.packed_bytes(rows, groups), dtype=torch.uint8, device=self.device)
                 ops.mxfp4_pack(b_dev, s_dev, out=packed)
                 done = torch.cuda.Event()
                 done.record(self._side)
             copied.synchronize()
-            self.cache.stats.transfer_time_s += time.perf_counter() - start
+            st.transfer_time_s += time.perf_counter() - start
             pack_start = time.perf_counter()
             done.synchronize()
-            self.cache.stats.dequant_time_s += time.perf_counter() - pack_start
-        self.cache.stats.loaded_bytes += loaded
-        self.cache.stats.miss_loaded_bytes += loaded
+            st.dequant_time_s += time.perf_counter() - pack_start
+        st.loaded_bytes += loaded
+        st.miss_loaded_bytes += loaded
         self.cache.layer_loaded_bytes[layer_idx] += loaded
-        self.cache.stats.materialization_time_s += time.perf_counter() - start
-        self.cache.stats.materializations += 1
+        st.materialization_time_s += time.perf_counter() - start
+        st.materializations += 1
         self._shapes[key] = (rows, groups)
         self.cache.put(key, packed, prefetched=prefetched)
         return packed
@@ -624,10 +717,7 @@ class ResidentExpertStore:
 
     def record_access(self, layer_idx: int, n_matrices: int) -> None:
         """Counts ``n_matrices`` expert-matrix reads of a resident layer as hits."""
-        with self.cache.lock:
-            self.cache.stats.hits += n_matrices
-            self.cache.stats.lifetime_accesses += n_matrices
-            self.cache.layer_hits[int(layer_idx)] += n_matrices
+        self.cache.count_hits(int(layer_idx), int(n_matrices))
 
     def load_expert_matrix(self, layer_idx: int, expert_idx: int, proj: str) -> torch.Tensor:
         w = self.layer(layer_idx)

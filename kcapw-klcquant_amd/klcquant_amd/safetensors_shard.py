@@ -160,8 +160,8 @@ class SafetensorShard:
 
         Chunks of 64-row tiles are read into this thread's pinned staging and
         packed by a kernel on ``stream`` that reads the staging over PCIe (the
-        packed tensor is allocated on the current stream and marked as used
-        by ``stream``).  With ``wait`` the call
+        packed tensor is allocated on ``stream``; a caller that uses it on
+        another stream records that stream on it).  With ``wait`` the call
         returns once the packed matrix is complete; without it, once the last
         pack is enqueued (work on ``stream`` then sees the finished matrix, and
         the next load from this thread overlaps the packs still running).
@@ -175,8 +175,11 @@ class SafetensorShard:
                              f"scales.shape={s_shape[1:]} ({b_dtype}/{s_dtype})")
         rows, groups = int(b_shape[1]), int(b_shape[2])
         staging = _thread_staging()
-        packed = torch.empty(_packed_bytes(rows, groups), dtype=torch.uint8, device=device)
-        packed.record_stream(stream)
+        # allocated on `stream`, the stream that writes it: the caching
+        # allocator then hands out only memory whose earlier users are done
+        # in that stream's order (or recorded by record_stream)
+        with torch.cuda.stream(stream):
+            packed = torch.empty(_packed_bytes(rows, groups), dtype=torch.uint8, device=device)
         _native.call("klc_st_load_mxfp4_packed", self._h(), blocks_name.encode(), scales_name.encode(), int(expert),
                      ctypes.c_void_p(staging.data_ptr()), staging.numel(), ctypes.c_void_p(packed.data_ptr()),
                      ctypes.c_void_p(stream.cuda_stream))

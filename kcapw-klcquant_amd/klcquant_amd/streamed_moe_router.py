@@ -525,37 +525,57 @@ class StreamedMoERouter:
             return []
         return [int(e) for e, _ in scores.most_common(max(int(limit or self.experts_per_token), 1))]
 
-    def _effective_expert_count(self, layer_idx: int, expert_count: int) -> int:
+    # ---- active-expert cap (streamed_moe_router.py:442-476) --------------------------------
+
+    def _cap_bounds(self) -> tuple[int, int]:
+        """(lowest, highest) per-layer cap the dynamic controller may reach."""
         cfg = self.locality_config
-        k = min(self.experts_per_token, expert_count)
-        if cfg.enabled and cfg.active_experts_per_token_cap > 0:
-            k = min(k, int(cfg.active_experts_per_token_cap))
-        if cfg.enabled and cfg.dynamic_active_expert_cap:
-            base = cfg.active_experts_per_token_cap or self.experts_per_token
-            start = min(max(base, cfg.min_active_experts_per_token),
-                        cfg.max_active_experts_per_token or self.experts_per_token)
-            k = min(k, self.dynamic_caps.setdefault(layer_idx, start))
-        return max(k, 1)
+        return max(int(cfg.min_active_experts_per_token), 1), int(cfg.max_active_experts_per_token
+                                                                  or self.experts_per_token)
+
+    def _effective_expert_count(self, layer_idx: int, expert_count: int) -> int:
+        """Experts per token for this call: ``experts_per_token`` limited by the
+        expert count and, with locality enabled, by the static cap and the
+        layer's dynamic cap.  A layer's dynamic cap starts at the static cap
+        (or ``experts_per_token``) brought into the controller's bounds."""
+        cfg = self.locality_config
+        limits = [self.experts_per_token, expert_count]
+        if cfg.enabled:
+            if cfg.active_experts_per_token_cap > 0:
+                limits.append(int(cfg.active_experts_per_token_cap))
+            if cfg.dynamic_active_expert_cap:
+                lo, hi = self._cap_bounds()
+                start = min(max(cfg.active_experts_per_token_cap or self.experts_per_token, lo), hi)
+                limits.append(self.dynamic_caps.setdefault(layer_idx, start))
+        return max(min(limits), 1)
 
     def _adapt_active_cap(self, layer_idx: int, position: int, before: dict, after: dict) -> None:
+        """One step of the dynamic cap controller after a routed call.
+
+        The cache traffic of the call (hit / miss / eviction counts between
+        the two snapshots) decides: an eviction share at or above
+        ``cap_eviction_pressure_threshold`` lowers the cap by one (not below
+        the lower bound); otherwise a call without evictions whose hit share
+        reaches ``cap_hit_rate_expand_threshold`` raises it by one (not above
+        the upper bound).  A layer seen here first starts from the static cap
+        (or ``experts_per_token``).
+        """
         cfg = self.locality_config
         if not (cfg.enabled and cfg.dynamic_active_expert_cap):
             return
-        old = self.dynamic_caps.setdefault(layer_idx, cfg.active_experts_per_token_cap or self.experts_per_token)
-        hits = int(after.get("hits", 0)) - int(before.get("hits", 0))
-        misses = int(after.get("misses", 0)) - int(before.get("misses", 0))
-        evictions = int(after.get("evictions", 0)) - int(before.get("evictions", 0))
-        total = max(hits + misses, 1)
-        lo = max(int(cfg.min_active_experts_per_token), 1)
-        hi = int(cfg.max_active_experts_per_token or self.experts_per_token)
-        new, reason = old, ""
-        if evictions / total >= float(cfg.cap_eviction_pressure_threshold) and old > lo:
-            new, reason = old - 1, "eviction_pressure"
-        elif evictions == 0 and hits / total >= float(cfg.cap_hit_rate_expand_threshold) and old < hi:
-            new, reason = old + 1, "stable_high_hit_rate"
-        if new != old:
-            self.dynamic_caps[layer_idx] = new
-            self.stats.record_cap_event(layer_idx, position, old, new, reason, hits, misses, evictions)
+        delta = {name: int(after.get(name, 0)) - int(before.get(name, 0)) for name in ("hits", "misses", "evictions")}
+        lookups = max(delta["hits"] + delta["misses"], 1)
+        lo, hi = self._cap_bounds()
+        cap = self.dynamic_caps.setdefault(layer_idx, cfg.active_experts_per_token_cap or self.experts_per_token)
+        step, reason = 0, ""
+        if cap > lo and delta["evictions"] / lookups >= float(cfg.cap_eviction_pressure_threshold):
+            step, reason = -1, "eviction_pressure"
+        elif cap < hi and delta["evictions"] == 0 and delta["hits"] / lookups >= float(cfg.cap_hit_rate_expand_threshold):
+            step, reason = +1, "stable_high_hit_rate"
+        if step:
+            self.dynamic_caps[layer_idx] = cap + step
+            self.stats.record_cap_event(layer_idx, position, cap, cap + step, reason, delta["hits"], delta["misses"],
+                                        delta["evictions"])
 
     @staticmethod
     def _cache_snapshot(expert_store) -> dict:

@@ -3,9 +3,10 @@
 Cases cover the single-split path (at most 256 keys) and the split path
 with its statistics and combine launches (up to 4500 keys, 18 splits).  RoPE
 and the stored keys/values are bit-exact (every bfloat16 op rounded as
-torch rounds it, then the cache type's rounding); the context is within
-1e-2 + 2e-2 |ref| of the oracle (probabilities rounded to the cache type can
-land one unit apart when the softmax sum is taken in another order).
+torch rounds it, then the cache type's rounding); the context is within a
+few cache-type ulps of |ref| plus 2^-9 of the head's largest |ref| of the
+oracle (probabilities rounded to the cache type can land one unit apart when
+the softmax sum is taken in another order).
 """
 
 from __future__ import annotations
@@ -35,10 +36,21 @@ def dev(b: np.ndarray, gpu) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16).to(gpu)
 
 
+def context_tolerance(ref: np.ndarray, kv: str) -> np.ndarray:
+    """Per-element bound for the context [heads, head_dim]: the context is rounded twice (cache
+    type, then bfloat16) and a probability rounded to the cache type may land one unit off, which
+    moves the head's weighted sum by at most that unit times its largest values; so a few cache-type
+    ulps of |ref| plus 2^-9 of the head's largest |ref|."""
+    ulp = 2.0 ** -10 if kv == "fp16" else 2.0 ** -7
+    head_max = np.abs(ref).max(axis=-1, keepdims=True)
+    return 4 * ulp * np.abs(ref) + 2.0 ** -8 * np.abs(ref) + 2.0 ** -9 * head_max
+
+
 @pytest.mark.parametrize("kv", ["fp16", "bf16"])
 @pytest.mark.parametrize("steps,cap,window,sinks", [(1, 64, None, True), (300, 512, None, True), (300, 512, 128, False),
-                                                    (700, 512, None, True), (1000, 1024, 128, True),
-                                                    (4500, 8192, None, True)])
+                                                    (700, 512, None, True), (700, 1024, None, False),
+                                                    (1000, 1024, 128, True), (4500, 8192, None, True),
+                                                    (4500, 8192, None, False)])
 def test_rope_append_and_decode_match_oracle(gpu, kv, steps, cap, window, sinks):
     cfg = AttentionConfig(**CFG)
     nh, nkv, d = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
@@ -80,7 +92,7 @@ def test_rope_append_and_decode_match_oracle(gpu, kv, steps, cap, window, sinks)
                  ws.numel(), P(ctx.data_ptr()), stream)
     want, _ = oat.decode_attention(q_rot, np.stack(keys_rot[-count:]), np.stack(vals[-count:]), sk, kv=kv)
     got, ref = bf16_to_f32(bits(ctx)), bf16_to_f32(want)
-    assert np.all(np.abs(got - ref) <= 1e-2 + 2e-2 * np.abs(ref)), np.abs(got - ref).max()
+    assert np.all(np.abs(got - ref) <= context_tolerance(ref, kv)), np.abs(got - ref).max()
 
 
 @pytest.mark.parametrize("kv", ["fp16", "bf16"])
@@ -178,7 +190,7 @@ def test_other_head_shapes(gpu, nh, nkv, d, window):
                  steps - count, count, nh, nkv, d, 0, P(ws.data_ptr()), ws.numel(), P(ctx.data_ptr()), stream)
     want, _ = oat.decode_attention(q_rot, np.stack(keys[-count:]), np.stack(vals[-count:]), sk, kv="bf16")
     got, ref = bf16_to_f32(bits(ctx)), bf16_to_f32(want)
-    assert np.all(np.abs(got - ref) <= 1e-2 + 2e-2 * np.abs(ref)), np.abs(got - ref).max()
+    assert np.all(np.abs(got - ref) <= context_tolerance(ref, "bf16")), np.abs(got - ref).max()
 
 
 def test_attention_rejects_bad_shapes(gpu):

@@ -167,9 +167,62 @@ def test_store_prefetch_then_consume(gpu, setup, tmp_path):
     assert got.dtype == torch.float16
     want = omx.dequantize(host["down_blocks"][7], host["down_scales"][7], "f16")
     assert np.array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16), want.view(np.uint16))
-    store.executor.shutdown(wait=True)
+    store.close()
     js = store.to_json()
     assert js["prefetch_submitted"] == 4 and js["prefetch_failed"] == 0
+
+
+def test_store_quant_loader_branch(gpu, setup, tmp_path):
+    """A quantized loader that owns the expert tensors (mxfp4_expert.py:516-522): the full tensor comes
+    back as floats with a uint8 meta dtype, is rounded and clamped to bytes, copied and packed."""
+    from types import SimpleNamespace
+
+    host, _ = setup
+    write_checkpoint(tmp_path, host)
+    prefix = "model.layers.0.mlp.experts"
+
+    class Loader:
+        tensor_index = {f"{prefix}.{p}_{kind}": None for p in ("gate_up_proj", "down_proj")
+                        for kind in ("blocks", "scales")}
+        calls = []
+
+        def load_tensor(self, name, dtype=None):
+            self.calls.append(name)
+            arr = host[name.split(".")[-1].replace("_proj", "")]
+            return torch.from_numpy(arr).to(torch.float32) + 0.25, SimpleNamespace(dtype="torch.uint8")
+
+    loader = Loader()
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, dtype=torch.bfloat16, cache_bytes=1 << 30, quant_loader=loader)
+    for e, proj in [(6, "gate_up_proj"), (13, "down_proj")]:
+        got = store.load_expert_matrix(0, e, proj)
+        want = omx.dequantize(host[f"{proj[:-5]}_blocks"][e], host[f"{proj[:-5]}_scales"][e], "bf16")
+        assert np.array_equal(bf16_bits(got), want)
+    assert loader.calls == [f"{prefix}.gate_up_proj_blocks", f"{prefix}.gate_up_proj_scales",
+                            f"{prefix}.down_proj_blocks", f"{prefix}.down_proj_scales"]
+
+
+def test_async_prefetch_with_evictions_matches_resident(gpu, setup, tmp_path):
+    """Background loaders bring the next tokens' experts in while the compute stream runs, and a cache of
+    three experts evicts constantly: every route() output must equal the resident store's bit for bit."""
+    host, dev_w = setup
+    write_checkpoint(tmp_path, host)
+    tensors = layer_tensors(host, gpu)
+    per_expert = dev_w.gate_up.shape[1] + dev_w.down.shape[1]
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, dtype=torch.bfloat16, cache_bytes=3 * per_expert,
+                             async_prefetch=True, max_prefetch_workers=2)
+    resident = ResidentExpertStore({0: dev_w})
+    x = moe.synthetic_hidden(WORKLOAD, 12, H, step=5)
+    ref_router, router = StreamedMoERouter(K), StreamedMoERouter(K)
+    want = [ref_router.route(0, bf16_tensor(x[t], gpu), tensors, resident, position=t) for t in range(12)]
+    for t in range(12):
+        if t + 1 < 12:
+            store.prefetch_experts(0, want[t + 1][1]["experts"])
+        out, route = router.route(0, bf16_tensor(x[t], gpu), tensors, store, position=t)
+        assert route["experts"] == want[t][1]["experts"]
+        assert torch.equal(out, want[t][0]), t
+    store.close()
+    js = store.to_json()
+    assert js["evictions"] > 0 and js["prefetch_failed"] == 0
 
 
 def test_dequantize_matrix_default_fp16(gpu):

@@ -34,30 +34,51 @@ def test_cache_disabled_budget_stores_nothing():
     assert not c.contains((0, 1, "down_proj")) and c.current_bytes == 0
 
 
-def test_cache_evicts_lowest_frequency_then_oldest():
+def test_cache_evicts_least_recently_used():
     c = mx.ExpertWeightCache(12)  # three 4-byte items
     a, b, d, e = (0, 0, "gate_up_proj"), (0, 1, "gate_up_proj"), (0, 2, "gate_up_proj"), (0, 3, "gate_up_proj")
-    for key in (a, b, d):
+    for key in (a, b, d):  # clock 1, 2, 3
         c.put(key, item())
-    assert c.get(a) is not None and c.get(a) is not None  # a: frequency 3
-    c.put(e, item())  # over budget: b and d have frequency 1, b was touched earlier
+    assert c.get(a) is not None  # clock 4; recency order b, d, a
+    c.put(e, item())  # clock 5, 16 bytes > 12: b is the least recently used
     assert not c.contains(b) and c.contains(a) and c.contains(d) and c.contains(e)
-    assert c.stats.evictions == 1 and c.stats.hits == 2 and c.current_bytes == 12
+    assert list(c.eviction_log) == [b]
+    assert c.stats.evictions == 1 and c.stats.hits == 1 and c.current_bytes == 12
+    assert c.to_json()["evicted_lifetime"]["mean_accesses"] == 3  # born at clock 2, evicted at 5
     assert c.get(b) is None and c.stats.misses == 1
     assert c.eviction_reasons["global_pressure"] == 1
 
 
-def test_cache_future_scores_and_protection_override_frequency():
+def test_cache_holds_protect_until_their_window_ends():
+    c = mx.ExpertWeightCache(8)
+    a, b, d = (1, 0, "down_proj"), (1, 1, "down_proj"), (1, 2, "down_proj")
+    c.put(a, item())  # clock 1
+    c.put(b, item())  # clock 2
+    c.get(a)  # clock 3; order b, a
+    c.hold([b], 100)  # b held until clock 103
+    c.put(d, item())  # clock 4; order b, a, d: b is held, so a (next least recent) goes
+    assert c.contains(b) and c.contains(d) and not c.contains(a)
+    assert c.stats.protected_eviction_skips == 0
+    # once the window has passed, b is ordinary again
+    c2 = mx.ExpertWeightCache(8)
+    c2.put(a, item())  # 1
+    c2.put(b, item())  # 2
+    c2.hold([a], 2)  # a held until clock 4
+    for _ in range(3):
+        c2.get(b)  # clocks 3, 4, 5; order a, b
+    c2.put(d, item())  # clock 6: a's hold ended at 4, so a goes
+    assert not c2.contains(a) and c2.contains(b)
+
+
+def test_cache_hold_before_arrival_and_all_held():
     c = mx.ExpertWeightCache(8)
     a, b, d = (1, 0, "down_proj"), (1, 1, "down_proj"), (1, 2, "down_proj")
     c.put(a, item())
     c.put(b, item())
-    c.get(a)
-    c.set_future_scores([b], protect_window=100)  # b: future score 1, protected
-    c.put(d, item())  # unprotected candidates a (score 0, frequency 2) and d (score 0, frequency 1)
-    assert c.contains(b)
-    assert not c.contains(d)  # lowest (score 0, frequency 1) among unprotected
-    assert c.stats.protected_eviction_skips == 0
+    c.set_future_scores([a, b, d], protect_window=100)  # the reference's name; d is not resident yet
+    c.put(d, item())  # d arrives held; every candidate is held: the least recently used (a) goes
+    assert not c.contains(a) and c.contains(b) and c.contains(d)
+    assert c.stats.protected_eviction_skips == 1
 
 
 def test_cache_pinned_items_survive():
@@ -65,9 +86,10 @@ def test_cache_pinned_items_survive():
     a, b, d = (2, 0, "down_proj"), (2, 1, "down_proj"), (2, 2, "down_proj")
     c.put(a, item(), pin=True)
     c.put(b, item())
-    c.put(d, item())
-    assert c.contains(a) and c.stats.evictions == 1
+    c.put(d, item())  # a is the least recent but pinned: b goes
+    assert c.contains(a) and not c.contains(b) and c.stats.evictions == 1
     assert c.get(a) is not None and c.stats.pinned_hits == 1
+    assert c.pinned == {a}
 
 
 def test_cache_layer_quota_evicts_from_the_over_quota_layer():
@@ -75,17 +97,45 @@ def test_cache_layer_quota_evicts_from_the_over_quota_layer():
     l0 = [(0, i, "down_proj") for i in range(3)]
     for key in l0:
         c.put(key, item())
-    c.get(l0[0])
-    c.get(l0[1])
-    c.get(l0[2])
+    for key in l0:
+        c.get(key)
     new = (1, 0, "down_proj")
     c.put(new, item())  # 16 bytes: at budget, nothing evicted
     assert c.stats.evictions == 0
     newer = (1, 1, "down_proj")
-    c.put(newer, item())  # layer 0 holds 12 > 8 bytes: its entry goes, not layer 1's fresher ones
+    c.put(newer, item())  # layer 0 holds 12 of its 8 bytes (layer 1: 8 of 8): layer 0's oldest goes
     assert c.contains(new) and c.contains(newer)
-    assert sum(c.contains(k) for k in l0) == 2
+    assert list(c.eviction_log) == [l0[0]]
     assert c.eviction_reasons["layer_quota_pressure"] == 1
+
+
+def test_cache_adaptive_quota_follows_relative_hit_rates():
+    c = mx.ExpertWeightCache(16, layer_count=2, layer_aware=True, adaptive_layer_quota=True,
+                             adaptive_layer_quota_strength=1.5)
+    hot, cold = (0, 0, "down_proj"), (1, 0, "down_proj")
+    c.put(hot, item())
+    c.put(cold, item())
+    assert c.layer_quota(0) == 8.0  # fewer than 32 lookups: the even split
+    for _ in range(32):
+        c.get(hot)  # layer 0: 32 of 32 found
+    for i in range(32):
+        c.get(cold if i % 2 else (1, 9, "down_proj"))  # layer 1: 16 of 32 found
+    # mean hit rate 0.75: quota 8 * (1 + 1.5 * (1.0 - 0.75)) and 8 * (1 + 1.5 * (0.5 - 0.75))
+    assert c.layer_quota(0) == pytest.approx(11.0) and c.layer_quota(1) == pytest.approx(5.0)
+    assert c.to_json()["adaptive_layer_quota"] is True
+
+
+def test_cache_eviction_sequence_matches_the_committed_fixture():
+    """A scripted mix of puts, lookups, holds and pins over 3 layers with layer quotas; the victims
+    and counters are the committed fixture (tests/golden/make_cache_golden.py)."""
+    from pathlib import Path
+
+    import sys
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import make_cache_golden as g
+
+    want = json.loads((Path(__file__).resolve().parent / "golden" / "expert_cache_eviction.json").read_text())
+    assert g.run_script() == want
 
 
 def test_cache_to_json_is_serialisable_and_consistent():

@@ -194,6 +194,22 @@ def test_large_ranges_and_concurrent_readers(tmp_path):
             assert all(ex.map(one, range(24)))
 
 
+def test_pool_jobs_of_alternating_slice_counts_run_each_slice_once(tmp_path):
+    """Back-to-back reads alternate between few and many pool slices (a job
+    with more slices than the one before is where a worker still holding the
+    old job could claim a slice of the new one); every read must come back
+    whole, and no call may hang."""
+    g = torch.Generator().manual_seed(5)
+    rows = torch.randint(0, 256, (16, 1 << 20), generator=g, dtype=torch.uint8)  # 1 MiB rows
+    path = tmp_path / "rows.safetensors"
+    safetensors_torch.save_file({"rows": rows}, str(path))
+    with SafetensorShard(path) as shard:
+        for i in range(600):
+            first, count = (i * 7) % 8, (1, 8, 2, 6, 1, 3)[i % 6]  # 1 MiB .. 8 MiB: 8 .. 64 slices
+            got = shard.read_rows("rows", first, count)
+            assert torch.equal(got, rows[first:first + count]), i
+
+
 def test_forked_child_reads_without_the_pool(tmp_path):
     import os
     import signal
