@@ -189,52 +189,16 @@ def stack_bench(torch, dev, n_layers: int, n_seqs: int, n_steps: int, precision:
             "unique_experts_mean": round(float(np.mean(uniq)), 2), "build_s": round(build_s, 1)}
 
 
-def zipf_router_bias(host_x, host_w, k: int, s: float, seed: int):
-    """bf16 router bias making expert popularity ~ Zipf(s) over a seeded permutation of the experts.
-
-    Target pair counts are n_pairs * r^-s / H(E, s) for expert rank r; the bias is fitted on the
-    host (float32 logits of the actual inputs) by 300 multiplicative steps on log(count / target),
-    keeping the best fit in L1."""
-    import numpy as np
-
-    from klcquant_amd import synth
-    from oracle.numerics import bf16_to_f32, f32_to_bf16
-
-    n_exp = host_w.shape[0]
-    perm = np.argsort(synth.random_ints(seed, n_exp, 0, 1 << 30), kind="stable")
-    rank = np.empty(n_exp, dtype=np.int64)
-    rank[perm] = np.arange(1, n_exp + 1)
-    p = rank.astype(np.float64) ** -s
-    p /= p.sum()
-    logits = bf16_to_f32(host_x) @ bf16_to_f32(host_w).T
-    target = p * logits.shape[0] * k
-
-    def counts_for(b_bits):
-        top = np.argpartition(-(logits + bf16_to_f32(b_bits)), k - 1, axis=1)[:, :k]
-        return np.bincount(top.ravel(), minlength=n_exp)
-
-    b = (-s * np.log(rank)).astype(np.float64)
-    best, best_err = None, None
-    for _ in range(300):
-        bits = f32_to_bf16(b.astype(np.float32))
-        c = counts_for(bits)
-        err = float(np.abs(c - target).sum())
-        if best_err is None or err < best_err:
-            best, best_err = bits, err
-        b += 0.25 * (np.log(target + 0.5) - np.log(c + 0.5))
-    return best, float(p.max())
-
-
 def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
     """One 120B-shape MoE layer over a prefill chunk of n_tok tokens with Zipf(1.1)-skewed routing."""
     import numpy as np
 
-    from klcquant_amd import moe
+    from klcquant_amd import moe, synth
 
     workload = 3
     host = moe.synthetic_host_layer(workload, 0, HIDDEN, INTER, EXPERTS)
     x_host = moe.synthetic_hidden(workload, n_tok, HIDDEN)
-    bias, target = zipf_router_bias(x_host, host["router_weight"], TOPK, 1.1, 1000 * workload + 11)
+    bias, target = synth.zipf_router_bias(x_host, host["router_weight"], TOPK, 1.1, 1000 * workload + 11)
     del host
     layers = [moe.MoELayer(moe.MoELayerWeights.synthetic(workload, l, HIDDEN, INTER, EXPERTS, dev, bias), TOPK, 7.0,
                            precision) for l in range(2)]

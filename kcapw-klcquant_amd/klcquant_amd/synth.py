@@ -132,3 +132,55 @@ def mxfp4_expert_tensors(seed_blocks: int, seed_scales: int, n_mat: int, out_dim
     blocks = random_bytes(seed_blocks, n_mat * out_dim * groups * 16).reshape(n_mat, out_dim, groups, 16)
     scales = random_ints(seed_scales, n_mat * out_dim * groups, scale_lo, scale_hi).astype(np.uint8)
     return blocks, scales.reshape(n_mat, out_dim, groups)
+
+
+def mxfp4_expert_slice(seed_blocks: int, seed_scales: int, expert: int, out_dim: int, in_dim: int,
+                       scale_lo: int = 118, scale_hi: int = 124) -> tuple[np.ndarray, np.ndarray]:
+    """Expert ``expert`` of :func:`mxfp4_expert_tensors` (``[out, in/32, 16]``, ``[out, in/32]``),
+    generated alone: the counter-based stream starts at the expert's first element."""
+    if in_dim % 32:
+        raise ValueError("in_dim must be a multiple of 32")
+    groups = in_dim // 32
+    per = out_dim * groups
+    words = draws(seed_blocks, expert * per * 2, per * 2)  # 16 bytes = 2 draws per (row, group)
+    blocks = words.view(np.uint8).reshape(out_dim, groups, 16).copy()
+    span = np.uint64(scale_hi - scale_lo + 1)
+    d = draws(seed_scales, expert * per, per) >> np.uint64(32)
+    with np.errstate(over="ignore"):
+        scales = ((d * span) >> np.uint64(32)).astype(np.int64) + scale_lo
+    return blocks, scales.astype(np.uint8).reshape(out_dim, groups)
+
+
+def zipf_router_bias(x_bits: np.ndarray, w_bits: np.ndarray, k: int, s: float, seed: int) -> tuple[np.ndarray, float]:
+    """bf16 router bias making expert popularity ~ Zipf(s) over a seeded permutation of the experts.
+
+    Target pair counts are ``n_pairs * r^-s / H(E, s)`` for expert rank ``r``;
+    the bias is fitted on the host (float32 logits of the actual inputs
+    ``x [T, H]`` and router weight ``w [E, H]``, bf16 patterns) by 300
+    multiplicative steps on ``log(count / target)``, keeping the best fit in
+    L1.  Returns ``(bias bits [E], the target share of the hottest expert)``.
+    """
+    n_exp = w_bits.shape[0]
+    perm = np.argsort(random_ints(seed, n_exp, 0, 1 << 30), kind="stable")
+    rank = np.empty(n_exp, dtype=np.int64)
+    rank[perm] = np.arange(1, n_exp + 1)
+    p = rank.astype(np.float64) ** -s
+    p /= p.sum()
+    logits = bf16_bits_to_f32(x_bits) @ bf16_bits_to_f32(w_bits).T
+    target = p * logits.shape[0] * k
+
+    def counts_for(b_bits):
+        top = np.argpartition(-(logits + bf16_bits_to_f32(b_bits)), k - 1, axis=1)[:, :k]
+        return np.bincount(top.ravel(), minlength=n_exp)
+
+    b = (-s * np.log(rank)).astype(np.float64)
+    best, best_err = None, None
+    for _ in range(300):
+        bits = f32_to_bf16_bits(b.astype(np.float32))
+        c = counts_for(bits)
+        err = float(np.abs(c - target).sum())
+        if best_err is None or err < best_err:
+            best, best_err = bits, err
+        b += 0.25 * (np.log(target + 0.5) - np.log(c + 0.5))
+    return best, float(p.max())
+

@@ -49,3 +49,10 @@ def test_mxfp4_tensor_shapes_and_codes():
 
 def test_tensor_seed_layout():
     assert synth.tensor_seed(2, "gate_up_blocks", 3) == 2000 + 300 + 4
+
+
+def test_expert_slice_equals_the_full_tensors():
+    blocks, scales = synth.mxfp4_expert_tensors(41, 42, 5, 64, 96)
+    for e in (0, 3, 4):
+        b, s = synth.mxfp4_expert_slice(41, 42, e, 64, 96)
+        assert np.array_equal(b, blocks[e]) and np.array_equal(s, scales[e])
