@@ -23,12 +23,18 @@ dominant kernel (the gate_up GEMV): algorithmic bytes (packed weights of the
 experts the batch touches + activations in + SwiGLU output) over its average
 duration measured with HIP events recorded by the library between its
 kernels, in a second timed pass over the same steps.
+
+Before each batch size is measured, its steps run untimed for at least 150 ms:
+the GPU reaches its working clocks only after ~20-30 ms of sustained load.
+Then come the per-kernel events pass (K steps), the W untimed warm-up steps,
+and the K timed steps.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import re
 import sys
@@ -46,6 +52,8 @@ EXPERTS = 128
 TOPK = 4
 WORKLOAD = 2  # seed namespace of the 120B-shape decode workload
 HBM_PEAK_GBPS = 8000.0
+STATIC_SCRATCH_BYTES = 32 * 1024 * 1024  # KLC_STATIC_SCRATCH_BYTES
+SETTLE_MS = 150.0  # untimed steps before each batch size's measurement
 GATE_UP_EXPERT_BYTES = 2 * INTER * (HIDDEN // 32) * 17  # 8,812,800: codes + E8M0 scales
 DOWN_EXPERT_BYTES = HIDDEN * (INTER // 32) * 17  # 4,406,400
 KERNELS = ["router_logits", "topk_softmax", "dispatch", "gate_up", "down", "combine"]
@@ -66,6 +74,8 @@ def parse_args():
     ap.add_argument("--inputs", type=int, default=16, help="distinct input batches the steps rotate over")
     ap.add_argument("--cpu-tokens", type=int, default=10, help="timed tokens of the CPU baseline sample (0 = skip)")
     ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16"])
+    ap.add_argument("--graph", action="store_true",
+                    help="replay one HIP graph per step in the headline pass instead of launching its kernels")
     ap.add_argument("--skip-dequant", action="store_true", help="skip the standalone dequant measurement")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of the prefill measurement (0 = skip)")
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
@@ -108,6 +118,17 @@ def layer_bytes(unique_experts: int, n_tok: int) -> int:
     router = EXPERTS * HIDDEN * 2 + EXPERTS * 2
     acts = n_tok * HIDDEN * 2 * 2  # hidden in, output out (bf16)
     return weights + biases + router + acts
+
+
+def kernel_breakdown(interval_us, n_tok: int) -> dict:
+    """Per-kernel times from the library's KLC_LAYER_EVENTS events.  Batches of up to 128 tokens run
+    router, top-k and dispatch as one launch (router_decode_kernel), so their events 1 and 2 follow
+    it back to back: those two intervals measure only the event records and are reported apart."""
+    us = [round(float(v), 3) for v in interval_us]
+    if n_tok <= 128:
+        return {"router_topk_dispatch": us[0], "gate_up": us[3], "down": us[4], "combine": us[5],
+                "event_records_only": round(us[1] + us[2], 3)}
+    return dict(zip(KERNELS, us))
 
 
 def gate_up_bytes(unique_experts: int, n_tok: int) -> int:
@@ -558,17 +579,34 @@ def main() -> int:
         xs = [torch.from_numpy(moe.synthetic_hidden(WORKLOAD, n_tok, HIDDEN, step=s).view(np.int16))
               .view(torch.bfloat16).to(dev) for s in range(args.inputs)]
         out = torch.empty((n_tok, HIDDEN), dtype=torch.bfloat16, device=dev)
-        ids = torch.empty((args.steps, n_tok, TOPK), dtype=torch.int32, device=dev)
-        for s in range(args.warmup):
-            layers[s % args.layers].forward(xs[s % args.inputs], out=out)
+        # the steps cycle through n_pairs distinct (layer, input batch) pairs
+        n_pairs = math.lcm(args.layers, args.inputs)
+        ids = torch.empty((n_pairs, n_tok, TOPK), dtype=torch.int32, device=dev)
+        graphs = None
+        if args.graph and _native.load().klc_moe_workspace_bytes(n_tok, HIDDEN, INTER, EXPERTS, TOPK) <= \
+                STATIC_SCRATCH_BYTES:
+            # one HIP graph per (layer, input) pair: a step is one graph launch from the host
+            graphs = [layers[j % args.layers].capture_graph(xs[j % args.inputs], out, ids=ids[j])
+                      for j in range(n_pairs)]
+
+        def step(s: int) -> None:
+            if graphs is not None:
+                graphs[s % n_pairs].replay()
+            else:
+                layers[s % args.layers].forward(xs[s % args.inputs], out=out, ids=ids[s % n_pairs])
+
+        # settle: the GPU reaches its working clocks only after ~20-30 ms of sustained load (a cold
+        # 20-step run of B = 64 measures ~7 % slow), so every batch size first runs at least
+        # SETTLE_MS of untimed steps
+        t_settle = time.perf_counter()
+        s = 0
+        while (time.perf_counter() - t_settle) * 1e3 < SETTLE_MS or s < 4:
+            step(s)
+            s += 1
+            if s % 16 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
-        # pass 1: the headline timing, no events between kernels
-        t0 = time.perf_counter()
-        for s in range(args.steps):
-            layers[s % args.layers].forward(xs[s % args.inputs], out=out, ids=ids[s])
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
-        # pass 2: same steps with events around each kernel
+        # per-kernel times: the same steps with events around each kernel
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(_native.LAYER_EVENTS)] for _ in range(args.steps)]
         for row in evs:
             for e in row:
@@ -577,10 +615,19 @@ def main() -> int:
         for s in range(args.steps):
             layers[s % args.layers].forward(xs[s % args.inputs], out=out, events=evs[s])
         torch.cuda.synchronize()
+        for s in range(args.warmup):
+            step(s)
+        torch.cuda.synchronize()
+        # the headline timing: W untimed steps, then K timed steps, no events between kernels
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            step(s)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
         kern_ms = np.array([[evs[s][i].elapsed_time(evs[s][i + 1]) for i in range(len(KERNELS))]
                             for s in range(args.steps)])
         ids_np = ids.cpu().numpy()
-        uniq = np.array([len(np.unique(ids_np[s])) for s in range(args.steps)])
+        uniq = np.array([len(np.unique(ids_np[s % n_pairs])) for s in range(args.steps)])
         ms_step = dt * 1e3 / args.steps
         bytes_total = float(sum(layer_bytes(int(u), n_tok) for u in uniq))
         gu_bytes = float(sum(gate_up_bytes(int(u), n_tok) for u in uniq))
@@ -593,9 +640,10 @@ def main() -> int:
             "unique_experts_mean": round(float(uniq.mean()), 2),
             "layer_hbm_gbps": round(bytes_total / (dt * 1e9 / 1.0) / 1.0, 1),
             "layer_frac_of_peak": round(bytes_total / dt / 1e9 / HBM_PEAK_GBPS, 4),
-            "kernel_us_mean": {k: round(float(kern_ms[:, i].mean()) * 1e3, 3) for i, k in enumerate(KERNELS)},
+            "kernel_us_mean": kernel_breakdown(kern_ms.mean(axis=0) * 1e3, n_tok),
             "gate_up_gbps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
             "gate_up_bytes_per_launch": round(gu_bytes / args.steps),
+            "hip_graph": graphs is not None,
         }
         per_batch.append(rec)
         print(f"[bench] B={n_tok}: {rec['us_per_step']} us/step, {rec['us_per_token']} us/token, "

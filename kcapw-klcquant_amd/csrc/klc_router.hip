@@ -50,7 +50,7 @@ typedef double f64x4_t __attribute__((ext_vector_type(4)));
 // current ones multiply.  The waves' sums are added through LDS in wave
 // order; the result is valid in wave 0.  x_f32, when given, receives the
 // float32 copy of the hidden rows the tile reads.
-__device__ f64x4_t router_block_dot(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int n_tok,
+__device__ __forceinline__ f64x4_t router_block_dot(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int n_tok,
                                     int hidden, int n_exp, int e0, int t0, int c_begin, int c_end,
                                     float* __restrict__ x_f32, double* red /* LDS [3][64][4] */) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -208,6 +208,30 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Wave-wide maximum of a 32-bit value (same DPP network as wave_max_u64).
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_max_u32_step(uint32_t v) {
+  const uint32_t o = dpp_u32<kCtrl, kRowMask>(v, v);
+  return o > v ? o : v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = dpp_max_u32_step<0xB1, 0xf>(v);
+  v = dpp_max_u32_step<0x4E, 0xf>(v);
+  v = dpp_max_u32_step<0x141, 0xf>(v);
+  v = dpp_max_u32_step<0x140, 0xf>(v);
+  v = dpp_max_u32_step<0x142, 0xa>(v);
+  v = dpp_max_u32_step<0x143, 0xc>(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads it
+// does not wait for the workgroup's outstanding global stores.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Orders LDS accesses of the lanes of one wave (no instruction: a wave's
 // LDS operations complete in order; this keeps the compiler from moving them).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -237,7 +261,7 @@ __host__ __device__ constexpr size_t decode_rows_bytes(int n_exp) {
 // scan returns L[0] (m = 0), min(L[m], R[m - 1]) or, with L used up,
 // R[m - 1].  Lane 0 runs the sequential pieces (median of three, insertion
 // sorts, heap select, the final std::sort of k - 1 entries).
-__device__ void wave_torch_topk(const uint16_t* row, int n, int k, uint32_t* scratch) {
+__device__ __forceinline__ void wave_torch_topk(const uint16_t* row, int n, int k, uint32_t* scratch) {
   const int lane = threadIdx.x & 63;
   uint32_t* a = scratch;
   uint16_t* lp = reinterpret_cast<uint16_t*>(scratch + n);
@@ -311,6 +335,196 @@ __device__ void wave_torch_topk(const uint16_t* row, int n, int k, uint32_t* scr
   wave_lds_sync();
 }
 
+// One row of up to 64 * S entries held in registers across a wave: position
+// p lives in slot p / 64 of lane p % 64.  get/set take a wave-uniform
+// position, so every lane runs the sequential pieces of libstdc++'s
+// algorithms in lockstep on the same values.
+template <int S>
+struct WaveRow {
+  uint32_t v[S];
+
+  __device__ __forceinline__ uint32_t get(int p) const {
+    // read the lane of every slot, then pick one (no run-time register index)
+    const int s = p >> 6, l = p & 63;
+    uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v[0], l);
+#pragma unroll
+    for (int i = 1; i < S; ++i) {
+      const uint32_t y = (uint32_t)__builtin_amdgcn_readlane((int)v[i], l);
+      x = s == i ? y : x;
+    }
+    return x;
+  }
+  __device__ __forceinline__ void set(int p, uint32_t val) {
+    const int s = p >> 6;
+    const bool mine = (int)(threadIdx.x & 63) == (p & 63);
+#pragma unroll
+    for (int i = 0; i < S; ++i) v[i] = (s == i && mine) ? val : v[i];
+  }
+  __device__ __forceinline__ void swap(int a, int b) {
+    const uint32_t va = get(a), vb = get(b);
+    set(a, vb);
+    set(b, va);
+  }
+  // __move_median_to_first(result, a, b, c)
+  __device__ __forceinline__ void move_median_to_first(int result, int a, int b, int c) {
+    const uint32_t va = get(a), vb = get(b), vc = get(c);
+    int pick;
+    if (entry_gt(va, vb)) pick = entry_gt(vb, vc) ? b : (entry_gt(va, vc) ? c : a);
+    else pick = entry_gt(va, vc) ? a : (entry_gt(vb, vc) ? c : b);
+    swap(result, pick);
+  }
+  // __insertion_sort(first, last)
+  __device__ __forceinline__ void insertion_sort(int first, int last) {
+    if (first == last) return;
+    for (int i = first + 1; i < last; ++i) {
+      const uint32_t val = get(i);
+      if (entry_gt(val, get(first))) {
+        for (int j = i; j > first; --j) set(j, get(j - 1));
+        set(first, val);
+      } else {  // __unguarded_linear_insert
+        int hole = i;
+        uint32_t prev = get(hole - 1);
+        while (entry_gt(val, prev)) {
+          set(hole, prev);
+          --hole;
+          prev = get(hole - 1);
+        }
+        set(hole, val);
+      }
+    }
+  }
+};
+
+// wave_torch_topk for rows of n <= 64 * S entries in the introselect regime
+// (k * 64 > n) with k - 1 <= 16, the row held in registers.  Each partition
+// step is ballots and prefix counts: with A(q) the left stops below position
+// q and B(q) the right stops at or above q, the swap count is
+// m = max_q min(A(q), B(q)); the i-th left stop (ascending) and the i-th
+// right stop (descending) exchange their entries through two small LDS
+// arrays, for i < m; the cut is L[0] (m = 0), else min(L[m], R[m - 1])
+// (R[m - 1] once L is used up).  The rare depth-limit branch (heap select)
+// spills the row to LDS and finishes sequentially in lane 0.  Returns, in
+// lane out_lane_base + j (j < k), the expert of result j; other lanes get
+// my_id back.  scratch: n * 8 bytes of LDS.
+template <int S>
+__device__ __forceinline__ int wave_torch_topk_regs(const uint16_t* row, int n, int k, uint32_t* scratch, int out_lane_base,
+                                    int my_id) {
+  constexpr int kNone = 1 << 30;
+  const int lane = threadIdx.x & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
+  WaveRow<S> r;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int p = s * kWave + lane;
+    r.v[s] = p < n ? order_entry(row[p], p) : 0u;
+  }
+  uint32_t* buf_l = scratch;
+  uint32_t* buf_r = scratch + (n + 1) / 2;
+  const int nth = k - 1;
+  int first = 0, last = n;
+  int depth = floor_log2(n) * 2;
+  bool spilled = false;
+  while (last - first > 3) {
+    if (depth == 0) {  // __heap_select on the range, sequentially in lane 0 on an LDS copy
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        if (s * kWave + lane < n) scratch[s * kWave + lane] = r.v[s];
+      wave_lds_sync();
+      if (lane == 0) {
+        stl_heap_select(scratch, first, nth + 1, last);
+        entry_swap(scratch, first, nth);
+        stl_sort(scratch, 0, k - 1);
+      }
+      wave_lds_sync();
+      spilled = true;
+      break;
+    }
+    --depth;
+    r.move_median_to_first(first, first + 1, first + (last - first) / 2, last - 1);
+    const uint32_t pk = r.get(first) >> 16;
+    int rank_l[S], rank_r[S];
+    bool fl[S], fr[S];
+    uint64_t bl[S], br[S];
+    int cl = 0, cr = 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int p = s * kWave + lane;
+      const bool in = p > first && p < last;
+      const uint32_t key = r.v[s] >> 16;
+      fl[s] = in && key <= pk;  // the left scan stops here
+      fr[s] = in && key >= pk;  // the right scan stops here
+      bl[s] = __ballot(fl[s]);
+      br[s] = __ballot(fr[s]);
+      rank_l[s] = cl + __popcll(bl[s] & below);
+      rank_r[s] = cr + __popcll(br[s] & below);
+      cl += __popcll(bl[s]);
+      cr += __popcll(br[s]);
+    }
+    int mm = 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int p = s * kWave + lane;
+      if (p > first && p < last) mm = max(mm, min(rank_l[s], cr - rank_r[s]));
+    }
+    const int m = (int)wave_max_u32((uint32_t)mm);
+    // exchange the m pairs' entries
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (fl[s] && rank_l[s] < m) buf_l[rank_l[s]] = r.v[s];
+      if (fr[s] && cr - 1 - rank_r[s] < m) buf_r[cr - 1 - rank_r[s]] = r.v[s];
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (fl[s] && rank_l[s] < m) r.v[s] = buf_r[rank_l[s]];
+      else if (fr[s] && cr - 1 - rank_r[s] < m) r.v[s] = buf_l[cr - 1 - rank_r[s]];
+    }
+    wave_lds_sync();
+    // where the left scan stopped: L[0], min(L[m], R[m - 1]) or R[m - 1]
+    int lm = kNone, rm1 = kNone;
+#pragma unroll
+    for (int s = S - 1; s >= 0; --s) {
+      const uint64_t at_l = __ballot(fl[s] && rank_l[s] == m);
+      const uint64_t at_r = __ballot(m > 0 && fr[s] && rank_r[s] == cr - m);
+      if (at_l) lm = s * kWave + __builtin_ctzll(at_l);
+      if (at_r) rm1 = s * kWave + __builtin_ctzll(at_r);
+    }
+    const int cut = min(lm, rm1);
+    if (cut <= nth) first = cut;
+    else last = cut;
+  }
+  if (!spilled) {
+    r.insertion_sort(first, last);
+    r.insertion_sort(0, k - 1);  // std::sort of k - 1 <= 16 entries
+    for (int j = 0; j < k; ++j) {
+      const int id = (int)(r.get(j) & 0xffffu);
+      if (lane == out_lane_base + j) my_id = id;
+    }
+  } else {
+    if (lane >= out_lane_base && lane < out_lane_base + k) my_id = (int)(scratch[lane - out_lane_base] & 0xffffu);
+    wave_lds_sync();
+  }
+  return my_id;
+}
+
+// torch's order for one tie row by the whole wave: the register form for
+// the rows the 4-tokens-per-wave kernel takes (n <= 256, k <= 16) in the
+// introselect regime, the LDS form otherwise.  Returns the expert of result
+// j in lane out_lane_base + j.
+__device__ __forceinline__ int wave_torch_topk_lanes(const uint16_t* row, int n, int k, uint32_t* scratch, int out_lane_base,
+                                     int my_id) {
+  if (k * 64 > n && k <= 16) {
+    if (n <= 64) return wave_torch_topk_regs<1>(row, n, k, scratch, out_lane_base, my_id);
+    if (n <= 128) return wave_torch_topk_regs<2>(row, n, k, scratch, out_lane_base, my_id);
+    if (n <= 256) return wave_torch_topk_regs<4>(row, n, k, scratch, out_lane_base, my_id);
+  }
+  wave_torch_topk(row, n, k, scratch);
+  const int lane = threadIdx.x & 63;
+  if (lane >= out_lane_base && lane < out_lane_base + k) my_id = (int)(scratch[lane - out_lane_base] & 0xffffu);
+  wave_lds_sync();
+  return my_id;
+}
+
 // torch's CPU softmax (klc_torch_order.h) of the k values held by lanes
 // base .. base + k - 1 (lane base + r holds slot r), evaluated by every
 // lane; returns the bfloat16 weight of the calling lane's slot.
@@ -362,11 +576,7 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
     prev = value_key;
     if (lane == r) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
   }
-  if (tie) {  // uniform: every lane saw the same maxima
-    wave_torch_topk(row, n_exp, k, tie_scratch);
-    if (lane < k) my_id = (int)(tie_scratch[lane] & 0xffffu);
-    wave_lds_sync();
-  }
+  if (tie) my_id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, my_id);  // uniform: the same maxima
   const float my_val = bf16_to_f32(row[lane < k ? my_id : 0]);
   const uint32_t w = torch_softmax_bf16(my_val, 0, k);
   if (lane < k) {
@@ -391,88 +601,118 @@ __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp,
   else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
 }
 
-// Top-k + softmax of 4 tokens at once by one wave: the 16 lanes of row q
-// (lanes 16 q .. 16 q + 15) take token t0 + q, lane r of the row holding the
-// keys of experts r + 16 s.  Each round's maximum comes from the lane's own
-// keys and 4 DPP steps inside the row (quad swaps, half-row and row
-// mirrors), so the 4 tokens' selections run side by side.  Same selection,
-// tie handling and softmax as topk_softmax_row (n_exp <= 16 kSlots,
-// k <= 16); a row with ties is replayed by the whole wave.  rows(q) gives
-// token q's logits row (any valid row for q >= n_valid, whose results are
-// not written).
+// Top-k + softmax of up to 16 tokens by one 256-thread workgroup; tokens
+// 4 w .. 4 w + 3 go to wave w, whose 16 lanes of row q (lanes 16 q ..
+// 16 q + 15) take token 4 w + q, lane r of the row holding the keys of
+// experts r + 16 s.  Each round's maximum comes from the lane's own keys and
+// 4 DPP steps inside the row (quad swaps, half-row and row mirrors), so a
+// wave's 4 selections run side by side: k + 1 rounds give the k largest
+// and the next value.  Rows without equal values among those k + 1 are
+// finished at once (torch's order is the descending order); rows with ties
+// go to a workgroup list, and the 4 waves replay them in turn
+// (wave_torch_topk_lanes), so a workgroup's ties are spread over its waves.
+// rows(t) gives local token t's logits row; n_block <= 16 tokens; token t
+// is written at t_base + t.  n_exp <= 16 kSlots, k <= 16.  Every thread of
+// the workgroup must call this (it synchronises the workgroup).
+// tie_scratch: the calling wave's topk_tie_scratch_bytes(n_exp) bytes of
+// LDS; tie_list: 17 ints of LDS shared by the workgroup.
 template <int kSlots, typename RowFn>
-__device__ __forceinline__ void topk_softmax_quad(RowFn rows, int n_valid, int n_exp, int k, int64_t t0,
-                                                  int32_t* __restrict__ ids, float* __restrict__ values,
-                                                  uint16_t* __restrict__ weights, int32_t* lds_ids,
-                                                  uint32_t* tie_scratch) {
+__device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block, int n_exp, int k, int64_t t_base,
+                                                        int32_t* __restrict__ ids, float* __restrict__ values,
+                                                        uint16_t* __restrict__ weights, int32_t* lds_ids,
+                                                        uint32_t* tie_scratch, int* tie_list) {
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
   const int r = lane & 15;
-  const uint16_t* row = rows(min(q, n_valid - 1));
-  uint64_t keys[kSlots];
+  const int n_valid = min(max(n_block - 4 * wave, 0), 4);
+  if (threadIdx.x == 0) tie_list[16] = 0;
+  lds_barrier();
+  if (n_valid > 0) {
+    const uint16_t* row = rows(4 * wave + min(q, n_valid - 1));
+    uint64_t keys[kSlots];
 #pragma unroll
-  for (int s = 0; s < kSlots; ++s) {
-    const int idx = r + s * 16;
-    keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
-  }
-  int my_id = 0;
-  bool tie = false;
-  uint32_t prev = 0;
-  const int rounds = k < n_exp ? k + 1 : k;
-  for (int rd = 0; rd < rounds; ++rd) {
-    uint64_t best = keys[0];
+    for (int s = 0; s < kSlots; ++s) {
+      const int idx = r + s * 16;
+      keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
+    }
+    int my_id = 0;
+    bool tie = false;
+    uint32_t prev = 0;
+    const int rounds = k < n_exp ? k + 1 : k;
+    for (int rd = 0; rd < rounds; ++rd) {
+      uint64_t best = keys[0];
 #pragma unroll
-    for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
-    best = dpp_max_step<0xB1, 0xf>(best);   // quad_perm [1, 0, 3, 2]
-    best = dpp_max_step<0x4E, 0xf>(best);   // quad_perm [2, 3, 0, 1]
-    best = dpp_max_step<0x141, 0xf>(best);  // row_half_mirror
-    best = dpp_max_step<0x140, 0xf>(best);  // row_mirror: every lane of the row holds its maximum
+      for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
+      best = dpp_max_step<0xB1, 0xf>(best);   // quad_perm [1, 0, 3, 2]
+      best = dpp_max_step<0x4E, 0xf>(best);   // quad_perm [2, 3, 0, 1]
+      best = dpp_max_step<0x141, 0xf>(best);  // row_half_mirror
+      best = dpp_max_step<0x140, 0xf>(best);  // row_mirror: every lane of the row holds its maximum
 #pragma unroll
-    for (int s = 0; s < kSlots; ++s)
-      if (keys[s] == best) keys[s] = 0ull;
-    const uint32_t value_key = (uint32_t)(best >> 32);
-    tie |= rd > 0 && value_key == prev;
-    prev = value_key;
-    if (r == rd) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
-  }
-  // rows whose k + 1 largest values include equal ones take torch's order
-  const uint64_t tie_rows = __ballot(tie && q < n_valid);
-  if (tie_rows != 0ull) {
-    for (int qq = 0; qq < 4; ++qq) {
-      if (((tie_rows >> (16 * qq)) & 1ull) == 0ull) continue;
-      wave_torch_topk(rows(qq), n_exp, k, tie_scratch);
-      if (q == qq && r < k) my_id = (int)(tie_scratch[r] & 0xffffu);
-      wave_lds_sync();
+      for (int s = 0; s < kSlots; ++s)
+        if (keys[s] == best) keys[s] = 0ull;
+      const uint32_t value_key = (uint32_t)(best >> 32);
+      tie |= rd > 0 && value_key == prev;
+      prev = value_key;
+      if (r == rd) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+    }
+    // every row's softmax is evaluated (the row's lanes exchange values); tie rows' results are dropped
+    const float my_val = bf16_to_f32(row[r < k ? my_id : 0]);
+    const uint32_t w = torch_softmax_bf16(my_val, q * 16, k);
+    if (q < n_valid) {
+      if (tie) {
+        if (r == 0) tie_list[atomicAdd(&tie_list[16], 1)] = 4 * wave + q;
+      } else if (r < k) {
+        const int64_t o = (t_base + 4 * wave + q) * k + r;
+        // agent scope: the decode router's final dispatch may run in another workgroup
+        __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lds_ids != nullptr) lds_ids[o] = my_id;
+        if (values) values[o] = my_val;
+        weights[o] = (uint16_t)w;
+      }
     }
   }
-  const float my_val = bf16_to_f32(row[r < k ? my_id : 0]);
-  const uint32_t w = torch_softmax_bf16(my_val, q * 16, k);
-  if (q < n_valid && r < k) {
-    const int64_t o = (t0 + q) * k + r;
-    // agent scope: the decode router's final dispatch may run in another workgroup
-    __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (lds_ids != nullptr) lds_ids[o] = my_id;
-    if (values) values[o] = my_val;
-    weights[o] = (uint16_t)w;
+  lds_barrier();
+  const int n_ties = tie_list[16];
+  for (int i = wave; i < n_ties; i += 4) {
+    const int t = tie_list[i];
+    const uint16_t* row = rows(t);
+    const int id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, 0);
+    const float v = bf16_to_f32(row[lane < k ? id : 0]);
+    const uint32_t w = torch_softmax_bf16(v, 0, k);
+    if (lane < k) {
+      const int64_t o = (t_base + t) * k + lane;
+      __hip_atomic_store(ids + o, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lds_ids != nullptr) lds_ids[o] = id;
+      if (values) values[o] = v;
+      weights[o] = (uint16_t)w;
+    }
   }
 }
 
-// Top-k of tokens t0 .. t0 + n - 1 (n <= 4) by one wave: the row-parallel
-// form when the row fits (n_exp <= 256, k <= 16), else token by token.
+// Top-k + softmax of up to 16 tokens (local t < n_block, written at
+// t_base + t) by one 256-thread workgroup: the 4-tokens-per-wave form when a
+// row fits (n_exp <= 256, k <= 16), else token by token, 4 per wave.
 // lds_ids (optional): a second copy of the ids in LDS, same indices.
-// tie_scratch: topk_tie_scratch_bytes(n_exp) bytes of LDS for this wave.
+// tie_scratch: the wave's topk_tie_scratch_bytes(n_exp) bytes of LDS;
+// tie_list: 17 ints of LDS.  Called by every thread of the workgroup.
 template <typename RowFn>
-__device__ __forceinline__ void topk_softmax_tokens(RowFn rows, int n, int n_exp, int k, int64_t t0,
-                                                    int32_t* __restrict__ ids, float* __restrict__ values,
-                                                    uint16_t* __restrict__ weights, int32_t* lds_ids,
-                                                    uint32_t* tie_scratch) {
+__device__ __forceinline__ void topk_softmax_block(RowFn rows, int n_block, int n_exp, int k, int64_t t_base,
+                                                   int32_t* __restrict__ ids, float* __restrict__ values,
+                                                   uint16_t* __restrict__ weights, int32_t* lds_ids,
+                                                   uint32_t* tie_scratch, int* tie_list) {
   if (k <= 16 && n_exp <= 256) {
-    if (n_exp <= 64) topk_softmax_quad<4>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids, tie_scratch);
-    else if (n_exp <= 128) topk_softmax_quad<8>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids, tie_scratch);
-    else topk_softmax_quad<16>(rows, n, n_exp, k, t0, ids, values, weights, lds_ids, tie_scratch);
+    if (n_exp <= 64)
+      topk_softmax_block_quad<4>(rows, n_block, n_exp, k, t_base, ids, values, weights, lds_ids, tie_scratch, tie_list);
+    else if (n_exp <= 128)
+      topk_softmax_block_quad<8>(rows, n_block, n_exp, k, t_base, ids, values, weights, lds_ids, tie_scratch, tie_list);
+    else
+      topk_softmax_block_quad<16>(rows, n_block, n_exp, k, t_base, ids, values, weights, lds_ids, tie_scratch,
+                                  tie_list);
   } else {
-    for (int q = 0; q < n; ++q)
-      topk_softmax_row(rows(q), n_exp, k, t0 + q, ids, values, weights, lds_ids, tie_scratch);
+    const int wave = threadIdx.x >> 6;
+    for (int q = 4 * wave; q < min(n_block, 4 * wave + 4); ++q)
+      topk_softmax_row(rows(q), n_exp, k, t_base + q, ids, values, weights, lds_ids, tie_scratch);
   }
 }
 
@@ -481,12 +721,12 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __res
                                                            uint16_t* __restrict__ weights, int n_tok, int n_exp,
                                                            int k) {
   extern __shared__ __align__(16) char lds[];  // topk_tie_scratch_bytes(n_exp) per wave
+  __shared__ int tie_list[17];
   const int wave = threadIdx.x >> 6;
-  const int t0 = (blockIdx.x * 4 + wave) * 4;  // 4 tokens per wave
-  if (t0 >= n_tok) return;
+  const int64_t t_base = (int64_t)blockIdx.x * 16;  // 16 tokens per workgroup
   uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + wave * topk_tie_scratch_bytes(n_exp));
-  topk_softmax_tokens([&](int q) { return logits + (int64_t)(t0 + q) * n_exp; }, min(4, n_tok - t0), n_exp, k, t0,
-                      ids, values, weights, nullptr, tie_scratch);
+  topk_softmax_block([&](int t) { return logits + (t_base + t) * n_exp; }, (int)min<int64_t>(16, n_tok - t_base),
+                     n_exp, k, t_base, ids, values, weights, nullptr, tie_scratch, tie_list);
 }
 
 // Softmax of caller-chosen scores (one thread per token), as torch's CPU
@@ -583,14 +823,6 @@ __device__ __forceinline__ void wave_peers(const uint32_t (&key)[N], uint64_t (&
       peers[i] &= bit ? m : ~m;
     }
   }
-}
-
-// Workgroup barrier that orders LDS accesses only: unlike __syncthreads it
-// does not wait for the workgroup's outstanding global stores.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Stable counting sort of the pairs by expert, by one 256-thread block, and
@@ -783,7 +1015,7 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
 // workgroup resets the counter for the next launch.  (An agent-scope fence
 // would write back and invalidate the whole L2.)  Returns the same value in
 // every thread.
-__device__ bool arrive_last(uint32_t* ctr, uint32_t expected, uint32_t* flag) {
+__device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t expected, uint32_t* flag) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -821,6 +1053,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   extern __shared__ __align__(16) char lds[];
   __shared__ uint32_t flag;
   __shared__ int32_t tile_ids[kRouterTile * kRouterMaxK];  // one token tile's ids, for its own dispatch
+  __shared__ int tie_list[17];  // the tile's rows with ties, and their count
   const int et = blockIdx.x, tt = blockIdx.y, ks = blockIdx.z;
   const int n_et = gridDim.x, n_tt = gridDim.y, n_ks = gridDim.z;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -891,13 +1124,11 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   }
   lds_barrier();  // the rows are in LDS; the logits' global stores need not have completed
   {
-    const int tw = t0 + 4 * wave;  // 4 tokens per wave
     // each wave's tie scratch follows the 16 logits rows
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp) +
                                                         wave * topk_tie_scratch_bytes(n_exp));
-    if (tw < n_tok)
-      topk_softmax_tokens([&](int q) { return rows + (tw - t0 + q) * n_exp; }, min(4, n_tok - tw), n_exp, k, tw, ids,
-                          values, weights, n_tt == 1 ? tile_ids : nullptr, tie_scratch);
+    topk_softmax_block([&](int t) { return rows + t * n_exp; }, min(kRouterTile, n_tok - t0), n_exp, k, t0, ids,
+                       values, weights, n_tt == 1 ? tile_ids : nullptr, tie_scratch, tie_list);
   }
   if (n_tt > 1) {
     if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;

@@ -45,7 +45,7 @@ __host__ __device__ __forceinline__ void entry_swap(uint32_t* a, int i, int j) {
   a[j] = t;
 }
 
-__host__ __device__ inline int floor_log2(int n) {
+__host__ __device__ __forceinline__ int floor_log2(int n) {
   int l = 0;
   while (n > 1) {
     n >>= 1;
@@ -55,7 +55,7 @@ __host__ __device__ inline int floor_log2(int n) {
 }
 
 // __move_median_to_first(result, a, b, c)
-__host__ __device__ inline void stl_move_median_to_first(uint32_t* v, int result, int a, int b, int c) {
+__host__ __device__ __forceinline__ void stl_move_median_to_first(uint32_t* v, int result, int a, int b, int c) {
   if (entry_gt(v[a], v[b])) {
     if (entry_gt(v[b], v[c])) entry_swap(v, result, b);
     else if (entry_gt(v[a], v[c])) entry_swap(v, result, c);
@@ -70,7 +70,7 @@ __host__ __device__ inline void stl_move_median_to_first(uint32_t* v, int result
 }
 
 // __unguarded_partition(first, last, pivot)
-__host__ __device__ inline int stl_unguarded_partition(uint32_t* v, int first, int last, int pivot) {
+__host__ __device__ __forceinline__ int stl_unguarded_partition(uint32_t* v, int first, int last, int pivot) {
   const uint32_t p = v[pivot];
   while (true) {
     while (entry_gt(v[first], p)) ++first;
@@ -82,13 +82,13 @@ __host__ __device__ inline int stl_unguarded_partition(uint32_t* v, int first, i
   }
 }
 
-__host__ __device__ inline int stl_unguarded_partition_pivot(uint32_t* v, int first, int last) {
+__host__ __device__ __forceinline__ int stl_unguarded_partition_pivot(uint32_t* v, int first, int last) {
   const int mid = first + (last - first) / 2;
   stl_move_median_to_first(v, first, first + 1, mid, last - 1);
   return stl_unguarded_partition(v, first + 1, last, first);
 }
 
-__host__ __device__ inline void stl_unguarded_linear_insert(uint32_t* v, int last) {
+__host__ __device__ __forceinline__ void stl_unguarded_linear_insert(uint32_t* v, int last) {
   const uint32_t val = v[last];
   int next = last - 1;
   while (entry_gt(val, v[next])) {
@@ -99,7 +99,7 @@ __host__ __device__ inline void stl_unguarded_linear_insert(uint32_t* v, int las
   v[last] = val;
 }
 
-__host__ __device__ inline void stl_insertion_sort(uint32_t* v, int first, int last) {
+__host__ __device__ __forceinline__ void stl_insertion_sort(uint32_t* v, int first, int last) {
   if (first == last) return;
   for (int i = first + 1; i < last; ++i) {
     if (entry_gt(v[i], v[first])) {
@@ -113,7 +113,7 @@ __host__ __device__ inline void stl_insertion_sort(uint32_t* v, int first, int l
 }
 
 // heap algorithms on v[base .. base + len)
-__host__ __device__ inline void stl_push_heap(uint32_t* v, int base, int hole, int top, uint32_t value) {
+__host__ __device__ __forceinline__ void stl_push_heap(uint32_t* v, int base, int hole, int top, uint32_t value) {
   int parent = (hole - 1) / 2;
   while (hole > top && entry_gt(v[base + parent], value)) {
     v[base + hole] = v[base + parent];
@@ -123,7 +123,7 @@ __host__ __device__ inline void stl_push_heap(uint32_t* v, int base, int hole, i
   v[base + hole] = value;
 }
 
-__host__ __device__ inline void stl_adjust_heap(uint32_t* v, int base, int hole, int len, uint32_t value) {
+__host__ __device__ __forceinline__ void stl_adjust_heap(uint32_t* v, int base, int hole, int len, uint32_t value) {
   const int top = hole;
   int child = hole;
   while (child < (len - 1) / 2) {
@@ -140,7 +140,7 @@ __host__ __device__ inline void stl_adjust_heap(uint32_t* v, int base, int hole,
   stl_push_heap(v, base, hole, top, value);
 }
 
-__host__ __device__ inline void stl_make_heap(uint32_t* v, int first, int last) {
+__host__ __device__ __forceinline__ void stl_make_heap(uint32_t* v, int first, int last) {
   const int len = last - first;
   if (len < 2) return;
   for (int parent = (len - 2) / 2;; --parent) {
@@ -149,19 +149,19 @@ __host__ __device__ inline void stl_make_heap(uint32_t* v, int first, int last) 
   }
 }
 
-__host__ __device__ inline void stl_pop_heap(uint32_t* v, int first, int last, int result) {
+__host__ __device__ __forceinline__ void stl_pop_heap(uint32_t* v, int first, int last, int result) {
   const uint32_t value = v[result];
   v[result] = v[first];
   stl_adjust_heap(v, first, 0, last - first, value);
 }
 
-__host__ __device__ inline void stl_heap_select(uint32_t* v, int first, int middle, int last) {
+__host__ __device__ __forceinline__ void stl_heap_select(uint32_t* v, int first, int middle, int last) {
   stl_make_heap(v, first, middle);
   for (int i = middle; i < last; ++i)
     if (entry_gt(v[i], v[first])) stl_pop_heap(v, first, middle, i);
 }
 
-__host__ __device__ inline void stl_partial_sort(uint32_t* v, int first, int middle, int last) {
+__host__ __device__ __forceinline__ void stl_partial_sort(uint32_t* v, int first, int middle, int last) {
   stl_heap_select(v, first, middle, last);
   for (int l = middle; l - first > 1;) {  // __sort_heap
     --l;
@@ -175,7 +175,7 @@ __host__ __device__ inline void stl_partial_sort(uint32_t* v, int first, int mid
 // with the same depth budget; the two ranges are disjoint, and for at most
 // 33 entries only one of them can hold more than 16, so following that one
 // alone does what the recursion does, without a stack.
-__host__ __device__ inline void stl_sort(uint32_t* v, int first, int last) {
+__host__ __device__ __forceinline__ void stl_sort(uint32_t* v, int first, int last) {
   if (first == last) return;
   constexpr int kThreshold = 16;
   int f = first, l = last, d = floor_log2(last - first) * 2;
@@ -199,7 +199,7 @@ __host__ __device__ inline void stl_sort(uint32_t* v, int first, int last) {
 
 // std::nth_element(first, nth, last), sequential (the host restatement of
 // what the router kernel runs with its partitions spread over a wave).
-__host__ __device__ inline void stl_nth_element(uint32_t* v, int first, int nth, int last) {
+__host__ __device__ __forceinline__ void stl_nth_element(uint32_t* v, int first, int nth, int last) {
   if (first == last || nth == last) return;
   int depth = floor_log2(last - first) * 2;
   while (last - first > 3) {
@@ -217,7 +217,7 @@ __host__ __device__ inline void stl_nth_element(uint32_t* v, int first, int nth,
 }
 
 // torch.topk(x, k) (largest, sorted) on CPU: v[0 .. k) ends as the result.
-__host__ __device__ inline void torch_topk_order(uint32_t* v, int n, int k) {
+__host__ __device__ __forceinline__ void torch_topk_order(uint32_t* v, int n, int k) {
   if (k <= 0) return;
   if (k * 64 <= n) {
     stl_partial_sort(v, 0, k, n);
@@ -234,14 +234,14 @@ __host__ __device__ inline void torch_topk_order(uint32_t* v, int n, int k) {
 // q ln 2 in two FMA steps (ln 2 split as 0.693145751953125 +
 // 1.428606765330187045e-06); a degree-6 polynomial in s by FMA;
 // u = 1 + (s^2 u + s); scaled by 2^(q >> 1) and 2^(q - (q >> 1)).
-__host__ __device__ inline float pow2i_f32(int q) {
+__host__ __device__ __forceinline__ float pow2i_f32(int q) {
   const uint32_t bits = (uint32_t)(q + 0x7f) << 23;
   float f;
   __builtin_memcpy(&f, &bits, 4);
   return f;
 }
 
-__host__ __device__ inline float sleef_expf_u10(float d) {
+__host__ __device__ __forceinline__ float sleef_expf_u10(float d) {
 #pragma clang fp contract(off)
   float q = __builtin_rintf(d * 1.442695040888963407359924681001892137426645954152985934135449406931f);
   q = q > 200.0f ? 200.0f : (q < -200.0f ? -200.0f : q);  // NaN stays NaN; outside this range d is saturated below

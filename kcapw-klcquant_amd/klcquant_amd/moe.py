@@ -226,6 +226,25 @@ class MoELayer:
                  ops._stream(x.device))
         return out
 
+    def capture_graph(self, x: torch.Tensor, out: torch.Tensor, ids: torch.Tensor | None = None,
+                      weights: torch.Tensor | None = None, residual: torch.Tensor | None = None
+                      ) -> "torch.cuda.CUDAGraph":
+        """A HIP graph of one :meth:`forward_static_scratch` call on these buffers.
+
+        ``graph.replay()`` then runs the layer's kernels with one launch from
+        the host, on the same tensors (refill ``x`` in place to route new
+        tokens).  The layer runs on the library's static scratch, so the call
+        allocates nothing and records no memset; one eager call made first
+        sets up that scratch on the device.  Replays share the scratch with
+        every other static-scratch call on the GPU: order them on one stream.
+        """
+        self.forward_static_scratch(x, out=out, ids=ids, weights=weights, residual=residual)
+        torch.cuda.synchronize(x.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.forward_static_scratch(x, out=out, ids=ids, weights=weights, residual=residual)
+        return graph
+
     def uses_gemm(self, n_tokens: int) -> bool:
         """Whether :meth:`forward` runs the grouped GEMM for ``n_tokens`` tokens (the library's rule)."""
         if self.path != "auto":

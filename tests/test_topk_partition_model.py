@@ -87,3 +87,24 @@ def test_wave_nth_element_equals_libstdcxx():
         if n > 0:
             wave_nth_element(b, k - 1)
         assert a == b
+
+
+def test_swap_count_from_prefix_counts():
+    """The kernel finds the swap count without building the lists: with A(q) the left stops below
+    position q and B(q) the right stops at or above q (pivot excluded), m = max over q of
+    min(A(q), B(q)); the cut and the partner of each stop follow from the ranks."""
+    rng = np.random.default_rng(23)
+    for _ in range(4000):
+        n = int(rng.integers(4, 260))
+        vals = rng.integers(0, int(rng.integers(1, 12)), n)
+        first = 0
+        p = vals[first]
+        pos = range(first + 1, n)
+        L = [q for q in pos if not vals[q] > p]
+        R = [q for q in reversed(pos) if not p > vals[q]]
+        m_lists = 0
+        while m_lists < min(len(L), len(R)) and L[m_lists] < R[m_lists]:
+            m_lists += 1
+        a = [sum(1 for x in L if x < q) for q in range(n + 1)]
+        b = [sum(1 for x in R if x >= q) for q in range(n + 1)]
+        assert max(min(a[q], b[q]) for q in range(first + 1, n + 1)) == m_lists
