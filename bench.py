@@ -360,6 +360,106 @@ def loader_bench(torch, dev, n_experts: int, rounds: int = 3) -> dict:
     }
 
 
+def layer_tensor_bench(torch, dev, n_layers: int = 4, rounds: int = 3) -> dict:
+    """The executor's per-layer dense tensors (120B shapes, bf16: attention
+    projections and biases, sinks, norms, router, expert biases; 56 MB per
+    layer) from a page-cache-resident shard to HBM.
+
+    ``native``: LayerTensorLoader (open shard, one staged batch copy per
+    shard).  ``safe_open_chain``: the executor's path
+    (streamed_transformer_executor.py:318-370: safe_open per load,
+    get_tensor, pin_memory().to(device), synchronize).  Layer 0 of each leg
+    is untimed; legs alternate over ``rounds`` and the medians are reported;
+    the tensors of both legs are compared.
+    """
+    import statistics
+    import tempfile
+
+    import numpy as np
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+
+    from klcquant_amd.layer_tensors import LayerTensorLoader, layer_tensor_names
+
+    nq, nkv, d = 64, 8, 64
+    shapes = {
+        "input_layernorm.weight": (HIDDEN,), "self_attn.o_proj.bias": (HIDDEN,),
+        "self_attn.o_proj.weight": (HIDDEN, nq * d), "self_attn.q_proj.bias": (nq * d,),
+        "self_attn.k_proj.bias": (nkv * d,), "self_attn.v_proj.bias": (nkv * d,),
+        "self_attn.q_proj.weight": (nq * d, HIDDEN), "self_attn.k_proj.weight": (nkv * d, HIDDEN),
+        "self_attn.v_proj.weight": (nkv * d, HIDDEN), "self_attn.sinks": (nq,), "mlp.router.bias": (EXPERTS,),
+        "mlp.router.weight": (EXPERTS, HIDDEN), "mlp.experts.gate_up_proj_bias": (EXPERTS, 2 * INTER),
+        "mlp.experts.down_proj_bias": (EXPERTS, HIDDEN), "post_attention_layernorm.weight": (HIDDEN,),
+    }
+    rng = np.random.default_rng(12)
+    tensors = {}
+    for layer in range(n_layers):
+        for suffix, shape in shapes.items():
+            bits = rng.integers(0, 1 << 16, shape, dtype=np.uint16) & 0xBFFF  # finite bf16 patterns
+            tensors[f"model.layers.{layer}.{suffix}"] = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    layer_bytes_ = sum(int(np.prod(s)) * 2 for s in shapes.values())
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "model-00001-of-00001.safetensors"
+        save_file(tensors, str(path))
+        with open(path, "rb+") as fh:
+            os.fsync(fh.fileno())
+        (Path(tmp) / "model.safetensors.index.json").write_text(
+            json.dumps({"weight_map": {name: path.name for name in tensors}}))
+        del tensors
+
+        def reference_chain(layer):
+            out = {}
+            with safe_open(str(path), framework="pt", device="cpu") as handle:
+                for name in layer_tensor_names(layer):
+                    t = handle.get_tensor(name).to(torch.bfloat16)
+                    out[name] = t.pin_memory().to(dev, non_blocking=True)
+            torch.cuda.synchronize()
+            return out
+
+        times = {"native": [], "safe_open_chain": []}
+        same = True
+        for r in range(rounds):
+            loader = LayerTensorLoader(tmp, dev, pin_layer_tensors=False)
+            got = {}
+            for label in (("native", "safe_open_chain") if r % 2 == 0 else ("safe_open_chain", "native")):
+                got[label] = []
+                for layer in range(n_layers):
+                    if layer == 1:
+                        torch.cuda.synchronize()
+                        t0 = time.perf_counter()
+                    got[label].append(loader.load(layer) if label == "native" else reference_chain(layer))
+                torch.cuda.synchronize()
+                times[label].append(time.perf_counter() - t0)
+            same = same and all(torch.equal(a[n], b[n]) for a, b in zip(got["native"], got["safe_open_chain"])
+                                for n in a)
+            del loader, got
+        torch.cuda.empty_cache()
+    # the link's own rate for comparison: one pinned 64 MiB buffer -> HBM
+    host = torch.empty(64 << 20, dtype=torch.uint8, pin_memory=True)
+    devbuf = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    devbuf.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        devbuf.copy_(host, non_blocking=True)
+    torch.cuda.synchronize()
+    h2d = 5 * (64 << 20) / (time.perf_counter() - t0) / 1e9
+    del host, devbuf
+    med = {k: statistics.median(v) for k, v in times.items()}
+    timed = (n_layers - 1) * layer_bytes_
+    return {
+        "layers_timed": n_layers - 1,
+        "rounds": rounds,
+        "bytes_per_layer": layer_bytes_,
+        "native_us_per_layer": round(med["native"] * 1e6 / (n_layers - 1), 1),
+        "native_gbps": round(timed / med["native"] / 1e9, 2),
+        "safe_open_chain_us_per_layer": round(med["safe_open_chain"] * 1e6 / (n_layers - 1), 1),
+        "safe_open_chain_gbps": round(timed / med["safe_open_chain"] / 1e9, 2),
+        "pinned_h2d_gbps": round(h2d, 2),
+        "tensors_equal": bool(same),
+    }
+
+
 def lm_head_bench(torch, dev, reps: int = 50) -> dict:
     """gpt-oss lm_head (201,088 x 2880 bf16, resident): one logits pass plus
     the greedy token, against the executor's chunked float32 matmul with a
@@ -703,6 +803,7 @@ def main() -> int:
         print(f"[bench] lm_head: {result['lm_head']}", file=sys.stderr, flush=True)
     if args.loader_experts > 1:
         result["loader"] = loader_bench(torch, dev, args.loader_experts)
+        result["loader"]["layer_tensors"] = layer_tensor_bench(torch, dev)
         print(f"[bench] loader: {result['loader']}", file=sys.stderr, flush=True)
     if not args.skip_dequant:
         result["dequant"] = dequant_bench(torch, dev)

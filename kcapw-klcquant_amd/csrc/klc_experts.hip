@@ -651,7 +651,7 @@ extern "C" int klc_moe_combine(const float* expert_out, const void* weights, con
                                int64_t n_tokens, int64_t k, int64_t hidden, void* out, void* stream) {
   KLC_REQUIRE(expert_out && weights && out, KLC_ERR_ARGUMENT, "klc_moe_combine: null pointer");
   KLC_REQUIRE(n_tokens > 0 && k > 0 && hidden > 0, KLC_ERR_ARGUMENT, "klc_moe_combine: bad sizes");
-  KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "klc_moe_combine: n_tokens=%lld > 65535", (long long)n_tokens);
+  KLC_REQUIRE(n_tokens <= KLC_LAYER_MAX_TOKENS, KLC_ERR_UNSUPPORTED, "klc_moe_combine: n_tokens=%lld > 65535", (long long)n_tokens);
   return launch_combine(expert_out, weights, residual, n_tokens, k, hidden, out, as_stream(stream));
 }
 
@@ -659,7 +659,7 @@ extern "C" int klc_moe_bias_combine(const void* down_bias, const int32_t* ids, c
                                     int64_t k, int64_t hidden, void* out, void* stream) {
   KLC_REQUIRE(down_bias && ids && weights && out, KLC_ERR_ARGUMENT, "klc_moe_bias_combine: null pointer");
   KLC_REQUIRE(n_tokens > 0 && k > 0 && hidden > 0, KLC_ERR_ARGUMENT, "klc_moe_bias_combine: bad sizes");
-  KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "klc_moe_bias_combine: n_tokens=%lld > 65535",
+  KLC_REQUIRE(n_tokens <= KLC_LAYER_MAX_TOKENS, KLC_ERR_UNSUPPORTED, "klc_moe_bias_combine: n_tokens=%lld > 65535",
               (long long)n_tokens);
   const dim3 grid((unsigned)((hidden + 255) / 256), (unsigned)n_tokens);
   bias_combine_kernel<<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(down_bias), ids,
@@ -706,7 +706,7 @@ int check_layer_args(const char* fn, const void* x, const void* router_w, const 
   if (rc) return rc;
   rc = check_gemv_shapes(hidden, inter, n_tokens * k, n_experts);
   if (rc) return rc;
-  KLC_REQUIRE(n_tokens <= 65535, KLC_ERR_UNSUPPORTED, "%s: n_tokens=%lld > 65535", fn, (long long)n_tokens);
+  KLC_REQUIRE(n_tokens <= KLC_LAYER_MAX_TOKENS, KLC_ERR_UNSUPPORTED, "%s: n_tokens=%lld > 65535", fn, (long long)n_tokens);
   return KLC_OK;
 }
 

@@ -804,7 +804,7 @@ __host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int /*n_exp
 }
 
 // Largest n_pairs whose staging fits in 160 KiB of LDS.
-constexpr int kDispatchMaxPairs = 38648;
+constexpr int kDispatchMaxPairs = KLC_DISPATCH_MAX_PAIRS;
 static_assert(dispatch_lds_bytes(kDispatchMaxPairs, kDispatchMaxExperts) <= 160 * 1024, "dispatch LDS");
 static_assert(dispatch_lds_bytes(kDispatchMaxPairs + 8, kDispatchMaxExperts) > 160 * 1024, "dispatch LDS");
 

@@ -172,6 +172,11 @@ class MoELayer:
 
         ``events``: optional list of ``KLC_LAYER_EVENTS`` recorded
         ``torch.cuda.Event`` objects, re-recorded around the six kernels.
+
+        More tokens than one library call takes (:meth:`max_tokens_per_call`)
+        run as consecutive calls on row chunks; every token's routing, expert
+        outputs and combine depend on that token alone, so the result is the
+        one a single call would give.
         """
         ops._check_gpu("hidden", x, torch.bfloat16, 2)
         n_tok, hidden = x.shape
@@ -183,6 +188,16 @@ class MoELayer:
                 raise ValueError(f"residual shape {tuple(residual.shape)} != hidden shape {tuple(x.shape)}")
         if out is None:
             out = torch.empty_like(x)
+        chunk = self.max_tokens_per_call()
+        if n_tok > chunk:
+            if events is not None:
+                raise ValueError(f"events are recorded around one call of at most {chunk} tokens, got {n_tok}")
+            for t0 in range(0, n_tok, chunk):
+                t1 = min(n_tok, t0 + chunk)
+                self.forward(x[t0:t1], out=out[t0:t1], ids=None if ids is None else ids[t0:t1],
+                             weights=None if weights is None else weights[t0:t1],
+                             residual=None if residual is None else residual[t0:t1])
+            return out
         ws = self.workspace(n_tok)
         w = self.w
         ev = None
@@ -244,6 +259,12 @@ class MoELayer:
         with torch.cuda.graph(graph):
             self.forward_static_scratch(x, out=out, ids=ids, weights=weights, residual=residual)
         return graph
+
+    def max_tokens_per_call(self) -> int:
+        """Tokens one klc_moe_layer call takes: the dispatch stages at most
+        KLC_DISPATCH_MAX_PAIRS (token, slot) pairs, the layer at most
+        KLC_LAYER_MAX_TOKENS tokens."""
+        return ops.max_tokens_per_call(self.k)
 
     def uses_gemm(self, n_tokens: int) -> bool:
         """Whether :meth:`forward` runs the grouped GEMM for ``n_tokens`` tokens (the library's rule)."""

@@ -168,6 +168,11 @@ class Dispatch(NamedTuple):
     n_experts: int
 
 
+def max_tokens_per_call(k: int) -> int:
+    """Tokens of top-``k`` routing that one dispatch / layer call takes."""
+    return min(nat.LAYER_MAX_TOKENS, nat.DISPATCH_MAX_PAIRS // max(1, int(k)))
+
+
 def dispatch(ids: torch.Tensor, n_experts: int) -> Dispatch:
     """int32 ids ``[B, k]`` -> :class:`Dispatch`."""
     _check_gpu("ids", ids, torch.int32)

@@ -294,7 +294,10 @@ class StreamedMoERouter:
         elif d_bias is None:
             output, mode = torch.zeros_like(hidden), "router_only"
         else:
-            output, mode = ops.bias_combine(d_bias, ids, weights).reshape(hidden.shape), "bias_only_moe"
+            chunk = ops.max_tokens_per_call(k)
+            output = torch.cat([ops.bias_combine(d_bias, ids[t0:t0 + chunk], weights[t0:t0 + chunk])
+                                for t0 in range(0, n_tok, chunk)])
+            output, mode = output.reshape(hidden.shape), "bias_only_moe"
 
         if host is None:
             host = self._read_back(ids, weights)
@@ -381,13 +384,19 @@ class StreamedMoERouter:
         if tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
             raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
                              f"E={n_exp} H={hidden} I={inter}")
-        disp = ops.dispatch(ids, n_exp)
-        gated, gated_raw = ops.gate_up(gu_table, gu_bias, x, k, disp, hidden, inter, self.swiglu_limit,
-                                       self.matmul_precision, want_raw=True)
-        eo = ops.down(d_table, d_bias, gated, disp, hidden, inter, self.matmul_precision)
-        out = ops.combine(eo, weights, n_tok, k)
-        norms = ops.pair_norms(gated_raw, eo)
-        return out, norms
+        chunk = ops.max_tokens_per_call(k)  # longer inputs: consecutive calls on row chunks
+        outs, norms = [], []
+        for t0 in range(0, n_tok, chunk):
+            t1 = min(n_tok, t0 + chunk)
+            disp = ops.dispatch(ids[t0:t1], n_exp)
+            gated, gated_raw = ops.gate_up(gu_table, gu_bias, x[t0:t1], k, disp, hidden, inter,
+                                           self.swiglu_limit, self.matmul_precision, want_raw=True)
+            eo = ops.down(d_table, d_bias, gated, disp, hidden, inter, self.matmul_precision)
+            outs.append(ops.combine(eo, weights[t0:t1], t1 - t0, k))
+            norms.append(ops.pair_norms(gated_raw, eo))
+        if len(outs) == 1:
+            return outs[0], norms[0]
+        return torch.cat(outs), torch.cat(norms)
 
     # ---- routing locality (host control logic, streamed_moe_router.py:331-476) ------------
 

@@ -39,7 +39,9 @@ def test_status_codes_match_header():
                         ("KLC_ERR_UNSUPPORTED", nat.KLC_ERR_UNSUPPORTED), ("KLC_ERR_HIP", nat.KLC_ERR_HIP),
                         ("KLC_DTYPE_BF16", nat.DTYPE_BF16), ("KLC_DTYPE_F16", nat.DTYPE_F16),
                         ("KLC_DTYPE_F32", nat.DTYPE_F32), ("KLC_PRECISION_FP32", nat.PRECISION_FP32),
-                        ("KLC_PRECISION_BF16", nat.PRECISION_BF16), ("KLC_LAYER_EVENTS", nat.LAYER_EVENTS)]:
+                        ("KLC_PRECISION_BF16", nat.PRECISION_BF16), ("KLC_LAYER_EVENTS", nat.LAYER_EVENTS),
+                        ("KLC_DISPATCH_MAX_PAIRS", nat.DISPATCH_MAX_PAIRS),
+                        ("KLC_LAYER_MAX_TOKENS", nat.LAYER_MAX_TOKENS)]:
         m = re.search(rf"#define {name} \(?(-?\d+)\)?", text)
         assert m and int(m.group(1)) == value, name
 

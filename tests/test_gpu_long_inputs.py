@@ -1,0 +1,66 @@
+"""Inputs longer than one library call takes (KLC_DISPATCH_MAX_PAIRS pairs).
+
+9,700 tokens at top-4 are 38,800 (token, slot) pairs, past the 38,648 that
+one dispatch stages; ``MoELayer.forward`` and ``StreamedMoERouter.route``
+split them into row chunks.  Every token depends on its own row only
+(streamed_moe_router.py:257-329 routes one token per call), so the chunked
+result must equal the oracle's exactly in routing and within the expert
+tolerance in the outputs, with no seam at the chunk boundary.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_bits, bf16_tensor
+from klcquant_amd import _native as nat
+from klcquant_amd import moe, ops
+from klcquant_amd.mxfp4_expert import ResidentExpertStore
+from klcquant_amd.streamed_moe_router import StreamedMoERouter
+from test_gpu_experts import assert_final_close, oracle_layer
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 256, 128, 16, 4
+WORKLOAD = 71
+N_TOK = 9700
+
+
+@pytest.fixture(scope="module")
+def setup(gpu):
+    assert N_TOK * K > nat.DISPATCH_MAX_PAIRS and N_TOK > ops.max_tokens_per_call(K)
+    host = moe.synthetic_host_layer(WORKLOAD, 0, H, I, E)
+    dev_w = moe.MoELayerWeights.synthetic(WORKLOAD, 0, H, I, E, gpu)
+    x = moe.synthetic_hidden(WORKLOAD, N_TOK, H)
+    return host, dev_w, x, oracle_layer(host, x, K)
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("path", ["auto", "gemv"])
+def test_layer_splits_past_dispatch_limit(gpu, setup, path):
+    host, dev_w, x, ref = setup
+    layer = moe.MoELayer(dev_w, K, path=path)
+    ids = torch.empty((N_TOK, K), dtype=torch.int32, device=gpu)
+    wts = torch.empty((N_TOK, K), dtype=torch.bfloat16, device=gpu)
+    out = layer.forward(bf16_tensor(x, gpu), ids=ids, weights=wts)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ref["ids"])
+    assert np.array_equal(bf16_bits(wts), ref["weights"])
+    assert_final_close(bf16_bits(out), ref)
+
+
+@pytest.mark.timeout(300)
+def test_route_splits_past_dispatch_limit(gpu, setup):
+    host, dev_w, x, ref = setup
+    names = {"router.weight": "router_weight", "router.bias": "router_bias",
+             "experts.gate_up_proj_bias": "gate_up_bias", "experts.down_proj_bias": "down_bias"}
+    tensors = {f"model.layers.0.mlp.{k}": bf16_tensor(host[v], gpu) for k, v in names.items()}
+    out, route = StreamedMoERouter(K).route(0, bf16_tensor(x, gpu), tensors, ResidentExpertStore({0: dev_w}),
+                                            position=0)
+    torch.cuda.synchronize()
+    assert out.shape == (N_TOK, H)
+    assert np.array_equal(np.array(route["experts"]), ref["ids"])
+    assert len(route["expert_logs"]) == N_TOK
+    assert_final_close(bf16_bits(out), ref)
