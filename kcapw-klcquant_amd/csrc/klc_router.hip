@@ -208,22 +208,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Wave-wide maximum of a 32-bit value (same DPP network as wave_max_u64).
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ uint32_t dpp_max_u32_step(uint32_t v) {
-  const uint32_t o = dpp_u32<kCtrl, kRowMask>(v, v);
-  return o > v ? o : v;
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = dpp_max_u32_step<0xB1, 0xf>(v);
-  v = dpp_max_u32_step<0x4E, 0xf>(v);
-  v = dpp_max_u32_step<0x141, 0xf>(v);
-  v = dpp_max_u32_step<0x140, 0xf>(v);
-  v = dpp_max_u32_step<0x142, 0xa>(v);
-  v = dpp_max_u32_step<0x143, 0xc>(v);
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
 // Workgroup barrier that orders LDS accesses only: unlike __syncthreads it
 // does not wait for the workgroup's outstanding global stores.
 __device__ __forceinline__ void lds_barrier() {
@@ -241,8 +225,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // LDS bytes one wave needs for wave_torch_topk over n logits: the entries
-// and the two stop-position lists of a partition step.
-__host__ __device__ constexpr size_t topk_tie_scratch_bytes(int n) { return ((size_t)n * 8 + 15) / 16 * 16; }
+// and the two stop-position lists of a partition step, and at least 64
+// words past a row of n words (the register form's per-lane dummy words).
+__host__ __device__ constexpr size_t topk_tie_scratch_bytes(int n) { return ((size_t)(n < 64 ? 64 : n) * 8 + 15) / 16 * 16; }
 
 // LDS bytes of the decode router's bfloat16 logits rows of one token tile.
 __host__ __device__ constexpr size_t decode_rows_bytes(int n_exp) {
@@ -335,100 +320,176 @@ __device__ __forceinline__ void wave_torch_topk(const uint16_t* row, int n, int 
   wave_lds_sync();
 }
 
-// One row of up to 64 * S entries held in registers across a wave: position
-// p lives in slot p / 64 of lane p % 64.  get/set take a wave-uniform
-// position, so every lane runs the sequential pieces of libstdc++'s
-// algorithms in lockstep on the same values.
+// Entry at wave-uniform position p of a row held in v[0 .. S) (position p in
+// slot p / 64 of lane p % 64): the lane is read from every slot, then one is
+// picked (a select between the slots' registers would turn into a run-time
+// indexed array in scratch).
 template <int S>
-struct WaveRow {
-  uint32_t v[S];
-
-  __device__ __forceinline__ uint32_t get(int p) const {
-    // read the lane of every slot, then pick one (no run-time register index)
-    const int s = p >> 6, l = p & 63;
-    uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v[0], l);
+__device__ __forceinline__ uint32_t row_get(const uint32_t (&v)[S], int p) {
+  const int slot = p >> 6, l = p & 63;
+  uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)v[0], l);
 #pragma unroll
-    for (int i = 1; i < S; ++i) {
-      const uint32_t y = (uint32_t)__builtin_amdgcn_readlane((int)v[i], l);
-      x = s == i ? y : x;
-    }
-    return x;
+  for (int i = 1; i < S; ++i) {
+    const uint32_t y = (uint32_t)__builtin_amdgcn_readlane((int)v[i], l);
+    x = slot == i ? y : x;
   }
-  __device__ __forceinline__ void set(int p, uint32_t val) {
-    const int s = p >> 6;
-    const bool mine = (int)(threadIdx.x & 63) == (p & 63);
-#pragma unroll
-    for (int i = 0; i < S; ++i) v[i] = (s == i && mine) ? val : v[i];
-  }
-  __device__ __forceinline__ void swap(int a, int b) {
-    const uint32_t va = get(a), vb = get(b);
-    set(a, vb);
-    set(b, va);
-  }
-  // __move_median_to_first(result, a, b, c)
-  __device__ __forceinline__ void move_median_to_first(int result, int a, int b, int c) {
-    const uint32_t va = get(a), vb = get(b), vc = get(c);
-    int pick;
-    if (entry_gt(va, vb)) pick = entry_gt(vb, vc) ? b : (entry_gt(va, vc) ? c : a);
-    else pick = entry_gt(va, vc) ? a : (entry_gt(vb, vc) ? c : b);
-    swap(result, pick);
-  }
-  // __insertion_sort(first, last)
-  __device__ __forceinline__ void insertion_sort(int first, int last) {
-    if (first == last) return;
-    for (int i = first + 1; i < last; ++i) {
-      const uint32_t val = get(i);
-      if (entry_gt(val, get(first))) {
-        for (int j = i; j > first; --j) set(j, get(j - 1));
-        set(first, val);
-      } else {  // __unguarded_linear_insert
-        int hole = i;
-        uint32_t prev = get(hole - 1);
-        while (entry_gt(val, prev)) {
-          set(hole, prev);
-          --hole;
-          prev = get(hole - 1);
-        }
-        set(hole, val);
-      }
-    }
-  }
-};
+  return x;
+}
 
-// wave_torch_topk for rows of n <= 64 * S entries in the introselect regime
-// (k * 64 > n) with k - 1 <= 16, the row held in registers.  Each partition
-// step is ballots and prefix counts: with A(q) the left stops below position
-// q and B(q) the right stops at or above q, the swap count is
-// m = max_q min(A(q), B(q)); the i-th left stop (ascending) and the i-th
-// right stop (descending) exchange their entries through two small LDS
-// arrays, for i < m; the cut is L[0] (m = 0), else min(L[m], R[m - 1])
-// (R[m - 1] once L is used up).  The rare depth-limit branch (heap select)
-// spills the row to LDS and finishes sequentially in lane 0.  Returns, in
-// lane out_lane_base + j (j < k), the expert of result j; other lanes get
-// my_id back.  scratch: n * 8 bytes of LDS.
+// Stable sort by key, descending, of the entries at positions [lo, hi) of
+// slot 0 (hi <= 64): each lane's rank among them, then a scatter through LDS
+// (dummy: one word per lane).  Equal keys keep their order, as libstdc++'s
+// insertion sort leaves them.
+__device__ __forceinline__ uint32_t lanes_stable_sort_desc(uint32_t v0, int lo, int hi, uint32_t* scratch,
+                                                           uint32_t* dummy) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t mk = v0 >> 16;
+  int rank = 0;
+  for (int i = lo; i < hi; ++i) {
+    const uint32_t ki = (uint32_t)__builtin_amdgcn_readlane((int)v0, i) >> 16;
+    rank += (ki > mk || (ki == mk && i < lane)) ? 1 : 0;
+  }
+  const bool in = lane >= lo && lane < hi;
+  scratch[in ? lo + rank : (int)(dummy - scratch) + lane] = v0;
+  wave_lds_sync();
+  const uint32_t x = scratch[lane];
+  wave_lds_sync();
+  return in ? x : v0;
+}
+
+// One __unguarded_partition step of the introselect on positions [first,
+// last) of a row held in v[0 .. S) (position p in slot p / 64 of lane
+// p % 64), with the median of three moved to `first` as the pivot P.  The
+// left scan stops at the positions L holding a value not greater than P
+// (ascending), the right scan at the positions R holding a value not less
+// than P (descending, then `first`).  The i-th left stop x swaps with the
+// i-th right stop while x lies below it, i.e. while at least i + 1 right
+// stops lie above x: m, the number of swaps, is the count of left stops
+// with that property.  The m pairs exchange their entries through LDS
+// (buf_l, buf_r: (n + 1) / 2 words each; dummy: one word per lane for
+// lanes without a partner, so every lane stores and loads unconditionally).
+// Returns the cut: L[0] (m = 0), min(L[m], R[m - 1]), or R[m - 1] once L is
+// used up.
 template <int S>
-__device__ __forceinline__ int wave_torch_topk_regs(const uint16_t* row, int n, int k, uint32_t* scratch, int out_lane_base,
-                                    int my_id) {
+__device__ __forceinline__ int wave_partition_round(uint32_t (&v)[S], int first, int last, uint32_t* buf_l,
+                                                    uint32_t* buf_r, uint32_t* dummy) {
   constexpr int kNone = 1 << 30;
   const int lane = threadIdx.x & 63;
-  const uint64_t below = (1ull << lane) - 1ull;
-  WaveRow<S> r;
+  // __move_median_to_first(first, first + 1, mid, last - 1)
+  const int pa = first + 1, pb = first + (last - first) / 2, pc = last - 1;
+  const uint32_t va = row_get(v, pa), vb = row_get(v, pb), vc = row_get(v, pc), vf = row_get(v, first);
+  int pick;
+  uint32_t vm;
+  if (entry_gt(va, vb)) {
+    if (entry_gt(vb, vc)) { pick = pb; vm = vb; }
+    else if (entry_gt(va, vc)) { pick = pc; vm = vc; }
+    else { pick = pa; vm = va; }
+  } else if (entry_gt(va, vc)) { pick = pa; vm = va; }
+  else if (entry_gt(vb, vc)) { pick = pc; vm = vc; }
+  else { pick = pb; vm = vb; }
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     const int p = s * kWave + lane;
-    r.v[s] = p < n ? order_entry(row[p], p) : 0u;
+    v[s] = p == first ? vm : (p == pick ? vf : v[s]);
+  }
+  const uint32_t pk = vm >> 16;
+  // the scans' stops: L (left, ascending), R (right, descending).  Per lane
+  // and slot: bl / br = left / right stops before the position, flags bit 0
+  // = a left stop, bit 1 = a right stop (VGPRs: lane masks of every slot
+  // kept live through the exchange would crowd the scalar registers)
+  int bl[S], br[S];
+  uint32_t flags[S];
+  int cl = 0, cr = 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int p = s * kWave + lane;
+    const bool in = p > first && p < last;
+    const uint32_t key = v[s] >> 16;
+    const bool is_l = in && key <= pk, is_r = in && key >= pk;
+    const uint64_t lmask = __builtin_amdgcn_ballot_w64(is_l);
+    const uint64_t rmask = __builtin_amdgcn_ballot_w64(is_r);
+    bl[s] = __builtin_amdgcn_mbcnt_hi((uint32_t)(lmask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)lmask, (uint32_t)cl));
+    br[s] = __builtin_amdgcn_mbcnt_hi((uint32_t)(rmask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)rmask, (uint32_t)cr));
+    flags[s] = (is_l ? 1u : 0u) | (is_r ? 2u : 0u);
+    cl += __popcll(lmask);
+    cr += __popcll(rmask);
+  }
+  // swap count: the i-th left stop x swaps while at least i + 1 right stops
+  // lie above x (cr - br - [x is a right stop] of them)
+  int m = 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int above = cr - br[s] - (int)(flags[s] >> 1);
+    m += __popcll(__builtin_amdgcn_ballot_w64((flags[s] & 1u) != 0u && above > bl[s]));
+  }
+  // exchange the m pairs' entries through LDS (every lane stores and loads;
+  // no branch): the i-th left stop's entry goes to buf_l[i], the i-th right
+  // stop's (counted from the top) to buf_r[i]
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int ir = cr - 1 - br[s];
+    const bool sl = (flags[s] & 1u) != 0u && bl[s] < m;
+    const bool sr = (flags[s] & 2u) != 0u && ir < m;
+    const int dum = (int)(dummy - buf_l) + lane;
+    buf_l[sl ? bl[s] : dum] = v[s];
+    buf_l[sr ? (int)(buf_r - buf_l) + ir : dum] = v[s];
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int ir = cr - 1 - br[s];
+    const bool sl = (flags[s] & 1u) != 0u && bl[s] < m;
+    const bool sr = (flags[s] & 2u) != 0u && ir < m;
+    // word offsets from buf_l (a select between LDS pointers put the row in scratch)
+    const int at = sl ? (int)(buf_r - buf_l) + bl[s] : (sr ? ir : (int)(dummy - buf_l) + lane);
+    const uint32_t x = buf_l[at];
+    v[s] = (sl || sr) ? x : v[s];
+  }
+  wave_lds_sync();
+  // where the left scan stopped: L[0] (m = 0), min(L[m], R[m - 1]), or R[m - 1] once L is used up
+  int lm = kNone, rm1 = kNone;
+#pragma unroll
+  for (int s = S - 1; s >= 0; --s) {
+    const uint64_t at_l = __builtin_amdgcn_ballot_w64((flags[s] & 1u) != 0u && bl[s] == m);
+    const uint64_t at_r = __builtin_amdgcn_ballot_w64(m > 0 && (flags[s] & 2u) != 0u && cr - 1 - br[s] == m - 1);
+    if (at_l) lm = s * kWave + __builtin_ctzll(at_l);
+    if (at_r) rm1 = s * kWave + __builtin_ctzll(at_r);
+  }
+  return min(lm, rm1);
+}
+
+// The register form of wave_torch_topk, for rows of n <= 64 * S entries in
+// the introselect regime (k * 64 > n) with k <= 16: position p of the row
+// lives in slot p / 64 of lane p % 64.  Each partition step is ballots and
+// prefix counts (wave_partition_round); once the range [first, last) lies
+// below position 64 (nth < 16 is always inside it) only slot 0 takes part.
+// After the loop every position involved is below 19, so the two insertion
+// sorts run as stable rank sorts of lanes of slot 0.  The rare depth-limit
+// branch (heap select) spills the row to LDS and finishes sequentially in
+// lane 0.  Returns, in lane out_lane_base + j (j < k), the expert of result
+// j; other lanes get my_id back.  scratch: topk_tie_scratch_bytes(n) bytes.
+template <int S>
+__device__ __forceinline__ int wave_torch_topk_regs(const uint16_t* row, int n, int k, uint32_t* scratch,
+                                                    int out_lane_base, int my_id) {
+  const int lane = threadIdx.x & 63;
+  uint32_t v[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int p = s * kWave + lane;
+    v[s] = p < n ? order_entry(row[p], p) : 0u;
   }
   uint32_t* buf_l = scratch;
   uint32_t* buf_r = scratch + (n + 1) / 2;
+  uint32_t* dummy = scratch + n;  // one word per lane for lanes without a partner
   const int nth = k - 1;
   int first = 0, last = n;
   int depth = floor_log2(n) * 2;
   bool spilled = false;
   while (last - first > 3) {
-    if (depth == 0) {  // __heap_select on the range, sequentially in lane 0 on an LDS copy
+    if (depth == 0) {
 #pragma unroll
       for (int s = 0; s < S; ++s)
-        if (s * kWave + lane < n) scratch[s * kWave + lane] = r.v[s];
+        if (s * kWave + lane < n) scratch[s * kWave + lane] = v[s];
       wave_lds_sync();
       if (lane == 0) {
         stl_heap_select(scratch, first, nth + 1, last);
@@ -440,66 +501,27 @@ __device__ __forceinline__ int wave_torch_topk_regs(const uint16_t* row, int n, 
       break;
     }
     --depth;
-    r.move_median_to_first(first, first + 1, first + (last - first) / 2, last - 1);
-    const uint32_t pk = r.get(first) >> 16;
-    int rank_l[S], rank_r[S];
-    bool fl[S], fr[S];
-    uint64_t bl[S], br[S];
-    int cl = 0, cr = 0;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const int p = s * kWave + lane;
-      const bool in = p > first && p < last;
-      const uint32_t key = r.v[s] >> 16;
-      fl[s] = in && key <= pk;  // the left scan stops here
-      fr[s] = in && key >= pk;  // the right scan stops here
-      bl[s] = __ballot(fl[s]);
-      br[s] = __ballot(fr[s]);
-      rank_l[s] = cl + __popcll(bl[s] & below);
-      rank_r[s] = cr + __popcll(br[s] & below);
-      cl += __popcll(bl[s]);
-      cr += __popcll(br[s]);
+    int cut;
+    if (S == 1 || last <= kWave) {
+      // the range lies in slot 0: the other slots hold positions >= last, which no longer move
+      uint32_t v0[1] = {v[0]};
+      cut = wave_partition_round<1>(v0, first, last, buf_l, buf_r, dummy);
+      v[0] = v0[0];
+    } else {
+      cut = wave_partition_round<S>(v, first, last, buf_l, buf_r, dummy);
     }
-    int mm = 0;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const int p = s * kWave + lane;
-      if (p > first && p < last) mm = max(mm, min(rank_l[s], cr - rank_r[s]));
-    }
-    const int m = (int)wave_max_u32((uint32_t)mm);
-    // exchange the m pairs' entries
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      if (fl[s] && rank_l[s] < m) buf_l[rank_l[s]] = r.v[s];
-      if (fr[s] && cr - 1 - rank_r[s] < m) buf_r[cr - 1 - rank_r[s]] = r.v[s];
-    }
-    wave_lds_sync();
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      if (fl[s] && rank_l[s] < m) r.v[s] = buf_r[rank_l[s]];
-      else if (fr[s] && cr - 1 - rank_r[s] < m) r.v[s] = buf_l[cr - 1 - rank_r[s]];
-    }
-    wave_lds_sync();
-    // where the left scan stopped: L[0], min(L[m], R[m - 1]) or R[m - 1]
-    int lm = kNone, rm1 = kNone;
-#pragma unroll
-    for (int s = S - 1; s >= 0; --s) {
-      const uint64_t at_l = __ballot(fl[s] && rank_l[s] == m);
-      const uint64_t at_r = __ballot(m > 0 && fr[s] && rank_r[s] == cr - m);
-      if (at_l) lm = s * kWave + __builtin_ctzll(at_l);
-      if (at_r) rm1 = s * kWave + __builtin_ctzll(at_r);
-    }
-    const int cut = min(lm, rm1);
     if (cut <= nth) first = cut;
     else last = cut;
   }
   if (!spilled) {
-    r.insertion_sort(first, last);
-    r.insertion_sort(0, k - 1);  // std::sort of k - 1 <= 16 entries
-    for (int j = 0; j < k; ++j) {
-      const int id = (int)(r.get(j) & 0xffffu);
-      if (lane == out_lane_base + j) my_id = id;
-    }
+    // std::__insertion_sort of [first, last), then std::sort of [0, k - 1) (<= 16 entries: insertion
+    // sort): both stable for equal keys.  nth < 16 lies in [first, last), so every position involved
+    // is below 19, in slot 0.
+    v[0] = lanes_stable_sort_desc(v[0], first, last, scratch, dummy);
+    v[0] = lanes_stable_sort_desc(v[0], 0, k - 1, scratch, dummy);
+    const int j = lane - out_lane_base;
+    const uint32_t id = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (j >= 0 && j < k ? j : 0), (int)(v[0] & 0xffffu));
+    if (j >= 0 && j < k) my_id = (int)id;
   } else {
     if (lane >= out_lane_base && lane < out_lane_base + k) my_id = (int)(scratch[lane - out_lane_base] & 0xffffu);
     wave_lds_sync();

@@ -108,3 +108,22 @@ def test_swap_count_from_prefix_counts():
         a = [sum(1 for x in L if x < q) for q in range(n + 1)]
         b = [sum(1 for x in R if x >= q) for q in range(n + 1)]
         assert max(min(a[q], b[q]) for q in range(first + 1, n + 1)) == m_lists
+
+
+def test_swap_count_from_right_stops_above():
+    """The kernel's form: the i-th left stop x (ascending) swaps while at least i + 1 right stops lie
+    strictly above x, so m is the number of left stops with that property (they form a prefix)."""
+    rng = np.random.default_rng(24)
+    for _ in range(4000):
+        n = int(rng.integers(4, 260))
+        vals = rng.integers(0, int(rng.integers(1, 12)), n)
+        p = vals[0]
+        pos = range(1, n)
+        L = [q for q in pos if not vals[q] > p]
+        R = [q for q in reversed(pos) if not p > vals[q]]
+        m_lists = 0
+        while m_lists < min(len(L), len(R)) and L[m_lists] < R[m_lists]:
+            m_lists += 1
+        flags = [sum(1 for y in R if y > x) >= i + 1 for i, x in enumerate(L)]
+        assert sum(flags) == m_lists
+        assert flags == sorted(flags, reverse=True)  # a prefix of L
