@@ -435,6 +435,7 @@ __device__ __forceinline__ int wave_partition_round(uint32_t (&v)[S], int first,
     buf_l[sr ? (int)(buf_r - buf_l) + ir : dum] = v[s];
   }
   wave_lds_sync();
+  uint32_t x[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     const int ir = cr - 1 - br[s];
@@ -442,11 +443,10 @@ __device__ __forceinline__ int wave_partition_round(uint32_t (&v)[S], int first,
     const bool sr = (flags[s] & 2u) != 0u && ir < m;
     // word offsets from buf_l (a select between LDS pointers put the row in scratch)
     const int at = sl ? (int)(buf_r - buf_l) + bl[s] : (sr ? ir : (int)(dummy - buf_l) + lane);
-    const uint32_t x = buf_l[at];
-    v[s] = (sl || sr) ? x : v[s];
+    x[s] = buf_l[at];
   }
-  wave_lds_sync();
-  // where the left scan stopped: L[0] (m = 0), min(L[m], R[m - 1]), or R[m - 1] once L is used up
+  // where the left scan stopped (while the loads are in flight): L[0]
+  // (m = 0), min(L[m], R[m - 1]), or R[m - 1] once L is used up
   int lm = kNone, rm1 = kNone;
 #pragma unroll
   for (int s = S - 1; s >= 0; --s) {
@@ -455,6 +455,13 @@ __device__ __forceinline__ int wave_partition_round(uint32_t (&v)[S], int first,
     if (at_l) lm = s * kWave + __builtin_ctzll(at_l);
     if (at_r) rm1 = s * kWave + __builtin_ctzll(at_r);
   }
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int ir = cr - 1 - br[s];
+    const bool swapped = ((flags[s] & 1u) != 0u && bl[s] < m) || ((flags[s] & 2u) != 0u && ir < m);
+    v[s] = swapped ? x[s] : v[s];
+  }
+  wave_lds_sync();
   return min(lm, rm1);
 }
 
