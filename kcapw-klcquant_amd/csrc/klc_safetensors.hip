@@ -523,9 +523,14 @@ extern "C" int klc_st_read_rows(void* handle, const char* name, int64_t first, i
 namespace klc {
 namespace {
 
-// Staging slots of at most this size: small enough that the first slot's
-// read is short and the PCIe copies, not the reads, set the pace.
+// Staging slots of the packing loads: small enough that the first slot's
+// read is short and the pack kernels over PCIe, not the reads, set the pace.
 constexpr int64_t kSlotBytes = 2 << 20;
+// Staging slots of the plain row copies.  A host-to-device copy moves
+// 45 GB/s in 2 MiB pieces against 53 GB/s in 8 MiB pieces (57 GB/s for one
+// 64 MiB copy) on MI355X over PCIe 5; the first chunk of a load is a quarter
+// slot, so its read stays short.
+constexpr int64_t kCopySlotBytes = 8 << 20;
 constexpr int kMaxSlots = 64;
 
 // Completion events of the staging slots, per calling thread and device:
@@ -653,8 +658,8 @@ int staged_copy(StFile* f, const RowCopy* copies, int n, void* staging, int64_t 
   if (total == 0) return KLC_OK;
   KLC_REQUIRE(staging != nullptr && staging_bytes >= 2 * 4096, KLC_ERR_ARGUMENT,
               "%s: staging of %lld bytes (at least 8 KiB, two slots)", fn, (long long)staging_bytes);
-  int slots = (int)std::min<int64_t>(kMaxSlots, std::max<int64_t>(2, staging_bytes / kSlotBytes));
-  const int64_t slot = std::min<int64_t>(kSlotBytes, staging_bytes / slots / 4096 * 4096);
+  int slots = (int)std::min<int64_t>(kMaxSlots, std::max<int64_t>(2, staging_bytes / kCopySlotBytes));
+  const int64_t slot = std::min<int64_t>(kCopySlotBytes, staging_bytes / slots / 4096 * 4096);
   // packs of earlier klc_st_load_mxfp4_packed calls may still read the staging
   hipError_t herr = rings_wait(staging, false);
   KLC_REQUIRE(herr == hipSuccess, KLC_ERR_HIP, "%s: %s", fn, hipGetErrorString(herr));

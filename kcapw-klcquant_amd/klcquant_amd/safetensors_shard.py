@@ -27,9 +27,9 @@ _DTYPES = {
     "F64": torch.float64, "I64": torch.int64, "U64": torch.uint64,
 }
 
-#: Pinned staging per thread: a ring of four 2 MiB slots, so reading later
+#: Pinned staging per thread: a ring of four 8 MiB slots, so reading later
 #: slots from the page cache overlaps the PCIe transfers of earlier ones.
-STAGING_BYTES = 8 << 20
+STAGING_BYTES = 32 << 20
 
 @functools.lru_cache(maxsize=64)
 def _packed_bytes(rows: int, groups: int) -> int:
