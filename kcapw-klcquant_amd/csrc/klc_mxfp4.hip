@@ -12,6 +12,7 @@
 // 255; the MX NaN scale 255 takes an integer path (mxfp4_f32_bits) that
 // reproduces the reference's +-inf / NaN.
 #include <algorithm>
+#include <type_traits>
 
 #include "klc_common.h"
 
@@ -34,6 +35,14 @@ __device__ __forceinline__ uint32_t to_out_bits(uint32_t f32bits) {
   } else {
     return f32bits;
   }
+}
+
+// Workgroup barrier that orders LDS accesses only: __syncthreads' release
+// fence would also wait for every outstanding global store.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -87,103 +96,156 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
   const uint8_t* mat = blocks;
   if constexpr (kPacked) mat = blocks + (int64_t)m * packed_stride;
 
-  // Each iteration moves 16 groups: all of a thread's loads are issued
-  // together, and the load -> LDS -> compute -> store round trip (whose waits
-  // cover the stores too: loads and stores share one counter) is paid once
-  // per 16 groups.
-  for (int g0 = 0; g0 < groups; g0 += kDqGroups) {
-    {
-      const int r = col0 + l_row;
-      uint4 v[4];
-      uint32_t e[4];
+  // ---- one iteration = 16 groups: loads into registers, staged in LDS,
+  // decoded 4 groups at a time and stored as 16-byte rows of [in, out] ----
+  const int r_ld = col0 + l_row;
+  uint4 v[4];
+  uint32_t e[4];
+  // kClamp: every load reads a valid chunk (groups past the end re-read the
+  // last one; their values are never stored), so no branch guards a load
+  auto load_chunks = [&](int g0, auto clamp) {
+    constexpr bool kClamp = decltype(clamp)::value;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int g = g0 + 4 * i + l_gi;
-        v[i] = make_uint4(0u, 0u, 0u, 0u);
-        e[i] = 127u;
-        if (r < rows && g < groups) {
-          if constexpr (kPacked) {
-            const uint8_t* src = mat + ((int64_t)(r / kTileRows) * groups + g) * 1024 + (r % kTileRows) * 16;
-            v[i] = *reinterpret_cast<const uint4*>(src);
-            e[i] = mat[packed_scale_offset(rows, groups, r, g)];
-          } else {
-            const int64_t chunk = ((int64_t)m * rows + r) * groups + g;
-            v[i] = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
-            e[i] = scales[chunk];
-          }
+    for (int i = 0; i < 4; ++i) {
+      int g = g0 + 4 * i + l_gi;
+      if constexpr (kClamp) g = min(g, groups - 1);
+      v[i] = make_uint4(0u, 0u, 0u, 0u);
+      e[i] = 127u;
+      if (kClamp || (r_ld < rows && g < groups)) {
+        if constexpr (kPacked) {
+          const uint8_t* src = mat + ((int64_t)(r_ld / kTileRows) * groups + g) * 1024 + (r_ld % kTileRows) * 16;
+          v[i] = *reinterpret_cast<const uint4*>(src);
+          e[i] = mat[packed_scale_offset(rows, groups, r_ld, g)];
+        } else {
+          const int64_t chunk = ((int64_t)m * rows + r_ld) * groups + g;
+          v[i] = *reinterpret_cast<const uint4*>(blocks + chunk * 16);
+          e[i] = scales[chunk];
         }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t* dst = s_blk + l_row * kLdsStride + (4 * i + l_gi) * 4;
-        dst[0] = v[i].x;
-        dst[1] = v[i].y;
-        dst[2] = v[i].z;
-        dst[3] = v[i].w;
-        s_scl[l_row * kSclStride + 4 * i + l_gi] = e[i];
       }
     }
-    __syncthreads();
-
-#pragma unroll 1
-    for (int sc = 0; sc < kDqGroups / 4; ++sc) {
-      const int gl = 4 * sc + c_gi;  // group within the iteration
-      if (g0 + gl >= groups) break;  // uniform per 8-lane group; no barrier inside
-      uint32_t bits[4][8];
+  };
+  auto stage = [&]() {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int lr = c_oc * 8 + j;
-        const uint32_t word = s_blk[lr * kLdsStride + gl * 4 + (c_q4 >> 1)];
-        const uint32_t v16 = (word >> ((c_q4 & 1) * 16)) & 0xffffu;
-        const uint32_t e = s_scl[lr * kSclStride + gl];
-        if (e != 255u) {
-          // hardware E2M1 x 2^(e-127) conversion, exact for e < 255 (e = 0:
-          // the float32 subnormal 2^-127 as scale)
-          const float scale = __uint_as_float(e == 0u ? 0x00400000u : (e << 23));
+    for (int i = 0; i < 4; ++i) {
+      uint32_t* dst = s_blk + l_row * kLdsStride + (4 * i + l_gi) * 4;
+      dst[0] = v[i].x;
+      dst[1] = v[i].y;
+      dst[2] = v[i].z;
+      dst[3] = v[i].w;
+      s_scl[l_row * kSclStride + 4 * i + l_gi] = e[i];
+    }
+  };
+  // 4 groups (sub-chunk sc) of the staged iteration: 4 input rows x 8 output
+  // columns per thread.  kFull: the strip's 64 columns and the 4 groups all
+  // exist and rows % 8 == 0, so every store is one unconditional 16-byte row.
+  auto compute = [&](int g0, int sc, auto full) {
+    constexpr bool kFull = decltype(full)::value;
+    const int gl = 4 * sc + c_gi;  // group within the iteration
+    uint32_t bits[4][8];
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {  // rows 2h and 2h + 1
-            if constexpr (kDtype == KLC_DTYPE_F32) {
-              const f32x2_t cv = cvt_pair_f32(v16, scale, h);
-              bits[2 * h][j] = __float_as_uint(cv.x);
-              bits[2 * h + 1][j] = __float_as_uint(cv.y);
-            } else {
-              const uint32_t pair = cvt_pair<kDtype>(v16, scale, h);
-              bits[2 * h][j] = pair & 0xffffu;
-              bits[2 * h + 1][j] = pair >> 16;
-            }
-          }
+    for (int j = 0; j < 8; ++j) {
+      const int lr = c_oc * 8 + j;
+      const uint32_t word = s_blk[lr * kLdsStride + gl * 4 + (c_q4 >> 1)];
+      const uint32_t v16 = (word >> ((c_q4 & 1) * 16)) & 0xffffu;
+      const uint32_t ee = s_scl[lr * kSclStride + gl];
+      // hardware E2M1 x 2^(e-127) conversion, exact for e < 255 (e = 0: the
+      // float32 subnormal 2^-127 as scale).  E8M0 255 (the MX NaN scale):
+      // the reference's fp32 ldexp gives +-inf, and NaN for the zero codes;
+      // that value is selected, not branched to, so the loop body has no
+      // branch (a branch made the compiler wait for every store at the
+      // next iteration's loads).
+      const bool nan_scale = ee == 255u;
+      const float scale = __uint_as_float(ee == 0u ? 0x00400000u : (ee << 23));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // rows 2h and 2h + 1
+        if constexpr (kDtype == KLC_DTYPE_F32) {
+          const f32x2_t cv = cvt_pair_f32(v16, scale, h);
+          bits[2 * h][j] = __float_as_uint(cv.x);
+          bits[2 * h + 1][j] = __float_as_uint(cv.y);
         } else {
-          // E8M0 255 (the MX NaN scale): the reference's fp32 ldexp gives +-inf,
-          // and NaN for the zero codes
-#pragma unroll
-          for (int r = 0; r < 4; ++r) bits[r][j] = to_out_bits<kDtype>(mxfp4_f32_bits((v16 >> (4 * r)) & 0xfu, e));
+          const uint32_t pair = cvt_pair<kDtype>(v16, scale, h);
+          bits[2 * h][j] = pair & 0xffffu;
+          bits[2 * h + 1][j] = pair >> 16;
         }
       }
-      const int i0 = (g0 + gl) * 32 + c_q4 * 4;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row_off = ((int64_t)m * in_dim + i0 + r) * rows;
-        if constexpr (kDtype == KLC_DTYPE_F32) {
-          float* o = static_cast<float*>(out) + row_off + col;
-          if (col + 8 <= rows && (rows & 3) == 0) {
-            reinterpret_cast<uint4*>(o)[0] = make_uint4(bits[r][0], bits[r][1], bits[r][2], bits[r][3]);
-            reinterpret_cast<uint4*>(o)[1] = make_uint4(bits[r][4], bits[r][5], bits[r][6], bits[r][7]);
-          } else {
-            for (int j = 0; j < 8; ++j)
-              if (col + j < rows) o[j] = __uint_as_float(bits[r][j]);
-          }
+        const uint32_t nan_bits = to_out_bits<kDtype>(mxfp4_f32_bits((v16 >> (4 * r)) & 0xfu, 255u));
+        bits[r][j] = nan_scale ? nan_bits : bits[r][j];
+      }
+    }
+    const int i0 = (g0 + gl) * 32 + c_q4 * 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row_off = ((int64_t)m * in_dim + i0 + r) * rows;
+      if constexpr (kDtype == KLC_DTYPE_F32) {
+        float* o = static_cast<float*>(out) + row_off + col;
+        if (kFull || (col + 8 <= rows && (rows & 3) == 0)) {
+          reinterpret_cast<uint4*>(o)[0] = make_uint4(bits[r][0], bits[r][1], bits[r][2], bits[r][3]);
+          reinterpret_cast<uint4*>(o)[1] = make_uint4(bits[r][4], bits[r][5], bits[r][6], bits[r][7]);
         } else {
-          uint16_t* o = static_cast<uint16_t*>(out) + row_off + col;
-          if (col + 8 <= rows && (rows & 7) == 0) {
-            *reinterpret_cast<uint4*>(o) =
-                make_uint4(bits[r][0] | (bits[r][1] << 16), bits[r][2] | (bits[r][3] << 16),
-                           bits[r][4] | (bits[r][5] << 16), bits[r][6] | (bits[r][7] << 16));
-          } else {
-            for (int j = 0; j < 8; ++j)
-              if (col + j < rows) o[j] = (uint16_t)bits[r][j];
-          }
+          for (int j = 0; j < 8; ++j)
+            if (col + j < rows) o[j] = __uint_as_float(bits[r][j]);
+        }
+      } else {
+        uint16_t* o = static_cast<uint16_t*>(out) + row_off + col;
+        if (kFull || (col + 8 <= rows && (rows & 7) == 0)) {
+          *reinterpret_cast<uint4*>(o) =
+              make_uint4(bits[r][0] | (bits[r][1] << 16), bits[r][2] | (bits[r][3] << 16),
+                         bits[r][4] | (bits[r][5] << 16), bits[r][6] | (bits[r][7] << 16));
+        } else {
+          for (int j = 0; j < 8; ++j)
+            if (col + j < rows) o[j] = (uint16_t)bits[r][j];
         }
       }
+    }
+  };
+
+  int g0 = 0;
+  if (col0 + kDqCols <= rows && (rows & 7) == 0 && groups >= kDqGroups) {
+    // Full iterations of a full strip, in straight-line code: the next
+    // iteration's loads are issued before this iteration's stores.  Loads and
+    // stores share one completion counter and retire in order, so waiting
+    // for those loads leaves the stores in flight; the LDS-only barriers do
+    // not wait for them either.
+    // The first iteration is peeled, so the loop is entered, like its back
+    // edge, with one iteration's loads and then its stores outstanding (a
+    // loop entered with only loads outstanding gets one wait for all).
+    const int full = groups / kDqGroups * kDqGroups;
+    auto iteration = [&](int g) {
+      stage();
+      lds_barrier();
+      load_chunks(g + kDqGroups < groups ? g + kDqGroups : g, std::true_type{});
+#pragma unroll
+      for (int sc = 0; sc < kDqGroups / 4; ++sc) compute(g, sc, std::true_type{});
+    };
+    load_chunks(0, std::true_type{});
+    iteration(0);
+    for (g0 = kDqGroups; g0 < full; g0 += kDqGroups) {
+      lds_barrier();  // every thread is done reading the staged chunks
+      iteration(g0);
+    }
+    if (g0 < groups) {  // the tail iteration's chunks are already loaded
+      lds_barrier();
+      stage();
+      lds_barrier();
+#pragma unroll 1
+      for (int sc = 0; sc < kDqGroups / 4; ++sc) {
+        if (g0 + 4 * sc + c_gi >= groups) break;  // uniform per 8-lane group; no barrier inside
+        compute(g0, sc, std::false_type{});
+      }
+    }
+    return;
+  }
+  // Partial strips: one iteration at a time.
+  for (; g0 < groups; g0 += kDqGroups) {
+    load_chunks(g0, std::false_type{});
+    stage();
+    __syncthreads();
+#pragma unroll 1
+    for (int sc = 0; sc < kDqGroups / 4; ++sc) {
+      if (g0 + 4 * sc + c_gi >= groups) break;  // uniform per 8-lane group; no barrier inside
+      compute(g0, sc, std::false_type{});
     }
     __syncthreads();
   }
