@@ -1072,6 +1072,45 @@ constexpr int kAgentScope = 16;
 // counters: [n_tt] token-tile counters and 1 final counter, zero before the
 // first launch and left zero by every launch.  partials: [n_tt][n_et]
 // [gridDim.z][256] float64.
+// The dispatch (block_dispatch's outputs) of one token's k pairs, by one
+// wave: the experts tile_ids[0 .. k) are distinct (a top-k), so pair j's
+// position among the expert-sorted pairs is the number of its experts below
+// its own, every expert has at most one pair, and each list's r-th unit is
+// pass 0 of the r-th expert in ascending order.
+__device__ __forceinline__ void single_token_dispatch(const int32_t* tile_ids, int n_exp, int k,
+                                                      int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
+                                                      int32_t* __restrict__ active, int32_t* __restrict__ n_active,
+                                                      int32_t* __restrict__ units) {
+  const int lane = threadIdx.x & 63;
+  const int n_pairs = k;
+  const int my = lane < k ? tile_ids[lane] : 0x7fffffff;
+  int rank = 0;
+  for (int i = 0; i < k; ++i) rank += __builtin_amdgcn_readlane(my, i) < my ? 1 : 0;
+  int32_t* const gu_list = units + kUnitHeader;
+  int32_t* const dn_list = units + units_offset_down(n_pairs, n_exp);
+  int32_t* const gm_list = units + units_offset_gemm(n_pairs, n_exp);
+  if (lane < k) {
+    sorted[rank] = lane;
+    active[rank] = my;
+    gu_list[rank] = make_unit(my, 0);
+    dn_list[rank] = make_unit(my, 0);
+    gm_list[rank] = make_unit(my, 0);
+  }
+  for (int e = lane; e <= n_exp; e += kWave) {
+    int c = 0;
+    for (int i = 0; i < k; ++i) c += __builtin_amdgcn_readlane(my, i) < e ? 1 : 0;
+    offsets[e] = c;
+  }
+  for (int e = k + lane; e < n_exp; e += kWave) active[e] = -1;
+  if (lane == 0) {
+    *n_active = k;
+    units[0] = k;
+    units[1] = k;
+    units[2] = k;
+    units[3] = 0;
+  }
+}
+
 __global__ __launch_bounds__(256) void router_decode_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b, uint16_t* logits,
     int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
@@ -1152,6 +1191,17 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     }
   }
   lds_barrier();  // the rows are in LDS; the logits' global stores need not have completed
+  if (n_tok == 1 && n_exp <= 4 * kWave) {
+    // One token: its k experts are distinct, so the dispatch reduces to
+    // ranking them; one wave does the top-k and the whole dispatch with no
+    // workgroup barrier (the block form below pays one per step).
+    if (wave != 0) return;
+    uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp));
+    topk_softmax_row(rows, n_exp, k, 0, ids, values, weights, tile_ids, tie_scratch);
+    wave_lds_sync();
+    single_token_dispatch(tile_ids, n_exp, k, offsets, sorted, active, n_active, units);
+    return;
+  }
   {
     // each wave's tie scratch follows the 16 logits rows
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp) +
