@@ -1072,6 +1072,70 @@ constexpr int kAgentScope = 16;
 // counters: [n_tt] token-tile counters and 1 final counter, zero before the
 // first launch and left zero by every launch.  partials: [n_tt][n_et]
 // [gridDim.z][256] float64.
+// block_dispatch's outputs for at most 64 pairs (one token tile), by one
+// wave: pair p sits in lane p; its rank among the earlier pairs of its
+// expert comes from the key ballots (wave_peers), the per-expert counts from
+// LDS atomics, and the offsets, active-list positions and the three lists'
+// first units from five scans of the wave, with no workgroup barrier.
+// ids: the pairs' experts in LDS; lds: 5 * 256 + 8 ints.
+__device__ __forceinline__ void wave_dispatch(const int32_t* ids, int n_pairs, int n_exp,
+                                              int32_t* __restrict__ offsets, int32_t* __restrict__ sorted,
+                                              int32_t* __restrict__ active, int32_t* __restrict__ n_active,
+                                              int32_t* __restrict__ units, int32_t* lds) {
+  const int lane = threadIdx.x & 63;
+  int32_t* cnt = lds;                          // counts, then offsets
+  int32_t* flags = cnt + kDispatchMaxExperts;  // expert has pairs, then its active-list position
+  int32_t* ugu = flags + kDispatchMaxExperts;  // units per expert, then the first one (gate_up)
+  int32_t* udn = ugu + kDispatchMaxExperts;    // same for down
+  int32_t* ugm = udn + kDispatchMaxExperts;    // same for the GEMM
+  int32_t* sums = ugm + kDispatchMaxExperts;
+  const int id = lane < n_pairs ? ids[lane] : -1;
+  const bool valid = id >= 0 && id < n_exp;
+  uint32_t key[1] = {valid ? (uint32_t)id : 511u};
+  uint64_t peers[1];
+  wave_peers(key, peers);
+  const int rank = __popcll(peers[0] & ((1ull << lane) - 1ull));
+  for (int e = lane; e < n_exp; e += kWave) cnt[e] = 0;
+  wave_lds_sync();
+  if (valid) atomicAdd(&cnt[id], 1);
+  wave_lds_sync();
+  for (int e = lane; e < n_exp; e += kWave) {
+    const int32_t c = cnt[e];
+    flags[e] = c > 0 ? 1 : 0;
+    ugu[e] = (c + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
+    udn[e] = (c + kUnitTokensDown - 1) / kUnitTokensDown;
+    ugm[e] = (c + kUnitTokensGemm - 1) / kUnitTokensGemm;
+  }
+  wave_lds_sync();
+  wave_exclusive_scan_256(cnt, n_exp, &sums[0], lane);
+  wave_exclusive_scan_256(flags, n_exp, &sums[1], lane);
+  wave_exclusive_scan_256(ugu, n_exp, &sums[2], lane);
+  wave_exclusive_scan_256(udn, n_exp, &sums[3], lane);
+  wave_exclusive_scan_256(ugm, n_exp, &sums[4], lane);
+  wave_lds_sync();
+  if (valid) sorted[cnt[id] + rank] = lane;
+  int32_t* const gu_list = units + kUnitHeader;
+  int32_t* const dn_list = units + units_offset_down(n_pairs, n_exp);
+  int32_t* const gm_list = units + units_offset_gemm(n_pairs, n_exp);
+  for (int e = lane; e < n_exp; e += kWave) {
+    const int c = (e + 1 < n_exp ? cnt[e + 1] : sums[0]) - cnt[e];
+    offsets[e] = cnt[e];
+    if (c > 0) active[flags[e]] = e;
+    if (e >= sums[1]) active[e] = -1;
+    for (int j = 0; j * kUnitTokensGateUp < c; ++j) gu_list[ugu[e] + j] = make_unit(e, j);
+    for (int j = 0; j * kUnitTokensDown < c; ++j) dn_list[udn[e] + j] = make_unit(e, j);
+    for (int j = 0; j * kUnitTokensGemm < c; ++j) gm_list[ugm[e] + j] = make_unit(e, j);
+  }
+  if (lane == 0) {
+    offsets[n_exp] = sums[0];
+    *n_active = sums[1];
+    units[0] = sums[2];
+    units[1] = sums[3];
+    units[2] = sums[4];
+    units[3] = 0;
+  }
+}
+
 // The dispatch (block_dispatch's outputs) of one token's k pairs, by one
 // wave: the experts tile_ids[0 .. k) are distinct (a top-k), so pair j's
 // position among the expert-sorted pairs is the number of its experts below
@@ -1213,6 +1277,12 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;
     block_dispatch([&](int p) { return __hip_atomic_load(ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },
                    n_tok * k, n_exp, offsets, sorted, active, n_active, units, lds);
+  } else if (n_tok * k <= kWave && n_exp <= kDispatchMaxExperts) {
+    // one token tile of at most 64 pairs: one wave dispatches from the ids in LDS
+    lds_barrier();  // every wave is done with the logits rows, whose LDS the dispatch reuses
+    if (wave != 0) return;
+    wave_dispatch(tile_ids, n_tok * k, n_exp, offsets, sorted, active, n_active, units,
+                  reinterpret_cast<int32_t*>(lds));
   } else {
     // one token tile: its ids are still in LDS
     lds_barrier();
