@@ -120,11 +120,15 @@ def layer_bytes(unique_experts: int, n_tok: int) -> int:
     return weights + biases + router + acts
 
 
-def kernel_breakdown(interval_us, n_tok: int) -> dict:
-    """Per-kernel times from the library's KLC_LAYER_EVENTS events.  Batches of up to 128 tokens run
-    router, top-k and dispatch as one launch (router_decode_kernel), so their events 1 and 2 follow
-    it back to back: those two intervals measure only the event records and are reported apart."""
+def kernel_breakdown(interval_us, n_tok: int, path: str) -> dict:
+    """Per-kernel times from the library's KLC_LAYER_EVENTS events.  A batch that runs as one launch
+    (path "fused", up to 16 tokens) records the first event before it and the other six after it.
+    Batches of up to 128 tokens run router, top-k and dispatch as one launch (router_decode_kernel),
+    so their events 1 and 2 follow it back to back.  Intervals between back-to-back events measure
+    only the event records and are reported apart."""
     us = [round(float(v), 3) for v in interval_us]
+    if path == "fused":
+        return {"fused_layer": us[0], "event_records_only": round(sum(us[1:]), 3)}
     if n_tok <= 128:
         return {"router_topk_dispatch": us[0], "gate_up": us[3], "down": us[4], "combine": us[5],
                 "event_records_only": round(us[1] + us[2], 3)}
@@ -731,6 +735,7 @@ def main() -> int:
         ms_step = dt * 1e3 / args.steps
         bytes_total = float(sum(layer_bytes(int(u), n_tok) for u in uniq))
         gu_bytes = float(sum(gate_up_bytes(int(u), n_tok) for u in uniq))
+        path = layers[0].layer_path(n_tok)
         gu_ms = float(kern_ms[:, 3].sum())
         rec = {
             "batch": n_tok,
@@ -740,8 +745,10 @@ def main() -> int:
             "unique_experts_mean": round(float(uniq.mean()), 2),
             "layer_hbm_gbps": round(bytes_total / (dt * 1e9 / 1.0) / 1.0, 1),
             "layer_frac_of_peak": round(bytes_total / dt / 1e9 / HBM_PEAK_GBPS, 4),
-            "kernel_us_mean": kernel_breakdown(kern_ms.mean(axis=0) * 1e3, n_tok),
-            "gate_up_gbps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+            "layer_path": path,
+            "kernel_us_mean": kernel_breakdown(kern_ms.mean(axis=0) * 1e3, n_tok, path),
+            # the one-launch layer has no separate gate_up kernel to time
+            "gate_up_gbps": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1) if path != "fused" else None,
             "gate_up_bytes_per_launch": round(gu_bytes / args.steps),
             "hip_graph": graphs is not None,
         }
@@ -782,7 +789,7 @@ def main() -> int:
             "achieved": gu_achieved,
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(gu_achieved / HBM_PEAK_GBPS, 4),
+            "frac": round(gu_achieved / HBM_PEAK_GBPS, 4) if gu_achieved is not None else None,
             "traffic": measured_traffic() if head["batch"] == 64 and args.precision == "fp32" else None,
             "algorithmic_bytes_per_launch": round(head["gate_up_bytes_per_launch"]),
         },

@@ -213,14 +213,33 @@ int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter,
  * residual); ids/weights (optional, may be NULL) receive the routing.  workspace must be 256-byte aligned, hold
  * klc_moe_workspace_bytes() bytes and be zero-filled before its first use.  events: optional host array of
  * KLC_LAYER_EVENTS hipEvent_t handles recorded on `stream` before each of the
- * six kernels and after the last (NULL: no events). */
+ * six kernels and after the last (NULL: no events); the one-launch path
+ * records the first before its launch and the other six after it. */
 #define KLC_LAYER_EVENTS 7
-/* Expert path of klc_moe_layer: AUTO picks the grouped GEMM once the batch
+/* Expert path of klc_moe_layer.  AUTO picks the grouped GEMM once the batch
  * gives experts 8 or more tokens on average (n_tokens * k >= 8 * n_experts),
- * the decode GEMVs below that. */
+ * the decode GEMVs below that.  GEMV and GEMM force that expert path.  FUSED
+ * runs the whole layer as one launch: batches of at most 16 tokens (at most
+ * 64 token-slot pairs, 256 experts, k <= 16), 8-byte aligned out/residual,
+ * and a stream that is not capturing a graph; other calls fail with
+ * KLC_ERR_UNSUPPORTED.  It gives the same bits as GEMV. */
 #define KLC_PATH_AUTO 0
 #define KLC_PATH_GEMV 1
 #define KLC_PATH_GEMM 2
+#define KLC_PATH_FUSED 3
+/* The path (KLC_PATH_GEMV, _GEMM or _FUSED) klc_moe_layer takes for these
+ * sizes and `path` on `stream` with 8-byte aligned out/residual, or a
+ * negative status.  No counterpart in the reference: it lets callers label
+ * per-kernel timings (the one-launch layer records its events back to back). */
+int klc_moe_layer_path(int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, int path,
+                       void* stream);
+/* Byte offset, inside a klc_moe_layer workspace for these sizes, of the
+ * one-launch layer's uint32 status word (-1 when the batch never runs as one
+ * launch).  The word starts zero and keeps bit 0 set once a wait of some
+ * launch ran out (which needs compute units held by other work for the whole
+ * wait: the launch then completes with undefined outputs).  No counterpart
+ * in the reference: a diagnostic for tests and monitoring. */
+int64_t klc_moe_layer_status_offset(int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k);
 int klc_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
                   const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,

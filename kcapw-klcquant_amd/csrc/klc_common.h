@@ -166,6 +166,11 @@ constexpr uint32_t kOutOfRange = 0x40000000u;
 // non-temporal hint (gfx950 cache-policy bit 1).  Streaming reads of expert
 // weights reach about 7.1 TB/s with it against about 6.2 TB/s without.
 constexpr int kStreamPolicy = 2;
+// Cache policy of raw buffer stores and loads that hand data to workgroups
+// on other XCDs within one launch (gfx950 cache-policy bit sc1, agent
+// scope): stores write through the XCD's L2, loads miss in the caches that
+// are not coherent across XCDs.
+constexpr int kAgentScope = 16;
 
 // Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
 __device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {

@@ -18,6 +18,7 @@
 #include <mutex>
 
 #include "klc_common.h"
+#include "klc_gemv.h"
 
 namespace klc {
 
@@ -43,48 +44,17 @@ int launch_gemm_down(const void* const* w, const void* bias, const void* gated_s
                      int precision, float* eo, hipStream_t stream);
 int check_topk_args(int64_t n_tok, int64_t n_exp, int64_t k);
 int check_dispatch_args(int64_t n_pairs, int64_t n_exp);
+bool fused_decode_supported(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k, const void* out,
+                            const void* residual);
+int64_t fused_decode_scratch_bytes(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k);
+int64_t fused_decode_status_offset(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k);
+int launch_moe_decode_fused(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                            const void* gate_up_bias, const void* const* w_down, const void* down_bias,
+                            int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k, float limit,
+                            int precision, char* fused_ws, void* logits, int32_t* ids, float* values, void* weights,
+                            void* gated, float* eo, void* out, const void* residual, hipStream_t stream);
 
 namespace {
-
-constexpr int kGemvWaves = 4;                 // 4 x 16 rows = one 64-row tile per workgroup
-constexpr int kGemvThreads = kGemvWaves * kWave;
-constexpr int kVRows = 8;                     // activation rows (MFMA N columns) staged per unit
-constexpr int kMaxSteps = 24;                 // 4-group steps per row (inputs <= 3072)
-
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-
-__device__ __forceinline__ float swiglu(float gate, float up, float limit) {
-  // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp
-  gate = gate > limit ? limit : gate;
-  up = up > limit ? limit : (up < -limit ? -limit : up);
-  const float glu = gate * (1.0f / (1.0f + expf(-(gate * 1.702f))));
-  return (up + 1.0f) * glu;
-}
-
-// Expert GEMV on MFMA.  A workgroup streams `tpw` consecutive 64-row tiles of
-// one active expert; wave w owns rows [16w, 16w + 16) of each tile over the
-// whole input dimension.  Per 4-group step a lane holds the 16 code bytes of
-// (row l % 16, group 4s + l/16) -- the A operand of four
-// v_mfma_f32_16x16x32_bf16 (k = 8 * (l/16) + i) once decoded -- and reads the
-// matching B operand from activation rows staged once in LDS as bfloat16.
-//
-// Weight chunks stream through a ring of kRing registers: step s's slot is
-// refilled with the chunk kRing steps ahead (in this tile or the next) right
-// after it is consumed, so every wave keeps kRing KiB of HBM reads in flight
-// across tile boundaries.  kSteps is a template constant and every load is
-// unconditional straight-line code, which lets the compiler wait for exactly
-// one chunk per step (vector loads retire in order).  Past the last tile the
-// refills are out-of-range buffer loads (they return 0 and touch no memory).
-// The activation-row loads are issued before the ring prologue, so waiting
-// for them (the oldest loads) does not wait for any weight chunk.
-//
-// Columns are up to kVRows activation rows.  gate_up stages one row per token
-// (the bfloat16 hidden state, exact).  down stages two rows per token, the hi
-// and lo bfloat16 planes written by gate_up (hi = bf16(y), lo = bf16(y - hi)),
-// so the float32 SwiGLU output enters the product with a 2^-17 residual.  A
-// unit therefore holds 4 tokens in down and 8 in gate_up.
-constexpr int kRing = 8;  // every compiled kSteps >= kRing is a multiple of it (slot s % kRing is step s of any tile)
 
 template <bool kDown, int kSteps>
 __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
@@ -116,246 +86,10 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gemv_mfma_kernel(
   const int tok_per_pass = kDown ? kUnitTokensDown : kUnitTokensGateUp;
   const int tc = unit_pass(unit) * tok_per_pass;  // first token of this unit
   const int nt = min(tok_per_pass, pe - pb - tc);
-  const int in_dim = groups * 32;
-  const int cpr = groups * 4;                   // 16-byte activation chunks per row
-  const int row_stride = kSteps * 128 + 8;      // bf16 elements per staged row (zero padded)
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int lr = lane & 15;                     // row within the wave's 16 (A) / column n (B, D)
-  const int lq = lane >> 4;                     // k-quarter: groups 4s + lq
-  constexpr int kLoads = (kVRows * kSteps * 16 + kGemvThreads - 1) / kGemvThreads;  // staging chunks per thread
-  constexpr int kR = kRing < kSteps ? kRing : kSteps;
-  static_assert(kSteps % kR == 0, "the ring must divide the step count");
-  static_assert(kUnitTokensGateUp <= kVRows && 2 * kUnitTokensDown <= kVRows, "a unit's rows fit one pass");
-  const int trow = wave * 16 + lr;              // row inside a 64-row tile
-  const int rec = ((groups + 3) / 4 + 7) / 8 * 8;
-  const uint32_t tile_bytes = (uint32_t)groups * 1024u;
-  // the expert matrix as a buffer: weight chunks and scale records are read
-  // with a per-lane VGPR offset and a uniform (SGPR) step offset
-  const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)wmat, (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
-  // chunk of step t in a tile = tile offset + 4096 t + voff.  kSteps is a
-  // multiple of the ring size and may exceed the real step count g4: lanes
-  // whose group 4t + lq is past the last group read out of range (0, no
-  // memory traffic) and decode with scale 0.
-  const int g4 = (groups + 3) >> 2;
-  const uint32_t voff = (uint32_t)(lq * 1024 + trow * 16);
-  const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;  // step g4 - 1
-  auto chunk = [&](uint32_t tile_off, int t, bool valid) -> u32x4_t {
-    const uint32_t v = !valid || t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
-    return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, kStreamPolicy);
-  };
-  const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
-
-  {
-    const int nrows = kDown ? 2 * nt : nt;
-
-    // ---- 1. the unit's pairs: one vector load, issued before the weight
-    //      stream so that waiting for it does not wait for any weight chunk.
-    //      Lane r < kVRows holds staged row r's pair; the lane's output pair
-    //      (the same for every tile) comes in the same round trip. ----
-    const int rr_l = min(lane & (kVRows - 1), nrows - 1);
-    const int pair_l = pairs[pb + tc + (kDown ? rr_l >> 1 : rr_l)];
-    const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
-    const int out_pair = pairs[pb + tc + min(out_col, nt - 1)];
-
-    // ---- 2. scale record of the first tile, the first tile's bias, then the
-    //      ring prologue ----
-    // the lane's scales of a tile: 8-byte word i holds steps 8i .. 8i + 7 of
-    // (row, quarter); a wave's load of word i is 512 contiguous bytes
-    constexpr int kRecWords = (kSteps + 7) / 8 * 2;
-    auto load_rec = [&](int tile, uint32_t* dst) {
-#pragma unroll
-      for (int i = 0; i < kRecWords / 2; ++i) {
-        const uint32_t off = (uint32_t)packed_scale_word(groups, tile * kTileRows + trow, min(i, rec / 8 - 1), lq);
-        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, off, scale_base, kStreamPolicy);
-        dst[2 * i] = v.x;
-        dst[2 * i + 1] = v.y;
-      }
-    };
-    // Epilogue operands are loaded ahead too: the bias of the lane's 4 rows
-    // one tile ahead, next to the scale record.  A load issued in the
-    // epilogue itself would be the youngest in flight, and waiting for it
-    // would drain the weight ring.
-    auto load_bias = [&](int tile) -> u32x2_t {
-      const int64_t row = (int64_t)e * rows + tile * kTileRows + wave * 16 + 4 * lq;
-      return *reinterpret_cast<const u32x2_t*>(bias + row);
-    };
-    uint32_t sc[kRecWords], sc_next[kRecWords];
-    load_rec(tile0, sc);
-    u32x2_t bias_cur = load_bias(tile0), bias_next = bias_cur;
-    uint32_t tb = (uint32_t)tile0 * tile_bytes;
-    u32x4_t ring[kR];
-    __builtin_amdgcn_sched_barrier(0);  // the ring goes out before the rows' loads
-#pragma unroll
-    for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- 3. activation-row loads (row sources read back from the pairs) ----
-    int src[kVRows];
-    {
-      const int src_l = kDown ? pair_l : pair_l / k_top;
-#pragma unroll
-      for (int r = 0; r < kVRows; ++r) src[r] = __builtin_amdgcn_readlane(src_l, r);
-    }
-    u32x4_t xv[kLoads];
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int id = min((int)threadIdx.x + i * kGemvThreads, nrows * cpr - 1);
-      const int r = id / cpr;
-      const int c = id - r * cpr;
-      int srow = src[0];
-#pragma unroll
-      for (int q = 1; q < kVRows; ++q) srow = r == q ? src[q] : srow;
-      const uint16_t* p = act + (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim + c * 8;
-      xv[i] = *reinterpret_cast<const u32x4_t*>(p);
-    }
-
-    // ---- 4. activation rows into LDS ----
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int id = (int)threadIdx.x + i * kGemvThreads;
-      const int r = id / cpr;
-      const int c = id - r * cpr;
-      // ids past the staged rows land in row 0's spare 16-byte slot, which nothing reads
-      const int dst = id < nrows * cpr ? r * row_stride + c * 8 : row_stride - 8;
-      *reinterpret_cast<u32x4_t*>(xs + dst) = xv[i];
-    }
-    {
-      const int pad = kSteps * 128 - in_dim;  // zero: its A operand is zero, keep 0 * pad finite
-      for (int i = threadIdx.x; i < nrows * pad; i += kGemvThreads) {
-        const int r = i / pad;
-        xs[r * row_stride + in_dim + (i - r * pad)] = 0;
-      }
-    }
-    __syncthreads();
-
-    // B operand rows: column n = lr reads staged row min(n, kVRows - 1) without
-    // masking; columns past the live rows produce outputs nobody stores (an
-    // MFMA output column depends only on its own B column)
-    const uint16_t* xrow = xs + min(lr, kVRows - 1) * row_stride + lq * 32;
-    for (int ti = 0; ti < ntile; ++ti) {
-      const int tile = tile0 + ti;
-      // refills past this tile read the next one; past the last tile they read
-      // out of range (0, no memory traffic) at a valid tile offset
-      const bool has_next = ti + 1 < ntile;
-      const uint32_t nb = has_next ? tb + tile_bytes : tb;
-      // the next tile's scale record is issued before the first refill that
-      // reads the next tile, so waiting for it never waits for a ring load
-      const int next_tile = has_next ? tile + 1 : tile;
-      if constexpr (kSteps <= kR) {
-        load_rec(next_tile, sc_next);
-        bias_next = load_bias(next_tile);
-      }
-
-      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      // B operands are read one step ahead of their MFMAs (LDS latency)
-      bf16x8_t bcur[4], bnext[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bcur[j] = *reinterpret_cast<const bf16x8_t*>(xrow + j * 8);
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        __builtin_amdgcn_sched_barrier(0);  // keep each step's decode next to its MFMAs
-        if constexpr (kSteps > kR) {
-          if (s == kSteps - kR) {
-            load_rec(next_tile, sc_next);
-            bias_next = load_bias(next_tile);
-          }
-        }
-        // an empty asm "modifying" the chunk pins each step's decode right
-        // here, so decoded operands (16 registers per step) are never
-        // computed early and kept live across steps
-        asm volatile("" : "+v"(ring[s % kR]));
-        const u32x4_t w = ring[s % kR];
-        {
-          const int t = s + kR;  // refill: kR steps ahead
-          ring[s % kR] = t < kSteps ? chunk(tb, t, true) : chunk(nb, t - kSteps, has_next);
-        }
-        if (s + 1 < kSteps) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            bnext[j] = *reinterpret_cast<const bf16x8_t*>(xrow + (s + 1) * 128 + j * 8);
-        }
-        // 2^(e-127) as float32 bits (e = 0: the subnormal 2^-127; e = 255: inf,
-        // which the conversion reads as the MX NaN scale); a lane past the
-        // last group uses scale 0 (finite E2M1 values times 0 are +-0)
-        const uint32_t eb = (sc[s >> 2] >> (8 * (s & 3))) & 0xffu;
-        uint32_t sbits = eb == 0u ? 0x00400000u : (eb << 23);
-        sbits = 4 * s + lq < groups ? sbits : 0u;
-        const float scale = __uint_as_float(sbits);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8_t a = decode8(w[j], scale);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bcur[j], acc, 0, 0, 0);
-        }
-        if (s + 1 < kSteps) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) bcur[j] = bnext[j];
-        }
-      }
-      tb = nb;
-#pragma unroll
-      for (int i = 0; i < kRecWords; ++i) sc[i] = sc_next[i];
-      // bias of rows row0 .. row0 + 3 as bfloat16 bits, low half first
-      const float bias_row[4] = {bf16_to_f32(bias_cur.x & 0xffffu), bf16_to_f32(bias_cur.x >> 16),
-                                 bf16_to_f32(bias_cur.y & 0xffffu), bf16_to_f32(bias_cur.y >> 16)};
-      bias_cur = bias_next;
-
-      // ---- epilogue: lane holds rows 4*lq + v (v = 0..3) of the wave's 16, column lr ----
-      const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
-      float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-      if constexpr (!kDown) {
-        if (lr < nt) {
-          const int pair = out_pair;
-          const int half = rows >> 1;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            float gate = v[2 * h], up = v[2 * h + 1];
-            if (precision == KLC_PRECISION_BF16) {
-              gate = round_bf16(gate);
-              up = round_bf16(up);
-            }
-            gate += bias_row[2 * h];
-            up += bias_row[2 * h + 1];
-            const float y = swiglu(gate, up, limit);
-            const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
-            if (out_raw) out_raw[idx] = y;
-            // down input: hi/lo bfloat16 planes (lo = 0 when the reference rounds to bf16)
-            const uint32_t hi = f32_to_bf16_rne(y);
-            const uint32_t lo = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y - bf16_to_f32(hi));
-            out_split[idx] = (uint16_t)hi;
-            out_split[out_plane + idx] = (uint16_t)lo;
-          }
-        }
-      } else {
-        // column 2t holds the hi part of token t, column 2t + 1 the lo part
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
-        if ((lr & 1) == 0 && (lr >> 1) < nt) {
-          const int pair = out_pair;
-          float o[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float t = precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i];
-            o[i] = t + bias_row[i];
-          }
-          *reinterpret_cast<float4*>(out + (int64_t)pair * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
-        }
-      }
-    }
-  }
+  gemv_unit<kDown, kSteps, false>(wmat, bias, e, act, act_plane, out, out_split, out_plane, out_raw, pairs + pb + tc,
+                                  nt, rows, groups, k_top, limit, precision, tile0, ntile, xs, NoWait{});
 }
 
-// Step counts with a compiled kernel; other shapes round up (the extra steps
-// read out of range and decode to zero).  Each is <= kRing or a multiple of it.
-constexpr int kStepSizes[] = {1, 2, 3, 4, 6, 8, 16, 24};
-
-int gemv_steps(int groups) {
-  const int g4 = (groups + 3) / 4;
-  for (int s : kStepSizes)
-    if (s >= g4) return s;
-  return -1;
-}
 
 template <bool kDown>
 using GemvKernel = void (*)(const uint8_t* const*, const uint16_t*, const uint16_t*, int64_t, float*, uint16_t*,
@@ -377,7 +111,6 @@ GemvKernel<kDown> gemv_kernel_for(int steps) {
   }
 }
 
-size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * (steps * 128 + 8) * 2; }
 
 // Tiles each workgroup streams: the unit capacity's tiles spread over about
 // `target` workgroups (768 are resident at once: 3 per CU), so workgroups
@@ -580,14 +313,32 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 // completion counters live in the workspace's first kCounterBytes.
 constexpr int64_t kDecodeRouterTokens = 128;
 constexpr int64_t kCounterBytes = 1024;
+// Batches up to this size can run as one launch (klc_decode.hip).
+constexpr int64_t kFusedDecodeTokens = 16;
 
-// The grouped GEMM pays off once experts see several MFMA column blocks of
-// tokens; below about 8 tokens per expert the GEMV streams the same weights
-// with less overhead.
-bool use_gemm_path(int64_t n_pairs, int64_t n_exp) { return n_pairs >= 8 * n_exp; }
+// The expert path klc_moe_layer takes for `path` (KLC_PATH_*).  AUTO picks
+// the multi-launch layer: the one-launch layer (KLC_PATH_FUSED) measured
+// 36.6 us against 35.6 us at batch 1 and 104 us against 93 us at batch 8
+// (gpt-oss-120B shape), so it runs only when asked for, on a batch it takes
+// and a stream that is not capturing a graph.
+int resolve_layer_path(int path, int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k,
+                       const void* out, const void* residual, hipStream_t stream) {
+  if (path == KLC_PATH_GEMV || path == KLC_PATH_GEMM) return path;
+  if (path == KLC_PATH_FUSED) {
+    bool fused = fused_decode_supported(n_tok, hidden, inter, n_exp, k, out, residual);
+    if (fused) {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) fused = false;
+    }
+    return fused ? KLC_PATH_FUSED : -1;
+  }
+  return n_tok * k >= 8 * n_exp ? KLC_PATH_GEMM : KLC_PATH_GEMV;
+}
+
 
 struct LayerScratch {
-  int64_t counters, partials, logits, ids, values, weights, offsets, sorted, active, n_active, units, gated, eo, total;
+  int64_t counters, partials, logits, ids, values, weights, offsets, sorted, active, n_active, units, gated, eo, fused,
+      total;
 };
 
 LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t n_exp, int64_t k) {
@@ -607,6 +358,8 @@ LayerScratch layer_scratch(int64_t n_tok, int64_t hidden, int64_t inter, int64_t
   s.units = off;    off += align256(units_size(pairs, n_exp) * 4);
   s.gated = off;    off += align256(pairs * inter * 4);  // hi and lo bf16 planes
   s.eo = off;       off += align256(pairs * hidden * 4);
+  // the one-launch decode layer's epoch-tagged logits and item flags
+  s.fused = off;    off += n_tok <= kFusedDecodeTokens ? fused_decode_scratch_bytes(n_tok, hidden, inter, n_exp, k) : 0;
   s.total = off;
   return s;
 }
@@ -685,6 +438,26 @@ extern "C" int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int
   return layer_scratch(n_tokens, hidden, inter, n_experts, k).total;
 }
 
+extern "C" int klc_moe_layer_path(int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                                  int path, void* stream) {
+  KLC_REQUIRE(n_tokens > 0 && hidden > 0 && inter > 0 && n_experts > 0 && k > 0, KLC_ERR_ARGUMENT,
+              "klc_moe_layer_path: bad sizes");
+  KLC_REQUIRE(path == KLC_PATH_AUTO || path == KLC_PATH_GEMV || path == KLC_PATH_GEMM || path == KLC_PATH_FUSED,
+              KLC_ERR_ARGUMENT, "klc_moe_layer_path: unknown path %d", path);
+  const int route = resolve_layer_path(path, n_tokens, hidden, inter, n_experts, k, nullptr, nullptr, as_stream(stream));
+  KLC_REQUIRE(route >= 0, KLC_ERR_UNSUPPORTED, "klc_moe_layer_path: KLC_PATH_FUSED does not take this batch");
+  return route;
+}
+
+extern "C" int64_t klc_moe_layer_status_offset(int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts,
+                                               int64_t k) {
+  KLC_REQUIRE(n_tokens > 0 && hidden > 0 && inter > 0 && n_experts > 0 && k > 0, KLC_ERR_ARGUMENT,
+              "klc_moe_layer_status_offset: bad sizes");
+  if (n_tokens > kFusedDecodeTokens) return -1;
+  return layer_scratch(n_tokens, hidden, inter, n_experts, k).fused +
+         fused_decode_status_offset(n_tokens, hidden, inter, n_experts, k);
+}
+
 namespace klc {
 namespace {
 
@@ -698,8 +471,8 @@ int check_layer_args(const char* fn, const void* x, const void* router_w, const 
               KLC_ERR_ARGUMENT, "%s: null pointer", fn);
   KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
               "%s: unknown precision %d", fn, precision);
-  KLC_REQUIRE(path == KLC_PATH_AUTO || path == KLC_PATH_GEMV || path == KLC_PATH_GEMM, KLC_ERR_ARGUMENT,
-              "%s: unknown path %d", fn, path);
+  KLC_REQUIRE(path == KLC_PATH_AUTO || path == KLC_PATH_GEMV || path == KLC_PATH_GEMM || path == KLC_PATH_FUSED,
+              KLC_ERR_ARGUMENT, "%s: unknown path %d", fn, path);
   int rc = check_router_args(n_tokens, hidden, n_experts);
   if (rc) return rc;
   rc = check_topk_args(n_tokens, n_experts, k);
@@ -738,7 +511,22 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
     return err == hipSuccess ? KLC_OK : set_error(KLC_ERR_HIP, "klc_moe_layer: hipEventRecord: %s", hipGetErrorString(err));
   };
 
+  const int route = resolve_layer_path(path, n_tokens, hidden, inter, n_experts, k, out, residual, st);
+  KLC_REQUIRE(route >= 0, KLC_ERR_UNSUPPORTED,
+              "klc_moe_layer: KLC_PATH_FUSED does not take n_tokens=%lld, n_experts=%lld, k=%lld (at most 16 tokens, "
+              "64 pairs, 256 experts, k <= 16, 8-byte aligned out/residual, no graph capture)",
+              (long long)n_tokens, (long long)n_experts, (long long)k);
   if ((rc = mark(0))) return rc;
+  if (route == KLC_PATH_FUSED) {
+    // the whole layer in one launch; the remaining events follow it back to back
+    if ((rc = launch_moe_decode_fused(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens,
+                                      hidden, inter, n_experts, k, swiglu_limit, precision, ws + s.fused, logits,
+                                      ids_buf, values, w_buf, gated, eo, out, residual, st)))
+      return rc;
+    for (int i = 1; i < KLC_LAYER_EVENTS; ++i)
+      if ((rc = mark(i))) return rc;
+    return KLC_OK;
+  }
   if (n_tokens <= kDecodeRouterTokens) {
     // decode batches: logits, top-k and dispatch in one launch
     KLC_REQUIRE(decode_router_counters(n_tokens, n_experts) * 4 <= kCounterBytes, KLC_ERR_UNSUPPORTED,
@@ -760,7 +548,7 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
       return rc;
   }
   if ((rc = mark(3))) return rc;
-  const bool gemm = path == KLC_PATH_GEMM || (path == KLC_PATH_AUTO && use_gemm_path(n_tokens * k, n_experts));
+  const bool gemm = route == KLC_PATH_GEMM;
   if (gemm) {
     if ((rc = launch_gemm_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden,
                                   inter, swiglu_limit, precision, gated, nullptr, st)))

@@ -1,0 +1,357 @@
+// Decode-path expert GEMV (gfx950): one work unit's pass over consecutive
+// 64-row tiles of one packed MXFP4 expert matrix.  Shared by the standalone
+// GEMV kernels (klc_experts.hip) and the fused small-batch decode layer
+// (klc_decode.hip).
+//
+// Mapping.  Wave w of the 256-thread workgroup owns rows [16w, 16w + 16) of
+// each tile over the whole input dimension.  Per 4-group step a lane holds
+// the 16 code bytes of (row l % 16, group 4s + l/16) -- the A operand of four
+// v_mfma_f32_16x16x32_bf16 (k = 8 * (l/16) + i) once decoded by
+// v_cvt_scalef32_pk_bf16_fp4 (E2M1 times the E8M0 scale, exact) -- and reads
+// the matching B operand from activation rows staged once in LDS as bfloat16.
+//
+// Weight chunks stream through a ring of kRing registers: step s's slot is
+// refilled with the chunk kRing steps ahead (in this tile or the next) right
+// after it is consumed, so every wave keeps kRing KiB of HBM reads in flight
+// across tile boundaries.  kSteps is a template constant and every load is
+// unconditional straight-line code, which lets the compiler wait for exactly
+// one chunk per step (vector loads retire in order).  Past the last tile the
+// refills are out-of-range buffer loads (they return 0 and touch no memory).
+// The activation-row loads are issued before the ring prologue, so waiting
+// for them (the oldest loads) does not wait for any weight chunk.
+//
+// Columns are up to kVRows activation rows.  gate_up stages one row per token
+// (the bfloat16 hidden state, exact).  down stages two rows per token, the hi
+// and lo bfloat16 planes written by gate_up (hi = bf16(y), lo = bf16(y - hi)),
+// so the float32 SwiGLU output enters the product with a 2^-17 residual.  A
+// unit therefore holds 4 tokens in down and 8 in gate_up.
+#pragma once
+
+#include "klc_common.h"
+
+namespace klc {
+namespace {
+
+constexpr int kGemvWaves = 4;                 // 4 x 16 rows = one 64-row tile per workgroup
+constexpr int kGemvThreads = kGemvWaves * kWave;
+constexpr int kVRows = 8;                     // activation rows (MFMA N columns) staged per unit
+constexpr int kMaxSteps = 24;                 // 4-group steps per row (inputs <= 3072)
+constexpr int kRing = 8;  // every compiled kSteps >= kRing is a multiple of it (slot s % kRing is step s of any tile)
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float swiglu(float gate, float up, float limit) {
+  // streamed_moe_router.py:524-529; comparisons keep NaN like torch.clamp
+  gate = gate > limit ? limit : gate;
+  up = up > limit ? limit : (up < -limit ? -limit : up);
+  const float glu = gate * (1.0f / (1.0f + expf(-(gate * 1.702f))));
+  return (up + 1.0f) * glu;
+}
+
+__host__ __device__ constexpr size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * (steps * 128 + 8) * 2; }
+
+// Step counts with a compiled kernel; other shapes round up (the extra steps
+// read out of range and decode to zero).  Each is <= kRing or a multiple of it.
+constexpr int kStepSizes[] = {1, 2, 3, 4, 6, 8, 16, 24};
+
+inline int gemv_steps(int groups) {
+  const int g4 = (groups + 3) / 4;
+  for (int s : kStepSizes)
+    if (s >= g4) return s;
+  return -1;
+}
+
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+// One unit's pass over tiles [tile0, tile0 + ntile) of expert matrix `wmat`
+// (packed row-tile layout, `rows` x `groups`).  unit_pairs[0 .. nt) are the
+// unit's (token, slot) pairs in expert-sorted order; `e` is the expert (for
+// its bias rows).  gate_up (kDown false) reads the tokens' rows of `act`
+// ([tokens][in] bfloat16) and writes the SwiGLU output as hi/lo bfloat16
+// planes (out_split, planes out_plane elements apart) and optionally as
+// float32 (out_raw); down reads the pairs' hi/lo rows of `act` (planes
+// act_plane apart) and writes float32 outputs (out, [pairs][rows]).
+//
+// kFused: the fused decode layer's form.  Outputs are stored at agent scope
+// (the consumers run on other XCDs of the same launch), down reads its input
+// rows at agent scope, out_raw is not written, and wait_inputs() is called
+// after the weight ring's prologue and before the input rows are read (down
+// waits there for the gate_up workgroups that produce them).  xs: the
+// workgroup's gemv_lds_bytes(kSteps) bytes of LDS, 16-byte aligned.
+template <bool kDown, int kSteps, bool kFused, int kRingDepth = kRing, typename WaitFn = NoWait>
+__device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, const uint16_t* __restrict__ bias, int e,
+                                          const uint16_t* __restrict__ act, int64_t act_plane, float* __restrict__ out,
+                                          uint16_t* __restrict__ out_split, int64_t out_plane,
+                                          float* __restrict__ out_raw, const int32_t* unit_pairs, int nt, int rows,
+                                          int groups, int k_top, float limit, int precision, int tile0, int ntile,
+                                          uint16_t* xs, WaitFn wait_inputs) {
+  // the thread index, opaque to the compiler: everything derived from it is
+  // computed here rather than hoisted out of a caller's loop over units
+  // (which would keep those values live across the whole loop)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int in_dim = groups * 32;
+  const int cpr = groups * 4;                   // 16-byte activation chunks per row
+  const int row_stride = kSteps * 128 + 8;      // bf16 elements per staged row (zero padded)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lr = lane & 15;                     // row within the wave's 16 (A) / column n (B, D)
+  const int lq = lane >> 4;                     // k-quarter: groups 4s + lq
+  constexpr int kLoads = (kVRows * kSteps * 16 + kGemvThreads - 1) / kGemvThreads;  // staging chunks per thread
+  constexpr int kR = kRingDepth < kSteps ? kRingDepth : kSteps;
+  static_assert(kSteps % kR == 0, "the ring must divide the step count");
+  static_assert(kUnitTokensGateUp <= kVRows && 2 * kUnitTokensDown <= kVRows, "a unit's rows fit one pass");
+  const int trow = wave * 16 + lr;              // row inside a 64-row tile
+  const int rec = ((groups + 3) / 4 + 7) / 8 * 8;
+  const uint32_t tile_bytes = (uint32_t)groups * 1024u;
+  // the expert matrix as a buffer: weight chunks and scale records are read
+  // with a per-lane VGPR offset and a uniform (SGPR) step offset
+  const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)wmat, (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
+  // chunk of step t in a tile = tile offset + 4096 t + voff.  kSteps is a
+  // multiple of the ring size and may exceed the real step count g4: lanes
+  // whose group 4t + lq is past the last group read out of range (0, no
+  // memory traffic) and decode with scale 0.
+  const int g4 = (groups + 3) >> 2;
+  const uint32_t voff = (uint32_t)(lq * 1024 + trow * 16);
+  const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;  // step g4 - 1
+  auto chunk = [&](uint32_t tile_off, int t, bool valid) -> u32x4_t {
+    const uint32_t v = !valid || t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
+    return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * t, kStreamPolicy);
+  };
+  const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
+
+  const int nrows = kDown ? 2 * nt : nt;
+
+  // ---- 1. the unit's pairs: one vector load, issued before the weight
+  //      stream so that waiting for it does not wait for any weight chunk.
+  //      Lane r < kVRows holds staged row r's pair; the lane's output pair
+  //      (the same for every tile) comes in the same round trip. ----
+  const int rr_l = min(lane & (kVRows - 1), nrows - 1);
+  const int pair_l = unit_pairs[kDown ? rr_l >> 1 : rr_l];
+  const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
+  const int out_pair = unit_pairs[min(out_col, nt - 1)];
+
+  // ---- 2. scale record of the first tile, the first tile's bias, then the
+  //      ring prologue ----
+  // the lane's scales of a tile: 8-byte word i holds steps 8i .. 8i + 7 of
+  // (row, quarter); a wave's load of word i is 512 contiguous bytes
+  constexpr int kRecWords = (kSteps + 7) / 8 * 2;
+  auto load_rec = [&](int tile, uint32_t* dst) {
+#pragma unroll
+    for (int i = 0; i < kRecWords / 2; ++i) {
+      const uint32_t off = (uint32_t)packed_scale_word(groups, tile * kTileRows + trow, min(i, rec / 8 - 1), lq);
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, off, scale_base, kStreamPolicy);
+      dst[2 * i] = v.x;
+      dst[2 * i + 1] = v.y;
+    }
+  };
+  // Epilogue operands are loaded ahead too: the bias of the lane's 4 rows
+  // one tile ahead, next to the scale record.  A load issued in the
+  // epilogue itself would be the youngest in flight, and waiting for it
+  // would drain the weight ring.
+  auto load_bias = [&](int tile) -> u32x2_t {
+    const int64_t row = (int64_t)e * rows + tile * kTileRows + wave * 16 + 4 * lq;
+    return *reinterpret_cast<const u32x2_t*>(bias + row);
+  };
+  uint32_t sc[kRecWords], sc_next[kRecWords];
+  load_rec(tile0, sc);
+  u32x2_t bias_cur = load_bias(tile0), bias_next = bias_cur;
+  uint32_t tb = (uint32_t)tile0 * tile_bytes;
+  u32x4_t ring[kR];
+  __builtin_amdgcn_sched_barrier(0);  // the ring goes out before the rows' loads
+#pragma unroll
+  for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
+  __builtin_amdgcn_sched_barrier(0);
+
+  wait_inputs();
+
+  // ---- 3. activation-row loads (row sources read back from the pairs) ----
+  int src[kVRows];
+  {
+    const int src_l = kDown ? pair_l : pair_l / k_top;
+#pragma unroll
+    for (int r = 0; r < kVRows; ++r) src[r] = __builtin_amdgcn_readlane(src_l, r);
+  }
+  u32x4_t xv[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int id = min(tid + i * kGemvThreads, nrows * cpr - 1);
+    const int r = id / cpr;
+    const int c = id - r * cpr;
+    int srow = src[0];
+#pragma unroll
+    for (int q = 1; q < kVRows; ++q) srow = r == q ? src[q] : srow;
+    const int64_t elem = (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim + c * 8;
+    if constexpr (kFused && kDown) {
+      // the hi/lo rows were stored by other workgroups of this launch
+      const __amdgpu_buffer_rsrc_t abuf =
+          __builtin_amdgcn_make_buffer_rsrc((void*)act, (short)0, 0x7fffffff, kBufferWord3);
+      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(abuf, (uint32_t)(elem * 2), 0, kAgentScope);
+    } else {
+      xv[i] = *reinterpret_cast<const u32x4_t*>(act + elem);
+    }
+  }
+
+  // ---- 4. activation rows into LDS ----
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int id = tid + i * kGemvThreads;
+    const int r = id / cpr;
+    const int c = id - r * cpr;
+    // ids past the staged rows land in row 0's spare 16-byte slot, which nothing reads
+    const int dst = id < nrows * cpr ? r * row_stride + c * 8 : row_stride - 8;
+    *reinterpret_cast<u32x4_t*>(xs + dst) = xv[i];
+  }
+  {
+    const int pad = kSteps * 128 - in_dim;  // zero: its A operand is zero, keep 0 * pad finite
+    for (int i = tid; i < nrows * pad; i += kGemvThreads) {
+      const int r = i / pad;
+      xs[r * row_stride + in_dim + (i - r * pad)] = 0;
+    }
+  }
+  __syncthreads();
+
+  // B operand rows: column n = lr reads staged row min(n, kVRows - 1) without
+  // masking; columns past the live rows produce outputs nobody stores (an
+  // MFMA output column depends only on its own B column)
+  const uint16_t* xrow = xs + min(lr, kVRows - 1) * row_stride + lq * 32;
+  for (int ti = 0; ti < ntile; ++ti) {
+    const int tile = tile0 + ti;
+    // refills past this tile read the next one; past the last tile they read
+    // out of range (0, no memory traffic) at a valid tile offset
+    const bool has_next = ti + 1 < ntile;
+    const uint32_t nb = has_next ? tb + tile_bytes : tb;
+    // the next tile's scale record is issued before the first refill that
+    // reads the next tile, so waiting for it never waits for a ring load
+    const int next_tile = has_next ? tile + 1 : tile;
+    if constexpr (kSteps <= kR) {
+      load_rec(next_tile, sc_next);
+      bias_next = load_bias(next_tile);
+    }
+
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // B operands are read one step ahead of their MFMAs (LDS latency)
+    bf16x8_t bcur[4], bnext[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bcur[j] = *reinterpret_cast<const bf16x8_t*>(xrow + j * 8);
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      __builtin_amdgcn_sched_barrier(0);  // keep each step's decode next to its MFMAs
+      if constexpr (kSteps > kR) {
+        if (s == kSteps - kR) {
+          load_rec(next_tile, sc_next);
+          bias_next = load_bias(next_tile);
+        }
+      }
+      // an empty asm "modifying" the chunk pins each step's decode right
+      // here, so decoded operands (16 registers per step) are never
+      // computed early and kept live across steps
+      asm volatile("" : "+v"(ring[s % kR]));
+      const u32x4_t w = ring[s % kR];
+      {
+        const int t = s + kR;  // refill: kR steps ahead
+        ring[s % kR] = t < kSteps ? chunk(tb, t, true) : chunk(nb, t - kSteps, has_next);
+      }
+      if (s + 1 < kSteps) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bnext[j] = *reinterpret_cast<const bf16x8_t*>(xrow + (s + 1) * 128 + j * 8);
+      }
+      // 2^(e-127) as float32 bits (e = 0: the subnormal 2^-127; e = 255: inf,
+      // which the conversion reads as the MX NaN scale); a lane past the
+      // last group uses scale 0 (finite E2M1 values times 0 are +-0)
+      const uint32_t eb = (sc[s >> 2] >> (8 * (s & 3))) & 0xffu;
+      uint32_t sbits = eb == 0u ? 0x00400000u : (eb << 23);
+      sbits = 4 * s + lq < groups ? sbits : 0u;
+      const float scale = __uint_as_float(sbits);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8_t a = decode8(w[j], scale);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bcur[j], acc, 0, 0, 0);
+      }
+      if (s + 1 < kSteps) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bcur[j] = bnext[j];
+      }
+    }
+    tb = nb;
+#pragma unroll
+    for (int i = 0; i < kRecWords; ++i) sc[i] = sc_next[i];
+    // bias of rows row0 .. row0 + 3 as bfloat16 bits, low half first
+    const float bias_row[4] = {bf16_to_f32(bias_cur.x & 0xffffu), bf16_to_f32(bias_cur.x >> 16),
+                               bf16_to_f32(bias_cur.y & 0xffffu), bf16_to_f32(bias_cur.y >> 16)};
+    bias_cur = bias_next;
+
+    // ---- epilogue: lane holds rows 4*lq + v (v = 0..3) of the wave's 16, column lr ----
+    const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
+    float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if constexpr (!kDown) {
+      if (lr < nt) {
+        const int pair = out_pair;
+        const int half = rows >> 1;
+        uint32_t hi2 = 0u, lo2 = 0u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float gate = v[2 * h], up = v[2 * h + 1];
+          if (precision == KLC_PRECISION_BF16) {
+            gate = round_bf16(gate);
+            up = round_bf16(up);
+          }
+          gate += bias_row[2 * h];
+          up += bias_row[2 * h + 1];
+          const float y = swiglu(gate, up, limit);
+          const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
+          // down input: hi/lo bfloat16 planes (lo = 0 when the reference rounds to bf16)
+          const uint32_t hi = f32_to_bf16_rne(y);
+          const uint32_t lo = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y - bf16_to_f32(hi));
+          if constexpr (kFused) {
+            hi2 |= hi << (16 * h);
+            lo2 |= lo << (16 * h);
+          } else {
+            if (out_raw) out_raw[idx] = y;
+            out_split[idx] = (uint16_t)hi;
+            out_split[out_plane + idx] = (uint16_t)lo;
+          }
+        }
+        if constexpr (kFused) {
+          // outputs (row0 / 2, row0 / 2 + 1) of the pair: one 4-byte word per
+          // plane (row0 is a multiple of 4 and half is even)
+          const int64_t idx = (int64_t)pair * half + (row0 >> 1);
+          uint32_t* p = reinterpret_cast<uint32_t*>(out_split + idx);
+          __hip_atomic_store(p, hi2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(reinterpret_cast<uint32_t*>(out_split + out_plane + idx), lo2, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    } else {
+      // column 2t holds the hi part of token t, column 2t + 1 the lo part
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
+      if ((lr & 1) == 0 && (lr >> 1) < nt) {
+        const int pair = out_pair;
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float t = precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i];
+          o[i] = t + bias_row[i];
+        }
+        if constexpr (kFused) {
+          const __amdgpu_buffer_rsrc_t obuf =
+              __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, 0x7fffffff, kBufferWord3);
+          const u32x4_t ov = {__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                              __float_as_uint(o[3])};
+          __builtin_amdgcn_raw_buffer_store_b128(ov, obuf, (uint32_t)(((int64_t)pair * rows + row0) * 4), 0,
+                                                 kAgentScope);
+        } else {
+          *reinterpret_cast<float4*>(out + (int64_t)pair * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace klc

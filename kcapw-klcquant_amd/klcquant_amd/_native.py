@@ -27,7 +27,7 @@ PRECISION_FP32 = 0
 PRECISION_BF16 = 1
 
 LAYER_EVENTS = 7  # KLC_LAYER_EVENTS
-PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2  # KLC_PATH_*
+PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_FUSED = 0, 1, 2, 3  # KLC_PATH_*
 DISPATCH_MAX_PAIRS = 38648  # KLC_DISPATCH_MAX_PAIRS
 LAYER_MAX_TOKENS = 65535  # KLC_LAYER_MAX_TOKENS
 
@@ -59,6 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     "klc_moe_bias_combine": (_I32, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_pair_norms": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "klc_moe_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "klc_moe_layer_path": (_I32, [_I64, _I64, _I64, _I64, _I64, _I32, _P]),
+    "klc_moe_layer_status_offset": (_I64, [_I64, _I64, _I64, _I64, _I64]),
     "klc_moe_layer": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
                              _P, _P, _P, _P, _P, _P]),
     "klc_moe_layer_static_scratch": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32,

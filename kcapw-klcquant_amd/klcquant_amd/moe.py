@@ -139,14 +139,14 @@ def synthetic_hidden(workload: int, n_tokens: int, hidden: int, step: int = 0) -
 class MoELayer:
     """Runs one MoE layer on batches of tokens (bf16 ``[B, H]`` in, bf16 ``[B, H]`` out)."""
 
-    PATHS = {"auto": nat.PATH_AUTO, "gemv": nat.PATH_GEMV, "gemm": nat.PATH_GEMM}
+    PATHS = {"auto": nat.PATH_AUTO, "gemv": nat.PATH_GEMV, "gemm": nat.PATH_GEMM, "fused": nat.PATH_FUSED}
 
     def __init__(self, weights: MoELayerWeights, experts_per_token: int = 4, swiglu_limit: float = 7.0,
                  precision: str = "fp32", path: str = "auto") -> None:
         if precision not in ops.PRECISIONS:
             raise ValueError(f"unknown matmul precision {precision!r}")
         if path not in self.PATHS:
-            raise ValueError(f"unknown expert path {path!r} (auto, gemv or gemm)")
+            raise ValueError(f"unknown expert path {path!r} (auto, gemv, gemm or fused)")
         self.w = weights
         self.k = min(int(experts_per_token), weights.n_experts)
         self.limit = float(swiglu_limit)
@@ -268,9 +268,25 @@ class MoELayer:
 
     def uses_gemm(self, n_tokens: int) -> bool:
         """Whether :meth:`forward` runs the grouped GEMM for ``n_tokens`` tokens (the library's rule)."""
-        if self.path != "auto":
-            return self.path == "gemm"
-        return n_tokens * self.k >= 8 * self.w.n_experts
+        return self.layer_path(n_tokens) == "gemm"
+
+    def fused_status(self, n_tokens: int) -> int:
+        """The one-launch layer's status word in this layer's workspace for ``n_tokens`` (0: every wait
+        of every launch ended on its condition; bit 0: some wait ran out).  Synchronises the device."""
+        w = self.w
+        off = nat.call("klc_moe_layer_status_offset", n_tokens, w.hidden, w.inter, w.n_experts, self.k)
+        if off < 0 or n_tokens not in self._ws:
+            return 0
+        return int(self._ws[n_tokens][off:off + 4].cpu().numpy().view(np.uint32)[0])
+
+    def layer_path(self, n_tokens: int) -> str:
+        """The path :meth:`forward` takes for ``n_tokens`` tokens on the current stream (the library's
+        rule, klc_moe_layer_path): ``"gemv"``, ``"gemm"``, or ``"fused"`` (the whole layer in one
+        launch, batches of at most 16 tokens; only when this layer's path is ``"fused"``)."""
+        w = self.w
+        code = nat.call("klc_moe_layer_path", n_tokens, w.hidden, w.inter, w.n_experts, self.k,
+                        self.PATHS[self.path], ops._stream(w.device))
+        return {nat.PATH_GEMV: "gemv", nat.PATH_GEMM: "gemm", nat.PATH_FUSED: "fused"}[code]
 
     def forward_detailed(self, x: torch.Tensor, routing: tuple[torch.Tensor, torch.Tensor] | None = None) -> dict:
         """Step-by-step path exposing every intermediate (same kernels as :meth:`forward`).
