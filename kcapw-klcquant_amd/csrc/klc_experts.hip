@@ -113,15 +113,18 @@ GemvKernel<kDown> gemv_kernel_for(int steps) {
 
 
 // Tiles each workgroup streams: the unit capacity's tiles spread over about
-// `target` workgroups (768 are resident at once: 3 per CU), so workgroups
-// that finish early are replaced and the tail stays short; one tile per
-// workgroup when few units exist.  max_units is an upper bound of the units.
-// Measured at batches 64 and 128 (120B shape): gate_up is fastest with 2
-// tiles per workgroup, down with 3 -- one tile per workgroup is much slower
-// for both, since every workgroup start stages 8 activation rows and waits
-// for a chain of index loads.
-constexpr int64_t kGemvWorkgroupsUp = 6144, kGemvMaxTilesUp = 2;
-constexpr int64_t kGemvWorkgroupsDown = 2304, kGemvMaxTilesDown = 3;
+// `target` workgroups (768 are resident at once: 3 per CU), at most 2
+// (gate_up) or 3 (down) tiles each, so workgroups that finish early are
+// replaced and the tail stays short; one tile per workgroup when few units
+// exist.  max_units is an upper bound of the units.  Every workgroup start
+// stages up to 8 activation rows and waits for a chain of index loads, so
+// one tile per workgroup is much slower at batches of 4 and more.  Measured
+// (120B shape): the targets 720 / 240 reach the 2 / 3 tile limits from
+// batch 4 on (batch 4 62.4 -> 59.1 us, 8 91.2 -> 86.3 us, 16 137.4 ->
+// 128.7 us against targets 6144 / 2304, which reached them only near batch
+// 64); 3 gate_up tiles per workgroup, or 4 down tiles, were slower.
+constexpr int64_t kGemvWorkgroupsUp = 720, kGemvMaxTilesUp = 2;
+constexpr int64_t kGemvWorkgroupsDown = 240, kGemvMaxTilesDown = 3;
 
 int tiles_per_workgroup(int tiles, int64_t max_units, int64_t target, int64_t max_tpw) {
   int64_t tpw = (int64_t)tiles * max_units / target;
