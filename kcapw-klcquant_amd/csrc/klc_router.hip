@@ -87,6 +87,117 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(const int32_
   block_dispatch([&](int p) { return ids[p]; }, n_pairs, n_exp, offsets, sorted, active, n_active, units, dlds);
 }
 
+// The same dispatch (block_dispatch's outputs) over one workgroup per
+// expert, for large batches.  Every workgroup reads all pair ids (from L2
+// after the first) and counts every expert's pairs in LDS, so it knows all
+// offsets, active-list positions and unit prefixes without a hand-off
+// between workgroups; it then writes its own expert's pairs in pair order,
+// offset, active-list entries and units.  Wave w takes the pairs
+// [w Q, (w + 1) Q), Q = ceil(n_pairs / 4), 64 consecutive pairs per
+// coalesced load and 8 loads in flight: a first pass counts (LDS atomics
+// for the histogram, a ballot for the own expert), a second pass places the
+// own expert's pairs at its offset + the earlier waves' count + the wave's
+// running count + the rank within the 64.
+constexpr int kDispatchMultiBatch = 8;
+__global__ __launch_bounds__(kDispatchThreads) void dispatch_multi_kernel(const int32_t* __restrict__ ids, int n_pairs,
+                                                                          int n_exp, int32_t* __restrict__ offsets,
+                                                                          int32_t* __restrict__ sorted,
+                                                                          int32_t* __restrict__ active,
+                                                                          int32_t* __restrict__ n_active,
+                                                                          int32_t* __restrict__ units) {
+  __shared__ int32_t hist[kDispatchMaxExperts];  // counts, then offsets
+  __shared__ int32_t flags[kDispatchMaxExperts];  // active, then active-list positions
+  __shared__ int32_t ucnt[3][kDispatchMaxExperts];  // units per expert, then first unit (gate_up, down, GEMM)
+  __shared__ int32_t sums[8];
+  __shared__ int32_t wave_own[kDispatchWaves];
+  const int own = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int e = tid; e < kDispatchMaxExperts; e += kDispatchThreads) hist[e] = 0;
+  lds_barrier();
+  const int q = (n_pairs + kDispatchWaves - 1) / kDispatchWaves;
+  const int w0 = min(wave * q, n_pairs), w1 = min(w0 + q, n_pairs);
+  // pass 1: histogram and the wave's count of the own expert
+  int own_count = 0;
+  for (int b = w0; b < w1; b += kDispatchMultiBatch * kWave) {
+    int32_t v[kDispatchMultiBatch];
+#pragma unroll
+    for (int i = 0; i < kDispatchMultiBatch; ++i) {
+      const int p = b + i * kWave + lane;
+      v[i] = p < w1 ? ids[p] : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kDispatchMultiBatch; ++i) {
+      const bool valid = v[i] >= 0 && v[i] < n_exp;
+      if (valid) atomicAdd(&hist[v[i]], 1);
+      own_count += __popcll(__ballot(v[i] == own));
+    }
+  }
+  if (lane == 0) wave_own[wave] = own_count;
+  lds_barrier();
+  const int32_t own_total = hist[own];  // read before the scan below turns counts into offsets
+  for (int e = tid; e < n_exp; e += kDispatchThreads) {
+    const int32_t c = hist[e];
+    flags[e] = c > 0 ? 1 : 0;
+    ucnt[0][e] = (c + kUnitTokensGateUp - 1) / kUnitTokensGateUp;
+    ucnt[1][e] = (c + kUnitTokensDown - 1) / kUnitTokensDown;
+    ucnt[2][e] = (c + kUnitTokensGemm - 1) / kUnitTokensGemm;
+  }
+  lds_barrier();
+  if (wave == 0) {
+    wave_exclusive_scan_256(hist, n_exp, &sums[0], lane);
+    wave_exclusive_scan_256(ucnt[2], n_exp, &sums[4], lane);
+  } else if (wave == 1) {
+    wave_exclusive_scan_256(flags, n_exp, &sums[1], lane);
+  } else if (wave == 2) {
+    wave_exclusive_scan_256(ucnt[0], n_exp, &sums[2], lane);
+  } else {
+    wave_exclusive_scan_256(ucnt[1], n_exp, &sums[3], lane);
+  }
+  lds_barrier();
+  // pass 2: the own expert's pairs
+  if (own_total > 0) {
+    int run = hist[own];
+    for (int w = 0; w < wave; ++w) run += wave_own[w];
+    for (int b = w0; b < w1; b += kDispatchMultiBatch * kWave) {
+      int32_t v[kDispatchMultiBatch];
+#pragma unroll
+      for (int i = 0; i < kDispatchMultiBatch; ++i) {
+        const int p = b + i * kWave + lane;
+        v[i] = p < w1 ? ids[p] : -1;
+      }
+#pragma unroll
+      for (int i = 0; i < kDispatchMultiBatch; ++i) {
+        const uint64_t m = __ballot(v[i] == own);
+        if (v[i] == own) sorted[run + __popcll(m & below)] = b + i * kWave + lane;
+        run += __popcll(m);
+      }
+    }
+  }
+  // the own expert's offset, active-list entries and units
+  int32_t* const gu_list = units + kUnitHeader;
+  int32_t* const dn_list = units + units_offset_down(n_pairs, n_exp);
+  int32_t* const gm_list = units + units_offset_gemm(n_pairs, n_exp);
+  for (int j = tid; j * kUnitTokensGateUp < own_total; j += kDispatchThreads) gu_list[ucnt[0][own] + j] = make_unit(own, j);
+  for (int j = tid; j * kUnitTokensDown < own_total; j += kDispatchThreads) dn_list[ucnt[1][own] + j] = make_unit(own, j);
+  for (int j = tid; j * kUnitTokensGemm < own_total; j += kDispatchThreads) gm_list[ucnt[2][own] + j] = make_unit(own, j);
+  if (tid == 0) {
+    offsets[own] = hist[own];
+    if (own_total > 0) active[flags[own]] = own;
+    if (own >= sums[1]) active[own] = -1;
+    if (own == 0) {
+      offsets[n_exp] = sums[0];
+      *n_active = sums[1];
+      units[0] = sums[2];
+      units[1] = sums[3];
+      units[2] = sums[4];
+      units[3] = 0;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void router_decode_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b, uint16_t* logits,
     int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
@@ -222,8 +333,16 @@ int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, 
   return check_launch("topk_softmax_kernel");
 }
 
+// Pairs at and above which the dispatch runs over one workgroup per expert.
+constexpr int kDispatchMultiPairs = 1024;
+
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
                     int32_t* active, int32_t* n_active, int32_t* units, hipStream_t stream) {
+  if (n_pairs >= kDispatchMultiPairs) {
+    dispatch_multi_kernel<<<(unsigned)n_exp, kDispatchThreads, 0, stream>>>(ids, (int)n_pairs, (int)n_exp, offsets,
+                                                                           sorted, active, n_active, units);
+    return check_launch("dispatch_multi_kernel");
+  }
   dispatch_kernel<<<1, kDispatchThreads, dispatch_lds_bytes((int)n_pairs, (int)n_exp), stream>>>(
       ids, (int)n_pairs, (int)n_exp, offsets, sorted, active, n_active, units);
   return check_launch("dispatch_kernel");

@@ -113,8 +113,11 @@ def test_topk_torch_order_past_the_introselect_depth_limit(gpu):
 
 
 @pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 128), (64, 4, 128), (2048, 4, 128), (7, 3, 5), (300, 2, 256),
-                                           (64, 4, 32)])
+                                           (64, 4, 32), (255, 4, 128), (256, 4, 128), (1031, 1, 256),
+                                           (600, 2, 1)])
 def test_dispatch_matches_stable_counting_sort(gpu, n_tok, k, n_exp):
+    """Below 1024 pairs one workgroup sorts; from 1024 on one workgroup per expert does (both give these
+    outputs)."""
     rng_ids = synth.random_ints(900 + n_tok, n_tok * k, 0, n_exp - 1).reshape(n_tok, k).astype(np.int32)
     disp = ops.dispatch(torch.from_numpy(rng_ids).to(gpu), n_exp)
     torch.cuda.synchronize()
