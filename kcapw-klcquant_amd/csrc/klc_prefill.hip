@@ -40,9 +40,20 @@ namespace {
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmThreads = 256;
-constexpr int kGemmWaves = 4;
-constexpr int kGemmRows = kGemmWaves * kTileRows;   // 256 output rows per workgroup
+// Waves (64-row tiles) per workgroup.  8 waves (512 rows) halve the B rows
+// each wave stages per step but were slower (gate_up 467-478 -> 480-496 us,
+// down 363-372 -> 381-398 us on the 2048-token layer): all 8 waves of a CU
+// then meet at one barrier every step.
+#ifndef KLC_GEMM_WAVES
+#define KLC_GEMM_WAVES 4
+#endif
+constexpr int kGemmWaves = KLC_GEMM_WAVES;          // one 64-row tile per wave
+constexpr int kGemmThreads = kGemmWaves * kWave;
+constexpr int kGemmRows = kGemmWaves * kTileRows;   // output rows per workgroup
+constexpr int kBRowsPerWave = kUnitTokensGemm / kGemmWaves;  // token rows each wave stages per step
+constexpr int kBInstr = kBRowsPerWave / 4;          // LDS-DMA instructions per wave, plane and step (4 rows each)
+static_assert(kBInstr >= 1 && kBRowsPerWave % 4 == 0, "token rows split evenly over the waves");
+constexpr int kYStride = kGemmRows / 2 + 1;         // gate_up epilogue: floats per token row (odd: spreads the banks)
 constexpr int kGemmCb = kUnitTokensGemm / 16;       // 8 column blocks of 16 tokens
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
 #ifndef KLC_GEMM_RING_UP
@@ -87,6 +98,13 @@ template <bool kDown>
 __host__ __device__ constexpr int gemm_ring() { return kDown ? KLC_GEMM_RING_DOWN : KLC_GEMM_RING_UP; }
 template <bool kDown>
 __host__ __device__ constexpr int gemm_stage_bytes() { return (kDown ? 2 : 1) * kUnitTokensGemm * 256; }
+// LDS of one workgroup: the B ring, or the gate_up epilogue's output tile if larger.
+template <bool kDown>
+__host__ __device__ constexpr int gemm_lds_bytes() {
+  const int ring = gemm_ring<kDown>() * gemm_stage_bytes<kDown>();
+  const int tile = kDown ? 0 : kUnitTokensGemm * kYStride * 4;
+  return ring > tile ? ring : tile;
+}
 
 // One GEMM unit x one 256-row tile.  gate_up: act = bfloat16 hidden state
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
@@ -103,7 +121,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   constexpr int kRing = gemm_ring<kDown>();
   constexpr int kStage = gemm_stage_bytes<kDown>();  // one step: 64 token rows x 256 bytes per plane
   constexpr int kPlaneStage = kStage / kPlanes;
-  constexpr int kLoadsPerStep = 4 + 4 * kPlanes;  // A: 4 chunks; B: 4 rows of 4 per plane
+  constexpr int kLoadsPerStep = 4 + kBInstr * kPlanes;  // A: 4 chunks; B: kBInstr instructions per plane
   extern __shared__ __align__(16) uint8_t stage[];    // kRing x kStage
 
   // XCD-aware order: workgroups are handed to the 8 XCDs round-robin, so XCD
@@ -135,11 +153,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // lane l brings piece (l % 16) ^ (r % 16) of row r = 16 w + 4 i + l / 16.
   // Rows past the unit's tokens repeat its last token (their columns are
   // discarded); k past the input repeats its last piece (A is zero there). ----
-  int64_t src_row[4];
-  int piece[4];
+  int64_t src_row[kBInstr];
+  int piece[kBInstr];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * wave + 4 * i + lq;
+  for (int i = 0; i < kBInstr; ++i) {
+    const int r = kBRowsPerWave * wave + 4 * i + lq;
     const int p = pairs[pb + tc + min(r, nt - 1)];
     src_row[i] = (int64_t)(kDown ? p : p / k_top) * in_dim;
     piece[i] = lr ^ (r & 15);
@@ -149,11 +167,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int pl = 0; pl < kPlanes; ++pl) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kBInstr; ++i) {
         const int kc = min(sc * 128 + piece[i] * 8, in_dim - 8);
         const uint16_t* g = act + pl * act_plane + src_row[i] + kc;
         __attribute__((address_space(3))) uint8_t* dst =
-            (__attribute__((address_space(3))) uint8_t*)stage + slot * kStage + pl * kPlaneStage + (16 * wave + 4 * i) * 256;
+            (__attribute__((address_space(3))) uint8_t*)stage + slot * kStage + pl * kPlaneStage + (kBRowsPerWave * wave + 4 * i) * 256;
         __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
       }
     }
@@ -281,8 +299,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     // SwiGLU outputs of the workgroup (128 columns x up to 64 tokens) go
     // through LDS (the ring is idle now), so each token's 128 outputs leave
     // as 16-byte stores instead of 2-byte ones scattered over 16 rows
-    constexpr int kYStride = 129;  // floats per token row (odd: spreads the banks)
-    static_assert(kUnitTokensGemm * kYStride * 4 <= kRing * kStage, "the output tile fits in the ring's LDS");
+    static_assert(kUnitTokensGemm * kYStride * 4 <= gemm_lds_bytes<false>(), "the output tile fits in the LDS");
     float* ytile = reinterpret_cast<float*>(stage);
     __syncthreads();  // every wave is done reading the ring
     if (wave_live) {
@@ -312,9 +329,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     const int half = rows >> 1;
     const int col0 = row_wg * (kGemmRows / 2);
     const int ncols = min(kGemmRows / 2, half - col0);
-    for (int i = tid; i < nt * 16; i += kGemmThreads) {  // (token, 8-column piece)
-      const int c = i >> 4;
-      const int ch = (i & 15) * 8;
+    constexpr int kPieces = kGemmRows / 16;  // 8-column pieces of a token's outputs
+    for (int i = tid; i < nt * kPieces; i += kGemmThreads) {  // (token, 8-column piece)
+      const int c = i / kPieces;
+      const int ch = (i % kPieces) * 8;
       if (ch >= ncols) continue;
       const int p = pairs[pb + tc + c];
       float y[8];
@@ -376,7 +394,7 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(hidden / 32);
-  moe_gemm_kernel<false><<<grid, kGemmThreads, gemm_ring<false>() * gemm_stage_bytes<false>(), stream>>>(
+  moe_gemm_kernel<false><<<grid, kGemmThreads, gemm_lds_bytes<false>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
       0, nullptr, static_cast<uint16_t*>(gated_split), n_pairs * inter, gated_raw, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, groups, (int)k, limit, precision,
@@ -391,7 +409,7 @@ int launch_gemm_down(const void* const* w, const void* bias, const void* gated_s
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(inter / 32);
-  moe_gemm_kernel<true><<<grid, kGemmThreads, gemm_ring<true>() * gemm_stage_bytes<true>(), stream>>>(
+  moe_gemm_kernel<true><<<grid, kGemmThreads, gemm_lds_bytes<true>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, groups, 1, 0.0f, precision,
