@@ -43,12 +43,12 @@ extern "C" {
 #define KLC_PRECISION_FP32 0 /* expert_matmul_precision="fp32" */
 #define KLC_PRECISION_BF16 1 /* expert_matmul_precision="bf16" */
 
-/* Size limits of one call.  klc_moe_dispatch stages every (token, slot) pair
- * in one workgroup's LDS; klc_moe_layer and the combines index tokens by a
- * grid dimension.  Longer inputs are split by the caller: tokens are
+/* Size limits of one call.  klc_moe_dispatch takes up to 2^21 (token, slot)
+ * pairs (65535 tokens at k = 32); klc_moe_layer and the combines index tokens
+ * by a grid dimension.  Longer inputs are split by the caller: tokens are
  * independent of each other along the whole path, so chunks give the same
  * bits as one call would. */
-#define KLC_DISPATCH_MAX_PAIRS 38648
+#define KLC_DISPATCH_MAX_PAIRS 2097152
 #define KLC_LAYER_MAX_TOKENS 65535
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -126,8 +126,9 @@ int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens
  *   order, with capacities C_m = (n_pairs + (m - 1) * min(n_pairs, n_experts)) / m.
  * A unit is expert | (pass << 10) and covers the pass-th run of m tokens of
  * that expert; experts ascending, then passes.
- * n_experts <= 256 and n_pairs <= KLC_DISPATCH_MAX_PAIRS (one workgroup stages
- * every pair's expert and rank in LDS). */
+ * n_experts <= 256 and n_pairs <= KLC_DISPATCH_MAX_PAIRS.  Below 1024 pairs
+ * one workgroup sorts; from 1024 on, one workgroup per expert counts every
+ * expert and places its own expert's pairs, with the same outputs. */
 int klc_moe_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_experts, int32_t* offsets,
                      int32_t* sorted_pairs, int32_t* active, int32_t* n_active, int32_t* units, void* stream);
 

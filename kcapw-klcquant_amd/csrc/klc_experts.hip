@@ -250,10 +250,17 @@ int check_gemv_shapes(int64_t hidden, int64_t inter, int64_t n_pairs, int64_t n_
   KLC_REQUIRE(hidden % 64 == 0 && inter % 32 == 0 && (2 * inter) % 64 == 0, KLC_ERR_SHAPE,
               "experts: hidden=%lld must be a multiple of 64 and inter=%lld a multiple of 32", (long long)hidden,
               (long long)inter);
-  KLC_REQUIRE(units_capacity(n_pairs, n_exp, kUnitTokensDown) <= 65535 && hidden <= 32 * 4 * kMaxSteps &&
-                  inter <= 32 * 4 * kMaxSteps,
-              KLC_ERR_UNSUPPORTED, "experts: unsupported sizes (hidden, inter <= %d, <= 65535 work units)",
-              32 * 4 * kMaxSteps);
+  KLC_REQUIRE(hidden <= 32 * 4 * kMaxSteps && inter <= 32 * 4 * kMaxSteps, KLC_ERR_UNSUPPORTED,
+              "experts: unsupported sizes (hidden, inter <= %d)", 32 * 4 * kMaxSteps);
+  return KLC_OK;
+}
+
+// The decode GEMVs run one grid row per work unit (a grid dimension holds
+// at most 65535); the grouped GEMM has no such limit.
+int check_gemv_grid(int64_t n_pairs, int64_t n_exp) {
+  KLC_REQUIRE(units_capacity(n_pairs, n_exp, kUnitTokensDown) <= 65535, KLC_ERR_UNSUPPORTED,
+              "experts: %lld pairs over %lld experts exceed the decode GEMVs' 65535 work units (use the grouped "
+              "GEMM)", (long long)n_pairs, (long long)n_exp);
   return KLC_OK;
 }
 
@@ -384,6 +391,8 @@ extern "C" int klc_moe_gate_up(const void* const* w_gate_up, const void* bias, c
               "klc_moe_gate_up: unknown precision %d", precision);
   const int rc = check_gemv_shapes(hidden, inter, n_tokens * k, n_experts);
   if (rc) return rc;
+  const int rc2 = check_gemv_grid(n_tokens * k, n_experts);
+  if (rc2) return rc2;
   return launch_gate_up(w_gate_up, bias, x, n_tokens, k, n_experts, offsets, sorted_pairs, units, hidden, inter,
                         swiglu_limit, precision, gated_split, gated_raw, as_stream(stream));
 }
@@ -399,6 +408,8 @@ extern "C" int klc_moe_down(const void* const* w_down, const void* bias, const v
               "klc_moe_down: unknown precision %d", precision);
   const int rc = check_gemv_shapes(hidden, inter, n_pairs, n_experts);
   if (rc) return rc;
+  const int rc2 = check_gemv_grid(n_pairs, n_experts);
+  if (rc2) return rc2;
   return launch_down(w_down, bias, gated_split, n_pairs, n_experts, offsets, sorted_pairs, units, hidden, inter,
                      precision, expert_out, as_stream(stream));
 }
@@ -552,6 +563,7 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
   }
   if ((rc = mark(3))) return rc;
   const bool gemm = route == KLC_PATH_GEMM;
+  if (!gemm && (rc = check_gemv_grid(n_tokens * k, n_experts))) return rc;
   if (gemm) {
     if ((rc = launch_gemm_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden,
                                   inter, swiglu_limit, precision, gated, nullptr, st)))

@@ -333,8 +333,10 @@ int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, 
   return check_launch("topk_softmax_kernel");
 }
 
-// Pairs at and above which the dispatch runs over one workgroup per expert.
+// Pairs at and above which the dispatch runs over one workgroup per expert
+// (below, block_dispatch's LDS staging holds them: 1024 < kDispatchLdsMaxPairs).
 constexpr int kDispatchMultiPairs = 1024;
+static_assert(kDispatchMultiPairs <= kDispatchLdsMaxPairs, "the one-workgroup dispatch stages its pairs in LDS");
 
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
                     int32_t* active, int32_t* n_active, int32_t* units, hipStream_t stream) {
@@ -409,9 +411,8 @@ int check_dispatch_args(int64_t n_pairs, int64_t n_exp) {
               (long long)n_pairs, (long long)n_exp);
   KLC_REQUIRE(n_exp <= kDispatchMaxExperts, KLC_ERR_UNSUPPORTED, "dispatch: n_experts=%lld > %d", (long long)n_exp,
               kDispatchMaxExperts);
-  KLC_REQUIRE(n_pairs <= kDispatchMaxPairs, KLC_ERR_UNSUPPORTED,
-              "dispatch: n_pairs=%lld > %d (the pairs' experts and ranks are staged in 160 KiB of LDS)",
-              (long long)n_pairs, kDispatchMaxPairs);
+  KLC_REQUIRE(n_pairs <= KLC_DISPATCH_MAX_PAIRS, KLC_ERR_UNSUPPORTED, "dispatch: n_pairs=%lld > %d",
+              (long long)n_pairs, KLC_DISPATCH_MAX_PAIRS);
   return KLC_OK;
 }
 

@@ -763,10 +763,11 @@ __host__ __device__ constexpr size_t dispatch_lds_bytes(int n_pairs, int /*n_exp
          (kDispatchWaves + 5) * kDispatchMaxExperts * sizeof(int32_t) + 8 * sizeof(int32_t);
 }
 
-// Largest n_pairs whose staging fits in 160 KiB of LDS.
-constexpr int kDispatchMaxPairs = KLC_DISPATCH_MAX_PAIRS;
-static_assert(dispatch_lds_bytes(kDispatchMaxPairs, kDispatchMaxExperts) <= 160 * 1024, "dispatch LDS");
-static_assert(dispatch_lds_bytes(kDispatchMaxPairs + 8, kDispatchMaxExperts) > 160 * 1024, "dispatch LDS");
+// Largest n_pairs whose staging fits in 160 KiB of LDS (block_dispatch's
+// limit; the decode router and the dispatch below 1024 pairs stay far under it).
+constexpr int kDispatchLdsMaxPairs = 38648;
+static_assert(dispatch_lds_bytes(kDispatchLdsMaxPairs, kDispatchMaxExperts) <= 160 * 1024, "dispatch LDS");
+static_assert(dispatch_lds_bytes(kDispatchLdsMaxPairs + 8, kDispatchMaxExperts) > 160 * 1024, "dispatch LDS");
 
 // For each of N keys (key < 512) held by this lane: the lanes of the wave
 // holding the same key, from one ballot per key bit.

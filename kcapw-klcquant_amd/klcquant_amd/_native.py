@@ -28,7 +28,7 @@ PRECISION_BF16 = 1
 
 LAYER_EVENTS = 7  # KLC_LAYER_EVENTS
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_FUSED = 0, 1, 2, 3  # KLC_PATH_*
-DISPATCH_MAX_PAIRS = 38648  # KLC_DISPATCH_MAX_PAIRS
+DISPATCH_MAX_PAIRS = 2097152  # KLC_DISPATCH_MAX_PAIRS
 LAYER_MAX_TOKENS = 65535  # KLC_LAYER_MAX_TOKENS
 
 _P = ctypes.c_void_p

@@ -261,10 +261,14 @@ class MoELayer:
         return graph
 
     def max_tokens_per_call(self) -> int:
-        """Tokens one klc_moe_layer call takes: the dispatch stages at most
-        KLC_DISPATCH_MAX_PAIRS (token, slot) pairs, the layer at most
-        KLC_LAYER_MAX_TOKENS tokens."""
-        return ops.max_tokens_per_call(self.k)
+        """Tokens one klc_moe_layer call takes: the layer takes at most
+        KLC_LAYER_MAX_TOKENS tokens (and KLC_DISPATCH_MAX_PAIRS token-slot
+        pairs); the decode GEMVs, when forced (path "gemv"), at most 65535
+        work units of 4 pairs."""
+        n = ops.max_tokens_per_call(self.k)
+        if self.path == "gemv":
+            n = min(n, (4 * 65535 - 3 * self.w.n_experts) // self.k)
+        return n
 
     def uses_gemm(self, n_tokens: int) -> bool:
         """Whether :meth:`forward` runs the grouped GEMM for ``n_tokens`` tokens (the library's rule)."""

@@ -1,11 +1,13 @@
-"""Inputs longer than one library call takes (KLC_DISPATCH_MAX_PAIRS pairs).
+"""Long inputs: one call up to KLC_LAYER_MAX_TOKENS tokens, row chunks past it.
 
-9,700 tokens at top-4 are 38,800 (token, slot) pairs, past the 38,648 that
-one dispatch stages; ``MoELayer.forward`` and ``StreamedMoERouter.route``
-split them into row chunks.  Every token depends on its own row only
-(streamed_moe_router.py:257-329 routes one token per call), so the chunked
-result must equal the oracle's exactly in routing and within the expert
-tolerance in the outputs, with no seam at the chunk boundary.
+9,700 tokens at top-4 are 38,800 (token, slot) pairs, which one call takes
+(the dispatch of 1024 pairs and more runs over one workgroup per expert and
+stages no pair in LDS): routing must equal the oracle's exactly and the
+outputs stay within the expert tolerance.  Past KLC_LAYER_MAX_TOKENS,
+``MoELayer.forward`` splits the rows into chunks; every token depends on its
+own row only (streamed_moe_router.py:257-329 routes one token per call), so
+the split result must equal separate calls on any split of the rows, bit for
+bit, with no seam at the chunk boundary.
 """
 
 from __future__ import annotations
@@ -30,7 +32,7 @@ N_TOK = 9700
 
 @pytest.fixture(scope="module")
 def setup(gpu):
-    assert N_TOK * K > nat.DISPATCH_MAX_PAIRS and N_TOK > ops.max_tokens_per_call(K)
+    assert N_TOK * K > 38648 and N_TOK <= ops.max_tokens_per_call(K)
     host = moe.synthetic_host_layer(WORKLOAD, 0, H, I, E)
     dev_w = moe.MoELayerWeights.synthetic(WORKLOAD, 0, H, I, E, gpu)
     x = moe.synthetic_hidden(WORKLOAD, N_TOK, H)
@@ -39,7 +41,7 @@ def setup(gpu):
 
 @pytest.mark.timeout(300)
 @pytest.mark.parametrize("path", ["auto", "gemv"])
-def test_layer_splits_past_dispatch_limit(gpu, setup, path):
+def test_layer_long_input(gpu, setup, path):
     host, dev_w, x, ref = setup
     layer = moe.MoELayer(dev_w, K, path=path)
     ids = torch.empty((N_TOK, K), dtype=torch.int32, device=gpu)
@@ -52,7 +54,7 @@ def test_layer_splits_past_dispatch_limit(gpu, setup, path):
 
 
 @pytest.mark.timeout(300)
-def test_route_splits_past_dispatch_limit(gpu, setup):
+def test_route_long_input(gpu, setup):
     host, dev_w, x, ref = setup
     names = {"router.weight": "router_weight", "router.bias": "router_bias",
              "experts.gate_up_proj_bias": "gate_up_bias", "experts.down_proj_bias": "down_bias"}
@@ -64,3 +66,25 @@ def test_route_splits_past_dispatch_limit(gpu, setup):
     assert np.array_equal(np.array(route["experts"]), ref["ids"])
     assert len(route["expert_logs"]) == N_TOK
     assert_final_close(bf16_bits(out), ref)
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("path", ["auto", "gemv"])
+def test_layer_splits_past_layer_limit(gpu, path):
+    """66,000 tokens (past KLC_LAYER_MAX_TOKENS): forward() runs two chunks; the result equals two
+    separate calls split elsewhere."""
+    h, i, e, k, n = 64, 32, 8, 2, 66000
+    assert n > nat.LAYER_MAX_TOKENS
+    dev_w = moe.MoELayerWeights.synthetic(72, 0, h, i, e, gpu)
+    layer = moe.MoELayer(dev_w, k, path=path)
+    x = bf16_tensor(moe.synthetic_hidden(72, n, h), gpu)
+    ids = torch.empty((n, k), dtype=torch.int32, device=gpu)
+    out = layer.forward(x, ids=ids)
+    cut = 33000
+    ids_a = torch.empty((cut, k), dtype=torch.int32, device=gpu)
+    ids_b = torch.empty((n - cut, k), dtype=torch.int32, device=gpu)
+    out_a = layer.forward(x[:cut], ids=ids_a)
+    out_b = layer.forward(x[cut:], ids=ids_b)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), np.concatenate([ids_a.cpu().numpy(), ids_b.cpu().numpy()]))
+    assert np.array_equal(bf16_bits(out), np.concatenate([bf16_bits(out_a), bf16_bits(out_b)]))

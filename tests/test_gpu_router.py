@@ -160,10 +160,10 @@ def check_dispatch(gpu, ids, n_exp):
         assert np.array_equal(u[starts[per]:starts[per] + want.size], want)
 
 
-@pytest.mark.parametrize("n_tok,n_exp", [(2048, 128), (9662, 128), (4001, 256), (5000, 3)])
+@pytest.mark.parametrize("n_tok,n_exp", [(2048, 128), (9662, 128), (4001, 256), (5000, 3), (40000, 128)])
 def test_dispatch_skewed_loads(gpu, n_tok, n_exp):
-    """Hot experts take most pairs (one expert > 64 pairs per chunk, runs across the waves' chunk ranges);
-    9662 x 4 = 38648 pairs is the largest dispatch the LDS staging holds."""
+    """Hot experts take most pairs (one expert > 64 pairs per load, runs across the waves' ranges);
+    40000 x 4 = 160000 pairs is past the 38648 a one-workgroup LDS staging could hold."""
     rng = np.random.default_rng(n_tok)
     hot = rng.random((n_tok, 4))
     ids = np.where(hot < 0.3, 7 % n_exp, np.where(hot < 0.45, (n_exp - 1), rng.integers(0, n_exp, (n_tok, 4))))
@@ -172,7 +172,8 @@ def test_dispatch_skewed_loads(gpu, n_tok, n_exp):
 
 def test_dispatch_rejects_too_many_pairs(gpu):
     from klcquant_amd._native import KlcError
-    ids = torch.zeros((38649,), dtype=torch.int32, device=gpu)
+    from klcquant_amd import _native as nat
+    ids = torch.zeros((nat.DISPATCH_MAX_PAIRS + 1,), dtype=torch.int32, device=gpu)
     with pytest.raises(KlcError, match="n_pairs"):
         ops.dispatch(ids.view(-1, 1), 128)
 
