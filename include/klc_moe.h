@@ -247,6 +247,22 @@ int klc_moe_layer(const void* x, const void* router_w, const void* router_b, con
                   int path, void* workspace, int64_t workspace_bytes, void* out, const void* residual, int32_t* ids,
                   void* weights, void* const* events, void* stream);
 
+/* route() of a layer whose experts are resident in HBM, with its expert_logs
+ * (streamed_moe_router.py:257-329 calling _execute_mxfp4_experts, :483-522):
+ * klc_moe_layer's work (no residual, no events; path AUTO, GEMV or GEMM —
+ * FUSED fails with KLC_ERR_UNSUPPORTED) that also writes the routing to ids
+ * (int32 [n_tokens][k]) and weights (bfloat16 [n_tokens][k]), the float32
+ * SwiGLU outputs to gated ([n_tokens*k][inter]) and the expert_logs norms of
+ * :518-519 to norms (float32 [n_tokens*k][2]: |gated|, |expert output|), all
+ * from one call with no host synchronisation.  A caller that places ids,
+ * weights and norms in one buffer reads the whole routing record back with
+ * one copy.  Workspace as klc_moe_layer. */
+int klc_moe_route(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                  const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
+                  int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
+                  int path, void* workspace, int64_t workspace_bytes, void* out, int32_t* ids, void* weights,
+                  float* gated, float* norms, void* stream);
+
 /* The same layer as klc_moe_layer without a workspace argument: it has no
  * counterpart in the reference and is for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses that

@@ -503,7 +503,7 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
                   const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
                   int path, char* ws, void* out, const void* residual, int32_t* ids, void* weights,
-                  void* const* events, void* stream) {
+                  float* gated_raw, float* norms, void* const* events, void* stream) {
   int rc = KLC_OK;
   const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
   void* logits = ws + s.logits;
@@ -566,7 +566,7 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
   if (!gemm && (rc = check_gemv_grid(n_tokens * k, n_experts))) return rc;
   if (gemm) {
     if ((rc = launch_gemm_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden,
-                                  inter, swiglu_limit, precision, gated, nullptr, st)))
+                                  inter, swiglu_limit, precision, gated, gated_raw, st)))
       return rc;
     if ((rc = mark(4))) return rc;
     if ((rc = launch_gemm_down(w_down, down_bias, gated, n_tokens * k, n_experts, offsets, sorted, units, hidden,
@@ -574,7 +574,7 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
       return rc;
   } else {
     if ((rc = launch_gate_up(w_gate_up, gate_up_bias, x, n_tokens, k, n_experts, offsets, sorted, units, hidden,
-                             inter, swiglu_limit, precision, gated, nullptr, st)))
+                             inter, swiglu_limit, precision, gated, gated_raw, st)))
       return rc;
     if ((rc = mark(4))) return rc;
     if ((rc = launch_down(w_down, down_bias, gated, n_tokens * k, n_experts, offsets, sorted, units, hidden, inter,
@@ -583,7 +583,9 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
   }
   if ((rc = mark(5))) return rc;
   if ((rc = launch_combine(eo, w_buf, residual, n_tokens, k, hidden, out, st))) return rc;
-  return mark(6);
+  if ((rc = mark(6))) return rc;
+  if (norms == nullptr) return KLC_OK;
+  return klc_moe_pair_norms(gated_raw, eo, n_tokens * k, inter, hidden, norms, st);
 }
 
 __global__ __launch_bounds__(256) void clear_words_kernel(uint32_t* p, int n) {
@@ -646,7 +648,28 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
   KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "klc_moe_layer: workspace must be 256-byte aligned");
   return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
                        n_experts, k, swiglu_limit, precision, path, static_cast<char*>(workspace), out, residual, ids,
-                       weights, events, stream);
+                       weights, nullptr, nullptr, events, stream);
+}
+
+extern "C" int klc_moe_route(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                             const void* gate_up_bias, const void* const* w_down, const void* down_bias,
+                             int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                             float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
+                             void* out, int32_t* ids, void* weights, float* gated, float* norms, void* stream) {
+  const char* fn = "klc_moe_route";
+  int rc = check_layer_args(fn, x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, out, n_tokens,
+                            hidden, inter, n_experts, k, precision, path);
+  if (rc) return rc;
+  KLC_REQUIRE(workspace && ids && weights && gated && norms, KLC_ERR_ARGUMENT, "%s: null pointer", fn);
+  KLC_REQUIRE(path != KLC_PATH_FUSED, KLC_ERR_UNSUPPORTED,
+              "%s: the one-launch layer keeps no float32 SwiGLU outputs for the norms", fn);
+  const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
+  KLC_REQUIRE(workspace_bytes >= s.total, KLC_ERR_ARGUMENT, "%s: workspace of %lld bytes < %lld needed", fn,
+              (long long)workspace_bytes, (long long)s.total);
+  KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "%s: workspace must be 256-byte aligned", fn);
+  return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
+                       n_experts, k, swiglu_limit, precision, path, static_cast<char*>(workspace), out, nullptr, ids,
+                       weights, gated, norms, nullptr, stream);
 }
 
 extern "C" int klc_moe_layer_static_scratch(const void* x, const void* router_w, const void* router_b,
@@ -668,5 +691,6 @@ extern "C" int klc_moe_layer_static_scratch(const void* x, const void* router_w,
   char* ws = nullptr;
   if ((rc = static_scratch_address(fn, as_stream(stream), &ws))) return rc;
   return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
-                       n_experts, k, swiglu_limit, precision, path, ws, out, residual, ids, weights, events, stream);
+                       n_experts, k, swiglu_limit, precision, path, ws, out, residual, ids, weights, nullptr, nullptr,
+                       events, stream);
 }

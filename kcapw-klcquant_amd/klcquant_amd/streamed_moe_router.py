@@ -36,6 +36,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from . import _native as nat
 from . import ops
 from .mxfp4_expert import Mxfp4ExpertStore, ResidentExpertStore
 
@@ -139,6 +140,17 @@ class RouterStats:
         delta = {name: int(after.get(name, 0)) - int(before.get(name, 0)) for name in ("hits", "misses", "evictions")}
         self.cache_delta_events.append({"position": int(position), "layer": int(layer_idx),
                                         "experts": [int(e) for e in experts], **delta})
+
+    def record_cache_deltas(self, layer_idx: int, positions: list[int], experts_rows: list[list[int]], before: dict,
+                            after: dict) -> None:
+        """record_cache_delta for each row of a batch: the first row carries the traffic between the two
+        snapshots, the later rows (snapshot ``after`` on both sides) none."""
+        layer_idx = int(layer_idx)
+        first = {name: int(after.get(name, 0)) - int(before.get(name, 0)) for name in ("hits", "misses", "evictions")}
+        later = {name: int(after.get(name, 0)) - int(after.get(name, 0)) for name in ("hits", "misses", "evictions")}
+        self.cache_delta_events.extend(
+            {"position": int(p), "layer": layer_idx, "experts": [int(e) for e in row], **(later if r else first)}
+            for r, (p, row) in enumerate(zip(positions, experts_rows)))
 
     def record_cap_event(self, layer_idx: int, position: int, old_cap: int, new_cap: int, reason: str, hits: int,
                          misses: int, evictions: int) -> None:
@@ -244,6 +256,9 @@ class StreamedMoERouter:
         self.workload_scores: dict[int, dict[int, float]] = {}
         self.recent_history: dict[int, deque[int]] = {}
         self.dynamic_caps: dict[int, int] = {}
+        # scratch of the resident-store path per (device, stream): workspace, float32 SwiGLU rows,
+        # routing record on the device and its pinned host copy
+        self._route_scratch: dict[tuple, tuple[torch.Tensor, ...]] = {}
 
     # ---- the routed layer -------------------------------------------------------------
 
@@ -262,12 +277,23 @@ class StreamedMoERouter:
         positions = [int(position)] * n_tok if isinstance(position, int) else [int(p) for p in position]
         if len(positions) != n_tok:
             raise ValueError(f"{len(positions)} positions for {n_tok} tokens")
-        logits = ops.router_logits(x, router_w, router_b)
-        n_exp = logits.shape[1]
-        k = self._effective_expert_count(layer_idx, n_exp)
         resident = sorted(int(e) for e in (resident_experts or set()))
         gu_bias = tensors.get(f"{prefix}.experts.gate_up_proj_bias")
         d_bias = tensors.get(f"{prefix}.experts.down_proj_bias")
+        run_experts = execute_experts and expert_store is not None
+        if (run_experts and not self.locality_config.enabled and isinstance(expert_store, ResidentExpertStore)
+                and gu_bias is not None and d_bias is not None):
+            # the whole layer and its expert_logs in one library call, read back with one copy
+            k = self._effective_expert_count(layer_idx, int(router_w.shape[0]))
+            before = self._cache_snapshot(expert_store)
+            output, host, norms = self._route_resident(layer_idx, x, router_w, router_b, gu_bias, d_bias,
+                                                       expert_store, k)
+            return self._finish_route(layer_idx, k, batched, positions, predicted_experts, resident, host,
+                                      output.reshape(hidden.shape), "mxfp4_expert_matmul", True, norms,
+                                      expert_store, before, False)
+        logits = ops.router_logits(x, router_w, router_b)
+        n_exp = logits.shape[1]
+        k = self._effective_expert_count(layer_idx, n_exp)
 
         if not self.locality_config.enabled:
             ids, _, weights = ops.topk_softmax(logits, k)
@@ -276,8 +302,8 @@ class StreamedMoERouter:
             ids, weights, host = self._select_on_host(layer_idx, logits, k, resident_experts or set(), positions)
         recorded = host is not None  # the locality path records each row while it selects
 
-        run_experts = execute_experts and expert_store is not None
         norms = None
+        before = None
         if run_experts:
             before = self._cache_snapshot(expert_store)
             if host is None and not isinstance(expert_store, ResidentExpertStore):
@@ -301,6 +327,15 @@ class StreamedMoERouter:
 
         if host is None:
             host = self._read_back(ids, weights)
+        if norms is not None:
+            norms = norms.cpu().tolist()
+        return self._finish_route(layer_idx, k, batched, positions, predicted_experts, resident, host, output,
+                                  mode, run_experts, norms, expert_store, before, recorded)
+
+    def _finish_route(self, layer_idx, k, batched, positions, predicted_experts, resident, host, output, mode,
+                      run_experts, norms, expert_store, before, recorded):
+        """RouterStats bookkeeping and the route dict (streamed_moe_router.py:296-329)."""
+        n_tok = len(positions)
         if not recorded:
             for r in range(n_tok):  # locality disabled: the selection is the raw top-k
                 predicted = [int(e) for e in (predicted_experts if predicted_experts is not None
@@ -325,15 +360,12 @@ class StreamedMoERouter:
 
         route = {"experts": per_token(experts_rows), "weights": per_token(weight_rows), "mode": mode}
         if norms is not None:
-            norms = norms.cpu().tolist()
             logs = [[{"expert": int(e), "routing_weight": float(w), "gate_up_norm": float(norms[r * k + j][0]),
                       "output_norm": float(norms[r * k + j][1])}
                      for j, (e, w) in enumerate(zip(experts_rows[r], weight_rows[r]))] for r in range(n_tok)]
             route["expert_logs"] = per_token(logs)
         after = self._cache_snapshot(expert_store)
-        for r in range(n_tok):  # a batch's cache traffic is booked on its first row
-            self.stats.record_cache_delta(layer_idx, positions[r], experts_rows[r], before if r == 0 else after,
-                                          after)
+        self.stats.record_cache_deltas(layer_idx, positions, experts_rows, before, after)  # booked on the first row
         self._adapt_active_cap(layer_idx, positions[-1], before, after)
         route.update({"raw_experts": per_token(raw_rows), "predicted_experts": per_token(predicted_rows),
                       "resident_experts": resident, "sticky_adjusted": per_token(adjusted_rows),
@@ -341,6 +373,84 @@ class StreamedMoERouter:
         return output, route
 
     # ---- device work ---------------------------------------------------------------------
+
+    # Workspaces up to this size stay with the router between calls; larger
+    # ones (long prefills) are allocated per call.
+    _KEEP_SCRATCH_BYTES = 256 << 20
+
+    def _scratch(self, dev, stream, n_tok, hidden, inter, n_exp, k):
+        """Workspace (zero-filled when made), float32 SwiGLU buffer and routing record (device and
+        pinned host) for one klc_moe_route call.
+
+        One set serves every batch size and layer on a stream: the call lays
+        the workspace out for its own sizes, any larger buffer will do, and
+        calls on one stream run in order; the host reads a record before the
+        next call on the stream is made.
+        """
+        need = (ops.workspace_bytes(n_tok, hidden, inter, n_exp, k), n_tok * k * inter, 4 * n_tok * k)
+        key = (dev, stream.value)
+        held = self._route_scratch.get(key)
+        if held is not None and all(t.numel() >= n for t, n in zip(held, need)):
+            return held
+        size = [max(n, held[i].numel() if held else 0) for i, n in enumerate(need)]
+        made = (torch.zeros(size[0], dtype=torch.uint8, device=dev),
+                torch.empty(size[1], dtype=torch.float32, device=dev),
+                torch.empty(size[2], dtype=torch.int32, device=dev),
+                torch.empty(size[2], dtype=torch.int32, pin_memory=True))
+        if need[0] + 4 * need[1] <= self._KEEP_SCRATCH_BYTES:
+            self._route_scratch[key] = made
+        return made
+
+    def _route_resident(self, layer_idx, x, router_w, router_b, gu_bias, d_bias, store, k):
+        """route() for a layer resident in HBM: klc_moe_route per chunk of at most
+        ``ops.max_tokens_per_call(k)`` tokens, then one device->host copy of
+        the routing record (ids, bf16 weights and expert_logs norms in one
+        int32 buffer).
+
+        Returns the bf16 output ``[B, H]``, the host row lists of
+        :meth:`_read_back` and the per-pair ``[gate_up_norm, output_norm]``.
+        """
+        ops._check_gpu("hidden", x, torch.bfloat16, 2)
+        ops._check_gpu("router weight", router_w, torch.bfloat16, 2)
+        ops._check_gpu("router bias", router_b, torch.bfloat16, 1)
+        ops._check_gpu("gate_up bias", gu_bias, torch.bfloat16, 2)
+        ops._check_gpu("down bias", d_bias, torch.bfloat16, 2)
+        w = store.layer(layer_idx)
+        dev = ops._same_device(x, router_w, router_b, gu_bias, d_bias, w.gate_up_table)
+        n_tok, hidden = x.shape
+        if n_tok == 0:
+            raise ValueError("route() needs at least one token")
+        n_exp, inter = w.n_experts, w.inter
+        if tuple(router_w.shape) != (n_exp, hidden) or tuple(router_b.shape) != (n_exp,):
+            raise ValueError(f"router shapes mismatch: x {tuple(x.shape)}, weight {tuple(router_w.shape)}, "
+                             f"bias {tuple(router_b.shape)}, {n_exp} resident experts")
+        if hidden != w.hidden or tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
+            raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
+                             f"E={n_exp} H={w.hidden} I={inter} (hidden {hidden})")
+        store.record_access(layer_idx, 2 * n_tok * k)
+        out = torch.empty_like(x)
+        stream = ops._stream(dev)
+        chunk = ops.max_tokens_per_call(k)
+        experts, weights, norms = [], [], []
+        for t0 in range(0, n_tok, chunk):
+            t1 = min(n_tok, t0 + chunk)
+            pairs = (t1 - t0) * k
+            half = (pairs + 1) // 2
+            ws, gated, rec, rec_host = self._scratch(dev, stream, t1 - t0, hidden, inter, n_exp, k)
+            n_rec = pairs + half + 2 * pairs
+            nat.call("klc_moe_route", ops._ptr(x[t0:t1]), ops._ptr(router_w), ops._ptr(router_b),
+                     ops._ptr(w.gate_up_table), ops._ptr(gu_bias), ops._ptr(w.down_table), ops._ptr(d_bias),
+                     t1 - t0, hidden, inter, n_exp, k, self.swiglu_limit, ops.PRECISIONS[self.matmul_precision],
+                     nat.PATH_AUTO, ops._ptr(ws), ws.numel(), ops._ptr(out[t0:t1]), ops._ptr(rec),
+                     ops._ptr(rec[pairs:]), ops._ptr(gated), ops._ptr(rec[pairs + half:]), stream)
+            rec_host[:n_rec].copy_(rec[:n_rec], non_blocking=True)
+            torch.cuda.current_stream(dev).synchronize()
+            r = rec_host[:n_rec].numpy()
+            experts += r[:pairs].reshape(t1 - t0, k).tolist()
+            bits = r[pairs:pairs + half].view(np.uint16)[:pairs].astype(np.uint32) << 16
+            weights += bits.view(np.float32).reshape(t1 - t0, k).tolist()
+            norms += r[pairs + half:].view(np.float32).reshape(pairs, 2).tolist()
+        return out, (experts, weights, [list(row) for row in experts], [False] * n_tok, []), norms
 
     @staticmethod
     def _read_back(ids: torch.Tensor, weights: torch.Tensor):
@@ -388,10 +498,13 @@ class StreamedMoERouter:
         outs, norms = [], []
         for t0 in range(0, n_tok, chunk):
             t1 = min(n_tok, t0 + chunk)
+            # the expert kernels klc_moe_layer would pick for this chunk, so both stores give the same bits
+            gemm = nat.call("klc_moe_layer_path", t1 - t0, hidden, inter, n_exp, k, nat.PATH_AUTO,
+                            ops._stream(x.device)) == nat.PATH_GEMM
             disp = ops.dispatch(ids[t0:t1], n_exp)
             gated, gated_raw = ops.gate_up(gu_table, gu_bias, x[t0:t1], k, disp, hidden, inter,
-                                           self.swiglu_limit, self.matmul_precision, want_raw=True)
-            eo = ops.down(d_table, d_bias, gated, disp, hidden, inter, self.matmul_precision)
+                                           self.swiglu_limit, self.matmul_precision, want_raw=True, gemm=gemm)
+            eo = ops.down(d_table, d_bias, gated, disp, hidden, inter, self.matmul_precision, gemm=gemm)
             outs.append(ops.combine(eo, weights[t0:t1], t1 - t0, k))
             norms.append(ops.pair_norms(gated_raw, eo))
         if len(outs) == 1:

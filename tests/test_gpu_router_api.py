@@ -289,3 +289,54 @@ def test_locality_sticky_bonus_changes_selection(gpu, setup):
     from oracle.router import softmax_weights
     assert route["weights"] == bf16_to_f32(softmax_weights(np.array([adjusted], np.float32)))[0].tolist()
     assert route["experts"][1:] == order[:K - 1]
+
+
+def test_route_batch_gemm_streaming_matches_resident(gpu, setup, tmp_path):
+    """40 tokens at E = 16 take the grouped GEMM (n_tokens * k >= 8 * n_experts) in both stores: the resident
+    store's one-call path (klc_moe_route) and the streaming store's separate kernels give the same bits,
+    the same routing and the same expert_logs."""
+    host, dev_w = setup
+    write_checkpoint(tmp_path, host)
+    tensors = layer_tensors(host, gpu)
+    per_expert = dev_w.gate_up.shape[1] + dev_w.down.shape[1]
+    store = Mxfp4ExpertStore(tmp_path, tmp_path, gpu, dtype=torch.bfloat16, cache_bytes=E * per_expert)
+    x = moe.synthetic_hidden(WORKLOAD, 40, H, step=6)
+    assert moe.MoELayer(dev_w, K).layer_path(40) == "gemm"
+    out_s, route_s = StreamedMoERouter(K).route(0, bf16_tensor(x, gpu), tensors, store, position=list(range(40)))
+    out_r, route_r = StreamedMoERouter(K).route(0, bf16_tensor(x, gpu), tensors, ResidentExpertStore({0: dev_w}),
+                                                position=list(range(40)))
+    assert torch.equal(out_s, out_r)
+    for key in ("experts", "weights", "raw_experts", "expert_logs", "mode", "active_expert_cap"):
+        assert route_s[key] == route_r[key], key
+    check_route(out_r, route_r, host, x, True)
+
+
+def layer_tensor_dict(w, layer=0):
+    p = f"model.layers.{layer}.mlp"
+    return {f"{p}.router.weight": w.router_weight, f"{p}.router.bias": w.router_bias,
+            f"{p}.experts.gate_up_proj_bias": w.gate_up_bias, f"{p}.experts.down_proj_bias": w.down_bias}
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_route_120b_matches_layer(gpu, precision):
+    """gpt-oss-120B shape: route() on a resident store gives klc_moe_layer's bits and routing at decode batches
+    (1, 8, 64, GEMV) and a prefill chunk (300 tokens, GEMM), one router serving every size in turn."""
+    w = moe.MoELayerWeights.synthetic(75, 0, 2880, 2880, 128, gpu)
+    layer = moe.MoELayer(w, 4, precision=precision)
+    router = StreamedMoERouter(4, matmul_precision=precision)
+    store = ResidentExpertStore({0: w})
+    tensors = layer_tensor_dict(w)
+    for step, n_tok in enumerate((8, 64, 1, 300, 8)):
+        print(f"[route-120b] {precision} B={n_tok}", flush=True)
+        xt = bf16_tensor(moe.synthetic_hidden(75, n_tok, 2880, step=step), gpu)
+        ids = torch.empty((n_tok, 4), dtype=torch.int32, device=gpu)
+        wts = torch.empty((n_tok, 4), dtype=torch.bfloat16, device=gpu)
+        want = layer.forward(xt, ids=ids, weights=wts)
+        out, route = router.route(0, xt, tensors, store, position=list(range(n_tok)))
+        assert torch.equal(out, want), f"B={n_tok}"
+        assert route["experts"] == ids.cpu().tolist()
+        assert route["weights"] == wts.float().cpu().tolist()
+        norms = np.array([[e["gate_up_norm"], e["output_norm"]] for row in route["expert_logs"] for e in row])
+        assert norms.shape == (n_tok * 4, 2) and np.isfinite(norms).all() and (norms > 0).all()
+    assert router.stats.routed_tokens == 8 + 64 + 1 + 300 + 8
+    assert store.cache.stats.hits == 2 * 4 * router.stats.routed_tokens
