@@ -47,14 +47,23 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 #ifndef KLC_GEMM_WAVES
 #define KLC_GEMM_WAVES 4
 #endif
-constexpr int kGemmWaves = KLC_GEMM_WAVES;          // one 64-row tile per wave
+#ifndef KLC_GEMM_WAVE_TILES
+#define KLC_GEMM_WAVE_TILES 1
+#endif
+constexpr int kGemmWaves = KLC_GEMM_WAVES;
+constexpr int kWaveTiles = KLC_GEMM_WAVE_TILES;     // 64-row packed tiles per wave
+constexpr int kRb = 4 * kWaveTiles;                 // 16-row MFMA blocks per wave
 constexpr int kGemmThreads = kGemmWaves * kWave;
-constexpr int kGemmRows = kGemmWaves * kTileRows;   // output rows per workgroup
+constexpr int kGemmRows = kGemmWaves * kWaveTiles * kTileRows;  // output rows per workgroup
 constexpr int kBRowsPerWave = kUnitTokensGemm / kGemmWaves;  // token rows each wave stages per step
 constexpr int kBInstr = kBRowsPerWave / 4;          // LDS-DMA instructions per wave, plane and step (4 rows each)
 static_assert(kBInstr >= 1 && kBRowsPerWave % 4 == 0, "token rows split evenly over the waves");
 constexpr int kYStride = kGemmRows / 2 + 1;         // gate_up epilogue: floats per token row (odd: spreads the banks)
-constexpr int kGemmCb = kUnitTokensGemm / 16;       // 8 column blocks of 16 tokens
+constexpr int kGemmCb = kUnitTokensGemm / 16;       // 4 column blocks of 16 tokens
+template <int N>
+struct ColumnBlocks {
+  static constexpr int value = N;
+};
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
 #ifndef KLC_GEMM_RING_UP
 #define KLC_GEMM_RING_UP 4
@@ -110,8 +119,11 @@ __host__ __device__ constexpr int gemm_lds_bytes() {
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
 // [2][pairs][in_down] (and float32 SwiGLU output to out_raw if set).  down:
 // act = those planes (rows by pair); writes float32 expert outputs.
+#ifndef KLC_GEMM_WAVES_PER_EU
+#define KLC_GEMM_WAVES_PER_EU 2
+#endif
 template <bool kDown>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_kernel(
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KLC_GEMM_WAVES_PER_EU))) void moe_gemm_kernel(
     const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
@@ -121,7 +133,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   constexpr int kRing = gemm_ring<kDown>();
   constexpr int kStage = gemm_stage_bytes<kDown>();  // one step: 64 token rows x 256 bytes per plane
   constexpr int kPlaneStage = kStage / kPlanes;
-  constexpr int kLoadsPerStep = 4 + kBInstr * kPlanes;  // A: 4 chunks; B: kBInstr instructions per plane
+  constexpr int kLoadsPerStep = kRb + kBInstr * kPlanes;  // A: a chunk per row block; B: kBInstr per plane
+  static_assert((kRing - 2) * kLoadsPerStep <= 63, "the ring's outstanding loads fit the vmcnt field");
   extern __shared__ __align__(16) uint8_t stage[];    // kRing x kStage
 
   // XCD-aware order: workgroups are handed to the 8 XCDs round-robin, so XCD
@@ -144,8 +157,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   const int lr = lane & 15;
   const int lq = lane >> 4;
   const int tiles = rows / kTileRows;
-  const int tile = row_wg * kGemmWaves + wave;
-  const bool wave_live = tile < tiles;
+  const int tile0 = (row_wg * kGemmWaves + wave) * kWaveTiles;  // the wave's first 64-row tile
+  const bool wave_live = tile0 < tiles;
   const int in_dim = groups * 32;
   const int steps = (groups + 3) >> 2;
 
@@ -179,10 +192,18 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 
   // ---- A stream: the wave's 64-row tile, 4 row blocks; steps past the end
   // load out of range (zeros, no traffic, no branch) ----
-  const int wtile = wave_live ? tile : 0;
+  // (a tile past the matrix reads tile 0's scales and no weights)
   const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
       (void*)wptr[e], (short)0, (int)packed_matrix_bytes(rows, groups), kBufferWord3);
-  const uint32_t tile_off = (uint32_t)wtile * (uint32_t)groups * 1024u;
+  int wtile[kWaveTiles];
+  bool tile_live[kWaveTiles];
+  uint32_t tile_off[kWaveTiles];
+#pragma unroll
+  for (int i = 0; i < kWaveTiles; ++i) {
+    tile_live[i] = tile0 + i < tiles;
+    wtile[i] = tile_live[i] ? tile0 + i : 0;
+    tile_off[i] = (uint32_t)wtile[i] * (uint32_t)groups * 1024u;
+  }
   const int rec = (int)packed_scale_record(groups);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
   // With the step loop unrolled, the lane's whole scale record (one byte per
@@ -195,29 +216,29 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // themselves.  (Words past a shorter record repeat its last word.)
   // (three separately named arrays: the per-step choice among them is a
   // select, where one array indexed by a run-time word would go to scratch)
-  u32x2_t srec0[4], srec1[4], srec2[4];
+  u32x2_t srec0[kRb], srec1[kRb], srec2[kRb];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    const int row = wtile * kTileRows + rb * 16 + lr;
+  for (int rb = 0; rb < kRb; ++rb) {
+    const int row = wtile[rb >> 2] * kTileRows + (rb & 3) * 16 + lr;
     srec0[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, (uint32_t)packed_scale_word(groups, row, 0, lq), scale_base, 0);
     srec1[rb] = __builtin_amdgcn_raw_buffer_load_b64(
         wbuf, (uint32_t)packed_scale_word(groups, row, min(1, rec / 8 - 1), lq), scale_base, 0);
     srec2[rb] = __builtin_amdgcn_raw_buffer_load_b64(
         wbuf, (uint32_t)packed_scale_word(groups, row, min(2, rec / 8 - 1), lq), scale_base, 0);
   }
-  auto a_load = [&](int s, u32x4_t (&a)[4]) {
+  auto a_load = [&](int s, u32x4_t (&a)[kRb]) {
     const bool ok = s < steps && 4 * s + lq < groups;
     const int sc = min(s, steps - 1);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const uint32_t v = ok ? (uint32_t)(lq * 1024 + (rb * 16 + lr) * 16) : kOutOfRange;
-      a[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off + 4096u * sc, 0);
+    for (int rb = 0; rb < kRb; ++rb) {
+      const uint32_t v = ok && tile_live[rb >> 2] ? (uint32_t)(lq * 1024 + ((rb & 3) * 16 + lr) * 16) : kOutOfRange;
+      a[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off[rb >> 2] + 4096u * sc, 0);
     }
   };
 
-  f32x4_t acc[4][kGemmCb];
+  f32x4_t acc[kRb][kGemmCb];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < kRb; ++rb)
 #pragma unroll
     for (int cb = 0; cb < kGemmCb; ++cb) acc[rb][cb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -226,23 +247,31 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
   for (int j = 0; j < 4; ++j) b_off[j] = lr * 256 + (((4 * lq + j) ^ lr) << 4);
 
-  auto compute = [&](int s, int slot, const u32x4_t (&a_cur)[4]) {
-    const bool live = 4 * s + lq < groups;
-    const int d = min(s >> 2, 5);  // dword of the lane's scales holding step s
-    float scale[4];
+  // The lane's scale dword holding step s (4 steps per dword, at most 6 dwords).
+  auto scale_words = [&](int s, uint32_t (&word)[kRb]) {
+    const int d = min(s >> 2, 5);
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < kRb; ++rb) {
       const u32x2_t pair = d >= 4 ? srec2[rb] : ((d & 2) ? srec1[rb] : srec0[rb]);
-      const uint32_t word = (d & 1) ? pair.y : pair.x;
-      scale[rb] = cvt_scale_operand((word >> (8 * (s & 3))) & 0xffu, live);
+      word[rb] = (d & 1) ? pair.y : pair.x;
     }
+  };
+
+  // Step s for a unit of kNcb 16-token column blocks (a compile-time count,
+  // so the MFMAs and their LDS reads are straight-line code the compiler can
+  // pipeline; blocks past the unit's tokens are neither read nor multiplied).
+  auto compute = [&](auto ncb_c, int s, int slot, const u32x4_t (&a_cur)[kRb], const uint32_t (&word)[kRb]) {
+    constexpr int kNcb = decltype(ncb_c)::value;
+    const bool live = 4 * s + lq < groups;
+    float scale[kRb];
+#pragma unroll
+    for (int rb = 0; rb < kRb; ++rb) scale[rb] = cvt_scale_operand((word[rb] >> (8 * (s & 3))) & 0xffu, live);
     const uint8_t* base = stage + slot * kStage;
     // the B operands of a quarter are read one quarter ahead of their MFMAs
-    // (unconditionally: the stage always holds 64 token rows)
-    bf16x8_t bq[2][kGemmCb][kPlanes];
-    auto load_b = [&](int j, bf16x8_t (&dst)[kGemmCb][kPlanes]) {
+    bf16x8_t bq[2][kNcb][kPlanes];
+    auto load_b = [&](int j, bf16x8_t (&dst)[kNcb][kPlanes]) {
 #pragma unroll
-      for (int cb = 0; cb < kGemmCb; ++cb)
+      for (int cb = 0; cb < kNcb; ++cb)
 #pragma unroll
         for (int pl = 0; pl < kPlanes; ++pl)
           dst[cb][pl] = *reinterpret_cast<const bf16x8_t*>(base + pl * kPlaneStage + cb * 16 * 256 + b_off[j]);
@@ -251,24 +280,20 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (j < 3) load_b(j + 1, bq[(j + 1) & 1]);
-      bf16x8_t a[4];
+      bf16x8_t a[kRb];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) a[rb] = decode8(a_cur[rb][j], scale[rb]);
+      for (int rb = 0; rb < kRb; ++rb) a[rb] = decode8(a_cur[rb][j], scale[rb]);
 #pragma unroll
-      for (int cb = 0; cb < kGemmCb; ++cb) {
-        if (cb < ncb) {
+      for (int cb = 0; cb < kNcb; ++cb)
 #pragma unroll
-          for (int pl = 0; pl < kPlanes; ++pl) {
+        for (int pl = 0; pl < kPlanes; ++pl)
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-              acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], bq[j & 1][cb][pl], acc[rb][cb], 0, 0, 0);
-          }
-        }
-      }
+          for (int rb = 0; rb < kRb; ++rb)
+            acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], bq[j & 1][cb][pl], acc[rb][cb], 0, 0, 0);
     }
   };
 
-  u32x4_t a_ring[kRing][4];
+  u32x4_t a_ring[kRing][kRb];
 #pragma unroll
   for (int i = 0; i < kRing - 1; ++i) {
     a_load(i, a_ring[i]);
@@ -281,16 +306,30 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
   // constants, and run to a multiple of kRing steps with no branch around a
   // step (the steps past the end multiply zeros: A loads out of range and
   // its scales are 0), so no register of an in-flight load is copied.
+  // The scale dwords are picked at a group's first step and again where a
+  // step starts a new dword (s % 4 == 0); with kRing dividing 4 every group
+  // starts at a multiple of kRing and needs only the first pick.
   const int steps_pad = (steps + kRing - 1) / kRing * kRing;
-  for (int s0 = 0; s0 < steps_pad; s0 += kRing) {
+  auto run = [&](auto ncb_c) {
+    for (int s0 = 0; s0 < steps_pad; s0 += kRing) {
+      uint32_t word[kRb];
 #pragma unroll
-    for (int uu = 0; uu < kRing; ++uu) {
-      const int s = s0 + uu;
-      ring_barrier<(kRing - 2) * kLoadsPerStep>();
-      a_load(s + kRing - 1, a_ring[(uu + kRing - 1) % kRing]);
-      b_dma(s + kRing - 1, (uu + kRing - 1) % kRing);
-      if (wave_live) compute(s, uu, a_ring[uu]);
+      for (int uu = 0; uu < kRing; ++uu) {
+        const int s = s0 + uu;
+        if (uu == 0 || (4 % kRing != 0 && (s & 3) == 0)) scale_words(s, word);
+        ring_barrier<(kRing - 2) * kLoadsPerStep>();
+        a_load(s + kRing - 1, a_ring[(uu + kRing - 1) % kRing]);
+        b_dma(s + kRing - 1, (uu + kRing - 1) % kRing);
+        if (wave_live) compute(ncb_c, s, uu, a_ring[uu], word);
+      }
     }
+  };
+  static_assert(kGemmCb == 4, "one loop per column-block count");
+  switch (ncb) {  // uniform over the workgroup
+    case 1: run(ColumnBlocks<1>{}); break;
+    case 2: run(ColumnBlocks<2>{}); break;
+    case 3: run(ColumnBlocks<3>{}); break;
+    default: run(ColumnBlocks<4>{}); break;
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no LDS-DMA may outlive the workgroup
 
@@ -308,8 +347,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         if (cb >= ncb) continue;
         const int c = cb * 16 + lr;
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-          const int row0 = tile * kTileRows + rb * 16 + 4 * lq;
+        for (int rb = 0; rb < kRb; ++rb) {
+          if (!tile_live[rb >> 2]) continue;
+          const int row0 = tile0 * kTileRows + rb * 16 + 4 * lq;
           const f32x4_t v4 = acc[rb][cb];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -320,7 +360,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
             }
             gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
             up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
-            ytile[c * kYStride + wave * 32 + rb * 8 + 2 * lq + h] = swiglu(gate, up, limit);
+            ytile[c * kYStride + wave * (kRb * 8) + rb * 8 + 2 * lq + h] = swiglu(gate, up, limit);
           }
         }
       }
@@ -367,8 +407,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
       if (c >= nt) continue;
       const int p = pairs[pb + tc + c];
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        const int row0 = tile * kTileRows + rb * 16 + 4 * lq;
+      for (int rb = 0; rb < kRb; ++rb) {
+        if (!tile_live[rb >> 2]) continue;
+        const int row0 = tile0 * kTileRows + rb * 16 + 4 * lq;
         const f32x4_t v4 = acc[rb][cb];
         float o[4];
 #pragma unroll
