@@ -65,8 +65,10 @@ struct ColumnBlocks {
   static constexpr int value = N;
 };
 constexpr int kXcds = 8;  // accelerator complex dies of an MI355X, each with its own L2
+// Ring depths (steps in flight + 1).  gate_up: 3 keeps the kernel within
+// 256 VGPRs without spilling (4 measured the same and spills 20 bytes).
 #ifndef KLC_GEMM_RING_UP
-#define KLC_GEMM_RING_UP 4
+#define KLC_GEMM_RING_UP 3
 #endif
 #ifndef KLC_GEMM_RING_DOWN
 #define KLC_GEMM_RING_DOWN 2
@@ -290,6 +292,17 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
 #pragma unroll
           for (int rb = 0; rb < kRb; ++rb)
             acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], bq[j & 1][cb][pl], acc[rb][cb], 0, 0, 0);
+      if constexpr (kDown) {
+        // down (two planes): each quarter's B read, its kRb MFMAs and kRb VALU
+        // instructions as one group, in order (330 against 345 us on the
+        // 2048-token layer; the same grouping made gate_up spill and slower)
+#pragma unroll
+        for (int i = 0; i < kNcb * kPlanes; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, kRb, 0); // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, kRb, 0); // VALU
+        }
+      }
     }
   };
 
