@@ -82,6 +82,22 @@ def test_argument_errors_before_any_launch():
     assert ei.value.status == nat.KLC_ERR_ARGUMENT
 
 
+def test_route_entry_argument_errors():
+    """klc_moe_route: its own outputs may not be NULL, and the one-launch path (which keeps no float32
+    SwiGLU outputs) is refused; both before any device work."""
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    args = [fake] * 7 + [2, 2880, 2880, 128, 4, 7.0, nat.PRECISION_FP32]
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_route", *args, nat.PATH_AUTO, fake, 1 << 30, fake, fake, fake, None, fake, None)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "null pointer" in ei.value.message
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_route", *args, nat.PATH_FUSED, fake, 1 << 30, fake, fake, fake, fake, fake, None)
+    assert ei.value.status == nat.KLC_ERR_UNSUPPORTED and "float32 SwiGLU" in ei.value.message
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_route", *args, nat.PATH_AUTO, fake, 256, fake, fake, fake, fake, fake, None)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "workspace" in ei.value.message
+
+
 def test_units_size():
     lib = nat.load()
     # 256 pairs over 128 experts: gate_up (256 + 7 * 128) // 8 = 144, down (256 + 3 * 128) // 4 = 160,
