@@ -88,3 +88,24 @@ def test_layer_splits_past_layer_limit(gpu, path):
     torch.cuda.synchronize()
     assert np.array_equal(ids.cpu().numpy(), np.concatenate([ids_a.cpu().numpy(), ids_b.cpu().numpy()]))
     assert np.array_equal(bf16_bits(out), np.concatenate([bf16_bits(out_a), bf16_bits(out_b)]))
+
+
+@pytest.mark.timeout(300)
+def test_route_splits_past_layer_limit(gpu):
+    """route() on a resident store past KLC_LAYER_MAX_TOKENS: one klc_moe_route call per row chunk and one
+    read-back each; outputs and routing equal one layer forward over the whole input, bit for bit."""
+    h, i, e, k, n = 64, 32, 8, 2, 66000
+    dev_w = moe.MoELayerWeights.synthetic(73, 0, h, i, e, gpu)
+    p = "model.layers.0.mlp"
+    tensors = {f"{p}.router.weight": dev_w.router_weight, f"{p}.router.bias": dev_w.router_bias,
+               f"{p}.experts.gate_up_proj_bias": dev_w.gate_up_bias, f"{p}.experts.down_proj_bias": dev_w.down_bias}
+    x = bf16_tensor(moe.synthetic_hidden(73, n, h), gpu)
+    ids = torch.empty((n, k), dtype=torch.int32, device=gpu)
+    wts = torch.empty((n, k), dtype=torch.bfloat16, device=gpu)
+    want = moe.MoELayer(dev_w, k).forward(x, ids=ids, weights=wts)
+    out, route = StreamedMoERouter(k).route(0, x, tensors, ResidentExpertStore({0: dev_w}))
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(out), bf16_bits(want))
+    assert route["experts"] == ids.cpu().tolist()
+    assert route["weights"] == wts.float().cpu().tolist()
+    assert len(route["expert_logs"]) == n and route["expert_logs"][-1][0]["expert"] == route["experts"][-1][0]
