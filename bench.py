@@ -81,6 +81,8 @@ def parse_args():
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
     ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
     ap.add_argument("--skip-lm-head", action="store_true", help="skip the lm_head logits measurement")
+    ap.add_argument("--route-calls", type=int, default=300,
+                    help="timed single-token StreamedMoERouter.route() calls (0 = skip)")
     ap.add_argument("--skip-attention", action="store_true", help="skip the decode attention measurement")
     ap.add_argument("--loader-experts", type=int, default=16,
                     help="experts of the expert-store miss measurement (0 = skip)")
@@ -464,6 +466,48 @@ def layer_tensor_bench(torch, dev, n_layers: int = 4, rounds: int = 3) -> dict:
     }
 
 
+def route_api_bench(torch, dev, weights, calls: int, precision: str) -> dict:
+    """The drop-in call itself: StreamedMoERouter.route() on one token per call (how the reference's
+    executor routes), resident store, with its read-back and RouterStats bookkeeping; median wall time
+    per call, next to one klc_moe_layer call plus a host synchronisation on the same token."""
+    import numpy as np
+
+    from klcquant_amd import moe
+    from klcquant_amd.mxfp4_expert import ResidentExpertStore
+    from klcquant_amd.streamed_moe_router import StreamedMoERouter
+
+    p = "model.layers.0.mlp"
+    tensors = {f"{p}.router.weight": weights.router_weight, f"{p}.router.bias": weights.router_bias,
+               f"{p}.experts.gate_up_proj_bias": weights.gate_up_bias,
+               f"{p}.experts.down_proj_bias": weights.down_bias}
+    store = ResidentExpertStore({0: weights})
+    router = StreamedMoERouter(TOPK, 7.0, matmul_precision=precision)
+    layer = moe.MoELayer(weights, TOPK, 7.0, precision)
+    xs = [torch.from_numpy(moe.synthetic_hidden(WORKLOAD, 1, HIDDEN, step=s).view(np.int16)).view(torch.bfloat16)
+          .to(dev) for s in range(8)]
+
+    def timed(fn) -> float:
+        for s in range(20):
+            fn(s)
+        torch.cuda.synchronize()
+        t = []
+        for s in range(calls):
+            t0 = time.perf_counter()
+            fn(s)
+            t.append(time.perf_counter() - t0)
+        return float(np.median(t)) * 1e6
+
+    route_us = timed(lambda s: router.route(0, xs[s % 8][0], tensors, store, position=s))
+
+    def layer_sync(s):
+        layer.forward(xs[s % 8])
+        torch.cuda.synchronize()
+
+    return {"workload": "StreamedMoERouter.route(), one token per call, resident 120B-shape layer, median wall time",
+            "route_us_per_call": round(route_us, 1), "layer_and_sync_us_per_call": round(timed(layer_sync), 1),
+            "calls": calls}
+
+
 def lm_head_bench(torch, dev, reps: int = 50) -> dict:
     """gpt-oss lm_head (201,088 x 2880 bf16, resident): one logits pass plus
     the greedy token, against the executor's chunked float32 matmul with a
@@ -794,6 +838,9 @@ def main() -> int:
             "algorithmic_bytes_per_launch": round(head["gate_up_bytes_per_launch"]),
         },
     }
+    if args.route_calls > 0:
+        result["route_api"] = route_api_bench(torch, dev, layers[0].w, args.route_calls, args.precision)
+        print(f"[bench] route(): {result['route_api']}", file=sys.stderr, flush=True)
     if args.prefill_tokens > 0:
         result["prefill"] = prefill_bench(torch, dev, args.prefill_tokens, 10, args.precision)
         print(f"[bench] prefill: {result['prefill']}", file=sys.stderr, flush=True)
