@@ -213,29 +213,65 @@ __global__ __launch_bounds__(256) void bias_combine_kernel(const uint16_t* __res
   out[(int64_t)t * hidden + h] = (uint16_t)f32_to_bf16_rne(acc);
 }
 
+// Sum of squares (float64) of this thread's elements of row[0 .. n): with
+// 16-byte aligned rows and n % 4 == 0, float4 chunks tid, tid + 256, ...,
+// four of them loaded before any is summed; else elements tid, tid + 256, ...
+__device__ __forceinline__ double row_sum_squares(const float* __restrict__ row, int n, bool vec) {
+  double s = 0.0;
+  if (vec) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const int n4 = n >> 2;
+    for (int c0 = 0; c0 < n4; c0 += 4 * 256) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + u * 256 + (int)threadIdx.x;
+        v[u] = c < n4 ? r4[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const double a = v[u].x, b = v[u].y, c = v[u].z, d = v[u].w;
+        s += a * a;
+        s += b * b;
+        s += c * c;
+        s += d * d;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const double v = row[i];
+      s += v * v;
+    }
+  }
+  return s;
+}
+
+// One workgroup per pair: its 256 threads read the pair's SwiGLU row and
+// expert-output row with all loads in flight at once, then reduce in a
+// fixed order (wave butterflies, then the four waves in order), so the
+// norms are the same on every run.
 __global__ __launch_bounds__(256) void pair_norms_kernel(const float* __restrict__ gated,
-                                                         const float* __restrict__ eo, int n_pairs, int inter,
-                                                         int hidden, float* __restrict__ norms) {
-  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                         const float* __restrict__ eo, int inter, int hidden,
+                                                         bool vec_g, bool vec_o, float* __restrict__ norms) {
+  __shared__ double red[2][4];
+  const int64_t p = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (p >= n_pairs) return;
-  double sg = 0.0, so = 0.0;
-  for (int i = lane; i < inter; i += kWave) {
-    const double v = gated[(int64_t)p * inter + i];
-    sg += v * v;
-  }
-  for (int i = lane; i < hidden; i += kWave) {
-    const double v = eo[(int64_t)p * hidden + i];
-    so += v * v;
-  }
+  double sg = row_sum_squares(gated + p * inter, inter, vec_g);
+  double so = row_sum_squares(eo + p * hidden, hidden, vec_o);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     sg += __shfl_xor(sg, off);
     so += __shfl_xor(so, off);
   }
   if (lane == 0) {
-    norms[2 * p] = (float)sqrt(sg);
-    norms[2 * p + 1] = (float)sqrt(so);
+    red[0][wave] = sg;
+    red[1][wave] = so;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    norms[2 * p] = (float)sqrt(((red[0][0] + red[0][1]) + red[0][2]) + red[0][3]);
+    norms[2 * p + 1] = (float)sqrt(((red[1][0] + red[1][1]) + red[1][2]) + red[1][3]);
   }
 }
 
@@ -440,8 +476,12 @@ extern "C" int klc_moe_pair_norms(const float* gated, const float* expert_out, i
   KLC_REQUIRE(gated && expert_out && norms, KLC_ERR_ARGUMENT, "klc_moe_pair_norms: null pointer");
   KLC_REQUIRE(n_pairs > 0 && inter > 0 && hidden > 0, KLC_ERR_ARGUMENT, "klc_moe_pair_norms: bad sizes");
   KLC_REQUIRE(n_pairs < ((int64_t)1 << 30), KLC_ERR_UNSUPPORTED, "klc_moe_pair_norms: too many pairs");
-  pair_norms_kernel<<<(unsigned)((n_pairs + 3) / 4), 256, 0, as_stream(stream)>>>(gated, expert_out, (int)n_pairs,
-                                                                                  (int)inter, (int)hidden, norms);
+  KLC_REQUIRE(inter < ((int64_t)1 << 30) && hidden < ((int64_t)1 << 30), KLC_ERR_UNSUPPORTED,
+              "klc_moe_pair_norms: rows too long");
+  const bool vec_g = inter % 4 == 0 && ((uintptr_t)gated & 15) == 0;
+  const bool vec_o = hidden % 4 == 0 && ((uintptr_t)expert_out & 15) == 0;
+  pair_norms_kernel<<<(unsigned)n_pairs, 256, 0, as_stream(stream)>>>(gated, expert_out, (int)inter, (int)hidden,
+                                                                      vec_g, vec_o, norms);
   return check_launch("pair_norms_kernel");
 }
 

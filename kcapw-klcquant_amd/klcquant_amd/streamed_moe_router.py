@@ -438,11 +438,13 @@ class StreamedMoERouter:
             half = (pairs + 1) // 2
             ws, gated, rec, rec_host = self._scratch(dev, stream, t1 - t0, hidden, inter, n_exp, k)
             n_rec = pairs + half + 2 * pairs
-            nat.call("klc_moe_route", ops._ptr(x[t0:t1]), ops._ptr(router_w), ops._ptr(router_b),
-                     ops._ptr(w.gate_up_table), ops._ptr(gu_bias), ops._ptr(w.down_table), ops._ptr(d_bias),
+            row0 = 2 * hidden * t0  # byte offset of row t0 of the bf16 input and output
+            rec_p = rec.data_ptr()  # ids, then the bf16 weights, then the norms (int32 words)
+            nat.call("klc_moe_route", x.data_ptr() + row0, router_w.data_ptr(), router_b.data_ptr(),
+                     w.gate_up_table.data_ptr(), gu_bias.data_ptr(), w.down_table.data_ptr(), d_bias.data_ptr(),
                      t1 - t0, hidden, inter, n_exp, k, self.swiglu_limit, ops.PRECISIONS[self.matmul_precision],
-                     nat.PATH_AUTO, ops._ptr(ws), ws.numel(), ops._ptr(out[t0:t1]), ops._ptr(rec),
-                     ops._ptr(rec[pairs:]), ops._ptr(gated), ops._ptr(rec[pairs + half:]), stream)
+                     nat.PATH_AUTO, ws.data_ptr(), ws.numel(), out.data_ptr() + row0, rec_p, rec_p + 4 * pairs,
+                     gated.data_ptr(), rec_p + 4 * (pairs + half), stream)
             rec_host[:n_rec].copy_(rec[:n_rec], non_blocking=True)
             torch.cuda.current_stream(dev).synchronize()
             r = rec_host[:n_rec].numpy()
