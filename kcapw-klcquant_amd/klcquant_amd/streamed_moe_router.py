@@ -110,7 +110,11 @@ class RouterStats:
         raw = [int(e) for e in raw_experts]
         self.routed_tokens += 1
         self.route_count += 1
-        entropy = _entropy(float(w) for w in weights)
+        entropy = 0
+        for w in weights:  # _entropy's sum, term by term in the same order
+            w = float(w)
+            entropy += w * math.log(max(w, 1e-12))
+        entropy = -entropy
         self.route_entropies.append(entropy)
         overlap = len(set(experts) & set(raw))
         self.raw_overlap_total += overlap
@@ -229,6 +233,84 @@ class RouterStats:
         }
 
 
+class _WorkloadScores:
+    """One layer's workload scores (streamed_moe_router.py:413-424) with the per-call decay applied
+    lazily.
+
+    The reference multiplies every score by ``decay`` on every routed token
+    and drops a score once it falls below 1e-4, then adds the token's
+    weights.  Here an entry holds its value as of the last call that touched
+    it (``[value, tick]``); the decays of the calls since are applied when it
+    is touched again or read, one multiplication at a time with the same
+    deletion test after each, so every value, every deletion and the dict
+    order (a deleted and re-added expert moves to the end) come out as the
+    eager loop's.  A change of ``decay`` first settles every entry with the
+    old factor.
+    """
+
+    __slots__ = ("entries", "tick", "decay")
+
+    def __init__(self) -> None:
+        self.entries: dict[int, list] = {}  # expert -> [value, tick of its last update]
+        self.tick = 0
+        self.decay: float | None = None
+
+    @staticmethod
+    def _decayed(value: float, n: int, decay: float):
+        """``value`` after n decays, or None once a step leaves it below 1e-4.
+
+        With 0 <= decay < 1 a rounded product never exceeds its positive
+        factor, so a positive value only shrinks: it went below 1e-4 at some
+        step exactly when it ends below.  A value <= 0 is below after the
+        first step and stays there; NaN and +inf never are.  So one test
+        after the n multiplications decides as the per-step test does.
+        """
+        if n <= 0:
+            return value
+        for _ in range(n):
+            value *= decay
+        return None if value < 1e-4 else value
+
+    def settle(self) -> None:
+        """Applies every pending decay (deleting the scores that fall below 1e-4)."""
+        if self.decay is None:
+            return
+        for e, ent in list(self.entries.items()):
+            if ent[1] != self.tick:
+                v = self._decayed(ent[0], self.tick - ent[1], self.decay)
+                if v is None:
+                    del self.entries[e]
+                else:
+                    ent[0], ent[1] = v, self.tick
+
+    def update(self, experts, weights, decay: float) -> None:
+        if decay != self.decay:
+            self.settle()
+            self.decay = decay
+        self.tick += 1
+        tick, entries = self.tick, self.entries
+        for e, w in zip(experts, weights):
+            e = int(e)
+            ent = entries.get(e)
+            if ent is not None:
+                v = self._decayed(ent[0], tick - ent[1], decay)
+                if v is not None:
+                    ent[0], ent[1] = v + float(w), tick
+                    continue
+                del entries[e]  # fell below 1e-4 before this call's add: re-added at the end
+            entries[e] = [0.0 + float(w), tick]
+
+    def as_dict(self) -> dict[int, float]:
+        self.settle()
+        return {e: ent[0] for e, ent in self.entries.items()}
+
+    @classmethod
+    def from_dict(cls, scores: dict) -> "_WorkloadScores":
+        st = cls()
+        st.entries = {int(e): [float(v), 0] for e, v in scores.items()}
+        return st
+
+
 def _topk_order(values: np.ndarray, k: int) -> list[int]:
     """``torch.topk(values, k).indices`` of float32 host values (streamed_moe_router.py:271-273).
 
@@ -253,7 +335,7 @@ class StreamedMoERouter:
         self.locality_config = locality_config or RoutingLocalityConfig()
         self.matmul_precision = matmul_precision
         self.sticky_scores: dict[int, dict[int, float]] = {}
-        self.workload_scores: dict[int, dict[int, float]] = {}
+        self._workload: dict[int, _WorkloadScores] = {}
         self.recent_history: dict[int, deque[int]] = {}
         self.dynamic_caps: dict[int, int] = {}
         # scratch of the resident-store path per (device, stream): workspace, float32 SwiGLU rows,
@@ -620,18 +702,27 @@ class StreamedMoERouter:
             for e in [e for e in scores if e not in keep]:
                 del scores[e]
 
+    @property
+    def workload_scores(self) -> dict[int, dict[int, float]]:
+        """Per-layer workload scores as the reference keeps them (a fresh dict per layer, in the
+        reference's insertion order); assigning a dict of dicts replaces them."""
+        return {layer: st.as_dict() for layer, st in self._workload.items()}
+
+    @workload_scores.setter
+    def workload_scores(self, value: dict) -> None:
+        self._workload = {int(layer): _WorkloadScores.from_dict(scores) for layer, scores in value.items()}
+
     def _update_workload_scores(self, layer_idx: int, experts: list[int], weights: list[float]) -> None:
+        """streamed_moe_router.py:413-424: decay every score, drop those below 1e-4, add the token's
+        weights (the decay is applied lazily, see _WorkloadScores)."""
         cfg = self.locality_config
-        scores = self.workload_scores.setdefault(layer_idx, {})
         decay = 1.0 - 1.0 / max(float(cfg.workload_window), 1.0)
-        for e in list(scores):
-            scores[e] *= decay
-            if scores[e] < 1e-4:
-                del scores[e]
+        st = self._workload.get(layer_idx)
+        if st is None:
+            st = self._workload[layer_idx] = _WorkloadScores()
+        st.update(experts, weights, decay)
         history = self.recent_history.setdefault(layer_idx, deque(maxlen=max(int(cfg.prediction_window), 1)))
-        for e, w in zip(experts, weights):
-            scores[int(e)] = scores.get(int(e), 0.0) + float(w)
-            history.append(int(e))
+        history.extend(int(e) for e, _ in zip(experts, weights))
 
     def predict_experts(self, layer_idx: int, limit: int | None = None) -> list[int]:
         """Experts likely next for ``layer_idx`` (streamed_moe_router.py:426-440)."""
@@ -639,7 +730,8 @@ class StreamedMoERouter:
         if not (cfg.enabled and cfg.predictive_prefetch):
             return []
         scores: Counter[int] = Counter()
-        for e, v in self.workload_scores.get(layer_idx, {}).items():
+        st = self._workload.get(layer_idx)
+        for e, v in (st.as_dict() if st is not None else {}).items():
             scores[int(e)] += float(v)
         for e, v in self.sticky_scores.get(layer_idx, {}).items():
             scores[int(e)] += 0.75 * float(v)

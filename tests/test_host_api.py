@@ -255,3 +255,59 @@ def test_predictions_caps_and_adaptation():
 def test_router_rejects_unknown_precision():
     with pytest.raises(ValueError):
         smr.StreamedMoERouter(matmul_precision="fp8")
+
+
+def _eager_workload_update(scores: dict, experts, weights, decay: float) -> int:
+    """The update as streamed_moe_router.py:413-424 writes it: every score decays each call.
+    Returns the number of scores it dropped."""
+    dropped = 0
+    for e in list(scores):
+        scores[e] *= decay
+        if scores[e] < 1e-4:
+            del scores[e]
+            dropped += 1
+    for e, w in zip(experts, weights):
+        scores[int(e)] = scores.get(int(e), 0.0) + float(w)
+    return dropped
+
+
+def _same_items(a: dict, b: dict) -> bool:
+    if list(a) != list(b):
+        return False
+    return all((x == y) or (math.isnan(x) and math.isnan(y)) for x, y in zip(a.values(), b.values()))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_lazy_workload_scores_equal_the_eager_update(seed):
+    """The lazily decayed workload scores equal the reference's eager loop after every call: values bit
+    for bit, deletions below 1e-4, dict order (re-added experts move to the end), NaN weights, repeated
+    experts in one call and a workload_window changed mid-run."""
+    rng = np.random.default_rng(seed)
+    r = make_router(predictive_prefetch=True, prediction_window=8, workload_window=3)
+    eager: dict[int, dict] = {0: {}, 1: {}}
+    dropped = 0
+    for call in range(400):
+        if call == 200:
+            r.locality_config.workload_window = 5
+        layer = int(rng.integers(0, 2))
+        n = int(rng.integers(1, 5))
+        experts = [int(e) for e in rng.integers(0, 12, size=n)]
+        weights = [float(w) for w in (rng.random(n) * (10.0 ** rng.integers(-5, 1, size=n)))]
+        if rng.random() < 0.01:
+            weights[0] = float("nan")
+        decay = 1.0 - 1.0 / max(float(r.locality_config.workload_window), 1.0)
+        dropped += _eager_workload_update(eager[layer], experts, weights, decay)
+        r._update_workload_scores(layer, experts, weights)
+        if call % 7 == 0 or call > 390:
+            got = r.workload_scores
+            for lyr in (0, 1):
+                assert _same_items(got.get(lyr, {}), eager[lyr]), (call, lyr)
+    assert dropped > 20  # scores fell below 1e-4 and were dropped (and some re-added) along the way
+
+
+def test_workload_scores_assignment_and_predictions():
+    r = make_router(predictive_prefetch=True, prediction_window=4, workload_window=2)
+    r.workload_scores = {0: {5: 1.0, 3: 0.25}}
+    r._update_workload_scores(0, [3], [0.5])
+    assert r.workload_scores == {0: {5: 0.5, 3: 0.625}}
+    assert r.predict_experts(0, 2) == [3, 5]
