@@ -293,8 +293,8 @@ def test_lazy_workload_scores_equal_the_eager_update(seed):
         n = int(rng.integers(1, 5))
         experts = [int(e) for e in rng.integers(0, 12, size=n)]
         weights = [float(w) for w in (rng.random(n) * (10.0 ** rng.integers(-5, 1, size=n)))]
-        if rng.random() < 0.01:
-            weights[0] = float("nan")
+        if rng.random() < 0.05:  # values the router never produces, but the rule must still match
+            weights[0] = [float("nan"), float("inf"), -0.5, 0.0, -0.0, 1e-300][int(rng.integers(0, 6))]
         decay = 1.0 - 1.0 / max(float(r.locality_config.workload_window), 1.0)
         dropped += _eager_workload_update(eager[layer], experts, weights, decay)
         r._update_workload_scores(layer, experts, weights)
