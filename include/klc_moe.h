@@ -263,6 +263,33 @@ int klc_moe_route(const void* x, const void* router_w, const void* router_b, con
                   int path, void* workspace, int64_t workspace_bytes, void* out, int32_t* ids, void* weights,
                   float* gated, float* norms, void* stream);
 
+/* The selection half of route() (streamed_moe_router.py:268-284): router
+ * logits -> top-k -> softmax weights for n_tokens rows, as klc_moe_layer
+ * computes them (one launch for up to 128 tokens), into ids (int32
+ * [n_tokens][k]) and weights (bfloat16 [n_tokens][k]).  For callers that need
+ * the experts on the host before the expert kernels run (a streaming store
+ * that must bring misses into HBM first).  workspace: a klc_moe_layer
+ * workspace for these sizes (any intermediate size), zero-filled before its
+ * first use. */
+int klc_moe_select(const void* x, const void* router_w, const void* router_b, int64_t n_tokens, int64_t hidden,
+                   int64_t n_experts, int64_t k, void* workspace, int64_t workspace_bytes, int32_t* ids,
+                   void* weights, void* stream);
+
+/* The expert half of route() for a selection made elsewhere
+ * (_execute_mxfp4_experts, streamed_moe_router.py:483-522, once the experts
+ * are known: the streaming store after it has brought misses into HBM, the
+ * routing-locality path after its host-side selection): dispatch ->
+ * gate_up/SwiGLU -> down -> combine (-> the expert_logs norms) for ids
+ * (int32 [n_tokens][k], each in [0, n_experts)) and bfloat16 weights
+ * [n_tokens][k], as klc_moe_layer runs them after its router.  gated and
+ * norms are both NULL (no norms) or both set (as klc_moe_route).  path AUTO,
+ * GEMV or GEMM; workspace as klc_moe_layer. */
+int klc_moe_experts(const void* x, const int32_t* ids, const void* weights, const void* const* w_gate_up,
+                    const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
+                    int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
+                    int path, void* workspace, int64_t workspace_bytes, void* out, float* gated, float* norms,
+                    void* stream);
+
 /* The same layer as klc_moe_layer without a workspace argument: it has no
  * counterpart in the reference and is for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses that

@@ -538,7 +538,8 @@ int check_layer_args(const char* fn, const void* x, const void* router_w, const 
 }
 
 // The layer's launches on scratch memory `ws` (layer_scratch layout, counters
-// zero on entry and left zero).
+// zero on entry and left zero).  router_w == NULL: ids / weights already hold
+// the selection (klc_moe_experts), and the layer starts at the dispatch.
 int run_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
                   const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
@@ -581,7 +582,13 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
       if ((rc = mark(i))) return rc;
     return KLC_OK;
   }
-  if (n_tokens <= kDecodeRouterTokens) {
+  if (router_w == nullptr) {
+    // the selection is given (ids / weights hold it): dispatch only
+    if ((rc = mark(1))) return rc;
+    if ((rc = mark(2))) return rc;
+    if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, units, st)))
+      return rc;
+  } else if (n_tokens <= kDecodeRouterTokens) {
     // decode batches: logits, top-k and dispatch in one launch
     KLC_REQUIRE(decode_router_counters(n_tokens, n_experts) * 4 <= kCounterBytes, KLC_ERR_UNSUPPORTED,
                 "klc_moe_layer: %lld experts need more completion counters than the workspace holds",
@@ -710,6 +717,69 @@ extern "C" int klc_moe_route(const void* x, const void* router_w, const void* ro
   return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
                        n_experts, k, swiglu_limit, precision, path, static_cast<char*>(workspace), out, nullptr, ids,
                        weights, gated, norms, nullptr, stream);
+}
+
+extern "C" int klc_moe_experts(const void* x, const int32_t* ids, const void* weights, const void* const* w_gate_up,
+                               const void* gate_up_bias, const void* const* w_down, const void* down_bias,
+                               int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                               float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
+                               void* out, float* gated, float* norms, void* stream) {
+  const char* fn = "klc_moe_experts";
+  KLC_REQUIRE(x && ids && weights && w_gate_up && gate_up_bias && w_down && down_bias && out && workspace,
+              KLC_ERR_ARGUMENT, "%s: null pointer", fn);
+  KLC_REQUIRE((gated == nullptr) == (norms == nullptr), KLC_ERR_ARGUMENT, "%s: gated and norms go together", fn);
+  KLC_REQUIRE(precision == KLC_PRECISION_FP32 || precision == KLC_PRECISION_BF16, KLC_ERR_ARGUMENT,
+              "%s: unknown precision %d", fn, precision);
+  KLC_REQUIRE(path == KLC_PATH_AUTO || path == KLC_PATH_GEMV || path == KLC_PATH_GEMM, KLC_ERR_UNSUPPORTED,
+              "%s: path %d (AUTO, GEMV or GEMM; the one-launch layer routes by itself)", fn, path);
+  KLC_REQUIRE(n_tokens > 0 && k > 0 && k <= n_experts, KLC_ERR_ARGUMENT, "%s: n_tokens=%lld k=%lld n_experts=%lld",
+              fn, (long long)n_tokens, (long long)k, (long long)n_experts);
+  KLC_REQUIRE(n_tokens <= KLC_LAYER_MAX_TOKENS, KLC_ERR_UNSUPPORTED, "%s: n_tokens=%lld > 65535", fn,
+              (long long)n_tokens);
+  int rc = check_gemv_shapes(hidden, inter, n_tokens * k, n_experts);
+  if (rc) return rc;
+  const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
+  KLC_REQUIRE(workspace_bytes >= s.total, KLC_ERR_ARGUMENT, "%s: workspace of %lld bytes < %lld needed", fn,
+              (long long)workspace_bytes, (long long)s.total);
+  KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "%s: workspace must be 256-byte aligned", fn);
+  return run_moe_layer(x, nullptr, nullptr, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
+                       n_experts, k, swiglu_limit, precision, path, static_cast<char*>(workspace), out, nullptr,
+                       const_cast<int32_t*>(ids), const_cast<void*>(weights), gated, norms, nullptr, stream);
+}
+
+extern "C" int klc_moe_select(const void* x, const void* router_w, const void* router_b, int64_t n_tokens,
+                              int64_t hidden, int64_t n_experts, int64_t k, void* workspace, int64_t workspace_bytes,
+                              int32_t* ids, void* weights, void* stream) {
+  const char* fn = "klc_moe_select";
+  KLC_REQUIRE(x && router_w && router_b && workspace && ids && weights, KLC_ERR_ARGUMENT, "%s: null pointer", fn);
+  int rc = check_router_args(n_tokens, hidden, n_experts);
+  if (rc) return rc;
+  if ((rc = check_topk_args(n_tokens, n_experts, k))) return rc;
+  if ((rc = check_dispatch_args(n_tokens * k, n_experts))) return rc;
+  KLC_REQUIRE(n_tokens <= KLC_LAYER_MAX_TOKENS, KLC_ERR_UNSUPPORTED, "%s: n_tokens=%lld > 65535", fn,
+              (long long)n_tokens);
+  // the routing regions of the layer workspace come before the expert
+  // regions, so their offsets do not depend on the intermediate size
+  const LayerScratch s = layer_scratch(n_tokens, hidden, 32, n_experts, k);
+  KLC_REQUIRE(workspace_bytes >= s.gated, KLC_ERR_ARGUMENT, "%s: workspace of %lld bytes < %lld needed", fn,
+              (long long)workspace_bytes, (long long)s.gated);
+  KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "%s: workspace must be 256-byte aligned", fn);
+  char* ws = static_cast<char*>(workspace);
+  float* values = reinterpret_cast<float*>(ws + s.values);
+  hipStream_t st = as_stream(stream);
+  if (n_tokens <= kDecodeRouterTokens) {
+    KLC_REQUIRE(decode_router_counters(n_tokens, n_experts) * 4 <= kCounterBytes, KLC_ERR_UNSUPPORTED,
+                "%s: %lld experts need more completion counters than the workspace holds", fn, (long long)n_experts);
+    return launch_router_decode(x, router_w, router_b, ws + s.logits, n_tokens, hidden, n_experts, k, ids, values,
+                                weights, reinterpret_cast<int32_t*>(ws + s.offsets),
+                                reinterpret_cast<int32_t*>(ws + s.sorted), reinterpret_cast<int32_t*>(ws + s.active),
+                                reinterpret_cast<int32_t*>(ws + s.n_active), reinterpret_cast<int32_t*>(ws + s.units),
+                                reinterpret_cast<uint32_t*>(ws + s.counters),
+                                reinterpret_cast<double*>(ws + s.partials), st);
+  }
+  if ((rc = launch_router_logits(x, router_w, router_b, ws + s.logits, nullptr, n_tokens, hidden, n_experts, st)))
+    return rc;
+  return launch_topk(ws + s.logits, ids, values, weights, n_tokens, n_experts, k, st);
 }
 
 extern "C" int klc_moe_layer_static_scratch(const void* x, const void* router_w, const void* router_b,

@@ -65,6 +65,9 @@ SIGNATURES: dict[str, tuple] = {
                              _P, _P, _P, _P, _P, _P]),
     "klc_moe_route": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
                              _P, _P, _P, _P, _P, _P]),
+    "klc_moe_select": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
+    "klc_moe_experts": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
+                               _P, _P, _P, _P]),
     "klc_moe_layer_static_scratch": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32,
                                             _I32, _P, _P, _P, _P, _P, _P]),
     "klc_st_open": (_I32, [ctypes.c_char_p, _P]),

@@ -373,26 +373,22 @@ class StreamedMoERouter:
             return self._finish_route(layer_idx, k, batched, positions, predicted_experts, resident, host,
                                       output.reshape(hidden.shape), "mxfp4_expert_matmul", True, norms,
                                       expert_store, before, False)
-        logits = ops.router_logits(x, router_w, router_b)
-        n_exp = logits.shape[1]
-        k = self._effective_expert_count(layer_idx, n_exp)
-
-        if not self.locality_config.enabled:
-            ids, _, weights = ops.topk_softmax(logits, k)
-            host = None  # read back after the expert kernels are enqueued
+        k = self._effective_expert_count(layer_idx, int(router_w.shape[0]))
+        recorded = self.locality_config.enabled  # the locality path records each row while it selects
+        if not recorded:
+            # one launch (up to 128 tokens) and one read-back: a streaming store needs the experts on the
+            # host to bring misses into HBM before the expert kernels run
+            ids, weights, host = self._select_on_device(x, router_w, router_b, k)
         else:
+            logits = ops.router_logits(x, router_w, router_b)
             ids, weights, host = self._select_on_host(layer_idx, logits, k, resident_experts or set(), positions)
-        recorded = host is not None  # the locality path records each row while it selects
 
         norms = None
         before = None
         if run_experts:
             before = self._cache_snapshot(expert_store)
-            if host is None and not isinstance(expert_store, ResidentExpertStore):
-                host = self._read_back(ids, weights)  # misses must be brought into HBM first
-            if host is not None:
-                for row in host[0]:
-                    expert_store.protect_experts(layer_idx, row)
+            for row in host[0]:
+                expert_store.protect_experts(layer_idx, row)
             if gu_bias is None or d_bias is None:
                 output, mode = torch.zeros_like(hidden), "mxfp4_missing_bias"
             else:
@@ -407,10 +403,6 @@ class StreamedMoERouter:
                                 for t0 in range(0, n_tok, chunk)])
             output, mode = output.reshape(hidden.shape), "bias_only_moe"
 
-        if host is None:
-            host = self._read_back(ids, weights)
-        if norms is not None:
-            norms = norms.cpu().tolist()
         return self._finish_route(layer_idx, k, batched, positions, predicted_experts, resident, host, output,
                                   mode, run_experts, norms, expert_store, before, recorded)
 
@@ -490,7 +482,7 @@ class StreamedMoERouter:
         int32 buffer).
 
         Returns the bf16 output ``[B, H]``, the host row lists of
-        :meth:`_read_back` and the per-pair ``[gate_up_norm, output_norm]``.
+        :meth:`_select_on_device` and the per-pair ``[gate_up_norm, output_norm]``.
         """
         ops._check_gpu("hidden", x, torch.bfloat16, 2)
         ops._check_gpu("router weight", router_w, torch.bfloat16, 2)
@@ -536,32 +528,64 @@ class StreamedMoERouter:
             norms += r[pairs + half:].view(np.float32).reshape(pairs, 2).tolist()
         return out, (experts, weights, [list(row) for row in experts], [False] * n_tok, []), norms
 
-    @staticmethod
-    def _read_back(ids: torch.Tensor, weights: torch.Tensor):
-        """One device->host read of the selection.
+    def _select_on_device(self, x, router_w, router_b, k):
+        """Top-k selection and softmax weights on the GPU (klc_moe_select, streamed_moe_router.py:268-284)
+        with one device->host read of ids and weights per chunk of rows.
 
-        Returns ``(experts, weights, raw_experts, blocked, predicted)`` row
-        lists; without routing locality the raw experts are the selection and
-        the predictions are filled in by the caller.
+        Returns the device ids / weights and ``(experts, weights, raw_experts, blocked, predicted)`` host
+        row lists; without routing locality the raw experts are the selection and the predictions are
+        filled in by the caller.
         """
-        experts = ids.cpu().tolist()
-        w = weights.float().cpu().tolist()
-        return experts, w, [list(r) for r in experts], [False] * len(experts), []
+        ops._check_gpu("hidden", x, torch.bfloat16, 2)
+        ops._check_gpu("router weight", router_w, torch.bfloat16, 2)
+        ops._check_gpu("router bias", router_b, torch.bfloat16, 1)
+        dev = ops._same_device(x, router_w, router_b)
+        n_tok, hidden = x.shape
+        n_exp = router_w.shape[0]
+        if router_w.shape[1] != hidden or router_b.shape[0] != n_exp:
+            raise ValueError(f"router shapes mismatch: x {tuple(x.shape)}, weight {tuple(router_w.shape)}, "
+                             f"bias {tuple(router_b.shape)}")
+        ids = torch.empty((n_tok, k), dtype=torch.int32, device=dev)
+        weights = torch.empty((n_tok, k), dtype=torch.bfloat16, device=dev)
+        stream = ops._stream(dev)
+        chunk = ops.max_tokens_per_call(k)
+        experts, w_rows = [], []
+        for t0 in range(0, n_tok, chunk):
+            t1 = min(n_tok, t0 + chunk)
+            pairs = (t1 - t0) * k
+            ws, _, _, rec_host = self._scratch(dev, stream, t1 - t0, hidden, 32, n_exp, k)
+            nat.call("klc_moe_select", x.data_ptr() + 2 * hidden * t0, router_w.data_ptr(), router_b.data_ptr(),
+                     t1 - t0, hidden, n_exp, k, ws.data_ptr(), ws.numel(), ids.data_ptr() + 4 * t0 * k,
+                     weights.data_ptr() + 2 * t0 * k, stream)
+            half = (pairs + 1) // 2
+            rec_host[:pairs].copy_(ids[t0:t1].view(-1), non_blocking=True)
+            rec_host[pairs:pairs + half].view(torch.int16)[:pairs].copy_(weights[t0:t1].view(-1).view(torch.int16),
+                                                                         non_blocking=True)
+            torch.cuda.current_stream(dev).synchronize()
+            r = rec_host[:pairs + half].numpy()
+            experts += r[:pairs].reshape(t1 - t0, k).tolist()
+            bits = r[pairs:pairs + half].view(np.uint16)[:pairs].astype(np.uint32) << 16
+            w_rows += bits.view(np.float32).reshape(t1 - t0, k).tolist()
+        return ids, weights, (experts, w_rows, [list(row) for row in experts], [False] * n_tok, [])
 
     def _execute_experts(self, layer_idx, x, ids, weights, gu_bias, d_bias, store, host):
-        """gate_up + SwiGLU + down + combine for every (token, slot) pair on the GPU."""
+        """gate_up + SwiGLU + down + combine and the expert_logs norms for every (token, slot) pair of a
+        selection already made (ids / weights on the device): one klc_moe_experts call per chunk of at
+        most ``ops.max_tokens_per_call(k)`` rows, the expert kernels klc_moe_layer picks (so every store
+        gives the same bits), then one read-back of the norms.  Returns the bf16 output and the per-pair
+        ``[gate_up_norm, output_norm]`` host list."""
         n_tok, k = ids.shape
         if isinstance(store, ResidentExpertStore):
             w = store.layer(layer_idx)
             hidden, inter, n_exp = w.hidden, w.inter, w.n_experts
-            gu_table, d_table = w.gate_up_table, w.down_table
+            gu_table, d_table = w.gate_up_table.data_ptr(), w.down_table.data_ptr()
             store.record_access(layer_idx, 2 * n_tok * k)
+            keep = None
         else:
             hidden = x.shape[1]
             inter = gu_bias.shape[1] // 2
             n_exp = gu_bias.shape[0]
-            gu_addr = [0] * n_exp
-            d_addr = [0] * n_exp
+            addr = [[0] * n_exp, [0] * n_exp]
             keep = []
             for row in host[0]:
                 for e in row:  # the reference's access order: gate_up then down, slot by slot
@@ -571,29 +595,36 @@ class StreamedMoERouter:
                             store.matrix_shape(layer_idx, e, "down_proj") != (hidden, inter // 32):
                         raise ValueError(f"expert {e} of layer {layer_idx} does not match hidden={hidden} "
                                          f"inter={inter}")
-                    gu_addr[e], d_addr[e] = gu.data_ptr(), dn.data_ptr()
+                    addr[0][e], addr[1][e] = gu.data_ptr(), dn.data_ptr()
                     keep += [gu, dn]
-            gu_table = torch.tensor(gu_addr, dtype=torch.int64).to(x.device)
-            d_table = torch.tensor(d_addr, dtype=torch.int64).to(x.device)
+            keep.append(torch.tensor(addr, dtype=torch.int64).to(x.device))  # [gate_up pointers, down pointers]
+            gu_table = keep[-1].data_ptr()
+            d_table = gu_table + 8 * n_exp
         if tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
             raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
                              f"E={n_exp} H={hidden} I={inter}")
+        ops._check_gpu("expert ids", ids, torch.int32, 2)
+        ops._check_gpu("routing weights", weights, torch.bfloat16, 2)
+        dev = ops._same_device(x, ids, weights, gu_bias, d_bias)
+        out = torch.empty((n_tok, hidden), dtype=torch.bfloat16, device=dev)
+        stream = ops._stream(dev)
         chunk = ops.max_tokens_per_call(k)  # longer inputs: consecutive calls on row chunks
-        outs, norms = [], []
+        norms = []
         for t0 in range(0, n_tok, chunk):
             t1 = min(n_tok, t0 + chunk)
-            # the expert kernels klc_moe_layer would pick for this chunk, so both stores give the same bits
-            gemm = nat.call("klc_moe_layer_path", t1 - t0, hidden, inter, n_exp, k, nat.PATH_AUTO,
-                            ops._stream(x.device)) == nat.PATH_GEMM
-            disp = ops.dispatch(ids[t0:t1], n_exp)
-            gated, gated_raw = ops.gate_up(gu_table, gu_bias, x[t0:t1], k, disp, hidden, inter,
-                                           self.swiglu_limit, self.matmul_precision, want_raw=True, gemm=gemm)
-            eo = ops.down(d_table, d_bias, gated, disp, hidden, inter, self.matmul_precision, gemm=gemm)
-            outs.append(ops.combine(eo, weights[t0:t1], t1 - t0, k))
-            norms.append(ops.pair_norms(gated_raw, eo))
-        if len(outs) == 1:
-            return outs[0], norms[0]
-        return torch.cat(outs), torch.cat(norms)
+            pairs = (t1 - t0) * k
+            ws, gated, rec, rec_host = self._scratch(dev, stream, t1 - t0, hidden, inter, n_exp, k)
+            row0 = 2 * hidden * t0
+            nat.call("klc_moe_experts", x.data_ptr() + row0, ids.data_ptr() + 4 * t0 * k,
+                     weights.data_ptr() + 2 * t0 * k, gu_table, gu_bias.data_ptr(), d_table, d_bias.data_ptr(),
+                     t1 - t0, hidden, inter, n_exp, k, self.swiglu_limit, ops.PRECISIONS[self.matmul_precision],
+                     nat.PATH_AUTO, ws.data_ptr(), ws.numel(), out.data_ptr() + row0, gated.data_ptr(),
+                     rec.data_ptr(), stream)
+            rec_host[:2 * pairs].copy_(rec[:2 * pairs], non_blocking=True)
+            torch.cuda.current_stream(dev).synchronize()
+            norms += rec_host[:2 * pairs].numpy().view(np.float32).reshape(pairs, 2).tolist()
+        del keep  # the packed matrices and pointer table outlive the kernels that read them (synchronised)
+        return out, norms
 
     # ---- routing locality (host control logic, streamed_moe_router.py:331-476) ------------
 

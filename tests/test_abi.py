@@ -124,3 +124,24 @@ def test_cpu_tensors_are_rejected():
         ops.router_logits(x, torch.zeros((4, 64), dtype=torch.bfloat16), torch.zeros(4, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="shape mismatch"):
         ops.mxfp4_dequant(torch.zeros((4, 2, 16), dtype=torch.uint8), torch.zeros((4, 3), dtype=torch.uint8))
+
+
+def test_select_and_experts_argument_errors():
+    """klc_moe_select / klc_moe_experts check their arguments before any device work."""
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_select", fake, fake, None, 2, 2880, 128, 4, fake, 1 << 30, fake, fake, None)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "null pointer" in ei.value.message
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_select", fake, fake, fake, 2, 2880, 128, 4, fake, 64, fake, fake, None)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "workspace" in ei.value.message
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_select", fake, fake, fake, 2, 2880, 8, 9, fake, 1 << 30, fake, fake, None)
+    assert ei.value.status == nat.KLC_ERR_SHAPE
+    args = [fake] * 7 + [2, 2880, 2880, 128, 4, 7.0, nat.PRECISION_FP32]
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_experts", *args, nat.PATH_FUSED, fake, 1 << 30, fake, None, None, None)
+    assert ei.value.status == nat.KLC_ERR_UNSUPPORTED
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_experts", *args, nat.PATH_AUTO, fake, 1 << 30, fake, fake, None, None)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "together" in ei.value.message
