@@ -340,3 +340,35 @@ def test_route_120b_matches_layer(gpu, precision):
         assert norms.shape == (n_tok * 4, 2) and np.isfinite(norms).all() and (norms > 0).all()
     assert router.stats.routed_tokens == 8 + 64 + 1 + 300 + 8
     assert store.cache.stats.hits == 2 * 4 * router.stats.routed_tokens
+
+
+@pytest.mark.parametrize("n_tok", [1, 37, 200])
+def test_select_then_experts_equal_the_layer(gpu, n_tok):
+    """klc_moe_select (one launch up to 128 tokens, logits + top-k above) and klc_moe_experts on its
+    selection give klc_moe_layer's ids, weights and output bits, at the 20B expert count (E = 32)."""
+    from klcquant_amd import _native as nat
+    from klcquant_amd import ops
+
+    h, i, e, k = 512, 256, 32, 4
+    w = moe.MoELayerWeights.synthetic(76, 0, h, i, e, gpu)
+    xt = bf16_tensor(moe.synthetic_hidden(76, n_tok, h), gpu)
+    ids_l = torch.empty((n_tok, k), dtype=torch.int32, device=gpu)
+    wts_l = torch.empty((n_tok, k), dtype=torch.bfloat16, device=gpu)
+    want = moe.MoELayer(w, k).forward(xt, ids=ids_l, weights=wts_l)
+    ws = torch.zeros(ops.workspace_bytes(n_tok, h, i, e, k), dtype=torch.uint8, device=gpu)
+    ids = torch.empty_like(ids_l)
+    wts = torch.empty_like(wts_l)
+    stream = ops._stream(gpu)
+    nat.call("klc_moe_select", ops._ptr(xt), ops._ptr(w.router_weight), ops._ptr(w.router_bias), n_tok, h, e, k,
+             ops._ptr(ws), ws.numel(), ops._ptr(ids), ops._ptr(wts), stream)
+    out = torch.empty_like(want)
+    gated = torch.empty((n_tok * k, i), dtype=torch.float32, device=gpu)
+    norms = torch.empty((n_tok * k, 2), dtype=torch.float32, device=gpu)
+    nat.call("klc_moe_experts", ops._ptr(xt), ops._ptr(ids), ops._ptr(wts), ops._ptr(w.gate_up_table),
+             ops._ptr(w.gate_up_bias), ops._ptr(w.down_table), ops._ptr(w.down_bias), n_tok, h, i, e, k, 7.0,
+             nat.PRECISION_FP32, nat.PATH_AUTO, ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(gated),
+             ops._ptr(norms), stream)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids_l) and torch.equal(wts.view(torch.int16), wts_l.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert torch.isfinite(norms).all() and (norms > 0).all()
