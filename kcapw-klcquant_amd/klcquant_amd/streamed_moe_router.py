@@ -341,6 +341,8 @@ class StreamedMoERouter:
         # scratch of the resident-store path per (device, stream): workspace, float32 SwiGLU rows,
         # routing record on the device and its pinned host copy
         self._route_scratch: dict[tuple, tuple[torch.Tensor, ...]] = {}
+        # a streaming store's expert pointers per (device, layer, experts): device table and host mirror
+        self._ptr_tables: dict[tuple, tuple[torch.Tensor, list]] = {}
 
     # ---- the routed layer -------------------------------------------------------------
 
@@ -585,7 +587,15 @@ class StreamedMoERouter:
             hidden = x.shape[1]
             inter = gu_bias.shape[1] // 2
             n_exp = gu_bias.shape[0]
-            addr = [[0] * n_exp, [0] * n_exp]
+            # [gate_up pointers, down pointers] of the layer's experts, uploaded only when a selected
+            # expert's packed matrices moved (a miss, an eviction); entries of experts not selected may be
+            # stale and are never read (the kernels visit the selected experts only)
+            key = (x.device, layer_idx, n_exp)
+            if key not in self._ptr_tables:
+                self._ptr_tables[key] = (torch.zeros((2, n_exp), dtype=torch.int64, device=x.device),
+                                         [[0] * n_exp, [0] * n_exp])
+            table, mirror = self._ptr_tables[key]
+            dirty = False
             keep = []
             for row in host[0]:
                 for e in row:  # the reference's access order: gate_up then down, slot by slot
@@ -595,10 +605,13 @@ class StreamedMoERouter:
                             store.matrix_shape(layer_idx, e, "down_proj") != (hidden, inter // 32):
                         raise ValueError(f"expert {e} of layer {layer_idx} does not match hidden={hidden} "
                                          f"inter={inter}")
-                    addr[0][e], addr[1][e] = gu.data_ptr(), dn.data_ptr()
+                    if mirror[0][e] != gu.data_ptr() or mirror[1][e] != dn.data_ptr():
+                        mirror[0][e], mirror[1][e] = gu.data_ptr(), dn.data_ptr()
+                        dirty = True
                     keep += [gu, dn]
-            keep.append(torch.tensor(addr, dtype=torch.int64).to(x.device))  # [gate_up pointers, down pointers]
-            gu_table = keep[-1].data_ptr()
+            if dirty:  # ordered on the stream before the kernels that read it (the last ones have finished)
+                table.copy_(torch.tensor(mirror, dtype=torch.int64))
+            gu_table = table.data_ptr()
             d_table = gu_table + 8 * n_exp
         if tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
             raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
