@@ -77,6 +77,7 @@ def parse_args():
     ap.add_argument("--graph", action="store_true",
                     help="replay one HIP graph per step in the headline pass instead of launching its kernels")
     ap.add_argument("--skip-dequant", action="store_true", help="skip the standalone dequant measurement")
+    ap.add_argument("--skip-config0", action="store_true", help="skip the 20B-shape single-token layer line")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of the prefill measurement (0 = skip)")
     ap.add_argument("--stack-layers", type=int, default=36, help="layers of the stacked decode (0 = skip)")
     ap.add_argument("--stack-steps", type=int, default=32, help="decode steps of the stacked decode")
@@ -113,11 +114,11 @@ def copy_calibration(torch, dev) -> None:
                       "launches": 5}), flush=True)
 
 
-def layer_bytes(unique_experts: int, n_tok: int) -> int:
+def layer_bytes(unique_experts: int, n_tok: int, n_exp: int = EXPERTS) -> int:
     """Algorithmic HBM bytes of one layer step."""
     weights = unique_experts * (GATE_UP_EXPERT_BYTES + DOWN_EXPERT_BYTES)
     biases = unique_experts * (2 * INTER + HIDDEN) * 2
-    router = EXPERTS * HIDDEN * 2 + EXPERTS * 2
+    router = n_exp * HIDDEN * 2 + n_exp * 2
     acts = n_tok * HIDDEN * 2 * 2  # hidden in, output out (bf16)
     return weights + biases + router + acts
 
@@ -135,6 +136,53 @@ def kernel_breakdown(interval_us, n_tok: int, path: str) -> dict:
         return {"router_topk_dispatch": us[0], "gate_up": us[3], "down": us[4], "combine": us[5],
                 "event_records_only": round(us[1] + us[2], 3)}
     return dict(zip(KERNELS, us))
+
+
+def config0_bench(torch, dev, steps: int, warmup: int, precision: str, n_layers: int = 8) -> dict:
+    """The gpt-oss-20B-shape layer (E = 32, top-4) decoding one token per step, fp32 expert math: the
+    single-token layer of the 20B model.  Steps rotate over n_layers seeded layers (425 MB of packed
+    experts each) and 16 inputs; per-kernel times from the library's events in a second pass."""
+    import numpy as np
+
+    from klcquant_amd import _native, moe
+
+    n_exp = 32
+    layers = [moe.MoELayer(moe.MoELayerWeights.synthetic(0, l, HIDDEN, INTER, n_exp, dev), TOPK, 7.0, precision)
+              for l in range(n_layers)]
+    xs = [torch.from_numpy(moe.synthetic_hidden(0, 1, HIDDEN, step=s).view(np.int16)).view(torch.bfloat16).to(dev)
+          for s in range(16)]
+    out = torch.empty((1, HIDDEN), dtype=torch.bfloat16, device=dev)
+    t0 = time.perf_counter()
+    s = 0
+    while (time.perf_counter() - t0) * 1e3 < SETTLE_MS or s < 4:
+        layers[s % n_layers].forward(xs[s % 16], out=out)
+        s += 1
+        if s % 16 == 0:
+            torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(_native.LAYER_EVENTS)] for _ in range(steps)]
+    for row in evs:
+        for e in row:
+            e.record()
+    torch.cuda.synchronize()
+    for s in range(steps):
+        layers[s % n_layers].forward(xs[s % 16], out=out, events=evs[s])
+    for s in range(warmup):
+        layers[s % n_layers].forward(xs[s % 16], out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        layers[s % n_layers].forward(xs[s % 16], out=out)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    kern = np.array([[evs[s][i].elapsed_time(evs[s][i + 1]) for i in range(len(KERNELS))] for s in range(steps)])
+    moved = layer_bytes(TOPK, 1, n_exp)  # a single token's top-4 are 4 distinct experts
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": "gpt-oss-20B-shape MoE layer: H=I=2880, 32 MXFP4 experts, top-4, 1 token per step, "
+                        "fp32 expert math", "us_per_token": round(dt * 1e6, 3), "tokens_per_s": round(1 / dt, 1),
+            "bytes_per_token": moved, "hbm_gbps": round(moved / dt / 1e9, 1),
+            "frac_of_peak": round(moved / dt / 1e9 / HBM_PEAK_GBPS, 4),
+            "kernel_us_mean": kernel_breakdown(kern.mean(axis=0) * 1e3, 1, "gemv"), "steps": steps}
 
 
 def gate_up_bytes(unique_experts: int, n_tok: int) -> int:
@@ -634,34 +682,35 @@ def attention_bench(torch, dev, context: int = 4096, reps: int = 100) -> dict:
     return out
 
 
-def cpu_baseline(n_tokens: int, warmups: int = 2) -> dict:
-    """The reference path restated in torch CPU ops (oracle/torch_ref.py) on single-token route() calls.
-
-    The same 120B-shape layer (workload 2, layer 0).  Cold: every call dequantizes its four experts again
-    (cache_bytes=0, the miss path with the checkpoint in RAM); warm: the dequantized bf16 matrices are
-    cached (the hit path with its .float() copies).  Each variant: ``warmups`` untimed calls, then the
-    median of ``n_tokens`` timed calls."""
-    import statistics
-
+def _cpu_layer(workload: int, n_exp: int, router_bias=None):
+    """torch_ref.Layer with the seeded router and biases of (workload, layer 0); experts are added per sample."""
     import numpy as np
     import torch
 
-    from klcquant_amd import moe, synth
+    from klcquant_amd import synth
     from oracle import torch_ref
 
     def t_bf16(bits):
         return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(torch.bfloat16)
 
-    seed = {n: synth.tensor_seed(WORKLOAD, n, 0) for n in synth.TENSOR_IDS}
-    rw = synth.random_normal_bf16(seed["router_weight"], EXPERTS * HIDDEN, 0.0, 0.02).reshape(EXPERTS, HIDDEN)
-    rb = synth.random_normal_bf16(seed["router_bias"], EXPERTS, 0.0, 0.01)
-    gub = synth.random_normal_bf16(seed["gate_up_bias"], EXPERTS * 2 * INTER, 0.0, 0.01).reshape(EXPERTS, -1)
-    db = synth.random_normal_bf16(seed["down_bias"], EXPERTS * HIDDEN, 0.0, 0.01).reshape(EXPERTS, -1)
-    layer = torch_ref.Layer(t_bf16(rw), t_bf16(rb), t_bf16(gub), t_bf16(db), {}, TOPK)
-    n = warmups + n_tokens
-    xs = [t_bf16(row) for row in moe.synthetic_hidden(WORKLOAD, n, HIDDEN, step=12345)]
-    # the checkpoint tensors of the experts these tokens select, as the store would read them (untimed)
-    for e in sorted({e for x in xs for e in layer.select(x)}):
+    seed = {n: synth.tensor_seed(workload, n, 0) for n in synth.TENSOR_IDS}
+    rw = synth.random_normal_bf16(seed["router_weight"], n_exp * HIDDEN, 0.0, 0.02).reshape(n_exp, HIDDEN)
+    rb = synth.random_normal_bf16(seed["router_bias"], n_exp, 0.0, 0.01) if router_bias is None else router_bias
+    gub = synth.random_normal_bf16(seed["gate_up_bias"], n_exp * 2 * INTER, 0.0, 0.01).reshape(n_exp, -1)
+    db = synth.random_normal_bf16(seed["down_bias"], n_exp * HIDDEN, 0.0, 0.01).reshape(n_exp, -1)
+    return torch_ref.Layer(t_bf16(rw), t_bf16(rb), t_bf16(gub), t_bf16(db), {}, TOPK), seed, t_bf16
+
+
+def _cpu_route_sample(layer, seed, xs, warmups: int) -> dict:
+    """Single-token route() calls over xs: cold (every call dequantizes its experts) and warm (the
+    dequantized matrices cached); medians over the calls after ``warmups``."""
+    import statistics
+
+    import torch
+
+    from klcquant_amd import synth
+
+    for e in sorted({e for x in xs for e in layer.select(x)}):  # checkpoint tensors as the store reads them
         parts = (synth.mxfp4_expert_slice(seed["gate_up_blocks"], seed["gate_up_scales"], e, 2 * INTER, HIDDEN)
                  + synth.mxfp4_expert_slice(seed["down_blocks"], seed["down_scales"], e, HIDDEN, INTER))
         layer.experts[e] = tuple(torch.from_numpy(p) for p in parts)
@@ -679,20 +728,119 @@ def cpu_baseline(n_tokens: int, warmups: int = 2) -> dict:
     for x in xs:  # fill the warm store with the sample's experts
         layer.route(x, True)
     warm = timed(True)
-    cold_us = statistics.median(cold) * 1e6
-    warm_us = statistics.median(warm) * 1e6
+    return {"warm_us_per_token": round(statistics.median(warm) * 1e6, 1),
+            "cold_us_per_token": round(statistics.median(cold) * 1e6, 1),
+            "tokens_timed": len(xs) - warmups, "unique_experts": len(layer.experts)}
+
+
+def cpu_baseline(n_tokens: int, warmups: int = 2) -> dict:
+    """The reference path restated in torch CPU ops (oracle/torch_ref.py), on the host cores.
+
+    The reference routes one token per route() call (streamed_moe_router.py:257-329), so every decode
+    and prefill configuration is a sequence of single-token calls; each is timed on a bounded sample and
+    the totals for the full configuration are extrapolated from the per-call medians (labelled so):
+    * 0: the 20B-shape layer (E = 32), single-token calls, cold and warm;
+    * 1: dequantize_mxfp4_matrix over 8 of the 128 down_proj matrices, scaled to 128;
+    * 2: the 120B-shape layer (E = 128), single-token calls (B = 8 and 64 are B calls per step);
+    * 3: single-token calls of the Zipf(1.1)-biased 2048-token prefill layer, scaled to 2048 tokens;
+    * 4: one stack layer per token = rms_norm + route() + residual, scaled to 64 tokens x 36 layers.
+    Cold: cache_bytes = 0, every call dequantizes its 4 experts from MXFP4 (the miss path with the
+    checkpoint in RAM); warm: the dequantized matrices are cached (the hit path with its .float()
+    copies).  ``value`` is configuration 2's warm per-token time."""
+    import statistics
+
+    import numpy as np
+    import torch
+
+    from klcquant_amd import moe, synth
+    from oracle import torch_ref
+
+    n = warmups + n_tokens
+    configs = {}
+    # 0: 20B shape, E = 32
+    layer, seed, _ = _cpu_layer(0, 32)
+    xs = [torch.from_numpy(r.view(np.int16)).view(torch.bfloat16)
+          for r in moe.synthetic_hidden(0, n, HIDDEN, step=12345)]
+    configs["0"] = {"workload": "gpt-oss-20B-shape MoE layer (E = 32, top-4), single-token route() calls",
+                    **_cpu_route_sample(layer, seed, xs, warmups)}
+    del layer
+    # 2: 120B shape, E = 128
+    layer, seed, t_bf16 = _cpu_layer(WORKLOAD, EXPERTS)
+    xs = [t_bf16(row) for row in moe.synthetic_hidden(WORKLOAD, n, HIDDEN, step=12345)]
+    c2 = _cpu_route_sample(layer, seed, xs, warmups)
+    configs["2"] = {"workload": "gpt-oss-120B-shape MoE layer (E = 128, top-4), single-token route() calls",
+                    **c2,
+                    "us_per_step_extrapolated": {str(b): round(b * c2["warm_us_per_token"], 1) for b in (1, 8, 64)}}
+    # 4: rms_norm + residual of a 64-row batch, measured; route() per token from configuration 2
+    h = t_bf16(moe.synthetic_hidden(4, 64, HIDDEN))
+    w_norm = t_bf16(moe.synthetic_norm_weight(4, 0, HIDDEN))
+    moe_out = t_bf16(moe.synthetic_hidden(5, 64, HIDDEN))
+
+    def norm_residual():
+        x = h.clone()
+        normed = x * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-5).to(x.dtype) * w_norm
+        x += moe_out
+        return normed
+
+    for _ in range(3):
+        norm_residual()
+    t = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        norm_residual()
+        t.append(time.perf_counter() - t0)
+    nr_us = statistics.median(t) * 1e6
+    layer_us = 64 * c2["warm_us_per_token"] + nr_us
+    configs["4"] = {"workload": "36-layer MoE-only stack, 64 sequences: rms_norm -> route() per token -> residual",
+                    "extrapolated": "36 layers x (64 warm single-token route() calls of configuration 2 + the "
+                                    "measured rms_norm and residual of the 64-row batch)",
+                    "rms_norm_residual_us_per_batch": round(nr_us, 1),
+                    "ms_per_step": round(36 * layer_us / 1e3, 1),
+                    "tokens_per_s": round(64 / (36 * layer_us * 1e-6), 2)}
+    del layer
+    # 1: dequantize_mxfp4_matrix over 128 down_proj matrices (8 timed)
+    d = []
+    for e in range(10):
+        b, sc = synth.mxfp4_expert_slice(synth.tensor_seed(1, "down_blocks"), synth.tensor_seed(1, "down_scales"),
+                                         e, HIDDEN, INTER)
+        bt, st = torch.from_numpy(b), torch.from_numpy(sc)
+        t0 = time.perf_counter()
+        torch_ref.dequantize(bt, st, torch.bfloat16)
+        if e >= 2:
+            d.append(time.perf_counter() - t0)
+    per = statistics.median(d)
+    moved = EXPERTS * HIDDEN * (INTER // 32) * 17 + EXPERTS * HIDDEN * INTER * 2
+    configs["1"] = {"workload": "dequantize_mxfp4_matrix, 128 x down_proj [2880, 90, 16] -> bf16 [2880, 2880]",
+                    "matrices_timed": len(d), "us_per_matrix": round(per * 1e6, 1),
+                    "s_total_extrapolated": round(per * EXPERTS, 3),
+                    "gbps": round(moved / (per * EXPERTS) / 1e9, 2)}
+    # 3: the Zipf(1.1) prefill layer, single-token calls (6 timed)
+    x_host = moe.synthetic_hidden(3, 2048, HIDDEN)
+    rw = synth.random_normal_bf16(synth.tensor_seed(3, "router_weight"), EXPERTS * HIDDEN, 0.0, 0.02)
+    bias, _ = synth.zipf_router_bias(x_host, rw.reshape(EXPERTS, HIDDEN), TOPK, 1.1, 1000 * 3 + 11)
+    layer, seed, _ = _cpu_layer(3, EXPERTS, bias)
+    xs = [t_bf16(row) for row in x_host[:warmups + 6]]
+    c3 = _cpu_route_sample(layer, seed, xs, warmups)
+    configs["3"] = {"workload": "gpt-oss-120B-shape layer with Zipf(1.1) router bias, 2048 prefill tokens as "
+                                "single-token route() calls", **c3,
+                    "extrapolated": "2048 x the per-call medians",
+                    "s_total_warm": round(2048 * c3["warm_us_per_token"] / 1e6, 2),
+                    "s_total_cold": round(2048 * c3["cold_us_per_token"] / 1e6, 2),
+                    "tokens_per_s_warm": round(1e6 / c3["warm_us_per_token"], 2)}
+    del layer
     return {
-        "value": round(warm_us, 1),
+        "value": c2["warm_us_per_token"],
         "unit": "us/token",
         "cores": int(torch.get_num_threads()),
         "kind": "port",
         "sample": (f"median of {n_tokens} single-token route() calls after {warmups} warm-ups (B = 1: the reference "
                    "routes one token per call), the 120B-shape layer, the reference's torch CPU ops in its "
                    "float32 matmul mode: warm = dequantized experts cached (the hit path); cold = every call "
-                   "dequantizes its 4 experts from MXFP4 (cache_bytes = 0)"),
-        "warm_us_per_token": round(warm_us, 1),
-        "cold_us_per_token": round(cold_us, 1),
-        "unique_experts": len(layer.experts),
+                   "dequantizes its 4 experts from MXFP4 (cache_bytes = 0); configs holds every configuration"),
+        "warm_us_per_token": c2["warm_us_per_token"],
+        "cold_us_per_token": c2["cold_us_per_token"],
+        "unique_experts": c2["unique_experts"],
+        "configs": {k: configs[k] for k in sorted(configs)},
     }
 
 
@@ -838,6 +986,9 @@ def main() -> int:
             "algorithmic_bytes_per_launch": round(head["gate_up_bytes_per_launch"]),
         },
     }
+    if not args.skip_config0:
+        result["config0"] = config0_bench(torch, dev, args.steps, args.warmup, args.precision)
+        print(f"[bench] config0: {result['config0']}", file=sys.stderr, flush=True)
     if args.route_calls > 0:
         result["route_api"] = route_api_bench(torch, dev, layers[0].w, args.route_calls, args.precision)
         print(f"[bench] route(): {result['route_api']}", file=sys.stderr, flush=True)

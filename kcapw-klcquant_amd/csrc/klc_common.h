@@ -172,6 +172,10 @@ constexpr int kStreamPolicy = 2;
 // are not coherent across XCDs.
 constexpr int kAgentScope = 16;
 
+// s_waitcnt immediate that waits until at most n vector memory operations
+// and no LDS operation are outstanding (gfx9 encoding; export counter free).
+constexpr int vmcnt_imm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70; }
+
 // Eight E2M1 codes (one dword, input order) times the scale -> 8 bf16 (MFMA A operand).
 __device__ __forceinline__ bf16x8_t decode8(uint32_t word, float scale) {
   const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, scale, 0);

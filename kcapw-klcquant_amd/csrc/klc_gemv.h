@@ -17,8 +17,10 @@
 // unconditional straight-line code, which lets the compiler wait for exactly
 // one chunk per step (vector loads retire in order).  Past the last tile the
 // refills are out-of-range buffer loads (they return 0 and touch no memory).
-// The activation-row loads are issued before the ring prologue, so waiting
-// for them (the oldest loads) does not wait for any weight chunk.
+// The activation rows go to LDS by buffer-to-LDS DMA issued before the ring
+// prologue, so waiting for them (the oldest loads) waits for no weight chunk
+// (the fused layer, whose down items wait for their inputs after starting
+// their weight stream, stages them through registers after the ring).
 //
 // Columns are up to kVRows activation rows.  gate_up stages one row per token
 // (the bfloat16 hidden state, exact).  down stages two rows per token, the hi
@@ -48,7 +50,13 @@ __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
   return (up + 1.0f) * glu;
 }
 
-__host__ __device__ constexpr size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * (steps * 128 + 8) * 2; }
+// Staged activation rows in LDS: each row holds its 16-byte chunks rounded
+// up to whole 64-chunk blocks (one wave-wide LDS-DMA load fills one block)
+// plus one spare chunk, so consecutive rows start 16 bytes apart modulo 256
+// and the B reads of the 8 rows at one offset hit different banks.
+__host__ __device__ constexpr int gemv_row_chunks(int steps) { return (steps * 16 + 63) / 64 * 64; }
+__host__ __device__ constexpr int gemv_row_stride(int steps) { return (gemv_row_chunks(steps) + 1) * 8; }  // bf16
+__host__ __device__ constexpr size_t gemv_lds_bytes(int steps) { return (size_t)kVRows * gemv_row_stride(steps) * 2; }
 
 // Step counts with a compiled kernel; other shapes round up (the extra steps
 // read out of range and decode to zero).  Each is <= kRing or a multiple of it.
@@ -94,7 +102,7 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
   asm volatile("" : "+v"(tid));
   const int in_dim = groups * 32;
   const int cpr = groups * 4;                   // 16-byte activation chunks per row
-  const int row_stride = kSteps * 128 + 8;      // bf16 elements per staged row (zero padded)
+  constexpr int row_stride = gemv_row_stride(kSteps);  // bf16 elements per staged row (zero padded)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int lr = lane & 15;                     // row within the wave's 16 (A) / column n (B, D)
@@ -124,18 +132,13 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
 
   const int nrows = kDown ? 2 * nt : nt;
-
-  // ---- 1. the unit's pairs: one vector load, issued before the weight
-  //      stream so that waiting for it does not wait for any weight chunk.
-  //      Lane r < kVRows holds staged row r's pair; the lane's output pair
-  //      (the same for every tile) comes in the same round trip. ----
+  const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
+  // Lane r < kVRows holds staged row r's pair; every lane its output pair
+  // (the same for every tile); one vector load each, issued together.
   const int rr_l = min(lane & (kVRows - 1), nrows - 1);
   const int pair_l = unit_pairs[kDown ? rr_l >> 1 : rr_l];
-  const int out_col = kDown ? lr >> 1 : lr;  // the lane's token within the unit
   const int out_pair = unit_pairs[min(out_col, nt - 1)];
 
-  // ---- 2. scale record of the first tile, the first tile's bias, then the
-  //      ring prologue ----
   // the lane's scales of a tile: 8-byte word i holds steps 8i .. 8i + 7 of
   // (row, quarter); a wave's load of word i is 512 contiguous bytes
   constexpr int kRecWords = (kSteps + 7) / 8 * 2;
@@ -157,62 +160,108 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
     return *reinterpret_cast<const u32x2_t*>(bias + row);
   };
   uint32_t sc[kRecWords], sc_next[kRecWords];
-  load_rec(tile0, sc);
-  u32x2_t bias_cur = load_bias(tile0), bias_next = bias_cur;
+  u32x2_t bias_cur, bias_next;
   uint32_t tb = (uint32_t)tile0 * tile_bytes;
   u32x4_t ring[kR];
-  __builtin_amdgcn_sched_barrier(0);  // the ring goes out before the rows' loads
-#pragma unroll
-  for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
-  __builtin_amdgcn_sched_barrier(0);
 
-  wait_inputs();
-
-  // ---- 3. activation-row loads (row sources read back from the pairs) ----
-  int src[kVRows];
-  {
+  if constexpr (!kFused) {
+    // ---- activation rows by LDS-DMA, before any weight load: waiting for
+    //      them (the oldest loads) then waits for no weight chunk.  Row r's
+    //      64-chunk block b is one wave-wide buffer load into LDS (lane l
+    //      writes chunk 64 b + l); chunks past the row and rows past the
+    //      unit's are out of range (no memory traffic).  The pad chunks of
+    //      live rows are also zeroed by ds_write: their A operand is zero,
+    //      and 0 * pad must stay finite. ----
+    constexpr int kBlocks = gemv_row_chunks(kSteps) / 64;
+    static_assert((kVRows * kBlocks) % kGemvWaves == 0, "row blocks split evenly over the waves");
     const int src_l = kDown ? pair_l : pair_l / k_top;
 #pragma unroll
-    for (int r = 0; r < kVRows; ++r) src[r] = __builtin_amdgcn_readlane(src_l, r);
-  }
-  u32x4_t xv[kLoads];
-#pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
-    const int id = min(tid + i * kGemvThreads, nrows * cpr - 1);
-    const int r = id / cpr;
-    const int c = id - r * cpr;
-    int srow = src[0];
-#pragma unroll
-    for (int q = 1; q < kVRows; ++q) srow = r == q ? src[q] : srow;
-    const int64_t elem = (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim + c * 8;
-    if constexpr (kFused && kDown) {
-      // the hi/lo rows were stored by other workgroups of this launch
-      const __amdgpu_buffer_rsrc_t abuf =
-          __builtin_amdgcn_make_buffer_rsrc((void*)act, (short)0, 0x7fffffff, kBufferWord3);
-      xv[i] = __builtin_amdgcn_raw_buffer_load_b128(abuf, (uint32_t)(elem * 2), 0, kAgentScope);
-    } else {
-      xv[i] = *reinterpret_cast<const u32x4_t*>(act + elem);
+    for (int m = 0; m < kVRows * kBlocks / kGemvWaves; ++m) {
+      const int i = wave + kGemvWaves * m;  // uniform
+      const int r = i / kBlocks;
+      const int b = i - r * kBlocks;
+      const int srow = __builtin_amdgcn_readlane(src_l, r);
+      const uint16_t* row = act + (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim;
+      const __amdgpu_buffer_rsrc_t rbuf = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)row, (short)0, r < nrows ? cpr * 16 : 0, kBufferWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rbuf, (__attribute__((address_space(3))) void*)(xs + r * row_stride + b * 512), 16,
+          (uint32_t)((b * 64 + lane) * 16), 0, 0, 0);
     }
-  }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = tid >> 5;
+      const int c = cpr + (tid & 31) + 32 * j;
+      if (r < nrows && c < gemv_row_chunks(kSteps)) *reinterpret_cast<u32x4_t*>(xs + r * row_stride + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- scale record and bias of the first tile, then the ring prologue ----
+    load_rec(tile0, sc);
+    bias_cur = load_bias(tile0);
+    bias_next = bias_cur;
+#pragma unroll
+    for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
+    __builtin_amdgcn_sched_barrier(0);
+    // every wave's rows have landed (the loads after them stay in flight)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRecWords / 2 + 1 + kR));
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  } else {
+    // ---- the fused layer's order: scale record, bias, ring prologue, then
+    //      (after wait_inputs) the activation rows through registers ----
+    load_rec(tile0, sc);
+    bias_cur = load_bias(tile0);
+    bias_next = bias_cur;
+    __builtin_amdgcn_sched_barrier(0);  // the ring goes out before the rows' loads
+#pragma unroll
+    for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
+    __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 4. activation rows into LDS ----
+    wait_inputs();
+
+    int src[kVRows];
+    {
+      const int src_l = kDown ? pair_l : pair_l / k_top;
 #pragma unroll
-  for (int i = 0; i < kLoads; ++i) {
-    const int id = tid + i * kGemvThreads;
-    const int r = id / cpr;
-    const int c = id - r * cpr;
-    // ids past the staged rows land in row 0's spare 16-byte slot, which nothing reads
-    const int dst = id < nrows * cpr ? r * row_stride + c * 8 : row_stride - 8;
-    *reinterpret_cast<u32x4_t*>(xs + dst) = xv[i];
-  }
-  {
-    const int pad = kSteps * 128 - in_dim;  // zero: its A operand is zero, keep 0 * pad finite
-    for (int i = tid; i < nrows * pad; i += kGemvThreads) {
-      const int r = i / pad;
-      xs[r * row_stride + in_dim + (i - r * pad)] = 0;
+      for (int r = 0; r < kVRows; ++r) src[r] = __builtin_amdgcn_readlane(src_l, r);
     }
+    u32x4_t xv[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int id = min(tid + i * kGemvThreads, nrows * cpr - 1);
+      const int r = id / cpr;
+      const int c = id - r * cpr;
+      int srow = src[0];
+#pragma unroll
+      for (int q = 1; q < kVRows; ++q) srow = r == q ? src[q] : srow;
+      const int64_t elem = (kDown ? (r & 1) * act_plane : 0) + (int64_t)srow * in_dim + c * 8;
+      if constexpr (kDown) {
+        // the hi/lo rows were stored by other workgroups of this launch
+        const __amdgpu_buffer_rsrc_t abuf =
+            __builtin_amdgcn_make_buffer_rsrc((void*)act, (short)0, 0x7fffffff, kBufferWord3);
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(abuf, (uint32_t)(elem * 2), 0, kAgentScope);
+      } else {
+        xv[i] = *reinterpret_cast<const u32x4_t*>(act + elem);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int id = tid + i * kGemvThreads;
+      const int r = id / cpr;
+      const int c = id - r * cpr;
+      // ids past the staged rows land in row 0's spare 16-byte slot, which nothing reads
+      const int dst = id < nrows * cpr ? r * row_stride + c * 8 : row_stride - 8;
+      *reinterpret_cast<u32x4_t*>(xs + dst) = xv[i];
+    }
+    {
+      const int pad = kSteps * 128 - in_dim;  // zero: its A operand is zero, keep 0 * pad finite
+      for (int i = tid; i < nrows * pad; i += kGemvThreads) {
+        const int r = i / pad;
+        xs[r * row_stride + in_dim + (i - r * pad)] = 0;
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   // B operand rows: column n = lr reads staged row min(n, kVRows - 1) without
   // masking; columns past the live rows produce outputs nobody stores (an

@@ -89,9 +89,6 @@ __device__ __forceinline__ float swiglu(float gate, float up, float limit) {
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
 // [2][pairs][in_down] (and float32 SwiGLU output to out_raw if set).  down:
 // act = those planes (rows by pair); writes float32 expert outputs.
-// s_waitcnt immediate that waits until at most n vector memory operations
-// and no LDS operation are outstanding (gfx9 encoding; export counter free).
-constexpr int vmcnt_imm(int n) { return (n & 0xf) | ((n >> 4) << 14) | 0x70; }
 
 // Step barrier of the LDS ring.  Each wave first waits for its own step-s
 // loads (vmcnt) and its LDS reads (lgkmcnt 0); the barrier then orders every

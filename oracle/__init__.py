@@ -33,7 +33,10 @@ Modules and what pins them (tests/test_oracle_*.py):
 * ``rmsnorm``   — streamed_attention.py:27-28 (the stacked workload only).
 
 Parity of every function above is pinned; no function is "parity unpinned".
-The one documented divergence is the top-k tie rule: equal bfloat16 logits
-are ordered by lower expert index first, where torch.topk's order on ties is
-implementation defined.
+Equal bfloat16 logits come out in torch.topk's CPU order (``torch_cpu``).  The
+one documented divergence is the router's accumulation: the logits are the
+correctly rounded bf16(f32(x . w) + b), where torch's F.linear accumulates in
+float32 and lands one bf16 ulp away on a few tokens; the golden vectors record
+every such logit, and tests/golden/router_boundary.npz the crafted routers on
+which it changes the routing.
 """

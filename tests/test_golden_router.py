@@ -85,3 +85,56 @@ def test_golden_ties_are_present():
         vals = np.sort(synth.bf16_bits_to_f32(logits), axis=1)[:, ::-1]
         ties = np.any(vals[:, :4] == vals[:, 1:5], axis=1)
         assert int(ties.sum()) >= 40, name
+
+
+def boundary_cases():
+    """tests/golden/router_boundary.npz (make_router_boundary_golden.py): per case the token's hidden row, the
+    crafted router (weight row f = row e, bias vector) and what torch's CPU ops made of it."""
+    g = np.load(GOLDEN / "router_boundary.npz", allow_pickle=False)
+    routers = {}
+    for ri, name in enumerate(("router_e32", "router_e128")):
+        gg, x, host = load_case(name)
+        routers[ri] = (x, host, int(gg["n_experts"]))
+    cases = []
+    for i in range(g["token"].shape[0]):
+        x, host, n_exp = routers[int(g["router"][i])]
+        e, f = int(g["e"][i]), int(g["f"][i])
+        w = host["router_weight"].copy()
+        if f >= 0:
+            w[f] = g["w_row"][i]
+        cases.append(dict(x=x[int(g["token"][i])][None, :], w=w, b=g["bias"][i][:n_exp], e=e, f=f,
+                          ids=g["ids"][i].astype(np.int64), weights=g["weights"][i],
+                          logits=g["logits"][i][:n_exp], oracle_same=bool(g["oracle_same"][i])))
+    return cases
+
+
+def test_oracle_on_crafted_boundary_routers():
+    """Routers crafted so that the logit where torch's F.linear differs from the correctly rounded value is a
+    selected one (44 cases) or sits at the top-4 boundary against a copy of its own row (40 cases)."""
+    cases = boundary_cases()
+    assert len(cases) >= 80
+    n_diff = 0
+    for c in cases:
+        ours = router.router_logits(c["x"], c["w"], c["b"])[0]
+        theirs = c["logits"]
+        # torch's row differs from the correctly rounded one at e (and at f, the copy of row e) only
+        differ = set(np.nonzero(ours != theirs)[0].tolist())
+        assert c["e"] in differ and differ <= {c["e"], c["f"]}
+        srt = np.argsort(-synth.bf16_bits_to_f32(theirs), kind="stable")
+        if c["f"] < 0:
+            assert srt[3] == c["e"]  # e is torch's 4th largest
+        else:
+            assert {int(srt[3]), int(srt[4])} == {c["e"], c["f"]}  # e and f are torch's 4th and 5th
+        # the oracle's top-k (torch's order) on torch's own logits gives torch's routing
+        ids, vals = router.topk(theirs[None, :], 4)
+        assert np.array_equal(ids[0], c["ids"])
+        assert np.array_equal(router.softmax_weights(vals)[0], c["weights"])
+        # on the correctly rounded logits the routing is torch's exactly where the fixture says so
+        own_ids, own_vals = router.topk(ours[None, :], 4)
+        same = np.array_equal(own_ids[0], c["ids"]) and np.array_equal(router.softmax_weights(own_vals)[0],
+                                                                         c["weights"])
+        assert same == c["oracle_same"]
+        n_diff += not same
+    # these cases are where the correctly rounded router and torch's part ways
+    assert n_diff == sum(not c["oracle_same"] for c in cases) and n_diff > 0
+    print(f"{len(cases)} crafted boundary cases, {n_diff} route differently from torch")

@@ -111,9 +111,11 @@ def test_small_layer_matches_oracle(gpu, n_tok, k, n_exp):
 
 
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
-def test_gpt_oss_20b_shape_layer(gpu, precision):
-    """gpt-oss-20B shape: H = I = 2880, 32 experts, top-4, a few decode tokens."""
-    host, dev_w, x = build(gpu, 0, 2880, 2880, 32, 3)
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_gpt_oss_20b_shape_layer(gpu, precision, n_tok):
+    """gpt-oss-20B shape: H = I = 2880, 32 experts, top-4; one decode token (the single-token layer of the
+    20B-shape benchmark) and three."""
+    host, dev_w, x = build(gpu, 0, 2880, 2880, 32, n_tok)
     check_layer(gpu, host, dev_w, x, 4, precision)
 
 

@@ -5,9 +5,11 @@ seeded tokens of the 20B-shape (E = 32) and 120B-shape (E = 128) router
 (streamed_moe_router.py:268-284, 497, 512-513; tests/golden/make_router_golden.py).
 The GPU's logits are the correctly rounded bf16(f32(x . w) + b); torch's
 F.linear accumulates in float32 and differs from that by one bf16 ulp in one
-logit on a few tokens (listed in the fixture).  On every other token the
-expert ids, their order (ties included) and the bf16 weights must be
-torch's exactly; the tokens with a differing logit are counted and reported.
+logit on a few tokens (listed in the fixture).  None of those logits is a
+selected one or sits at the top-k boundary on these tokens, so the expert ids,
+their order (ties included) and the bf16 weights must be torch's exactly on
+all 2048 tokens.  The crafted boundary cases, where such a logit does decide
+the routing, are in tests/test_gpu_router_boundary.py.
 """
 
 from __future__ import annotations
@@ -39,19 +41,17 @@ def load(name):
 
 def check_against_golden(name, g, logits_bits, ids, weights):
     diff_tokens = np.unique(g["logit_diffs"][:, 0])
-    same = np.ones(ids.shape[0], bool)
-    same[diff_tokens] = False
     # the GPU's logits differ from torch's exactly at the fixture's recorded positions
     theirs = logits_bits.copy()
     d = g["logit_diffs"]
     theirs[d[:, 0], d[:, 1]] = d[:, 2].astype(np.uint16)
     crc = np.array([zlib.crc32(theirs[t].tobytes()) for t in range(theirs.shape[0])], dtype=np.uint32)
     assert np.array_equal(crc, g["logits_crc"])
-    assert np.array_equal(ids[same], g["ids"][same].astype(ids.dtype))
-    assert np.array_equal(weights[same], g["weights"][same])
-    routed_differently = int(np.count_nonzero(np.any(ids[~same] != g["ids"][~same], axis=1)))
-    print(f"{name}: {int(same.sum())} tokens identical to torch; {len(diff_tokens)} tokens with a differing "
-          f"F.linear logit, {routed_differently} of them routed differently", flush=True)
+    # every token, those with a differing F.linear logit included
+    assert np.array_equal(ids, g["ids"].astype(ids.dtype))
+    assert np.array_equal(weights, g["weights"])
+    print(f"{name}: all {ids.shape[0]} tokens identical to torch ({len(diff_tokens)} with a differing F.linear "
+          f"logit)", flush=True)
 
 
 @pytest.mark.parametrize("name", ["router_e32", "router_e128"])
