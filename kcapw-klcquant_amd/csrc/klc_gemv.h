@@ -121,7 +121,8 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
   // chunk of step t in a tile = tile offset + 4096 t + voff.  kSteps is a
   // multiple of the ring size and may exceed the real step count g4: lanes
   // whose group 4t + lq is past the last group read out of range (0, no
-  // memory traffic) and decode with scale 0.
+  // memory traffic); their scale byte is record padding (0), so they decode
+  // to 0 * 2^-127 = 0.
   const int g4 = (groups + 3) >> 2;
   const uint32_t voff = (uint32_t)(lq * 1024 + trow * 16);
   const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;  // step g4 - 1
@@ -309,13 +310,12 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
         for (int j = 0; j < 4; ++j)
           bnext[j] = *reinterpret_cast<const bf16x8_t*>(xrow + (s + 1) * 128 + j * 8);
       }
-      // 2^(e-127) as float32 bits (e = 0: the subnormal 2^-127; e = 255: inf,
-      // which the conversion reads as the MX NaN scale); a lane past the
-      // last group uses scale 0 (finite E2M1 values times 0 are +-0)
-      const uint32_t eb = (sc[s >> 2] >> (8 * (s & 3))) & 0xffu;
-      uint32_t sbits = eb == 0u ? 0x00400000u : (eb << 23);
-      sbits = 4 * s + lq < groups ? sbits : 0u;
-      const float scale = __uint_as_float(sbits);
+      // 2^(e-127) as float32 by v_ldexp_f32: e = 0 gives the subnormal
+      // 2^-127, e = 255 gives inf, which the conversion reads as the MX NaN
+      // scale.  A lane past the last group reads out-of-range codes (0) and
+      // its scale byte is record padding, 0 in the packed layout: 0 * 2^-127.
+      const int eb = (int)((sc[s >> 2] >> (8 * (s & 3))) & 0xffu);
+      const float scale = __builtin_amdgcn_ldexpf(1.0f, eb - 127);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bf16x8_t a = decode8(w[j], scale);
@@ -338,41 +338,45 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
     const int row0 = tile * kTileRows + wave * 16 + 4 * lq;
     float v[4] = {acc[0], acc[1], acc[2], acc[3]};
     if constexpr (!kDown) {
+      // Lane (lq, lr) holds rows 4 lq .. 4 lq + 3 = (gate, up) of outputs
+      // 2 lq and 2 lq + 1 (h = 0, 1) for token lr.  Tokens are < 8, so the
+      // lanes lr >= 8 are free: they take output h = 1 of token lr - 8
+      // (row_shr:8 inside each 16-lane row), and every active lane evaluates
+      // one SwiGLU instead of two.
+      static_assert(kUnitTokensGateUp <= 8, "gate_up tokens fit lanes 0-7 of a row");
+      const int hs = lr >> 3;
+      const float g1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[2]), 0x118, 0xf, 0xf, false));
+      const float u1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[3]), 0x118, 0xf, 0xf, false));
+      float gate = hs ? g1 : v[0], up = hs ? u1 : v[1];
+      if (precision == KLC_PRECISION_BF16) {
+        gate = round_bf16(gate);
+        up = round_bf16(up);
+      }
+      gate += hs ? bias_row[2] : bias_row[0];
+      up += hs ? bias_row[3] : bias_row[1];
+      const float y = swiglu(gate, up, limit);
+      // down input: hi/lo bfloat16 planes (lo = 0 when the reference rounds to bf16)
+      const uint32_t hi = f32_to_bf16_rne(y);
+      const uint32_t lo = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y - bf16_to_f32(hi));
+      // lane lr < 8 collects h = 1 back from lane lr + 8 (row_shl:8)
+      const uint32_t hi_1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0x108, 0xf, 0xf, false);
+      const uint32_t lo_1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0x108, 0xf, 0xf, false);
+      const float y_1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x108, 0xf, 0xf, false));
       if (lr < nt) {
-        const int pair = out_pair;
         const int half = rows >> 1;
-        uint32_t hi2 = 0u, lo2 = 0u;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float gate = v[2 * h], up = v[2 * h + 1];
-          if (precision == KLC_PRECISION_BF16) {
-            gate = round_bf16(gate);
-            up = round_bf16(up);
-          }
-          gate += bias_row[2 * h];
-          up += bias_row[2 * h + 1];
-          const float y = swiglu(gate, up, limit);
-          const int64_t idx = (int64_t)pair * half + (row0 >> 1) + h;
-          // down input: hi/lo bfloat16 planes (lo = 0 when the reference rounds to bf16)
-          const uint32_t hi = f32_to_bf16_rne(y);
-          const uint32_t lo = precision == KLC_PRECISION_BF16 ? 0u : f32_to_bf16_rne(y - bf16_to_f32(hi));
-          if constexpr (kFused) {
-            hi2 |= hi << (16 * h);
-            lo2 |= lo << (16 * h);
-          } else {
-            if (out_raw) out_raw[idx] = y;
-            out_split[idx] = (uint16_t)hi;
-            out_split[out_plane + idx] = (uint16_t)lo;
-          }
-        }
+        // outputs (row0 / 2, row0 / 2 + 1) of the pair: one 4-byte word per
+        // plane (row0 is a multiple of 4 and half is even)
+        const int64_t idx = (int64_t)out_pair * half + (row0 >> 1);
+        const uint32_t hi2 = hi | (hi_1 << 16), lo2 = lo | (lo_1 << 16);
+        uint32_t* p = reinterpret_cast<uint32_t*>(out_split + idx);
+        uint32_t* q = reinterpret_cast<uint32_t*>(out_split + out_plane + idx);
         if constexpr (kFused) {
-          // outputs (row0 / 2, row0 / 2 + 1) of the pair: one 4-byte word per
-          // plane (row0 is a multiple of 4 and half is even)
-          const int64_t idx = (int64_t)pair * half + (row0 >> 1);
-          uint32_t* p = reinterpret_cast<uint32_t*>(out_split + idx);
           __hip_atomic_store(p, hi2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(reinterpret_cast<uint32_t*>(out_split + out_plane + idx), lo2, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(q, lo2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          if (out_raw) *reinterpret_cast<float2*>(out_raw + idx) = make_float2(y, y_1);
+          *p = hi2;
+          *q = lo2;
         }
       }
     } else {
