@@ -33,17 +33,15 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t*
   __shared__ double red[3 * 64 * 4];
   const int e0 = blockIdx.x * kRouterTile;
   const int t0 = blockIdx.y * kRouterTile;
+  // the tile's biases first (branch-free: out-of-range experts read 0), so
+  // they arrive with the weights instead of after the dot product
+  const __amdgpu_buffer_rsrc_t bbuf = bias_rsrc(b, n_exp);
+  float bias4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bias4[i] = load_bias_f32(bbuf, e0 + ((threadIdx.x & 63) >> 4) + 4 * i);
   const f64x4_t acc = router_block_dot(x, w, n_tok, hidden, n_exp, e0, t0, 0, (hidden + 31) >> 5,
                                        blockIdx.x == 0 ? x_f32 : nullptr, red);
-  if (threadIdx.x < kWave) {
-    float bias4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = e0 + ((threadIdx.x & 63) >> 4) + 4 * i;
-      bias4[i] = e < n_exp ? bf16_to_f32(b[e]) : 0.0f;
-    }
-    router_tile_store(acc, bias4, logits, n_tok, n_exp, e0, t0);
-  }
+  if (threadIdx.x < kWave) router_tile_store(acc, bias4, logits, n_tok, n_exp, e0, t0);
 }
 
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
@@ -237,20 +235,19 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   uint16_t* rows = reinterpret_cast<uint16_t*>(lds);  // [16][n_exp]
   // sums: wave w takes expert tiles w, w + 4, w + 8, ..., two per pass with
   // both tiles' loads in flight before the first is summed
+  const __amdgpu_buffer_rsrc_t bbuf = bias_rsrc(b, n_exp);
   for (int e_t = wave; e_t < n_et; e_t += 8) {
     if (!real_tok) continue;
     const bool second = e_t + 4 < n_et;
-    // the bias loads go first: they are independent of the partials
+    // the bias loads go first: they are independent of the partials, and
+    // branch-free (a branch around each would wait for it before the next)
     float bias4[2][4];
     u32x4_t v[2][2 * kRouterMaxSlices];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int et_h = h == 1 && second ? e_t + 4 : e_t;  // a missing second tile reloads the first
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = et_h * kRouterTile + (lane >> 4) + 4 * i;
-        bias4[h][i] = e < n_exp ? bf16_to_f32(b[e]) : 0.0f;
-      }
+      for (int i = 0; i < 4; ++i) bias4[h][i] = load_bias_f32(bbuf, et_h * kRouterTile + (lane >> 4) + 4 * i);
 #pragma unroll
       for (int q = 0; q < kRouterMaxSlices; ++q) {
         const int qq = min(q, n_ks - 1);

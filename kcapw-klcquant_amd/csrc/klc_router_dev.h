@@ -106,6 +106,16 @@ __device__ __forceinline__ f64x4_t router_block_dot(const uint16_t* __restrict__
   return acc;
 }
 
+// The router bias as a raw buffer of n_exp bfloat16 values.  load_bias_f32
+// reads expert e's as float32 and 0 for e >= n_exp (out of range: no memory
+// access), with no branch, so a tile's bias loads all go out together.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bias_rsrc(const uint16_t* b, int n_exp) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)b, (short)0, n_exp * 2, kBufferWord3);
+}
+__device__ __forceinline__ float load_bias_f32(__amdgpu_buffer_rsrc_t bbuf, int e) {
+  return bf16_to_f32((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(bbuf, (uint32_t)e * 2u, 0, 0));
+}
+
 // The calling wave rounds a tile's sums (its lanes holding them in the MFMA
 // D layout) like F.linear in bfloat16: bf16(f32(sum) + b).  Optionally also
 // into an LDS copy [16 tokens][n_exp] of the token tile's logits.
