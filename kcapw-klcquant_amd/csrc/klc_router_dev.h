@@ -135,18 +135,12 @@ __device__ __forceinline__ void router_tile_store(f64x4_t acc, const float (&bia
   }
 }
 
-// Orderable key: larger key = larger logit; NaN is the largest value; -0 == +0;
-// among equal values the lower expert index has the larger key.
-__device__ __forceinline__ uint64_t logit_key(uint32_t bf16bits, int idx) {
-  uint32_t u = bf16bits << 16;
-  uint32_t k32;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    k32 = 0xffffffffu;
-  } else {
-    if ((u & 0x7fffffffu) == 0u) u = 0u;
-    k32 = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  }
-  return ((uint64_t)k32 << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+// Selection key of a bfloat16 logit: its comparator key (order_key16: NaN
+// largest, -0 == +0) above the inverted expert index, so the maximum of the
+// keys is the largest value and, among equal values, the lower expert; 0 is
+// below every real key.
+__device__ __forceinline__ uint32_t sel_key(uint32_t bf16bits, int idx) {
+  return (order_key16(bf16bits) << 16) | (uint32_t)(0xffff - idx);
 }
 
 constexpr int kTopkMaxPerLane = 16;  // n_experts <= 1024
@@ -158,26 +152,33 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, kCtrl, kRowMask, 0xf, false);
 }
 template <int kCtrl, int kRowMask>
-__device__ __forceinline__ uint64_t dpp_max_step(uint64_t v) {
-  const uint32_t lo = dpp_u32<kCtrl, kRowMask>((uint32_t)v, (uint32_t)v);
-  const uint32_t hi = dpp_u32<kCtrl, kRowMask>((uint32_t)(v >> 32), (uint32_t)(v >> 32));
-  const uint64_t o = ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
+  const uint32_t o = dpp_u32<kCtrl, kRowMask>(v, v);
   return o > v ? o : v;
 }
 
-// Wave-wide maximum of a 64-bit key, returned to every lane: quad swaps,
-// half-row and row mirrors make every row hold its maximum, two row
-// broadcasts carry it into row 3, and lane 63 is read back.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = dpp_max_step<0xB1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
-  v = dpp_max_step<0x4E, 0xf>(v);   // quad_perm [2, 3, 0, 1]
-  v = dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
-  v = dpp_max_step<0x140, 0xf>(v);  // row_mirror
-  v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-  v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-  return ((uint64_t)hi << 32) | lo;
+// Maximum of a 32-bit key over each 16-lane row, in every lane of the row:
+// quad swaps, then half-row and row mirrors.
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = dpp_max_u32<0xB1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_max_u32<0x4E, 0xf>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_max_u32<0x141, 0xf>(v);  // row_half_mirror
+  return dpp_max_u32<0x140, 0xf>(v);  // row_mirror
+}
+
+// Wave-wide maximum of a 32-bit key, uniform: the row maxima, two row
+// broadcasts carry them into row 3, and lane 63 is read back.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = row_max_u32(v);
+  v = dpp_max_u32<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_max_u32<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Lane r of the caller's 16-lane row, in every lane of the row (DPP row_newbcast).
+template <int kR>
+__device__ __forceinline__ float row_lane_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + kR, 0xf, 0xf, false));
 }
 
 // Workgroup barrier that orders LDS accesses only: unlike __syncthreads it
@@ -527,15 +528,72 @@ __device__ __forceinline__ int wave_torch_topk_lanes(const uint16_t* row, int n,
 }
 
 // torch's CPU softmax (klc_torch_order.h) of the k values held by lanes
-// base .. base + k - 1 (lane base + r holds slot r), evaluated by every
-// lane; returns the bfloat16 weight of the calling lane's slot.
-__device__ __forceinline__ uint32_t torch_softmax_bf16(float v, int base, int k) {
+// 0 .. k - 1 of the wave (lane r holds slot r), evaluated by every lane:
+// the maximum in slot order, exp(v - max), the sum left to right, one
+// reciprocal; returns the bfloat16 weight of the calling lane's slot.  The
+// slot values are read with readlane (no LDS round trip).
+__device__ __forceinline__ uint32_t torch_softmax_bf16(float v, int k) {
 #pragma clang fp contract(off)
-  float mx = __shfl(v, base);
-  for (int r = 1; r < k; ++r) mx = torch_vec_max(mx, __shfl(v, base + r));
+  float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  for (int r = 1; r < k; ++r) mx = torch_vec_max(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r)));
   const float e = sleef_expf_u10(v - mx);
-  float sum = __shfl(e, base);
-  for (int r = 1; r < k; ++r) sum = sum + __shfl(e, base + r);
+  float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), 0));
+  for (int r = 1; r < k; ++r) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), r));
+  const float inv = 1.0f / sum;
+  return f32_to_bf16_rne(e * inv);
+}
+
+// The same softmax per 16-lane row: lane r < k of each row holds that row's
+// slot r (k <= 16); the values are broadcast inside the row by DPP.
+__device__ __forceinline__ uint32_t torch_softmax_bf16_row(float v, int k) {
+#pragma clang fp contract(off)
+  float mx = row_lane_f32<0>(v);
+#pragma unroll
+  for (int r = 1; r < 16; ++r) {
+    float x;
+    switch (r) {
+      case 1: x = row_lane_f32<1>(v); break;
+      case 2: x = row_lane_f32<2>(v); break;
+      case 3: x = row_lane_f32<3>(v); break;
+      case 4: x = row_lane_f32<4>(v); break;
+      case 5: x = row_lane_f32<5>(v); break;
+      case 6: x = row_lane_f32<6>(v); break;
+      case 7: x = row_lane_f32<7>(v); break;
+      case 8: x = row_lane_f32<8>(v); break;
+      case 9: x = row_lane_f32<9>(v); break;
+      case 10: x = row_lane_f32<10>(v); break;
+      case 11: x = row_lane_f32<11>(v); break;
+      case 12: x = row_lane_f32<12>(v); break;
+      case 13: x = row_lane_f32<13>(v); break;
+      case 14: x = row_lane_f32<14>(v); break;
+      default: x = row_lane_f32<15>(v); break;
+    }
+    if (r < k) mx = torch_vec_max(mx, x);
+  }
+  const float e = sleef_expf_u10(v - mx);
+  float sum = row_lane_f32<0>(e);
+#pragma unroll
+  for (int r = 1; r < 16; ++r) {
+    float x;
+    switch (r) {
+      case 1: x = row_lane_f32<1>(e); break;
+      case 2: x = row_lane_f32<2>(e); break;
+      case 3: x = row_lane_f32<3>(e); break;
+      case 4: x = row_lane_f32<4>(e); break;
+      case 5: x = row_lane_f32<5>(e); break;
+      case 6: x = row_lane_f32<6>(e); break;
+      case 7: x = row_lane_f32<7>(e); break;
+      case 8: x = row_lane_f32<8>(e); break;
+      case 9: x = row_lane_f32<9>(e); break;
+      case 10: x = row_lane_f32<10>(e); break;
+      case 11: x = row_lane_f32<11>(e); break;
+      case 12: x = row_lane_f32<12>(e); break;
+      case 13: x = row_lane_f32<13>(e); break;
+      case 14: x = row_lane_f32<14>(e); break;
+      default: x = row_lane_f32<15>(e); break;
+    }
+    if (r < k) sum = sum + x;
+  }
   const float inv = 1.0f / sum;
   return f32_to_bf16_rne(e * inv);
 }
@@ -553,11 +611,11 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
                                                    uint16_t* __restrict__ weights, int32_t* lds_ids,
                                                    uint32_t* tie_scratch) {
   const int lane = threadIdx.x & 63;
-  uint64_t keys[kSlots];
+  uint32_t keys[kSlots];
 #pragma unroll
   for (int s = 0; s < kSlots; ++s) {
     const int idx = lane + s * kWave;
-    keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
+    keys[s] = idx < n_exp ? sel_key(row[idx], idx) : 0u;  // a real key is never 0
   }
   // lane r keeps the r-th selection
   int my_id = 0;
@@ -565,21 +623,21 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
   uint32_t prev = 0;
   const int rounds = k < n_exp ? k + 1 : k;
   for (int r = 0; r < rounds; ++r) {
-    uint64_t best = keys[0];
+    uint32_t best = keys[0];
 #pragma unroll
     for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
-    best = wave_max_u64(best);
+    best = wave_max_u32(best);
 #pragma unroll
     for (int s = 0; s < kSlots; ++s)
-      if (keys[s] == best) keys[s] = 0ull;
-    const uint32_t value_key = (uint32_t)(best >> 32);
+      if (keys[s] == best) keys[s] = 0u;
+    const uint32_t value_key = best >> 16;
     tie |= r > 0 && value_key == prev;
     prev = value_key;
-    if (lane == r) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+    if (lane == r) my_id = (int)(0xffffu - (best & 0xffffu));
   }
   if (tie) my_id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, my_id);  // uniform: the same maxima
   const float my_val = bf16_to_f32(row[lane < k ? my_id : 0]);
-  const uint32_t w = torch_softmax_bf16(my_val, 0, k);
+  const uint32_t w = torch_softmax_bf16(my_val, k);
   if (lane < k) {
     const int64_t o = t * k + lane;
     // agent scope: the decode router's final dispatch may run in another workgroup
@@ -631,35 +689,32 @@ __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block,
   lds_barrier();
   if (n_valid > 0) {
     const uint16_t* row = rows(4 * wave + min(q, n_valid - 1));
-    uint64_t keys[kSlots];
+    uint32_t keys[kSlots];
 #pragma unroll
     for (int s = 0; s < kSlots; ++s) {
       const int idx = r + s * 16;
-      keys[s] = idx < n_exp ? logit_key(row[idx], idx) : 0ull;  // a real key is never 0
+      keys[s] = idx < n_exp ? sel_key(row[idx], idx) : 0u;  // a real key is never 0
     }
     int my_id = 0;
     bool tie = false;
     uint32_t prev = 0;
     const int rounds = k < n_exp ? k + 1 : k;
     for (int rd = 0; rd < rounds; ++rd) {
-      uint64_t best = keys[0];
+      uint32_t best = keys[0];
 #pragma unroll
       for (int s = 1; s < kSlots; ++s) best = keys[s] > best ? keys[s] : best;
-      best = dpp_max_step<0xB1, 0xf>(best);   // quad_perm [1, 0, 3, 2]
-      best = dpp_max_step<0x4E, 0xf>(best);   // quad_perm [2, 3, 0, 1]
-      best = dpp_max_step<0x141, 0xf>(best);  // row_half_mirror
-      best = dpp_max_step<0x140, 0xf>(best);  // row_mirror: every lane of the row holds its maximum
+      best = row_max_u32(best);  // every lane of the row holds its maximum
 #pragma unroll
       for (int s = 0; s < kSlots; ++s)
-        if (keys[s] == best) keys[s] = 0ull;
-      const uint32_t value_key = (uint32_t)(best >> 32);
+        if (keys[s] == best) keys[s] = 0u;
+      const uint32_t value_key = best >> 16;
       tie |= rd > 0 && value_key == prev;
       prev = value_key;
-      if (r == rd) my_id = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffull));
+      if (r == rd) my_id = (int)(0xffffu - (best & 0xffffu));
     }
     // every row's softmax is evaluated (the row's lanes exchange values); tie rows' results are dropped
     const float my_val = bf16_to_f32(row[r < k ? my_id : 0]);
-    const uint32_t w = torch_softmax_bf16(my_val, q * 16, k);
+    const uint32_t w = torch_softmax_bf16_row(my_val, k);
     if (q < n_valid) {
       if (tie) {
         if (r == 0) tie_list[atomicAdd(&tie_list[16], 1)] = 4 * wave + q;
@@ -680,7 +735,7 @@ __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block,
     const uint16_t* row = rows(t);
     const int id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, 0);
     const float v = bf16_to_f32(row[lane < k ? id : 0]);
-    const uint32_t w = torch_softmax_bf16(v, 0, k);
+    const uint32_t w = torch_softmax_bf16(v, k);
     if (lane < k) {
       const int64_t o = (t_base + t) * k + lane;
       __hip_atomic_store(ids + o, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
