@@ -15,6 +15,7 @@
 // klc_common.h).  gate_up applies bias and the
 // clamped SwiGLU on interleaved row pairs in registers and writes the down
 // input; down applies bias and writes float32 expert outputs.
+#include <functional>
 #include <mutex>
 
 #include "klc_common.h"
@@ -198,6 +199,198 @@ __global__ __launch_bounds__(256) void combine4_kernel(const float* __restrict__
   *reinterpret_cast<uint2*>(out + (int64_t)t * hidden + h) = o;
 }
 
+// ---- one token (decode batch of 1): no dispatch ---------------------------
+//
+// The token's k <= 4 experts come straight from the router's ids; its pair
+// for slot j is j.  gate_up runs the GEMV unit body with unit j = slot j.
+// down and the combine run as one launch: workgroup b owns output rows
+// [16 b, 16 b + 16) and wave j computes them for slot j (expert ids[j], the
+// pair's hi/lo rows staged by the wave itself), with the same operations in
+// the same order as the multi-launch GEMV (an MFMA output column depends on
+// its own B column only), so the expert outputs are bit-identical; the k
+// slots' rows then meet in LDS and 16 threads combine them in slot order
+// with the combine kernel's roundings.
+
+// pair index of slot j of the token (unit j's only pair)
+__device__ const int32_t kSlotPairs[kCombineMaxK] = {0, 1, 2, 3};
+
+template <int kSteps>
+__global__ __launch_bounds__(kGemvThreads) void gate_up_single_kernel(
+    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ out_split, int64_t out_plane, float* __restrict__ out_raw, const int32_t* __restrict__ ids,
+    int rows, int groups, int k_top, float limit, int precision, int tpw) {
+  extern __shared__ __align__(16) uint16_t xs[];
+  const int tiles = rows / kTileRows;
+  const int tile0 = blockIdx.x * tpw;
+  const int ntile = min(tpw, tiles - tile0);
+  if (ntile <= 0) return;
+  const int u = blockIdx.y;  // slot u < k_top
+  const int e = ids[u];
+  gemv_unit<false, kSteps, false>(wptr[e], bias, e, x, 0, nullptr, out_split, out_plane, out_raw, kSlotPairs + u, 1,
+                                  rows, groups, k_top, limit, precision, tile0, ntile, xs, NoWait{});
+}
+
+template <int kSteps>
+__global__ __launch_bounds__(kGemvThreads) void down_combine_single_kernel(
+    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
+    int64_t act_plane, const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int k,
+    float* __restrict__ eo, const uint16_t* residual, uint16_t* out, int rows, int groups, int precision) {
+  // [kVRows][row_stride] staged rows (slot j: rows 2 j and 2 j + 1), then [4][16] float32 outputs
+  extern __shared__ __align__(16) uint16_t xs[];
+  constexpr int kR = kRing < kSteps ? kRing : kSteps;
+  constexpr int row_stride = gemv_row_stride(kSteps);
+  constexpr int kRowChunks = gemv_row_chunks(kSteps);
+  constexpr int kBlocks = kRowChunks / 64;
+  constexpr int kRecWords = (kSteps + 7) / 8 * 2;
+  float* comb = reinterpret_cast<float*>(xs + kVRows * row_stride);
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, lr = lane & 15, lq = lane >> 4;
+  const int r0 = blockIdx.x * 16;  // first output row of the workgroup
+  const bool live = wave < k;
+  const int e = ids[live ? wave : 0];
+  const int cpr = groups * 4, in_dim = groups * 32;
+  const int g4 = (groups + 3) >> 2;
+  // the combine's operands, loaded first and converted only when used (a
+  // conversion here would wait for the loads before the weight stream starts)
+  uint32_t wj_bits[kCombineMaxK];
+#pragma unroll
+  for (int j = 0; j < kCombineMaxK; ++j) wj_bits[j] = wts[min(j, k - 1)];
+  // branch-free: a null residual is an empty buffer (out-of-range reads are 0)
+  const __amdgpu_buffer_rsrc_t rsbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)residual, (short)0, residual != nullptr ? rows * 2 : 0, kBufferWord3);
+  const uint32_t res_bits = __builtin_amdgcn_raw_buffer_load_b16(rsbuf, (uint32_t)(r0 + (tid & 15)) * 2u, 0, 0);
+  // ---- the wave's 16 rows of expert e: scale words and bias (before the
+  //      rows' DMA: only the ring's loads come between it and its wait) ----
+  const int trow = (r0 & (kTileRows - 1)) + lr;  // row inside its 64-row tile
+  const __amdgpu_buffer_rsrc_t wbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)wptr[e], (short)0, live ? (int)packed_matrix_bytes(rows, groups) : 0, kBufferWord3);
+  const uint32_t tb = (uint32_t)(r0 / kTileRows) * (uint32_t)groups * 1024u;
+  const uint32_t voff = (uint32_t)(lq * 1024 + trow * 16);
+  const uint32_t voff_tail = 4 * (g4 - 1) + lq < groups ? voff : kOutOfRange;
+  auto chunk = [&](int t) -> u32x4_t {
+    const uint32_t v = t >= g4 ? kOutOfRange : (t == g4 - 1 ? voff_tail : voff);
+    return __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tb + 4096u * t, kStreamPolicy);
+  };
+  const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
+  const int rec = ((groups + 3) / 4 + 7) / 8 * 8;
+  uint32_t sc[kRecWords];
+#pragma unroll
+  for (int i = 0; i < kRecWords / 2; ++i) {
+    const uint32_t off = (uint32_t)packed_scale_word(groups, r0 + lr, min(i, rec / 8 - 1), lq);
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(wbuf, off, scale_base, kStreamPolicy);
+    sc[2 * i] = v.x;
+    sc[2 * i + 1] = v.y;
+  }
+  const u32x2_t bias4 = *reinterpret_cast<const u32x2_t*>(bias + (int64_t)e * rows + r0 + 4 * lq);
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- the wave's hi and lo rows of pair `wave` by LDS-DMA (out of range
+  //      for a slot past k), then the pad chunks zeroed ----
+#pragma unroll
+  for (int m = 0; m < 2 * kBlocks; ++m) {
+    const int pl = m / kBlocks, b = m - pl * kBlocks;
+    const uint16_t* row = act + pl * act_plane + (int64_t)(live ? wave : 0) * in_dim;
+    const __amdgpu_buffer_rsrc_t rbuf =
+        __builtin_amdgcn_make_buffer_rsrc((void*)row, (short)0, live ? cpr * 16 : 0, kBufferWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rbuf, (__attribute__((address_space(3))) void*)(xs + (2 * wave + pl) * row_stride + b * 512), 16,
+        (uint32_t)((b * 64 + lane) * 16), 0, 0, 0);
+  }
+  for (int c = cpr + lane; c < kRowChunks; c += kWave) {
+    *reinterpret_cast<u32x4_t*>(xs + (2 * wave) * row_stride + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4_t*>(xs + (2 * wave + 1) * row_stride + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4_t ring[kR];
+#pragma unroll
+  for (int t = 0; t < kR; ++t) ring[t] = chunk(t);
+  __builtin_amdgcn_sched_barrier(0);
+  // the rows have landed (the ring's loads after them stay in flight); the
+  // barrier and the workgroup-scope acquire keep the LDS reads below the wait
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kR));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+  // B: column 0 the hi row, columns 1..15 the lo row (only columns 0 and 1 are used)
+  const uint16_t* xrow = xs + (2 * wave + min(lr, 1)) * row_stride + lq * 32;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  bf16x8_t bcur[4], bnext[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bcur[j] = *reinterpret_cast<const bf16x8_t*>(xrow + j * 8);
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(ring[s % kR]));
+    const u32x4_t w = ring[s % kR];
+    ring[s % kR] = chunk(s + kR);
+    if (s + 1 < kSteps) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bnext[j] = *reinterpret_cast<const bf16x8_t*>(xrow + (s + 1) * 128 + j * 8);
+    }
+    const int eb = (int)((sc[s >> 2] >> (8 * (s & 3))) & 0xffu);
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, eb - 127);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(decode8(w[j], scale), bcur[j], acc, 0, 0, 0);
+    if (s + 1 < kSteps) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bcur[j] = bnext[j];
+    }
+  }
+  // ---- epilogue: hi + lo (columns 0 and 1), bias, this slot's expert output ----
+  float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], 1);
+  if (live && lr == 0) {
+    const float bias_row[4] = {bf16_to_f32(bias4.x & 0xffffu), bf16_to_f32(bias4.x >> 16),
+                               bf16_to_f32(bias4.y & 0xffffu), bf16_to_f32(bias4.y >> 16)};
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (precision == KLC_PRECISION_BF16 ? round_bf16(v[i]) : v[i]) + bias_row[i];
+    *reinterpret_cast<float4*>(eo + (int64_t)wave * rows + r0 + 4 * lq) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(comb + wave * 16 + 4 * lq) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+  __syncthreads();
+  // ---- combine: the slots in order, every step rounded to bfloat16 ----
+  if (tid < 16) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kCombineMaxK; ++j)
+      if (j < k) a = round_bf16(a + round_bf16(round_bf16(comb[j * 16 + tid]) * bf16_to_f32(wj_bits[j])));
+    if (residual != nullptr) a = bf16_to_f32(res_bits) + a;
+    out[r0 + tid] = (uint16_t)f32_to_bf16_rne(a);
+  }
+}
+
+using GateUpSingleKernel = void (*)(const uint8_t* const*, const uint16_t*, const uint16_t*, uint16_t*, int64_t,
+                                   float*, const int32_t*, int, int, int, float, int, int);
+using DownCombineSingleKernel = void (*)(const uint8_t* const*, const uint16_t*, const uint16_t*, int64_t,
+                                         const int32_t*, const uint16_t*, int, float*, const uint16_t*, uint16_t*,
+                                         int, int, int);
+
+template <typename K, template <int> class Pick>
+K single_kernel_for(int steps) {
+  switch (steps) {
+    case 1: return Pick<1>::fn;
+    case 2: return Pick<2>::fn;
+    case 3: return Pick<3>::fn;
+    case 4: return Pick<4>::fn;
+    case 6: return Pick<6>::fn;
+    case 8: return Pick<8>::fn;
+    case 16: return Pick<16>::fn;
+    case 24: return Pick<24>::fn;
+    default: return nullptr;
+  }
+}
+template <int kSteps>
+struct PickGateUpSingle {
+  static constexpr GateUpSingleKernel fn = gate_up_single_kernel<kSteps>;
+};
+template <int kSteps>
+struct PickDownCombineSingle {
+  static constexpr DownCombineSingleKernel fn = down_combine_single_kernel<kSteps>;
+};
+
 __global__ __launch_bounds__(256) void bias_combine_kernel(const uint16_t* __restrict__ bias,
                                                            const int32_t* __restrict__ ids,
                                                            const uint16_t* __restrict__ w, int k, int hidden,
@@ -333,6 +526,35 @@ int launch_down(const void* const* w, const void* bias, const void* gated_split,
       static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs, list,
       units + 1, (int)hidden, (int)(inter / 32), 1, 0.0f, precision, tpw);
   return check_launch("moe_gemv_mfma_kernel<down>");
+}
+
+// One token's gate_up GEMV, one grid row per slot of its top-k (ids).
+int launch_gate_up_single(const void* const* w, const void* bias, const void* x, const int32_t* ids, int64_t k,
+                          int64_t hidden, int64_t inter, float limit, int precision, void* gated_split,
+                          float* gated_raw, hipStream_t stream) {
+  const int tiles = (int)(2 * inter / kTileRows);
+  const int tpw = tiles_per_workgroup(tiles, k, kGemvWorkgroupsUp, kGemvMaxTilesUp);
+  const int steps = gemv_steps((int)(hidden / 32));
+  single_kernel_for<GateUpSingleKernel, PickGateUpSingle>(steps)<<<
+      dim3((unsigned)((tiles + tpw - 1) / tpw), (unsigned)k), kGemvThreads, gemv_lds_bytes(steps), stream>>>(
+      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
+      static_cast<uint16_t*>(gated_split), k * inter, gated_raw, ids, (int)(2 * inter), (int)(hidden / 32), (int)k,
+      limit, precision, tpw);
+  return check_launch("gate_up_single_kernel");
+}
+
+// One token's down GEMV for its k <= 4 slots and the combine, one workgroup per 16 output rows.
+int launch_down_combine_single(const void* const* w, const void* bias, const void* gated_split, const int32_t* ids,
+                               const void* weights, int64_t k, int64_t hidden, int64_t inter, int precision,
+                               float* eo, const void* residual, void* out, hipStream_t stream) {
+  const int steps = gemv_steps((int)(inter / 32));
+  single_kernel_for<DownCombineSingleKernel, PickDownCombineSingle>(steps)<<<
+      (unsigned)(hidden / 16), kGemvThreads, gemv_lds_bytes(steps) + 4 * 16 * sizeof(float), stream>>>(
+      reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
+      static_cast<const uint16_t*>(gated_split), k * inter, ids, static_cast<const uint16_t*>(weights), (int)k, eo,
+      static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(out), (int)hidden, (int)(inter / 32),
+      precision);
+  return check_launch("down_combine_single_kernel");
 }
 
 int launch_combine(const float* eo, const void* w, const void* residual, int64_t n_tok, int64_t k, int64_t hidden,
@@ -571,6 +793,8 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
               "klc_moe_layer: KLC_PATH_FUSED does not take n_tokens=%lld, n_experts=%lld, k=%lld (at most 16 tokens, "
               "64 pairs, 256 experts, k <= 16, 8-byte aligned out/residual, no graph capture)",
               (long long)n_tokens, (long long)n_experts, (long long)k);
+  // one token routed here, by the GEMVs: the single-token kernels
+  const bool single = route == KLC_PATH_GEMV && router_w != nullptr && n_tokens == 1 && k <= kCombineMaxK;
   if ((rc = mark(0))) return rc;
   if (route == KLC_PATH_FUSED) {
     // the whole layer in one launch; the remaining events follow it back to back
@@ -588,6 +812,15 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
     if ((rc = mark(2))) return rc;
     if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, units, st)))
       return rc;
+  } else if (single) {
+    // one token: logits and top-k in one launch, no dispatch (the expert
+    // kernels take the token's slots from the ids)
+    if ((rc = launch_router_decode(x, router_w, router_b, logits, 1, hidden, n_experts, k, ids_buf, values, w_buf,
+                                   nullptr, nullptr, nullptr, nullptr, nullptr, counters,
+                                   reinterpret_cast<double*>(ws + s.partials), st)))
+      return rc;
+    if ((rc = mark(1))) return rc;
+    if ((rc = mark(2))) return rc;
   } else if (n_tokens <= kDecodeRouterTokens) {
     // decode batches: logits, top-k and dispatch in one launch
     KLC_REQUIRE(decode_router_counters(n_tokens, n_experts) * 4 <= kCounterBytes, KLC_ERR_UNSUPPORTED,
@@ -609,6 +842,19 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
       return rc;
   }
   if ((rc = mark(3))) return rc;
+  if (single) {
+    if ((rc = launch_gate_up_single(w_gate_up, gate_up_bias, x, ids_buf, k, hidden, inter, swiglu_limit, precision,
+                                    gated, gated_raw, st)))
+      return rc;
+    if ((rc = mark(4))) return rc;
+    if ((rc = launch_down_combine_single(w_down, down_bias, gated, ids_buf, w_buf, k, hidden, inter, precision, eo,
+                                         residual, out, st)))
+      return rc;
+    if ((rc = mark(5))) return rc;
+    if ((rc = mark(6))) return rc;
+    if (norms == nullptr) return KLC_OK;
+    return klc_moe_pair_norms(gated_raw, eo, k, inter, hidden, norms, st);
+  }
   const bool gemm = route == KLC_PATH_GEMM;
   if (!gemm && (rc = check_gemv_grid(n_tokens * k, n_experts))) return rc;
   if (gemm) {
@@ -770,10 +1016,9 @@ extern "C" int klc_moe_select(const void* x, const void* router_w, const void* r
   if (n_tokens <= kDecodeRouterTokens) {
     KLC_REQUIRE(decode_router_counters(n_tokens, n_experts) * 4 <= kCounterBytes, KLC_ERR_UNSUPPORTED,
                 "%s: %lld experts need more completion counters than the workspace holds", fn, (long long)n_experts);
+    // routing only: the expert half (klc_moe_experts) builds its own dispatch
     return launch_router_decode(x, router_w, router_b, ws + s.logits, n_tokens, hidden, n_experts, k, ids, values,
-                                weights, reinterpret_cast<int32_t*>(ws + s.offsets),
-                                reinterpret_cast<int32_t*>(ws + s.sorted), reinterpret_cast<int32_t*>(ws + s.active),
-                                reinterpret_cast<int32_t*>(ws + s.n_active), reinterpret_cast<int32_t*>(ws + s.units),
+                                weights, nullptr, nullptr, nullptr, nullptr, nullptr,
                                 reinterpret_cast<uint32_t*>(ws + s.counters),
                                 reinterpret_cast<double*>(ws + s.partials), st);
   }

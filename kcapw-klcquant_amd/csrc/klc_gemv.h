@@ -166,8 +166,16 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
   u32x4_t ring[kR];
 
   if constexpr (!kFused) {
-    // ---- activation rows by LDS-DMA, before any weight load: waiting for
-    //      them (the oldest loads) then waits for no weight chunk.  Row r's
+    // scale record and bias of the first tile first: the only loads issued
+    // between the rows' DMA and the wait for it are then the ring's, whose
+    // count is fixed (a load the compiler moved past the wait, as it may
+    // move one whose only use is in a later block, would be counted wrongly)
+    load_rec(tile0, sc);
+    bias_cur = load_bias(tile0);
+    bias_next = bias_cur;
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- activation rows by LDS-DMA, before any weight chunk: waiting for
+    //      them then waits for no weight chunk.  Row r's
     //      64-chunk block b is one wave-wide buffer load into LDS (lane l
     //      writes chunk 64 b + l); chunks past the row and rows past the
     //      unit's are out of range (no memory traffic).  The pad chunks of
@@ -196,15 +204,12 @@ __device__ __forceinline__ void gemv_unit(const uint8_t* __restrict__ wmat, cons
       if (r < nrows && c < gemv_row_chunks(kSteps)) *reinterpret_cast<u32x4_t*>(xs + r * row_stride + c * 8) = u32x4_t{0u, 0u, 0u, 0u};
     }
     __builtin_amdgcn_sched_barrier(0);
-    // ---- scale record and bias of the first tile, then the ring prologue ----
-    load_rec(tile0, sc);
-    bias_cur = load_bias(tile0);
-    bias_next = bias_cur;
+    // ---- the ring prologue ----
 #pragma unroll
     for (int t = 0; t < kR; ++t) ring[t] = chunk(tb, t, true);
     __builtin_amdgcn_sched_barrier(0);
-    // every wave's rows have landed (the loads after them stay in flight)
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kRecWords / 2 + 1 + kR));
+    // every wave's rows have landed (the ring's loads after them stay in flight)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kR));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   } else {

@@ -196,6 +196,19 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_multi_kernel(const 
   }
 }
 
+// Router of a decode batch in one launch.  Workgroup (et, tt, ks) computes
+// the partial logits of the tile (experts 16 et.., tokens 16 tt..) over the
+// ks-th of gridDim.z slices of the hidden dimension and stores them.  The
+// last of a token tile's workgroups to arrive (counted in a self-resetting
+// counter) sums every expert tile's slices in slice order (a fixed order, so
+// the result does not depend on which workgroup is last), rounds the logits,
+// and selects the top-k + softmax of the tile's tokens from an LDS copy.
+// With one token tile it then builds the expert-sorted dispatch itself;
+// otherwise the last token tile to finish does.  With units == nullptr the
+// launch routes only (ids, values, weights, logits) and builds no dispatch.
+// counters: [n_tt] token-tile counters and 1 final counter, zero before the
+// first launch and left zero by every launch.  partials: [n_tt][n_et]
+// [gridDim.z][256] float64.
 __global__ __launch_bounds__(256) void router_decode_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b, uint16_t* logits,
     int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
@@ -283,7 +296,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp));
     topk_softmax_row(rows, n_exp, k, 0, ids, values, weights, tile_ids, tie_scratch);
     wave_lds_sync();
-    single_token_dispatch(tile_ids, n_exp, k, offsets, sorted, active, n_active, units);
+    if (units != nullptr) single_token_dispatch(tile_ids, n_exp, k, offsets, sorted, active, n_active, units);
     return;
   }
   {
@@ -293,6 +306,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     topk_softmax_block([&](int t) { return rows + t * n_exp; }, min(kRouterTile, n_tok - t0), n_exp, k, t0, ids,
                        values, weights, n_tt == 1 ? tile_ids : nullptr, tie_scratch, tie_list);
   }
+  if (units == nullptr) return;  // routing only: no dispatch
   if (n_tt > 1) {
     if (!arrive_last(counters + n_tt, (uint32_t)n_tt, &flag)) return;
     block_dispatch([&](int p) { return __hip_atomic_load(ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); },

@@ -1044,18 +1044,6 @@ __device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t expected, ui
   return *flag != 0u;
 }
 
-// Router of a decode batch in one launch.  Workgroup (et, tt, ks) computes
-// the partial logits of the tile (experts 16 et.., tokens 16 tt..) over the
-// ks-th of gridDim.z slices of the hidden dimension and stores them.  The
-// last of a token tile's workgroups to arrive (counted in a self-resetting
-// counter) sums every expert tile's slices in slice order (a fixed order, so
-// the result does not depend on which workgroup is last), rounds the logits,
-// and selects the top-k + softmax of the tile's tokens from an LDS copy.
-// With one token tile it then builds the expert-sorted dispatch itself;
-// otherwise the last token tile to finish does.
-// counters: [n_tt] token-tile counters and 1 final counter, zero before the
-// first launch and left zero by every launch.  partials: [n_tt][n_et]
-// [gridDim.z][256] float64.
 // block_dispatch's outputs for at most 64 pairs (one token tile), by one
 // wave: pair p sits in lane p; its rank among the earlier pairs of its
 // expert comes from the key ballots (wave_peers), the per-expert counts from

@@ -104,7 +104,8 @@ def assert_final_close(out_bits, ref, precision="fp32"):
     assert (err <= ATOL + RTOL * np.abs(want) + slack).all(), f"final output worst error {err.max():.3e}"
 
 
-@pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 8), (16, 4, 8), (5, 2, 3), (33, 4, 16), (97, 2, 37), (128, 4, 256)])
+@pytest.mark.parametrize("n_tok,k,n_exp", [(1, 4, 8), (1, 2, 8), (1, 3, 37), (1, 1, 4), (16, 4, 8), (5, 2, 3),
+                                           (33, 4, 16), (97, 2, 37), (128, 4, 256)])
 def test_small_layer_matches_oracle(gpu, n_tok, k, n_exp):
     host, dev_w, x = build(gpu, 50 + n_tok, 128, 64, n_exp, n_tok)
     check_layer(gpu, host, dev_w, x, k, "fp32")
@@ -165,3 +166,18 @@ def test_pair_norms(gpu):
     o = det["expert_out"].cpu().numpy().astype(np.float64)
     np.testing.assert_allclose(norms[:, 0], np.linalg.norm(g, axis=1), rtol=1e-6)
     np.testing.assert_allclose(norms[:, 1], np.linalg.norm(o, axis=1), rtol=1e-6)
+
+
+@pytest.mark.parametrize("k", [4, 2])
+def test_single_token_layer_with_residual(gpu, k):
+    """One token takes the single-token kernels (gate_up by slot, down with the combine in one launch); with a
+    residual its output is the step-by-step path's combine plus the residual, bit for bit."""
+    host, dev_w, x = build(gpu, 91, 2880, 2880, 128, 1)
+    layer = moe.MoELayer(dev_w, k)
+    xt = bf16_tensor(x, gpu)
+    res = bf16_tensor(moe.synthetic_hidden(92, 1, 2880), gpu)
+    out = layer.forward(xt, residual=res)
+    det = layer.forward_detailed(xt)
+    want = ops.combine(det["expert_out"], det["weights"], 1, k, residual=res)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(out), bf16_bits(want))
