@@ -126,12 +126,17 @@ def layer_bytes(unique_experts: int, n_tok: int, n_exp: int = EXPERTS) -> int:
 def kernel_breakdown(interval_us, n_tok: int, path: str) -> dict:
     """Per-kernel times from the library's KLC_LAYER_EVENTS events.  A batch that runs as one launch
     (path "fused", up to 16 tokens) records the first event before it and the other six after it.
+    One token runs three launches (router, gate_up, down with the combine).
     Batches of up to 128 tokens run router, top-k and dispatch as one launch (router_decode_kernel),
     so their events 1 and 2 follow it back to back.  Intervals between back-to-back events measure
     only the event records and are reported apart."""
     us = [round(float(v), 3) for v in interval_us]
     if path == "fused":
         return {"fused_layer": us[0], "event_records_only": round(sum(us[1:]), 3)}
+    if n_tok == 1 and path == "gemv":
+        # one token: router without dispatch, gate_up by slot, down GEMV + combine in one launch
+        return {"router_topk": us[0], "gate_up": us[3], "down_combine": us[4],
+                "event_records_only": round(us[1] + us[2] + us[5], 3)}
     if n_tok <= 128:
         return {"router_topk_dispatch": us[0], "gate_up": us[3], "down": us[4], "combine": us[5],
                 "event_records_only": round(us[1] + us[2], 3)}
