@@ -38,8 +38,10 @@
 // needs resetting and the layer leaves no state behind.  A launch inside HIP
 // graph capture would replay one tag, so captured calls use the multi-launch
 // layer.  Every wait is bounded: a wait that runs out (which
-// needs a GPU shared with kernels that hold its compute units) sets a status
-// bit and goes on, so the launch always ends.
+// needs a GPU shared with kernels that hold its compute units) sets a sticky
+// status bit, records the launch's tag and goes on, so the launch always
+// ends; the launch then poisons what it writes after that point (ids -1,
+// NaN weights, NaN outputs), so the failure shows without a host sync.
 //
 // Numerics are the multi-launch layer's: the GEMVs are the same device code
 // (klc_gemv.h) and the combine performs the same operations in the same
@@ -47,6 +49,7 @@
 // float64 sums are exact for bfloat16 products short of a 2^53 spread of
 // magnitudes, so the logits are the correctly rounded ones, as there.
 #include <atomic>
+#include <cstdlib>
 #include <mutex>
 
 #include "klc_gemv.h"
@@ -97,7 +100,9 @@ struct FusedArgs {
   uint64_t* flags;                 // [max_up_items + max_dn_items] tags of finished items
   uint16_t* gated;                 // hi/lo planes [2][pairs][inter]
   float* eo;                       // [pairs][hidden]
-  uint32_t* status;                // bit 0: a wait ran out
+  uint32_t* status;                // bit 0: a wait ran out (sticky: never cleared by a launch)
+  uint64_t* fail_tag;              // the tag of the last launch in which a wait ran out
+  int spin_limit;                  // polls of a wait before it gives up; < 0: give up at once
   int n_tok, hidden, inter, n_exp, k, precision;
   float limit;
   uint64_t tag;                    // the launch's flag value; tag_word(tag) tags the logit words
@@ -234,16 +239,31 @@ __device__ __forceinline__ void router_expert(const FusedArgs& a, int e, double*
   }
 }
 
-// The calling wave polls n flag words until all hold `tag`.
-__device__ __forceinline__ void wait_flags(const uint64_t* flags, int n, uint64_t tag, uint32_t* status) {
+// A wait that ran out: the sticky status bit for the host, and the launch's
+// tag for this launch's workgroups (their outputs are then poisoned).
+// The stores complete before the wave goes on, so the workgroup's other
+// waves (after its next barrier) and the consumers of its later flags see them.
+__device__ __forceinline__ void ran_out(uint32_t* status, uint64_t* fail_tag, uint64_t tag) {
+  __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(fail_tag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+}
+__device__ __forceinline__ bool launch_failed(const FusedArgs& a) {
+  return __hip_atomic_load(a.fail_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.tag;
+}
+
+// The calling wave polls n flag words until all hold `tag`, at most
+// `limit` times (limit < 0: none).  A wait that runs out reports it (ran_out).
+__device__ __forceinline__ void wait_flags(const uint64_t* flags, int n, uint64_t tag, uint32_t* status,
+                                           uint64_t* fail_tag, int limit) {
   const int lane = threadIdx.x & 63;
   for (int it = 0;; ++it) {
-    bool done = true;
-    for (int i = lane; i < n; i += kWave)
+    bool done = limit >= 0;
+    for (int i = lane; done && i < n; i += kWave)
       done &= __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
     if (__ballot(!done) == 0) return;
-    if (it >= kSpinLimit) {
-      if (lane == 0) __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (it >= limit) {
+      if (lane == 0) ran_out(status, fail_tag, tag);
       return;
     }
     __builtin_amdgcn_s_sleep(2);
@@ -295,7 +315,7 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
       // every poll writes the logits it read into the rows [16][n_exp]: once
       // all words carry the tag, the rows hold this launch's logits
       for (int it = 0;; ++it) {
-        bool done = true;
+        bool done = a.spin_limit >= 0;  // a negative limit gives up after the first read
         for (int i = lane; i < total; i += kWave) {
           const uint64_t wd = __hip_atomic_load(a.words + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           done &= (wd & ~0xffffull) == wtag;
@@ -303,8 +323,8 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
           rows[t * n_exp + e] = (uint16_t)(wd & 0xffffu);
         }
         if (__ballot(!done) == 0) break;
-        if (it >= kSpinLimit) {
-          if (lane == 0) __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (it >= a.spin_limit) {
+          if (lane == 0) ran_out(a.status, a.fail_tag, a.tag);
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -330,10 +350,14 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
     }
     lds_barrier();
     if (blockIdx.x == 0) {
+      // a routing wait of this launch that ran out (here or in another
+      // workgroup so far) poisons the routing outputs: ids -1, NaN weights
+      // and values
+      const bool failed = launch_failed(a);
       for (int i = threadIdx.x; i < n_pairs; i += kFusedThreads) {
-        a.ids[i] = R.ids[i];
-        a.weights[i] = R.wts[i];
-        a.values[i] = values[i];
+        a.ids[i] = failed ? -1 : R.ids[i];
+        a.weights[i] = failed ? (uint16_t)0x7fc0u : R.wts[i];
+        a.values[i] = failed ? __uint_as_float(0x7fc00000u) : values[i];
       }
       for (int i = threadIdx.x; i < n_tok * n_exp; i += kFusedThreads) a.logits[i] = rows[i];
     }
@@ -385,7 +409,7 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
       const uint64_t* need = a.flags + ug * tg_up;
       const int tile0 = j * tpw_dn;
       auto wait_inputs = [&]() {
-        if (wave == 0) wait_flags(need, tg_up, a.tag, a.status);
+        if (wave == 0) wait_flags(need, tg_up, a.tag, a.status, a.fail_tag, a.spin_limit);
         lds_barrier();
       };
       gemv_unit<true, kSteps, true, kRingDn>(a.w_dn[e], a.b_dn, e, a.gated, plane, a.eo, nullptr, 0, nullptr,
@@ -398,20 +422,24 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
       const int j = item - n_up - n_dn;
       if (wave == 0) {
         const uint64_t* base = a.flags + a.max_up_items;
-        const int lim = kSpinLimit;
+        const int lim = a.spin_limit;
         for (int it = 0;; ++it) {
-          const bool done = lane >= n_dn_units ||
-                            __hip_atomic_load(base + lane * tg_dn + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                                a.tag;
+          const bool done = lim >= 0 && (lane >= n_dn_units ||
+                                         __hip_atomic_load(base + lane * tg_dn + j, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT) == a.tag);
           if (__ballot(!done) == 0) break;
           if (it >= lim) {
-            if (lane == 0) __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) ran_out(a.status, a.fail_tag, a.tag);
             break;
           }
           __builtin_amdgcn_s_sleep(2);
         }
       }
       lds_barrier();
+      // a wait of this launch that ran out before this point (the workgroup
+      // that ran out records it before it publishes its flag) poisons this
+      // tile group's outputs: NaN, with or without the residual
+      const bool failed = launch_failed(a);
       const int r0 = j * tpw_dn * kTileRows;
       const int nq = (min(a.hidden, r0 + tpw_dn * kTileRows) - r0) >> 2;  // 4-output groups per token
       const __amdgpu_buffer_rsrc_t ebuf =
@@ -445,8 +473,9 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
           acc[2] = bf16_to_f32(rv.y & 0xffffu) + acc[2];
           acc[3] = bf16_to_f32(rv.y >> 16) + acc[3];
         }
-        const uint2 o = make_uint2(f32_to_bf16_rne(acc[0]) | (f32_to_bf16_rne(acc[1]) << 16),
-                                   f32_to_bf16_rne(acc[2]) | (f32_to_bf16_rne(acc[3]) << 16));
+        const uint2 o = failed ? make_uint2(0x7fc07fc0u, 0x7fc07fc0u)
+                               : make_uint2(f32_to_bf16_rne(acc[0]) | (f32_to_bf16_rne(acc[1]) << 16),
+                                            f32_to_bf16_rne(acc[2]) | (f32_to_bf16_rne(acc[3]) << 16));
         *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.hidden + h) = o;
       }
     }
@@ -499,7 +528,8 @@ int64_t fused_decode_scratch_bytes(int64_t n_tok, int64_t hidden, int64_t inter,
   const int64_t words = n_exp * n_tok * 8;
   const int64_t flags = (units_capacity(pairs, n_exp, kUnitTokensGateUp) * (2 * inter / kTileRows) +
                          units_capacity(pairs, n_exp, kUnitTokensDown) * (hidden / kTileRows)) * 8;
-  return ((words + 255) & ~(int64_t)255) + ((flags + 8 + 255) & ~(int64_t)255);
+  // flags, then the status word, 4 spare bytes and the failed launch's tag
+  return ((words + 255) & ~(int64_t)255) + ((flags + 16 + 255) & ~(int64_t)255);
 }
 
 int launch_moe_decode_fused(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
@@ -555,6 +585,7 @@ int launch_moe_decode_fused(const void* x, const void* router_w, const void* rou
   a.max_up_items = (int)(units_capacity(pairs, n_exp, kUnitTokensGateUp) * (2 * inter / kTileRows));
   const int64_t max_dn_items = units_capacity(pairs, n_exp, kUnitTokensDown) * (hidden / kTileRows);
   a.status = reinterpret_cast<uint32_t*>(a.flags + a.max_up_items + max_dn_items);
+  a.fail_tag = reinterpret_cast<uint64_t*>(a.status + 2);
   a.gated = static_cast<uint16_t*>(gated);
   a.eo = eo;
   a.n_tok = (int)n_tok;
@@ -565,6 +596,10 @@ int launch_moe_decode_fused(const void* x, const void* router_w, const void* rou
   a.precision = precision;
   a.limit = limit;
   a.tag = tag;
+  // KLC_FUSED_SPIN_LIMIT overrides the polls a wait makes before it gives
+  // up (a negative value: none; for tests of the failure path)
+  a.spin_limit = kSpinLimit;
+  if (const char* env = getenv("KLC_FUSED_SPIN_LIMIT")) a.spin_limit = atoi(env);
   kern<<<grid, kFusedThreads, lds, stream>>>(a);
   return check_launch("moe_decode_fused_kernel");
 }

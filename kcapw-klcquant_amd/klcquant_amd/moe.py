@@ -153,6 +153,8 @@ class MoELayer:
         self.precision = precision
         self.path = path
         self._ws: dict[int, torch.Tensor] = {}
+        # the one-launch layer's status word of the last call, copied to the host without a sync
+        self._pending_status: tuple | None = None
 
     def workspace(self, n_tokens: int) -> torch.Tensor:
         ws = self._ws.get(n_tokens)
@@ -200,6 +202,8 @@ class MoELayer:
             return out
         ws = self.workspace(n_tok)
         w = self.w
+        if self.path == "fused":
+            self._check_fused_status(block=False)
         ev = None
         if events is not None:
             if len(events) != nat.LAYER_EVENTS:
@@ -210,9 +214,43 @@ class MoELayer:
                  n_tok, hidden, w.inter, w.n_experts, self.k, self.limit, ops.PRECISIONS[self.precision],
                  self.PATHS[self.path], ops._ptr(ws), ws.numel(), ops._ptr(out), ops._ptr(residual), ops._ptr(ids),
                  ops._ptr(weights), ev, ops._stream(x.device))
+        if self.path == "fused":
+            self._copy_fused_status(n_tok)
         return out
 
     __call__ = forward
+
+    def _copy_fused_status(self, n_tokens: int) -> None:
+        """Queues a copy of the one-launch layer's status word to pinned host memory (no sync)."""
+        w = self.w
+        off = nat.call("klc_moe_layer_status_offset", n_tokens, w.hidden, w.inter, w.n_experts, self.k)
+        if off < 0:
+            return
+        host = torch.empty(4, dtype=torch.uint8, pin_memory=True)
+        host.copy_(self._ws[n_tokens][off:off + 4], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(w.device))
+        self._pending_status = (event, host)
+
+    def _check_fused_status(self, block: bool) -> None:
+        """Raises if a wait of the last one-launch call ran out (its outputs are then poisoned: NaN
+        outputs and weights, ids -1).  Without ``block`` an unfinished call is checked at a later one."""
+        if self._pending_status is None:
+            return
+        event, host = self._pending_status
+        if block:
+            event.synchronize()
+        elif not event.query():
+            return
+        self._pending_status = None
+        if int(host.numpy().view(np.uint32)[0]) & 1:
+            raise RuntimeError("one-launch MoE layer: a cross-workgroup wait ran out (the GPU's compute units "
+                               "were held by other work); that call's outputs are NaN and its ids -1, and this "
+                               "layer's workspace keeps the failure flag")
+
+    def check_fused_status(self) -> None:
+        """Synchronises with the last one-launch call and raises if one of its waits ran out."""
+        self._check_fused_status(block=True)
 
     def forward_static_scratch(self, x: torch.Tensor, out: torch.Tensor | None = None,
                                ids: torch.Tensor | None = None, weights: torch.Tensor | None = None,

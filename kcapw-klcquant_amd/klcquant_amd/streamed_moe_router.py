@@ -596,7 +596,10 @@ class StreamedMoERouter:
                                          [[0] * n_exp, [0] * n_exp])
             table, mirror = self._ptr_tables[key]
             dirty = False
-            keep = []
+            # one (gate_up, down) pair per distinct expert of the call: with a cache too small to hold
+            # them (cache_bytes = 0, the reference's default) every lookup returns a fresh copy, and a
+            # batched call must not keep one per (token, slot); the call holds at most one layer's experts
+            keep = {}
             for row in host[0]:
                 for e in row:  # the reference's access order: gate_up then down, slot by slot
                     gu = store.packed_expert(layer_idx, e, "gate_up_proj")
@@ -605,10 +608,12 @@ class StreamedMoERouter:
                             store.matrix_shape(layer_idx, e, "down_proj") != (hidden, inter // 32):
                         raise ValueError(f"expert {e} of layer {layer_idx} does not match hidden={hidden} "
                                          f"inter={inter}")
+                    if e in keep:
+                        continue  # the pointer table already holds this call's copy (the same bits)
+                    keep[e] = (gu, dn)
                     if mirror[0][e] != gu.data_ptr() or mirror[1][e] != dn.data_ptr():
                         mirror[0][e], mirror[1][e] = gu.data_ptr(), dn.data_ptr()
                         dirty = True
-                    keep += [gu, dn]
             if dirty:  # ordered on the stream before the kernels that read it (the last ones have finished)
                 table.copy_(torch.tensor(mirror, dtype=torch.int64))
             gu_table = table.data_ptr()

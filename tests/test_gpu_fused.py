@@ -139,3 +139,30 @@ def test_fused_refusals(gpu):
     assert moe.MoELayer(dev_w, 4).layer_path(17) == "gemv"
     assert moe.MoELayer(dev_w, 4).layer_path(16) == "gemv"  # the default keeps the multi-launch layer
     assert fused.layer_path(16) == "fused"
+
+
+def test_fused_wait_that_runs_out_poisons_outputs(gpu, monkeypatch):
+    """KLC_FUSED_SPIN_LIMIT=-1 makes every wait of the one-launch layer give up at once, from the host (no
+    kernel spins or faults; every workgroup still ends).  That launch's outputs are NaN and its ids -1, so the
+    failure shows without a sync, and the layer raises on the host.  A fresh layer computes normally again."""
+    hidden, inter, n_exp, k, n_tok = 256, 128, 16, 4, 4
+    dev_w = moe.MoELayerWeights.synthetic(75, 0, hidden, inter, n_exp, gpu)
+    xt = bf16_tensor(moe.synthetic_hidden(75, n_tok, hidden), gpu)
+    layer = moe.MoELayer(dev_w, k, path="fused")
+    monkeypatch.setenv("KLC_FUSED_SPIN_LIMIT", "-1")
+    out, ids, w = run(layer, xt)
+    torch.cuda.synchronize()
+    assert np.isnan(out.float().cpu().numpy()).all()
+    assert (ids.cpu().numpy() == -1).all()
+    assert np.isnan(w.float().cpu().numpy()).all()
+    with pytest.raises(RuntimeError, match="ran out"):
+        layer.check_fused_status()
+    assert layer.fused_status(n_tok) & 1
+    monkeypatch.delenv("KLC_FUSED_SPIN_LIMIT")
+    fresh = moe.MoELayer(dev_w, k, path="fused")
+    a = fresh.forward(xt)
+    b = moe.MoELayer(dev_w, k, path="gemv").forward(xt)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(a), bf16_bits(b))
+    fresh.check_fused_status()
+    assert fresh.fused_status(n_tok) == 0

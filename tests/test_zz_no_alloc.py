@@ -61,3 +61,22 @@ def test_static_scratch_refuses_batches_beyond_its_size(gpu):
     x = torch.zeros((1024, hidden), dtype=torch.bfloat16, device=gpu)
     with pytest.raises(KlcError, match="static scratch"):
         layer.forward_static_scratch(x)
+
+
+def test_static_scratch_allocates_nothing(gpu):
+    """After a first call (which looks the scratch up), repeated calls with preallocated out, ids and
+    weights leave the device's free memory and torch's reserved memory unchanged."""
+    hidden, inter, n_exp, n = 2880, 2880, 128, 8
+    layer = moe.MoELayer(moe.MoELayerWeights.synthetic(9, 0, hidden, inter, n_exp, gpu), 4)
+    x = bf16_tensor(synth.random_normal_bf16(950, n * hidden).reshape(n, hidden), gpu)
+    out = torch.empty_like(x)
+    ids = torch.empty((n, 4), dtype=torch.int32, device=gpu)
+    w = torch.empty((n, 4), dtype=torch.bfloat16, device=gpu)
+    layer.forward_static_scratch(x, out=out, ids=ids, weights=w)
+    torch.cuda.synchronize()
+    free0, reserved0 = torch.cuda.mem_get_info(gpu)[0], torch.cuda.memory_reserved(gpu)
+    for _ in range(20):
+        layer.forward_static_scratch(x, out=out, ids=ids, weights=w)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(gpu)[0] == free0
+    assert torch.cuda.memory_reserved(gpu) == reserved0
