@@ -311,6 +311,12 @@ def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
         "kernel_us_mean": {k: round(float(v) * 1e3, 2) for k, v in zip(KERNELS, kern)},
         "flop": flop, "tflops": round(flop / dt / 1e12, 1),
         "mfma_util_bf16": round(flop / (expert_ms * 1e-3) / bf16_peak, 4),
+        # the scaled FP4 MFMA is not used: its 128-term sums lose up to 1.6e-4 of sum|terms| (float32:
+        # 4.6e-7), and with three FP8 activation planes 12 of 737280 expert outputs of a 256-token 120B-shape
+        # expert still fail 1e-2 + 2e-2|ref| (tests/test_gpu_fp4_mfma.py)
+        "scaled_fp4_mfma": {"used": False, "worst_block_err_over_sum_abs_terms": 1.641e-4,
+                            "float32_sum_worst": 4.589e-7, "failing_outputs_3_fp8_planes": 12,
+                            "profile": "profiles/scaled_fp4_mfma_accumulation_error.txt"},
         "weight_gbps": round(weights / (expert_ms * 1e-3) / 1e9, 1),
         "expert_load": {"max": int(counts.max()), "mean": round(float(counts.mean()), 2),
                         "min": int(counts.min()), "max_over_mean": round(float(counts.max() / counts.mean()), 2),

@@ -82,5 +82,20 @@ def build_library(verbose: bool = True) -> Path:
     return LIB_PATH
 
 
+def build_single(src: Path, out: Path, verbose: bool = True) -> Path:
+    """Compiles one self-contained ``.hip`` file into its own shared library
+    (the measurement libraries under ``tests/native``)."""
+    cc = hipcc()
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [cc, *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(src)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 if __name__ == "__main__":
     build_library()
