@@ -263,6 +263,25 @@ int klc_moe_route(const void* x, const void* router_w, const void* router_b, con
                   int path, void* workspace, int64_t workspace_bytes, void* out, int32_t* ids, void* weights,
                   float* gated, float* norms, void* stream);
 
+/* klc_moe_route with its routing record written to pinned host memory by
+ * the GPU, for route() (streamed_moe_router.py:257-329), whose bookkeeping
+ * (:296-329) needs only the selection: the kernel that selects the experts
+ * also writes ids and weights into host_record, then `tag` into the record's
+ * tag word; the norms kernel writes the norms there.  The host spins on the
+ * tag word (cleared to 0 before the call) and books the selection while the
+ * expert kernels still run, then synchronises `stream` for the norms.
+ * host_record: pinned host memory mapped into the device (hipHostMalloc;
+ * torch's pin_memory) of 4-byte words: ids (int32 [n_tokens*k]), weights
+ * (bfloat16 [n_tokens*k], padded to a word), norms (float32 [n_tokens*k][2]),
+ * the tag word.  tag: nonzero.  ids and weights are the device outputs as in
+ * klc_moe_route; there is no device norms output. */
+int klc_moe_route_readback(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                           const void* gate_up_bias, const void* const* w_down, const void* down_bias,
+                           int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                           float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
+                           void* out, int32_t* ids, void* weights, float* gated, void* host_record, uint32_t tag,
+                           void* stream);
+
 /* The selection half of route() (streamed_moe_router.py:268-284): router
  * logits -> top-k -> softmax weights for n_tokens rows, as klc_moe_layer
  * computes them (one launch for up to 128 tokens), into ids (int32

@@ -37,6 +37,12 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 constexpr int kWave = 64;
 
+// The decode router's one-token form: one wave selects the token's experts
+// (and, given a host record, writes its tag) with no workgroup barrier.
+__host__ __device__ constexpr bool router_decode_one_wave(int64_t n_tok, int64_t n_exp) {
+  return n_tok == 1 && n_exp <= 4 * kWave;
+}
+
 // Packed ("row-tile") MXFP4 layout used by the expert GEMV kernels.  One
 // matrix of `rows` x `groups` MX blocks (rows a multiple of 64) is stored as
 //   blocks: [rows / 64][groups][64 rows][16 bytes]

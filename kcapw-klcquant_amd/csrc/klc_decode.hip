@@ -334,15 +334,15 @@ __global__ __launch_bounds__(kFusedThreads, KLC_FUSED_WAVES_PER_EU) void moe_dec
     uint32_t* tie = reinterpret_cast<uint32_t*>(area + sl.tie + wave * topk_tie_scratch_bytes(n_exp));
     float* values = reinterpret_cast<float*>(area + sl.values);
     int32_t* active = reinterpret_cast<int32_t*>(area + sl.active);
+    const SelectionOut sel{R.ids, values, R.wts, nullptr, nullptr, nullptr};
     if (n_tok == 1) {
       if (wave == 0) {
-        topk_softmax_row(rows, n_exp, k, 0, R.ids, values, R.wts, nullptr, tie);
+        topk_softmax_row(rows, n_exp, k, 0, sel, tie);
         wave_lds_sync();
         single_token_dispatch(R.ids, n_exp, k, R.offsets, R.sorted, active, active + kFusedMaxExperts + 2, R.units);
       }
     } else {
-      topk_softmax_block([&](int t) { return rows + t * n_exp; }, n_tok, n_exp, k, 0, R.ids, values, R.wts, nullptr,
-                         tie, tie_list);
+      topk_softmax_block([&](int t) { return rows + t * n_exp; }, n_tok, n_exp, k, 0, sel, tie, tie_list);
       lds_barrier();
       if (wave == 0)
         wave_dispatch(R.ids, n_pairs, n_exp, R.offsets, R.sorted, active, active + kFusedMaxExperts + 2, R.units,

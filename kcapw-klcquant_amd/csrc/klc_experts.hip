@@ -25,14 +25,17 @@ namespace klc {
 
 int launch_router_logits(const void* x, const void* w, const void* b, void* logits, float* x_f32, int64_t n_tok,
                          int64_t hidden, int64_t n_exp, hipStream_t stream);
+// host_ids / host_weights (optional): copies of the selection in a host
+// record, pinned host memory mapped into the device
 int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
-                int64_t k, hipStream_t stream);
+                int64_t k, hipStream_t stream, int32_t* host_ids = nullptr, void* host_weights = nullptr);
 int launch_dispatch(const int32_t* ids, int64_t n_pairs, int64_t n_exp, int32_t* offsets, int32_t* sorted,
                     int32_t* active, int32_t* n_active, int32_t* units, hipStream_t stream);
 int launch_router_decode(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
                          int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
                          int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* counters,
-                         double* partials, hipStream_t stream);
+                         double* partials, hipStream_t stream, int32_t* host_ids = nullptr,
+                         void* host_weights = nullptr, uint32_t* host_tag = nullptr, uint32_t tag_value = 0);
 int64_t decode_router_counters(int64_t n_tok, int64_t n_exp);
 int64_t decode_router_partial_bytes(int64_t n_tok, int64_t hidden, int64_t n_exp);
 int check_router_args(int64_t n_tok, int64_t hidden, int64_t n_exp);
@@ -759,14 +762,46 @@ int check_layer_args(const char* fn, const void* x, const void* router_w, const 
   return KLC_OK;
 }
 
+// Host copy of a route call's record (klc_moe_route_readback): pinned host
+// memory mapped into the device (`rec`, the record's device address).  The
+// kernel that selects the experts writes ids and weights there as well; the
+// record's tag word then receives `tag` (from the one-token router itself,
+// else from write_tag_kernel after the selecting kernel), and the norms
+// kernel writes the norms.  Record layout (4-byte words): ids (pairs), bf16
+// weights (pairs, padded to a word), norms (float32, 2 * pairs), tag.
+struct Readback {
+  char* rec;
+  int64_t pairs;
+  uint32_t tag;
+  int32_t* ids() const { return reinterpret_cast<int32_t*>(rec); }
+  void* weights() const { return rec + 4 * pairs; }
+  float* norms() const { return reinterpret_cast<float*>(rec + 4 * (pairs + (pairs + 1) / 2)); }
+  uint32_t* tag_word() const { return reinterpret_cast<uint32_t*>(rec + 4 * (3 * pairs + (pairs + 1) / 2)); }
+};
+
+__global__ __launch_bounds__(64) void write_tag_kernel(uint32_t* tag_word, uint32_t tag) {
+  // the selecting kernel has finished (stream order) and fenced its host stores
+  if (threadIdx.x == 0) __hip_atomic_store(tag_word, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+int write_tag(const Readback* rb, hipStream_t st) {
+  if (rb == nullptr) return KLC_OK;
+  write_tag_kernel<<<1, 64, 0, st>>>(rb->tag_word(), rb->tag);
+  return check_launch("write_tag_kernel");
+}
+
 // The layer's launches on scratch memory `ws` (layer_scratch layout, counters
 // zero on entry and left zero).  router_w == NULL: ids / weights already hold
 // the selection (klc_moe_experts), and the layer starts at the dispatch.
+// rb != NULL (with router_w): the selecting kernel also writes the
+// selection to the host record, followed by its tag (the caller passes the
+// record's norms as `norms`).
 int run_moe_layer(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
                   const void* gate_up_bias, const void* const* w_down, const void* down_bias, int64_t n_tokens,
                   int64_t hidden, int64_t inter, int64_t n_experts, int64_t k, float swiglu_limit, int precision,
                   int path, char* ws, void* out, const void* residual, int32_t* ids, void* weights,
-                  float* gated_raw, float* norms, void* const* events, void* stream) {
+                  float* gated_raw, float* norms, void* const* events, void* stream,
+                  const Readback* rb = nullptr) {
   int rc = KLC_OK;
   const LayerScratch s = layer_scratch(n_tokens, hidden, inter, n_experts, k);
   void* logits = ws + s.logits;
@@ -817,8 +852,11 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
     // kernels take the token's slots from the ids)
     if ((rc = launch_router_decode(x, router_w, router_b, logits, 1, hidden, n_experts, k, ids_buf, values, w_buf,
                                    nullptr, nullptr, nullptr, nullptr, nullptr, counters,
-                                   reinterpret_cast<double*>(ws + s.partials), st)))
+                                   reinterpret_cast<double*>(ws + s.partials), st, rb ? rb->ids() : nullptr,
+                                   rb ? rb->weights() : nullptr, rb ? rb->tag_word() : nullptr,
+                                   rb ? rb->tag : 0u)))
       return rc;
+    if (!router_decode_one_wave(1, n_experts) && (rc = write_tag(rb, st))) return rc;
     if ((rc = mark(1))) return rc;
     if ((rc = mark(2))) return rc;
   } else if (n_tokens <= kDecodeRouterTokens) {
@@ -828,15 +866,20 @@ int run_moe_layer(const void* x, const void* router_w, const void* router_b, con
                 (long long)n_experts);
     if ((rc = launch_router_decode(x, router_w, router_b, logits, n_tokens, hidden, n_experts, k, ids_buf, values,
                                    w_buf, offsets, sorted, active, n_active, units, counters,
-                                   reinterpret_cast<double*>(ws + s.partials), st)))
+                                   reinterpret_cast<double*>(ws + s.partials), st, rb ? rb->ids() : nullptr,
+                                   rb ? rb->weights() : nullptr)))
       return rc;
+    if ((rc = write_tag(rb, st))) return rc;
     if ((rc = mark(1))) return rc;
     if ((rc = mark(2))) return rc;
   } else {
     if ((rc = launch_router_logits(x, router_w, router_b, logits, nullptr, n_tokens, hidden, n_experts, st)))
       return rc;
     if ((rc = mark(1))) return rc;
-    if ((rc = launch_topk(logits, ids_buf, values, w_buf, n_tokens, n_experts, k, st))) return rc;
+    if ((rc = launch_topk(logits, ids_buf, values, w_buf, n_tokens, n_experts, k, st, rb ? rb->ids() : nullptr,
+                          rb ? rb->weights() : nullptr)))
+      return rc;
+    if ((rc = write_tag(rb, st))) return rc;
     if ((rc = mark(2))) return rc;
     if ((rc = launch_dispatch(ids_buf, n_tokens * k, n_experts, offsets, sorted, active, n_active, units, st)))
       return rc;
@@ -944,12 +987,14 @@ extern "C" int klc_moe_layer(const void* x, const void* router_w, const void* ro
                        weights, nullptr, nullptr, events, stream);
 }
 
-extern "C" int klc_moe_route(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
-                             const void* gate_up_bias, const void* const* w_down, const void* down_bias,
-                             int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
-                             float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
-                             void* out, int32_t* ids, void* weights, float* gated, float* norms, void* stream) {
-  const char* fn = "klc_moe_route";
+namespace klc {
+namespace {
+
+int route_layer(const char* fn, const void* x, const void* router_w, const void* router_b,
+                const void* const* w_gate_up, const void* gate_up_bias, const void* const* w_down,
+                const void* down_bias, int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes, void* out,
+                int32_t* ids, void* weights, float* gated, float* norms, void* stream, const Readback* rb) {
   int rc = check_layer_args(fn, x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, out, n_tokens,
                             hidden, inter, n_experts, k, precision, path);
   if (rc) return rc;
@@ -962,7 +1007,45 @@ extern "C" int klc_moe_route(const void* x, const void* router_w, const void* ro
   KLC_REQUIRE(((uintptr_t)workspace & 255) == 0, KLC_ERR_ARGUMENT, "%s: workspace must be 256-byte aligned", fn);
   return run_moe_layer(x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
                        n_experts, k, swiglu_limit, precision, path, static_cast<char*>(workspace), out, nullptr, ids,
-                       weights, gated, norms, nullptr, stream);
+                       weights, gated, norms, nullptr, stream, rb);
+}
+
+}  // namespace
+}  // namespace klc
+
+extern "C" int klc_moe_route(const void* x, const void* router_w, const void* router_b, const void* const* w_gate_up,
+                             const void* gate_up_bias, const void* const* w_down, const void* down_bias,
+                             int64_t n_tokens, int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                             float swiglu_limit, int precision, int path, void* workspace, int64_t workspace_bytes,
+                             void* out, int32_t* ids, void* weights, float* gated, float* norms, void* stream) {
+  return route_layer("klc_moe_route", x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens,
+                     hidden, inter, n_experts, k, swiglu_limit, precision, path, workspace, workspace_bytes, out, ids,
+                     weights, gated, norms, stream, nullptr);
+}
+
+extern "C" int klc_moe_route_readback(const void* x, const void* router_w, const void* router_b,
+                                      const void* const* w_gate_up, const void* gate_up_bias,
+                                      const void* const* w_down, const void* down_bias, int64_t n_tokens,
+                                      int64_t hidden, int64_t inter, int64_t n_experts, int64_t k,
+                                      float swiglu_limit, int precision, int path, void* workspace,
+                                      int64_t workspace_bytes, void* out, int32_t* ids, void* weights, float* gated,
+                                      void* host_record, uint32_t tag, void* stream) {
+  const char* fn = "klc_moe_route_readback";
+  KLC_REQUIRE(host_record != nullptr, KLC_ERR_ARGUMENT, "%s: null host record", fn);
+  KLC_REQUIRE(tag != 0u, KLC_ERR_ARGUMENT, "%s: tag 0 (the caller clears the tag word to 0)", fn);
+  KLC_REQUIRE(n_tokens > 0 && k > 0 && n_tokens * k <= KLC_DISPATCH_MAX_PAIRS, KLC_ERR_ARGUMENT,
+              "%s: n_tokens=%lld k=%lld", fn, (long long)n_tokens, (long long)k);
+  // the record must be host memory the runtime maps into the device; its
+  // device address comes from the runtime (pageable memory is refused)
+  hipPointerAttribute_t attr{};
+  const hipError_t err = hipPointerGetAttributes(&attr, host_record);
+  KLC_REQUIRE(err == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr,
+              KLC_ERR_ARGUMENT, "%s: host_record is not pinned host memory mapped into the device (%s)", fn,
+              hipGetErrorString(err));
+  const Readback rb{static_cast<char*>(attr.devicePointer), n_tokens * k, tag};
+  return route_layer(fn, x, router_w, router_b, w_gate_up, gate_up_bias, w_down, down_bias, n_tokens, hidden, inter,
+                     n_experts, k, swiglu_limit, precision, path, workspace, workspace_bytes, out, ids, weights, gated,
+                     rb.norms(), stream, &rb);
 }
 
 extern "C" int klc_moe_experts(const void* x, const int32_t* ids, const void* weights, const void* const* w_gate_up,

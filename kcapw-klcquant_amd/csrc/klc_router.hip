@@ -47,14 +47,15 @@ __global__ __launch_bounds__(256) void router_logits_mfma_kernel(const uint16_t*
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const uint16_t* __restrict__ logits,
                                                            int32_t* __restrict__ ids, float* __restrict__ values,
                                                            uint16_t* __restrict__ weights, int n_tok, int n_exp,
-                                                           int k) {
+                                                           int k, int32_t* host_ids, uint16_t* host_weights) {
   extern __shared__ __align__(16) char lds[];  // topk_tie_scratch_bytes(n_exp) per wave
   __shared__ int tie_list[17];
   const int wave = threadIdx.x >> 6;
   const int64_t t_base = (int64_t)blockIdx.x * 16;  // 16 tokens per workgroup
   uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + wave * topk_tie_scratch_bytes(n_exp));
+  const SelectionOut sel{ids, values, weights, nullptr, host_ids, host_weights};
   topk_softmax_block([&](int t) { return logits + (t_base + t) * n_exp; }, (int)min<int64_t>(16, n_tok - t_base),
-                     n_exp, k, t_base, ids, values, weights, nullptr, tie_scratch, tie_list);
+                     n_exp, k, t_base, sel, tie_scratch, tie_list);
 }
 
 // Softmax of caller-chosen scores (one thread per token), as torch's CPU
@@ -208,12 +209,15 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_multi_kernel(const 
 // launch routes only (ids, values, weights, logits) and builds no dispatch.
 // counters: [n_tt] token-tile counters and 1 final counter, zero before the
 // first launch and left zero by every launch.  partials: [n_tt][n_et]
-// [gridDim.z][256] float64.
+// [gridDim.z][256] float64.  host_ids / host_weights (optional): copies of
+// the selection in a host record (SelectionOut); with one token, host_tag
+// (optional) then receives tag_value once they are in host memory.
 __global__ __launch_bounds__(256) void router_decode_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b, uint16_t* logits,
     int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
     int32_t* __restrict__ offsets, int32_t* __restrict__ sorted, int32_t* __restrict__ active,
-    int32_t* __restrict__ n_active, int32_t* __restrict__ units, uint32_t* counters, double* partials) {
+    int32_t* __restrict__ n_active, int32_t* __restrict__ units, uint32_t* counters, double* partials,
+    int32_t* host_ids, uint16_t* host_weights, uint32_t* host_tag, uint32_t tag_value) {
   // wave sums (float64); then the token tile's logits; then the dispatch's
   // staging.  16-byte aligned: the static flag below comes first in LDS.
   extern __shared__ __align__(16) char lds[];
@@ -288,13 +292,17 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     }
   }
   lds_barrier();  // the rows are in LDS; the logits' global stores need not have completed
-  if (n_tok == 1 && n_exp <= 4 * kWave) {
+  if (router_decode_one_wave(n_tok, n_exp)) {
     // One token: its k experts are distinct, so the dispatch reduces to
     // ranking them; one wave does the top-k and the whole dispatch with no
     // workgroup barrier (the block form below pays one per step).
     if (wave != 0) return;
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp));
-    topk_softmax_row(rows, n_exp, k, 0, ids, values, weights, tile_ids, tie_scratch);
+    topk_softmax_row(rows, n_exp, k, 0, SelectionOut{ids, values, weights, tile_ids, host_ids, host_weights},
+                     tie_scratch);
+    // the selection's host stores are fenced (SelectionOut::put, lanes < k of this wave): the tag follows
+    if (host_tag != nullptr && lane == 0)
+      __hip_atomic_store(host_tag, tag_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     wave_lds_sync();
     if (units != nullptr) single_token_dispatch(tile_ids, n_exp, k, offsets, sorted, active, n_active, units);
     return;
@@ -303,8 +311,9 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     // each wave's tie scratch follows the 16 logits rows
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp) +
                                                         wave * topk_tie_scratch_bytes(n_exp));
-    topk_softmax_block([&](int t) { return rows + t * n_exp; }, min(kRouterTile, n_tok - t0), n_exp, k, t0, ids,
-                       values, weights, n_tt == 1 ? tile_ids : nullptr, tie_scratch, tie_list);
+    const SelectionOut sel{ids, values, weights, n_tt == 1 ? tile_ids : nullptr, host_ids, host_weights};
+    topk_softmax_block([&](int t) { return rows + t * n_exp; }, min(kRouterTile, n_tok - t0), n_exp, k, t0, sel,
+                       tie_scratch, tie_list);
   }
   if (units == nullptr) return;  // routing only: no dispatch
   if (n_tt > 1) {
@@ -337,10 +346,10 @@ int launch_router_logits(const void* x, const void* w, const void* b, void* logi
 }
 
 int launch_topk(const void* logits, int32_t* ids, float* values, void* weights, int64_t n_tok, int64_t n_exp,
-                int64_t k, hipStream_t stream) {
+                int64_t k, hipStream_t stream, int32_t* host_ids, void* host_weights) {
   topk_softmax_kernel<<<(unsigned)((n_tok + 15) / 16), 256, 4 * topk_tie_scratch_bytes((int)n_exp), stream>>>(
       static_cast<const uint16_t*>(logits), ids, values, static_cast<uint16_t*>(weights), (int)n_tok, (int)n_exp,
-      (int)k);
+      (int)k, host_ids, static_cast<uint16_t*>(host_weights));
   return check_launch("topk_softmax_kernel");
 }
 
@@ -383,7 +392,8 @@ int64_t decode_router_partial_bytes(int64_t n_tok, int64_t hidden, int64_t n_exp
 int launch_router_decode(const void* x, const void* w, const void* b, void* logits, int64_t n_tok, int64_t hidden,
                          int64_t n_exp, int64_t k, int32_t* ids, float* values, void* weights, int32_t* offsets,
                          int32_t* sorted, int32_t* active, int32_t* n_active, int32_t* units, uint32_t* counters,
-                         double* partials, hipStream_t stream) {
+                         double* partials, hipStream_t stream, int32_t* host_ids, void* host_weights,
+                         uint32_t* host_tag, uint32_t tag_value) {
   const dim3 grid((unsigned)((n_exp + kRouterTile - 1) / kRouterTile), (unsigned)((n_tok + kRouterTile - 1) / kRouterTile),
                   (unsigned)decode_router_slices(n_tok, hidden, n_exp));
   size_t lds = 3 * 64 * 4 * sizeof(double);
@@ -392,7 +402,8 @@ int launch_router_decode(const void* x, const void* w, const void* b, void* logi
   router_decode_kernel<<<grid, 256, lds, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
       static_cast<uint16_t*>(logits), (int)n_tok, (int)hidden, (int)n_exp, (int)k, ids, values,
-      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, units, counters, partials);
+      static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, units, counters, partials, host_ids,
+      static_cast<uint16_t*>(host_weights), router_decode_one_wave(n_tok, n_exp) ? host_tag : nullptr, tag_value);
   return check_launch("router_decode_kernel");
 }
 
@@ -444,7 +455,7 @@ extern "C" int klc_moe_topk_softmax(const void* logits, int32_t* ids, float* val
   KLC_REQUIRE(logits && ids && weights, KLC_ERR_ARGUMENT, "klc_moe_topk_softmax: null pointer");
   const int rc = check_topk_args(n_tokens, n_experts, k);
   if (rc) return rc;
-  return launch_topk(logits, ids, values, weights, n_tokens, n_experts, k, as_stream(stream));
+  return launch_topk(logits, ids, values, weights, n_tokens, n_experts, k, as_stream(stream), nullptr, nullptr);
 }
 
 extern "C" int klc_moe_softmax_weights(const float* values, void* weights, int64_t n_tokens, int64_t k,

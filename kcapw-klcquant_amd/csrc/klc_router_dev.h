@@ -598,6 +598,33 @@ __device__ __forceinline__ uint32_t torch_softmax_bf16_row(float v, int k) {
   return f32_to_bf16_rne(e * inv);
 }
 
+// Where a token's selection goes: ids (agent-scope stores: the decode
+// router's final dispatch may run in another workgroup), the float32 values
+// (optional), the bf16 weights, a second copy of the ids in LDS (optional,
+// same indices) and copies of ids and weights in a host record (pinned host
+// memory mapped into the device; optional), fenced at system scope so that
+// an event recorded after the kernel finds them in host memory.
+struct SelectionOut {
+  int32_t* ids;
+  float* values;
+  uint16_t* weights;
+  int32_t* lds_ids;
+  int32_t* host_ids;
+  uint16_t* host_weights;
+
+  __device__ __forceinline__ void put(int64_t o, int id, float v, uint32_t w) const {
+    __hip_atomic_store(ids + o, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lds_ids != nullptr) lds_ids[o] = id;
+    if (values != nullptr) values[o] = v;
+    weights[o] = (uint16_t)w;
+    if (host_ids != nullptr) {
+      host_ids[o] = id;
+      host_weights[o] = (uint16_t)w;
+      __threadfence_system();
+    }
+  }
+};
+
 // Top-k + softmax of one token's logits row by one wave, kSlots keys per
 // lane.  The keys order values (NaN largest, -0 == +0), then lower expert
 // index first; k + 1 rounds of wave maxima give the k largest and the next
@@ -607,9 +634,7 @@ __device__ __forceinline__ uint32_t torch_softmax_bf16_row(float v, int k) {
 // the wave's LDS).
 template <int kSlots>
 __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_exp, int k, int64_t t,
-                                                   int32_t* __restrict__ ids, float* __restrict__ values,
-                                                   uint16_t* __restrict__ weights, int32_t* lds_ids,
-                                                   uint32_t* tie_scratch) {
+                                                   const SelectionOut& out, uint32_t* tie_scratch) {
   const int lane = threadIdx.x & 63;
   uint32_t keys[kSlots];
 #pragma unroll
@@ -638,26 +663,17 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
   if (tie) my_id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, my_id);  // uniform: the same maxima
   const float my_val = bf16_to_f32(row[lane < k ? my_id : 0]);
   const uint32_t w = torch_softmax_bf16(my_val, k);
-  if (lane < k) {
-    const int64_t o = t * k + lane;
-    // agent scope: the decode router's final dispatch may run in another workgroup
-    __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (lds_ids != nullptr) lds_ids[o] = my_id;
-    if (values) values[o] = my_val;
-    weights[o] = (uint16_t)w;
-  }
+  if (lane < k) out.put(t * k + lane, my_id, my_val, w);
 }
 
 __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t,
-                                                 int32_t* __restrict__ ids, float* __restrict__ values,
-                                                 uint16_t* __restrict__ weights, int32_t* lds_ids,
-                                                 uint32_t* tie_scratch) {
+                                                 const SelectionOut& out, uint32_t* tie_scratch) {
   const int slots = (n_exp + kWave - 1) / kWave;  // <= kTopkMaxPerLane (checked on the host)
-  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
-  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
-  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
-  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
-  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, ids, values, weights, lds_ids, tie_scratch);
+  if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, out, tie_scratch);
+  else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, out, tie_scratch);
+  else if (slots <= 4) topk_softmax_row_n<4>(row, n_exp, k, t, out, tie_scratch);
+  else if (slots <= 8) topk_softmax_row_n<8>(row, n_exp, k, t, out, tie_scratch);
+  else topk_softmax_row_n<kTopkMaxPerLane>(row, n_exp, k, t, out, tie_scratch);
 }
 
 // Top-k + softmax of up to 16 tokens by one 256-thread workgroup; tokens
@@ -677,9 +693,8 @@ __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp,
 // LDS; tie_list: 17 ints of LDS shared by the workgroup.
 template <int kSlots, typename RowFn>
 __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block, int n_exp, int k, int64_t t_base,
-                                                        int32_t* __restrict__ ids, float* __restrict__ values,
-                                                        uint16_t* __restrict__ weights, int32_t* lds_ids,
-                                                        uint32_t* tie_scratch, int* tie_list) {
+                                                        const SelectionOut& out, uint32_t* tie_scratch,
+                                                        int* tie_list) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4;
@@ -719,12 +734,7 @@ __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block,
       if (tie) {
         if (r == 0) tie_list[atomicAdd(&tie_list[16], 1)] = 4 * wave + q;
       } else if (r < k) {
-        const int64_t o = (t_base + 4 * wave + q) * k + r;
-        // agent scope: the decode router's final dispatch may run in another workgroup
-        __hip_atomic_store(ids + o, my_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (lds_ids != nullptr) lds_ids[o] = my_id;
-        if (values) values[o] = my_val;
-        weights[o] = (uint16_t)w;
+        out.put((t_base + 4 * wave + q) * k + r, my_id, my_val, w);
       }
     }
   }
@@ -736,39 +746,30 @@ __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block,
     const int id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, 0);
     const float v = bf16_to_f32(row[lane < k ? id : 0]);
     const uint32_t w = torch_softmax_bf16(v, k);
-    if (lane < k) {
-      const int64_t o = (t_base + t) * k + lane;
-      __hip_atomic_store(ids + o, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (lds_ids != nullptr) lds_ids[o] = id;
-      if (values) values[o] = v;
-      weights[o] = (uint16_t)w;
-    }
+    if (lane < k) out.put((t_base + t) * k + lane, id, v, w);
   }
 }
 
 // Top-k + softmax of up to 16 tokens (local t < n_block, written at
 // t_base + t) by one 256-thread workgroup: the 4-tokens-per-wave form when a
 // row fits (n_exp <= 256, k <= 16), else token by token, 4 per wave.
-// lds_ids (optional): a second copy of the ids in LDS, same indices.
-// tie_scratch: the wave's topk_tie_scratch_bytes(n_exp) bytes of LDS;
-// tie_list: 17 ints of LDS.  Called by every thread of the workgroup.
+// out: where the selections go (SelectionOut).  tie_scratch: the wave's
+// topk_tie_scratch_bytes(n_exp) bytes of LDS; tie_list: 17 ints of LDS.
+// Called by every thread of the workgroup.
 template <typename RowFn>
 __device__ __forceinline__ void topk_softmax_block(RowFn rows, int n_block, int n_exp, int k, int64_t t_base,
-                                                   int32_t* __restrict__ ids, float* __restrict__ values,
-                                                   uint16_t* __restrict__ weights, int32_t* lds_ids,
-                                                   uint32_t* tie_scratch, int* tie_list) {
+                                                   const SelectionOut& out, uint32_t* tie_scratch, int* tie_list) {
   if (k <= 16 && n_exp <= 256) {
     if (n_exp <= 64)
-      topk_softmax_block_quad<4>(rows, n_block, n_exp, k, t_base, ids, values, weights, lds_ids, tie_scratch, tie_list);
+      topk_softmax_block_quad<4>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
     else if (n_exp <= 128)
-      topk_softmax_block_quad<8>(rows, n_block, n_exp, k, t_base, ids, values, weights, lds_ids, tie_scratch, tie_list);
+      topk_softmax_block_quad<8>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
     else
-      topk_softmax_block_quad<16>(rows, n_block, n_exp, k, t_base, ids, values, weights, lds_ids, tie_scratch,
-                                  tie_list);
+      topk_softmax_block_quad<16>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
   } else {
     const int wave = threadIdx.x >> 6;
     for (int q = 4 * wave; q < min(n_block, 4 * wave + 4); ++q)
-      topk_softmax_row(rows(q), n_exp, k, t_base + q, ids, values, weights, lds_ids, tie_scratch);
+      topk_softmax_row(rows(q), n_exp, k, t_base + q, out, tie_scratch);
   }
 }
 

@@ -65,6 +65,8 @@ SIGNATURES: dict[str, tuple] = {
                              _P, _P, _P, _P, _P, _P]),
     "klc_moe_route": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
                              _P, _P, _P, _P, _P, _P]),
+    "klc_moe_route_readback": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P,
+                                      _I64, _P, _P, _P, _P, _P, ctypes.c_uint32, _P]),
     "klc_moe_select": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P]),
     "klc_moe_experts": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _I32, _I32, _P, _I64,
                                _P, _P, _P, _P]),

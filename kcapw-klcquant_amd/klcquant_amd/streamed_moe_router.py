@@ -29,9 +29,13 @@ host needs the experts first to bring misses into HBM.
 
 from __future__ import annotations
 
+import ctypes
+import functools
 import math
+import time
 from collections import Counter, deque
 from dataclasses import dataclass, field
+from typing import NamedTuple
 
 import numpy as np
 import torch
@@ -39,6 +43,24 @@ import torch
 from . import _native as nat
 from . import ops
 from .mxfp4_expert import Mxfp4ExpertStore, ResidentExpertStore
+
+
+class _ResidentPlan(NamedTuple):
+    """A resident layer's checked tensors (router weight, router bias, gate_up bias, down bias, the store's
+    layer weights), their pointers (the four tensors, then the gate_up and down pointer tables), device and
+    sizes."""
+    objects: tuple
+    ptrs: tuple
+    dev: torch.device
+    dev_index: int
+    n_exp: int
+    hidden: int
+    inter: int
+
+
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(n_tok: int, hidden: int, inter: int, n_exp: int, k: int) -> int:
+    return ops.workspace_bytes(n_tok, hidden, inter, n_exp, k)
 
 
 @dataclass
@@ -341,6 +363,10 @@ class StreamedMoERouter:
         # scratch of the resident-store path per (device, stream): workspace, float32 SwiGLU rows,
         # routing record on the device and its pinned host copy
         self._route_scratch: dict[tuple, tuple[torch.Tensor, ...]] = {}
+        self._tag = 0  # klc_moe_route_readback's tag of the last call (1 .. 2^31 - 1, then again from 1)
+        self._plans: dict[int, _ResidentPlan] = {}
+        self._layer_names: dict[int, tuple[str, str, str, str]] = {}
+        self._scratch_fit: dict[tuple, tuple[torch.Tensor, ...]] = {}
         # a streaming store's expert pointers per (device, layer, experts): device table and host mirror
         self._ptr_tables: dict[tuple, tuple[torch.Tensor, list]] = {}
 
@@ -350,31 +376,35 @@ class StreamedMoERouter:
               expert_store: Mxfp4ExpertStore | ResidentExpertStore | None = None, execute_experts: bool = True,
               position: int | list[int] = 0, predicted_experts: list[int] | None = None,
               resident_experts: set[int] | None = None) -> tuple[torch.Tensor, dict]:
-        prefix = f"model.layers.{layer_idx}.mlp"
-        router_w = tensors[f"{prefix}.router.weight"]
-        router_b = tensors[f"{prefix}.router.bias"]
+        names = self._layer_names.get(layer_idx)
+        if names is None:
+            prefix = f"model.layers.{layer_idx}.mlp"
+            names = self._layer_names[layer_idx] = (f"{prefix}.router.weight", f"{prefix}.router.bias",
+                                                    f"{prefix}.experts.gate_up_proj_bias",
+                                                    f"{prefix}.experts.down_proj_bias")
+        router_w = tensors[names[0]]
+        router_b = tensors[names[1]]
         if hidden.dim() not in (1, 2):
             raise ValueError(f"hidden must be [H] or [B, H], got shape {tuple(hidden.shape)}")
         batched = hidden.dim() == 2
-        x = (hidden if batched else hidden.reshape(1, -1)).contiguous()
-        n_tok = x.shape[0]
+        n_tok = hidden.shape[0] if batched else 1
         positions = [int(position)] * n_tok if isinstance(position, int) else [int(p) for p in position]
         if len(positions) != n_tok:
             raise ValueError(f"{len(positions)} positions for {n_tok} tokens")
-        resident = sorted(int(e) for e in (resident_experts or set()))
-        gu_bias = tensors.get(f"{prefix}.experts.gate_up_proj_bias")
-        d_bias = tensors.get(f"{prefix}.experts.down_proj_bias")
+        resident = sorted(int(e) for e in (resident_experts or ()))
+        gu_bias = tensors.get(names[2])
+        d_bias = tensors.get(names[3])
         run_experts = execute_experts and expert_store is not None
         if (run_experts and not self.locality_config.enabled and isinstance(expert_store, ResidentExpertStore)
                 and gu_bias is not None and d_bias is not None):
-            # the whole layer and its expert_logs in one library call, read back with one copy
+            # the whole layer and its expert_logs in one library call
             k = self._effective_expert_count(layer_idx, int(router_w.shape[0]))
             before = self._cache_snapshot(expert_store)
-            output, host, norms = self._route_resident(layer_idx, x, router_w, router_b, gu_bias, d_bias,
-                                                       expert_store, k)
-            return self._finish_route(layer_idx, k, batched, positions, predicted_experts, resident, host,
-                                      output.reshape(hidden.shape), "mxfp4_expert_matmul", True, norms,
-                                      expert_store, before, False)
+            output, host, norms = self._route_resident(layer_idx, hidden.contiguous(), n_tok, router_w, router_b,
+                                                       gu_bias, d_bias, expert_store, k)
+            return self._finish_route(layer_idx, k, batched, positions, predicted_experts, resident, host, output,
+                                      "mxfp4_expert_matmul", True, norms, expert_store, before, False)
+        x = (hidden if batched else hidden.reshape(1, -1)).contiguous()
         k = self._effective_expert_count(layer_idx, int(router_w.shape[0]))
         recorded = self.locality_config.enabled  # the locality path records each row while it selects
         if not recorded:
@@ -434,15 +464,19 @@ class StreamedMoERouter:
                             "weights": per_token(weight_rows), "mode": mode,
                             "sticky_adjusted": per_token(adjusted_rows)}
 
-        route = {"experts": per_token(experts_rows), "weights": per_token(weight_rows), "mode": mode}
-        if norms is not None:
-            logs = [[{"expert": int(e), "routing_weight": float(w), "gate_up_norm": float(norms[r * k + j][0]),
-                      "output_norm": float(norms[r * k + j][1])}
-                     for j, (e, w) in enumerate(zip(experts_rows[r], weight_rows[r]))] for r in range(n_tok)]
-            route["expert_logs"] = per_token(logs)
         after = self._cache_snapshot(expert_store)
         self.stats.record_cache_deltas(layer_idx, positions, experts_rows, before, after)  # booked on the first row
         self._adapt_active_cap(layer_idx, positions[-1], before, after)
+        route = {"experts": per_token(experts_rows), "weights": per_token(weight_rows), "mode": mode}
+        if norms is not None:
+            logs = [[{"expert": int(e), "routing_weight": float(w), "gate_up_norm": 0.0, "output_norm": 0.0}
+                     for e, w in zip(experts_rows[r], weight_rows[r])] for r in range(n_tok)]
+            if callable(norms):  # the norms arrive with the expert kernels, after everything above
+                norms = norms()
+            for r in range(n_tok):
+                for j, entry in enumerate(logs[r]):
+                    entry["gate_up_norm"], entry["output_norm"] = (float(v) for v in norms[r * k + j])
+            route["expert_logs"] = per_token(logs)
         route.update({"raw_experts": per_token(raw_rows), "predicted_experts": per_token(predicted_rows),
                       "resident_experts": resident, "sticky_adjusted": per_token(adjusted_rows),
                       "active_expert_cap": k})
@@ -458,15 +492,23 @@ class StreamedMoERouter:
         """Workspace (zero-filled when made), float32 SwiGLU buffer and routing record (device and
         pinned host) for one klc_moe_route call.
 
-        One set serves every batch size and layer on a stream: the call lays
-        the workspace out for its own sizes, any larger buffer will do, and
-        calls on one stream run in order; the host reads a record before the
-        next call on the stream is made.
+        ``stream`` is the raw stream handle (an int).  One set serves every
+        batch size and layer on a stream: the call lays the workspace out for
+        its own sizes, any larger buffer will do, and calls on one stream run
+        in order; the host reads a record before the next call on the stream
+        is made.
         """
-        need = (ops.workspace_bytes(n_tok, hidden, inter, n_exp, k), n_tok * k * inter, 4 * n_tok * k)
-        key = (dev, stream.value)
+        fit_key = (dev, stream, n_tok, hidden, inter, n_exp, k)
+        held = self._scratch_fit.get(fit_key)
+        if held is not None:
+            return held
+        # record: ids, bf16 weights, norms and klc_moe_route_readback's tag word
+        need = (_workspace_bytes(n_tok, hidden, inter, n_exp, k), n_tok * k * inter, 4 * n_tok * k + 4)
+        key = (dev, stream)
         held = self._route_scratch.get(key)
         if held is not None and all(t.numel() >= n for t, n in zip(held, need)):
+            if len(self._scratch_fit) < 64:
+                self._scratch_fit[fit_key] = held
             return held
         size = [max(n, held[i].numel() if held else 0) for i, n in enumerate(need)]
         made = (torch.zeros(size[0], dtype=torch.uint8, device=dev),
@@ -475,60 +517,144 @@ class StreamedMoERouter:
                 torch.empty(size[2], dtype=torch.int32, pin_memory=True))
         if need[0] + 4 * need[1] <= self._KEEP_SCRATCH_BYTES:
             self._route_scratch[key] = made
+            # sizes that fitted the old set now map to the new one
+            self._scratch_fit = {f: t for f, t in self._scratch_fit.items() if f[:2] != key}
         return made
 
-    def _route_resident(self, layer_idx, x, router_w, router_b, gu_bias, d_bias, store, k):
-        """route() for a layer resident in HBM: klc_moe_route per chunk of at most
-        ``ops.max_tokens_per_call(k)`` tokens, then one device->host copy of
-        the routing record (ids, bf16 weights and expert_logs norms in one
-        int32 buffer).
+    # A selection that has not reached the host record after this long (with
+    # the GPU still busy) is waited for by a synchronisation of the stream.
+    _TAG_WAIT_S = 2.0
 
-        Returns the bf16 output ``[B, H]``, the host row lists of
-        :meth:`_select_on_device` and the per-pair ``[gate_up_norm, output_norm]``.
-        """
-        ops._check_gpu("hidden", x, torch.bfloat16, 2)
+    def _wait_tag(self, record: np.ndarray, index: int, tag: int, dev) -> None:
+        """Spins until the GPU has written ``tag`` into ``record[index]`` (klc_moe_route_readback).  Past
+        ``_TAG_WAIT_S`` it synchronises the layer's stream instead, which raises if the device failed."""
+        spins = 0
+        deadline = None
+        while record[index] != tag:
+            spins += 1
+            if spins & 1023 == 0:
+                now = time.perf_counter()
+                if deadline is None:
+                    deadline = now + self._TAG_WAIT_S
+                elif now > deadline:
+                    torch.cuda.current_stream(dev).synchronize()
+                    if record[index] != tag:
+                        raise RuntimeError("route(): the layer finished without its selection in the host record")
+                    return
+
+    def _resident_plan(self, layer_idx, router_w, router_b, gu_bias, d_bias, store) -> _ResidentPlan:
+        """The checked device, sizes and pointers of a resident layer.  Kept while the router and bias
+        tensors and the store's layer are the same objects over the same storage; checked again
+        otherwise."""
+        w = store.layer(layer_idx)
+        ptrs = (router_w.data_ptr(), router_b.data_ptr(), gu_bias.data_ptr(), d_bias.data_ptr(),
+                w.gate_up_table.data_ptr(), w.down_table.data_ptr())
+        plan = self._plans.get(layer_idx)
+        if plan is not None and plan.ptrs == ptrs:
+            held = plan.objects
+            if held[0] is router_w and held[1] is router_b and held[2] is gu_bias and held[3] is d_bias and held[4] is w:
+                return plan
         ops._check_gpu("router weight", router_w, torch.bfloat16, 2)
         ops._check_gpu("router bias", router_b, torch.bfloat16, 1)
         ops._check_gpu("gate_up bias", gu_bias, torch.bfloat16, 2)
         ops._check_gpu("down bias", d_bias, torch.bfloat16, 2)
-        w = store.layer(layer_idx)
-        dev = ops._same_device(x, router_w, router_b, gu_bias, d_bias, w.gate_up_table)
-        n_tok, hidden = x.shape
+        dev = ops._same_device(router_w, router_b, gu_bias, d_bias, w.gate_up_table)
+        n_exp, inter, hidden = w.n_experts, w.inter, w.hidden
+        if tuple(router_w.shape) != (n_exp, hidden) or tuple(router_b.shape) != (n_exp,):
+            raise ValueError(f"router shapes mismatch: weight {tuple(router_w.shape)}, bias {tuple(router_b.shape)}, "
+                             f"{n_exp} resident experts of hidden size {hidden}")
+        if tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
+            raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
+                             f"E={n_exp} H={hidden} I={inter}")
+        plan = _ResidentPlan((router_w, router_b, gu_bias, d_bias, w), ptrs, dev, dev.index, n_exp, hidden, inter)
+        self._plans[layer_idx] = plan
+        return plan
+
+    def _route_resident(self, layer_idx, x, n_tok, router_w, router_b, gu_bias, d_bias, store, k):
+        """route() for a layer resident in HBM; ``x`` is the contiguous hidden ``[H]`` or ``[B, H]``.
+
+        Up to ``ops.max_tokens_per_call(k)`` tokens: one klc_moe_route_readback
+        call, in which the kernel that selects the experts also writes the
+        selection (ids, bf16 weights) into the pinned host record, followed by
+        the call's tag, and the norms kernel writes the expert_logs norms
+        there; the host spins on the tag only, so the caller's bookkeeping
+        overlaps the expert kernels, and the norms are returned as a callable
+        that waits for the layer's stream.  Longer inputs: klc_moe_route per
+        chunk, each followed by one device->host copy of its record (ids,
+        bf16 weights and norms in one int32 buffer).
+
+        Returns the bf16 output (``x``'s shape), the host row lists of
+        :meth:`_select_on_device` and the per-pair ``[gate_up_norm, output_norm]`` (or the callable
+        that returns them).
+        """
+        plan = self._resident_plan(layer_idx, router_w, router_b, gu_bias, d_bias, store)
+        if not isinstance(x, torch.Tensor):
+            raise TypeError(f"hidden must be a torch.Tensor, got {type(x).__name__}")
+        if x.dtype is not torch.bfloat16:
+            raise TypeError(f"hidden must be torch.bfloat16, got {x.dtype}")
+        if x.device != plan.dev:
+            raise ValueError(f"hidden is on {x.device}, the layer on {plan.dev}")
+        hidden, inter, n_exp = plan.hidden, plan.inter, plan.n_exp
+        if x.shape[-1] != hidden:
+            raise ValueError(f"hidden size {x.shape[-1]} does not match the layer's {hidden}")
         if n_tok == 0:
             raise ValueError("route() needs at least one token")
-        n_exp, inter = w.n_experts, w.inter
-        if tuple(router_w.shape) != (n_exp, hidden) or tuple(router_b.shape) != (n_exp,):
-            raise ValueError(f"router shapes mismatch: x {tuple(x.shape)}, weight {tuple(router_w.shape)}, "
-                             f"bias {tuple(router_b.shape)}, {n_exp} resident experts")
-        if hidden != w.hidden or tuple(gu_bias.shape) != (n_exp, 2 * inter) or tuple(d_bias.shape) != (n_exp, hidden):
-            raise ValueError(f"expert biases {tuple(gu_bias.shape)} / {tuple(d_bias.shape)} do not match "
-                             f"E={n_exp} H={w.hidden} I={inter} (hidden {hidden})")
         store.record_access(layer_idx, 2 * n_tok * k)
         out = torch.empty_like(x)
-        stream = ops._stream(dev)
+        stream = torch._C._cuda_getCurrentRawStream(plan.dev_index)
+        w_ptrs = plan.ptrs
+        prec = ops.PRECISIONS[self.matmul_precision]
         chunk = ops.max_tokens_per_call(k)
+        if n_tok <= chunk:
+            pairs = n_tok * k
+            half = (pairs + 1) // 2
+            ws, gated, rec, rec_host = self._scratch(plan.dev, stream, n_tok, hidden, inter, n_exp, k)
+            r = rec_host.numpy()
+            tag_at = 3 * pairs + half
+            r[tag_at] = 0  # the previous call on this stream has finished (its norms were waited for)
+            self._tag = tag = self._tag % 0x7FFFFFFF + 1
+            rec_p = rec.data_ptr()
+            rc = self._route_readback_fn(x.data_ptr(), w_ptrs[0], w_ptrs[1], w_ptrs[4], w_ptrs[2], w_ptrs[5],
+                                         w_ptrs[3], n_tok, hidden, inter, n_exp, k, self.swiglu_limit, prec,
+                                         nat.PATH_AUTO, ws.data_ptr(), ws.numel(), out.data_ptr(), rec_p,
+                                         rec_p + 4 * pairs, gated.data_ptr(), rec_host.data_ptr(), tag, stream)
+            if rc < 0:
+                raise nat.KlcError("klc_moe_route_readback", int(rc), nat.last_error())
+            self._wait_tag(r, tag_at, tag, plan.dev)
+            experts = r[:pairs].reshape(n_tok, k).tolist()
+            bits = r[pairs:pairs + half].view(np.uint16)[:pairs].astype(np.uint32) << 16
+            weights = bits.view(np.float32).reshape(n_tok, k).tolist()
+
+            def norms():
+                torch.cuda.current_stream(plan.dev).synchronize()
+                return r[pairs + half:pairs + half + 2 * pairs].view(np.float32).reshape(pairs, 2).tolist()
+
+            return out, (experts, weights, [list(row) for row in experts], [False] * n_tok, []), norms
         experts, weights, norms = [], [], []
         for t0 in range(0, n_tok, chunk):
             t1 = min(n_tok, t0 + chunk)
             pairs = (t1 - t0) * k
             half = (pairs + 1) // 2
-            ws, gated, rec, rec_host = self._scratch(dev, stream, t1 - t0, hidden, inter, n_exp, k)
+            ws, gated, rec, rec_host = self._scratch(plan.dev, stream, t1 - t0, hidden, inter, n_exp, k)
             n_rec = pairs + half + 2 * pairs
             row0 = 2 * hidden * t0  # byte offset of row t0 of the bf16 input and output
             rec_p = rec.data_ptr()  # ids, then the bf16 weights, then the norms (int32 words)
-            nat.call("klc_moe_route", x.data_ptr() + row0, router_w.data_ptr(), router_b.data_ptr(),
-                     w.gate_up_table.data_ptr(), gu_bias.data_ptr(), w.down_table.data_ptr(), d_bias.data_ptr(),
-                     t1 - t0, hidden, inter, n_exp, k, self.swiglu_limit, ops.PRECISIONS[self.matmul_precision],
-                     nat.PATH_AUTO, ws.data_ptr(), ws.numel(), out.data_ptr() + row0, rec_p, rec_p + 4 * pairs,
-                     gated.data_ptr(), rec_p + 4 * (pairs + half), stream)
+            nat.call("klc_moe_route", x.data_ptr() + row0, w_ptrs[0], w_ptrs[1], w_ptrs[4], w_ptrs[2], w_ptrs[5],
+                     w_ptrs[3], t1 - t0, hidden, inter, n_exp, k, self.swiglu_limit, prec, nat.PATH_AUTO,
+                     ws.data_ptr(), ws.numel(), out.data_ptr() + row0, rec_p, rec_p + 4 * pairs, gated.data_ptr(),
+                     rec_p + 4 * (pairs + half), stream)
             rec_host[:n_rec].copy_(rec[:n_rec], non_blocking=True)
-            torch.cuda.current_stream(dev).synchronize()
+            torch.cuda.current_stream(plan.dev).synchronize()
             r = rec_host[:n_rec].numpy()
             experts += r[:pairs].reshape(t1 - t0, k).tolist()
             bits = r[pairs:pairs + half].view(np.uint16)[:pairs].astype(np.uint32) << 16
             weights += bits.view(np.float32).reshape(t1 - t0, k).tolist()
             norms += r[pairs + half:].view(np.float32).reshape(pairs, 2).tolist()
         return out, (experts, weights, [list(row) for row in experts], [False] * n_tok, []), norms
+
+    @functools.cached_property
+    def _route_readback_fn(self):
+        return getattr(nat.load(), "klc_moe_route_readback")
 
     def _select_on_device(self, x, router_w, router_b, k):
         """Top-k selection and softmax weights on the GPU (klc_moe_select, streamed_moe_router.py:268-284)
@@ -555,7 +681,7 @@ class StreamedMoERouter:
         for t0 in range(0, n_tok, chunk):
             t1 = min(n_tok, t0 + chunk)
             pairs = (t1 - t0) * k
-            ws, _, _, rec_host = self._scratch(dev, stream, t1 - t0, hidden, 32, n_exp, k)
+            ws, _, _, rec_host = self._scratch(dev, stream.value, t1 - t0, hidden, 32, n_exp, k)
             nat.call("klc_moe_select", x.data_ptr() + 2 * hidden * t0, router_w.data_ptr(), router_b.data_ptr(),
                      t1 - t0, hidden, n_exp, k, ws.data_ptr(), ws.numel(), ids.data_ptr() + 4 * t0 * k,
                      weights.data_ptr() + 2 * t0 * k, stream)
@@ -631,7 +757,7 @@ class StreamedMoERouter:
         for t0 in range(0, n_tok, chunk):
             t1 = min(n_tok, t0 + chunk)
             pairs = (t1 - t0) * k
-            ws, gated, rec, rec_host = self._scratch(dev, stream, t1 - t0, hidden, inter, n_exp, k)
+            ws, gated, rec, rec_host = self._scratch(dev, stream.value, t1 - t0, hidden, inter, n_exp, k)
             row0 = 2 * hidden * t0
             nat.call("klc_moe_experts", x.data_ptr() + row0, ids.data_ptr() + 4 * t0 * k,
                      weights.data_ptr() + 2 * t0 * k, gu_table, gu_bias.data_ptr(), d_table, d_bias.data_ptr(),

@@ -145,3 +145,16 @@ def test_select_and_experts_argument_errors():
     with pytest.raises(nat.KlcError) as ei:
         nat.call("klc_moe_experts", *args, nat.PATH_AUTO, fake, 1 << 30, fake, fake, None, None)
     assert ei.value.status == nat.KLC_ERR_ARGUMENT and "together" in ei.value.message
+
+
+def test_route_readback_argument_errors():
+    """klc_moe_route_readback: a host record and a nonzero tag are required, before any device work."""
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    head = [fake] * 7 + [1, 2880, 2880, 128, 4, 7.0, nat.PRECISION_FP32, nat.PATH_AUTO, fake, 1 << 30]
+    outs = [fake] * 4
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_route_readback", *head, *outs, None, 1, fake)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "null host record" in ei.value.message
+    with pytest.raises(nat.KlcError) as ei:
+        nat.call("klc_moe_route_readback", *head, *outs, fake, 0, fake)
+    assert ei.value.status == nat.KLC_ERR_ARGUMENT and "tag 0" in ei.value.message
