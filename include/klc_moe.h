@@ -223,7 +223,13 @@ int64_t klc_moe_workspace_bytes(int64_t n_tokens, int64_t hidden, int64_t inter,
  * runs the whole layer as one launch: batches of at most 16 tokens (at most
  * 64 token-slot pairs, 256 experts, k <= 16), 8-byte aligned out/residual,
  * and a stream that is not capturing a graph; other calls fail with
- * KLC_ERR_UNSUPPORTED.  It gives the same bits as GEMV. */
+ * KLC_ERR_UNSUPPORTED.  It gives the same bits as GEMV.  Its workgroups wait
+ * for one another (bounded spins on tagged flags), so it needs the compute
+ * units to itself: do not run other work on the same GPU concurrently with a
+ * FUSED launch (another stream, another process).  A wait that runs out
+ * (KLC_FUSED_SPIN_LIMIT in the environment lowers the bound, for tests) sets
+ * bit 0 of the workspace's status word (klc_moe_layer_status_offset) and
+ * poisons that launch's outputs: ids -1, weights and out NaN. */
 #define KLC_PATH_AUTO 0
 #define KLC_PATH_GEMV 1
 #define KLC_PATH_GEMM 2
