@@ -255,6 +255,149 @@ __global__ __launch_bounds__(kDqThreads) void dequant_kernel(const uint8_t* __re
   }
 }
 
+// Checkpoint layout -> bfloat16 [in, out] in long output runs: workgroup
+// (matrix, column block, group quad) stages 4 groups' code chunks (a 64-byte
+// run of each checkpoint row) and scale bytes of up to kDqrCols checkpoint
+// rows (= output columns) in LDS, word-major (word w of row r at
+// sw[w * kDqrCols + r]), and writes output rows 128 q .. 128 q + 127 at its
+// columns: runs of 2 * ncols bytes.  The two quads that share a 128-byte
+// line of each row run side by side on one XCD (workgroups go to the XCDs
+// round-robin), so that line is fetched once.  A task is 8 output rows (a
+// band: one word of one group's chunks) x 8 output columns; the threads take
+// consecutive tasks, so a task's 8 16-byte stores are, across the workgroup,
+// runs of consecutive 16-byte pieces of output rows.  The scaled conversion
+// (exact for every scale byte below 255) gives pairs of input elements of one
+// row; v_perm_b32 pairs them up as pairs of columns.  Scale byte 255 (the MX
+// NaN scale) is rare: those tasks are written again with the exact integer
+// path (mxfp4_f32_bits) after the main loop, by the thread that wrote them
+// (program order), so the main loop has no branch for it.
+//
+// Measured (128 x 2880 x 2880 to bfloat16): 768 columns and 512 threads
+// (52 KB of LDS, 3 workgroups per CU) 511-518 us against 535-551 us for the
+// 64-column strips above; 1536 columns (one workgroup per CU) 551-558 us; one
+// group per workgroup (16-byte reads at the row stride) 1,010 us; several
+// items per workgroup with the next one's loads in flight, or buffer stores,
+// were slower.
+constexpr int kDqrThreads = 512;
+constexpr int kDqrGroups = 4;                                    // groups per workgroup
+constexpr int kDqrCols = 768;                                    // checkpoint rows per column block
+constexpr int kDqrRounds = kDqrCols * kDqrGroups / kDqrThreads;  // 16-byte loads per thread
+static_assert(kDqrCols * kDqrGroups % kDqrThreads == 0, "whole load rounds");
+
+__host__ __device__ constexpr int dqr_col_blocks(int rows) { return (rows + kDqrCols - 1) / kDqrCols; }
+// Column block cb of nb over rows (a multiple of 64): nearly equal widths, multiples of 64 columns
+__host__ __device__ inline int dqr_col0(int rows, int nb, int cb) { return (int)((int64_t)rows / 64 * cb / nb) * 64; }
+
+__global__ __launch_bounds__(kDqrThreads) void dequant_rows_bf16_kernel(const uint8_t* __restrict__ blocks,
+                                                                        const uint8_t* __restrict__ scales,
+                                                                        uint16_t* __restrict__ out, int n_mat,
+                                                                        int rows, int groups) {
+  extern __shared__ __align__(16) uint32_t lds_words[];  // [16][kDqrCols] code words, then scale bytes
+  // workgroup -> (pair of quads P, half h): P's two workgroups are 8 apart in a window of 16
+  const int nb = dqr_col_blocks(rows);
+  const int quads = (groups + kDqrGroups - 1) / kDqrGroups;
+  const int pairs = (quads + 1) / 2;
+  const int b = blockIdx.x;
+  const int pair = (b >> 4) * 8 + (b & 7);
+  const int quad = 2 * (pair % pairs) + ((b >> 3) & 1);
+  const int mcb = pair / pairs;  // (matrix, column block)
+  if (quad >= quads || mcb >= n_mat * nb) return;
+  const int m = mcb / nb;
+  const int cb = mcb - m * nb;
+  const int col0 = dqr_col0(rows, nb, cb);
+  const int ncols = dqr_col0(rows, nb, cb + 1) - col0;
+  const int g0 = quad * kDqrGroups;
+  const int ng = min(kDqrGroups, groups - g0);
+  uint32_t* sw = lds_words;
+  uint8_t* ss = reinterpret_cast<uint8_t*>(lds_words + 4 * kDqrGroups * kDqrCols);
+  const int tid = threadIdx.x;
+  const int64_t first = (int64_t)m * rows * groups + (int64_t)col0 * groups + g0;  // chunk (col0, g0)
+  const int span = (ncols - 1) * groups + ng;                                     // chunks to the last one
+  const __amdgpu_buffer_rsrc_t cbuf =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(blocks + first * 16), (short)0, span * 16, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t sbuf =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(scales + first), (short)0, span, kBufferWord3);
+  // load i: row r = (tid + i * threads) / 4, chunk c = tid % 4; rows and groups past the end read out of
+  // range (zeros, no traffic).  Every load first, then the LDS writes.
+  const int c = tid & 3;
+  u32x4_t v[kDqrRounds];
+  uint32_t e[kDqrRounds];
+#pragma unroll
+  for (int i = 0; i < kDqrRounds; ++i) {
+    const int r = (tid >> 2) + i * (kDqrThreads / 4);
+    const bool live = r < ncols && c < ng;
+    const uint32_t chunk = (uint32_t)r * (uint32_t)groups + (uint32_t)c;
+    v[i] = __builtin_amdgcn_raw_buffer_load_b128(cbuf, live ? chunk * 16u : kOutOfRange, 0, 0);
+    e[i] = __builtin_amdgcn_raw_buffer_load_b8(sbuf, live ? chunk : kOutOfRange, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < kDqrRounds; ++i) {
+    const int r = (tid >> 2) + i * (kDqrThreads / 4);
+    if (r < ncols) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) sw[(4 * c + w) * kDqrCols + r] = v[i][w];
+      ss[c * kDqrCols + r] = (uint8_t)e[i];
+    }
+  }
+  __syncthreads();
+
+  const int cpr = ncols >> 3;  // 16-byte pieces (8 columns) per output run
+  const int ntask = 4 * ng * cpr;
+  uint16_t* obase = out + ((int64_t)m * groups + g0) * 32 * rows + col0;
+  bool nan_scale = false;
+  for (int t = tid; t < ntask; t += kDqrThreads) {
+    const int band = t / cpr;  // group band / 4, word band % 4
+    const int oc = t - band * cpr;
+    const uint32_t* wrow = sw + band * kDqrCols + oc * 8;
+    const u32x4_t wa = *reinterpret_cast<const u32x4_t*>(wrow);
+    const u32x4_t wb = *reinterpret_cast<const u32x4_t*>(wrow + 4);
+    const uint2 sc8 = *reinterpret_cast<const uint2*>(ss + (band >> 2) * kDqrCols + oc * 8);
+    const uint32_t word[8] = {wa[0], wa[1], wa[2], wa[3], wb[0], wb[1], wb[2], wb[3]};
+    // pr[j][q]: elements 2q, 2q + 1 of the band for column j (checkpoint row col0 + 8 oc + j)
+    uint32_t pr[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t eb = ((j < 4 ? sc8.x : sc8.y) >> (8 * (j & 3))) & 0xffu;
+      nan_scale |= eb == 255u;
+      const float scale = __uint_as_float(eb == 0u ? 0x00400000u : (eb << 23));
+      pr[j][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word[j], scale, 0));
+      pr[j][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word[j], scale, 1));
+      pr[j][2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word[j], scale, 2));
+      pr[j][3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word[j], scale, 3));
+    }
+    uint16_t* o = obase + (int64_t)(8 * band) * rows + oc * 8;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // output row 8 band + 2 q + h: half h of every column's pair q, columns paired low-first
+        const uint32_t sel = h ? 0x07060302u : 0x05040100u;
+        const u32x4_t row = {__builtin_amdgcn_perm(pr[1][q], pr[0][q], sel), __builtin_amdgcn_perm(pr[3][q], pr[2][q], sel),
+                             __builtin_amdgcn_perm(pr[5][q], pr[4][q], sel), __builtin_amdgcn_perm(pr[7][q], pr[6][q], sel)};
+        __builtin_nontemporal_store(row, reinterpret_cast<u32x4_t*>(o + (int64_t)(2 * q + h) * rows));
+      }
+    }
+  }
+  if (!__syncthreads_or(nan_scale)) return;
+  // tasks with a scale byte 255, again with the integer path, by the same threads (same addresses,
+  // program order: these stores land after the first ones)
+  for (int t = tid; t < ntask; t += kDqrThreads) {
+    const int band = t / cpr;
+    const int oc = t - band * cpr;
+    const uint8_t* sc = ss + (band >> 2) * kDqrCols + oc * 8;
+    bool any = false;
+    for (int j = 0; j < 8; ++j) any |= sc[j] == 255u;
+    if (!any) continue;
+    uint16_t* o = obase + (int64_t)(8 * band) * rows + oc * 8;
+    for (int i = 0; i < 8; ++i) {
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t code = (sw[band * kDqrCols + oc * 8 + j] >> (4 * i)) & 0xfu;
+        o[(int64_t)i * rows + j] = (uint16_t)(mxfp4_f32_bits(code, sc[j]) >> 16);
+      }
+    }
+  }
+}
+
 // Checkpoint layout -> row-tile layout: one thread per (matrix, tile, group,
 // row in tile) 16-byte chunk, writes coalesced; runs once per load.  The
 // block and scale regions of matrix m start at out_blocks / out_scales +
@@ -396,6 +539,21 @@ namespace {
 template <bool kPacked>
 int launch_dequant(const void* blocks, const void* scales, void* out, int64_t n_mat, int64_t rows, int64_t groups,
                    int dtype, int64_t packed_stride, hipStream_t stream) {
+  if constexpr (!kPacked) {
+    // checkpoint layout to bfloat16, rows a multiple of 64: long output runs per workgroup (a
+    // matrix's codes below kOutOfRange bytes, so the out-of-range loads stay out of range)
+    if (dtype == KLC_DTYPE_BF16 && rows % 64 == 0 && rows * groups * 16 < (int64_t)kOutOfRange) {
+      const int64_t pairs = n_mat * dqr_col_blocks((int)rows) * (((groups + kDqrGroups - 1) / kDqrGroups + 1) / 2);
+      const int64_t grid = (pairs + 7) / 8 * 16;
+      if (grid <= 0x7fffffff) {
+        const size_t lds = (size_t)kDqrCols * kDqrGroups * 17;
+        dequant_rows_bf16_kernel<<<(unsigned)grid, kDqrThreads, lds, stream>>>(
+            static_cast<const uint8_t*>(blocks), static_cast<const uint8_t*>(scales), static_cast<uint16_t*>(out),
+            (int)n_mat, (int)rows, (int)groups);
+        return check_launch("dequant_rows_bf16_kernel");
+      }
+    }
+  }
   const int64_t strips = (rows + kDqCols - 1) / kDqCols;
   const int64_t grid = n_mat * strips;
   KLC_REQUIRE(grid <= 0x7fffffff, KLC_ERR_UNSUPPORTED, "dequant: too many matrices (%lld)", (long long)n_mat);

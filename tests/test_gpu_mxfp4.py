@@ -56,7 +56,9 @@ def test_dequant_all_code_scale_pairs(gpu, dtype, kind):
     same_bits_nan_aware(g, want, kind)
 
 
-@pytest.mark.parametrize("n_mat,out_dim,groups", [(3, 128, 6), (2, 192, 90), (1, 40, 3), (2, 72, 5)])
+@pytest.mark.parametrize("n_mat,out_dim,groups", [(3, 128, 6), (2, 192, 90), (1, 40, 3), (2, 72, 5), (1, 36, 3),
+                                                   (2, 3080, 2), (1, 4096, 3), (1, 4104, 2), (2, 2880, 7),
+                                                   (1, 1600, 5)])
 def test_dequant_seeded_matches_oracle(gpu, n_mat, out_dim, groups):
     blocks, scales = synth.mxfp4_expert_tensors(11, 12, n_mat, out_dim, groups * 32, 0, 255)
     got = ops.mxfp4_dequant(torch.from_numpy(blocks).to(gpu), torch.from_numpy(scales).to(gpu), torch.bfloat16)
