@@ -269,8 +269,13 @@ def stack_bench(torch, dev, n_layers: int, n_seqs: int, n_steps: int, precision:
             "unique_experts_mean": round(float(np.mean(uniq)), 2), "build_s": round(build_s, 1)}
 
 
-def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
-    """One 120B-shape MoE layer over a prefill chunk of n_tok tokens with Zipf(1.1)-skewed routing."""
+def prefill_bench(torch, dev, n_tok: int, reps: int) -> dict:
+    """One 120B-shape MoE layer over a prefill chunk of n_tok tokens with Zipf(1.1)-skewed routing.
+
+    The workload is defined in bfloat16 (bf16 x bf16 products summed in float32, the down input rounded to
+    bfloat16, as the reference's matmul_precision="bf16" path); the same layers are also timed with float32
+    expert math (the down input as hi + lo bfloat16 planes), reported under "fp32".
+    """
     import numpy as np
 
     from klcquant_amd import moe, synth
@@ -280,33 +285,42 @@ def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
     x_host = moe.synthetic_hidden(workload, n_tok, HIDDEN)
     bias, target = synth.zipf_router_bias(x_host, host["router_weight"], TOPK, 1.1, 1000 * workload + 11)
     del host
-    layers = [moe.MoELayer(moe.MoELayerWeights.synthetic(workload, l, HIDDEN, INTER, EXPERTS, dev, bias), TOPK, 7.0,
-                           precision) for l in range(2)]
+    weights_l = [moe.MoELayerWeights.synthetic(workload, l, HIDDEN, INTER, EXPERTS, dev, bias) for l in range(2)]
     x = torch.from_numpy(x_host.view(np.int16)).view(torch.bfloat16).to(dev)
     out = torch.empty_like(x)
     ids = torch.empty((n_tok, TOPK), dtype=torch.int32, device=dev)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(reps)]
-    for row in evs:  # torch creates the HIP event on its first record
-        for ev in row:
-            ev.record()
-    for r in range(2):
-        layers[r % 2].forward(x, out=out)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for r in range(reps):
-        layers[r % 2].forward(x, out=out, ids=ids if r == 0 else None, events=evs[r])
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / reps
-    kern = np.array([[evs[r][i].elapsed_time(evs[r][i + 1]) for i in range(6)] for r in range(reps)]).mean(axis=0)
+
+    def timed(precision):
+        layers = [moe.MoELayer(w, TOPK, 7.0, precision) for w in weights_l]
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(reps)]
+        for row in evs:  # torch creates the HIP event on its first record
+            for ev in row:
+                ev.record()
+        settle = time.perf_counter() + 0.15  # clocks ramp over the first tens of ms
+        while time.perf_counter() < settle:
+            layers[0].forward(x, out=out)
+            torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for r in range(reps):
+            layers[r % 2].forward(x, out=out, ids=ids if r == 0 else None, events=evs[r])
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        kern = np.array([[evs[r][i].elapsed_time(evs[r][i + 1]) for i in range(6)] for r in range(reps)]).mean(axis=0)
+        return dt, kern
+
+    dt, kern = timed("bf16")
+    dt32, kern32 = timed("fp32")
     counts = np.bincount(ids.cpu().numpy().ravel(), minlength=EXPERTS)
     flop = n_tok * TOPK * (2 * 2 * INTER * HIDDEN + 2 * HIDDEN * INTER) + 2 * n_tok * HIDDEN * EXPERTS
     weights = int(np.count_nonzero(counts)) * (GATE_UP_EXPERT_BYTES + DOWN_EXPERT_BYTES)
     expert_ms = float(kern[3] + kern[4])
     bf16_peak = 2.5e15
-    del layers
+    del weights_l
     torch.cuda.empty_cache()
     return {
-        "workload": f"gpt-oss-120B-shape MoE layer, prefill of {n_tok} tokens, top-4 of 128, Zipf(1.1) router bias",
+        "workload": f"gpt-oss-120B-shape MoE layer, prefill of {n_tok} tokens in bf16, top-4 of 128, "
+                    "Zipf(1.1) router bias",
+        "precision": "bf16",
         "us_per_layer": round(dt * 1e6, 1), "tokens_per_s": round(n_tok / dt, 1),
         "kernel_us_mean": {k: round(float(v) * 1e3, 2) for k, v in zip(KERNELS, kern)},
         "flop": flop, "tflops": round(flop / dt / 1e12, 1),
@@ -318,6 +332,9 @@ def prefill_bench(torch, dev, n_tok: int, reps: int, precision: str) -> dict:
                             "float32_sum_worst": 4.589e-7, "failing_outputs_3_fp8_planes": 12,
                             "profile": "profiles/scaled_fp4_mfma_accumulation_error.txt"},
         "weight_gbps": round(weights / (expert_ms * 1e-3) / 1e9, 1),
+        "fp32": {"us_per_layer": round(dt32 * 1e6, 1), "tokens_per_s": round(n_tok / dt32, 1),
+                 "kernel_us_mean": {k: round(float(v) * 1e3, 2) for k, v in zip(KERNELS, kern32)},
+                 "mfma_util_bf16": round(flop / (float(kern32[3] + kern32[4]) * 1e-3) / bf16_peak, 4)},
         "expert_load": {"max": int(counts.max()), "mean": round(float(counts.mean()), 2),
                         "min": int(counts.min()), "max_over_mean": round(float(counts.max() / counts.mean()), 2),
                         "hottest_share": round(float(counts.max() / counts.sum()), 4),
@@ -1004,7 +1021,7 @@ def main() -> int:
         result["route_api"] = route_api_bench(torch, dev, layers[0].w, args.route_calls, args.precision)
         print(f"[bench] route(): {result['route_api']}", file=sys.stderr, flush=True)
     if args.prefill_tokens > 0:
-        result["prefill"] = prefill_bench(torch, dev, args.prefill_tokens, 10, args.precision)
+        result["prefill"] = prefill_bench(torch, dev, args.prefill_tokens, 10)
         print(f"[bench] prefill: {result['prefill']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del layers

@@ -102,17 +102,32 @@ __device__ __forceinline__ void ring_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-template <bool kDown>
-__host__ __device__ constexpr int gemm_ring() { return kDown ? KLC_GEMM_RING_DOWN : KLC_GEMM_RING_UP; }
-template <bool kDown>
-__host__ __device__ constexpr int gemm_stage_bytes() { return (kDown ? 2 : 1) * kUnitTokensGemm * 256; }
-// LDS of one workgroup: the B ring, or the gate_up epilogue's output tile if larger.
-template <bool kDown>
+// kPl: activation planes of B (gate_up 1; down 2 = hi + lo of the float32
+// SwiGLU output, or 1 = its bfloat16 rounding, which is exactly the
+// bfloat16-precision input, so the lo plane's zero products are skipped).
+template <bool kDown, int kPl>
+__host__ __device__ constexpr int gemm_ring() { return kDown && kPl == 2 ? KLC_GEMM_RING_DOWN : KLC_GEMM_RING_UP; }
+template <bool kDown, int kPl>
+__host__ __device__ constexpr int gemm_stage_bytes() { return kPl * kUnitTokensGemm * 256; }
+// Each wave's tile of scale records copied into LDS (the packed layout,
+// [S / 8][64 rows][4 quarters][8 bytes], at most 6 KiB for inputs <= 3072),
+// where two workgroups of a CU still fit (not beside the two-plane down
+// ring: that one keeps the records in registers).
+constexpr int kScaleTileLds = kTileRows * 4 * 24;
+constexpr int kScaleLdsBytes = kGemmWaves * kWaveTiles * kScaleTileLds;
+template <bool kDown, int kPl>
+__host__ __device__ constexpr bool gemm_scales_in_lds() { return !(kDown && kPl == 2); }
+// LDS of one workgroup: the B ring, or the gate_up epilogue's output tile if
+// larger, then the staged scales.
+template <bool kDown, int kPl>
 __host__ __device__ constexpr int gemm_lds_bytes() {
-  const int ring = gemm_ring<kDown>() * gemm_stage_bytes<kDown>();
+  const int ring = gemm_ring<kDown, kPl>() * gemm_stage_bytes<kDown, kPl>();
   const int tile = kDown ? 0 : kUnitTokensGemm * kYStride * 4;
-  return ring > tile ? ring : tile;
+  return (ring > tile ? ring : tile) + (gemm_scales_in_lds<kDown, kPl>() ? kScaleLdsBytes : 0);
 }
+static_assert(2 * gemm_lds_bytes<false, 1>() <= 160 * 1024 && 2 * gemm_lds_bytes<true, 1>() <= 160 * 1024 &&
+                  2 * gemm_lds_bytes<true, 2>() <= 160 * 1024,
+              "two workgroups per CU");
 
 // One GEMM unit x one 256-row tile.  gate_up: act = bfloat16 hidden state
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
@@ -121,18 +136,20 @@ __host__ __device__ constexpr int gemm_lds_bytes() {
 #ifndef KLC_GEMM_WAVES_PER_EU
 #define KLC_GEMM_WAVES_PER_EU 2
 #endif
-template <bool kDown>
+template <bool kDown, int kPl>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KLC_GEMM_WAVES_PER_EU))) void moe_gemm_kernel(
     const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
     float limit, int precision, int row_wgs, int units_per_xcd) {
-  constexpr int kPlanes = kDown ? 2 : 1;
-  constexpr int kRing = gemm_ring<kDown>();
-  constexpr int kStage = gemm_stage_bytes<kDown>();  // one step: 64 token rows x 256 bytes per plane
+  static_assert(kPl == 1 || (kDown && kPl == 2), "gate_up reads one plane, down one or two");
+  constexpr int kPlanes = kPl;
+  constexpr int kRing = gemm_ring<kDown, kPl>();
+  constexpr int kStage = gemm_stage_bytes<kDown, kPl>();  // one step: 64 token rows x 256 bytes per plane
   constexpr int kPlaneStage = kStage / kPlanes;
   constexpr int kLoadsPerStep = kRb + kBInstr * kPlanes;  // A: a chunk per row block; B: kBInstr per plane
+  constexpr bool kScLds = gemm_scales_in_lds<kDown, kPl>();
   static_assert((kRing - 2) * kLoadsPerStep <= 63, "the ring's outstanding loads fit the vmcnt field");
   extern __shared__ __align__(16) uint8_t stage[];    // kRing x kStage
 
@@ -203,6 +220,23 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     wtile[i] = tile_live[i] ? tile0 + i : 0;
     tile_off[i] = (uint32_t)wtile[i] * (uint32_t)groups * 1024u;
   }
+  // The epilogue's operands are loaded now, so that their latency passes
+  // under the step loop: bias of the lane's rows (4 consecutive per row
+  // block) and the pair ids of the token columns the lane writes.
+  u32x2_t bias4[kRb];
+#pragma unroll
+  for (int rb = 0; rb < kRb; ++rb) {
+    const int row0 = wtile[rb >> 2] * kTileRows + (rb & 3) * 16 + 4 * lq;
+    bias4[rb] = *reinterpret_cast<const u32x2_t*>(bias + (int64_t)e * rows + row0);
+  }
+  int pcol[kGemmCb];
+#pragma unroll
+  for (int i = 0; i < kGemmCb; ++i) {
+    // gate_up: the store loop's token c = tid / 16 + 16 i; down: column c = 16 i + lr
+    const int c = kDown ? 16 * i + lr : (tid >> 4) + 16 * i;
+    pcol[i] = pairs[pb + tc + min(c, nt - 1)];
+  }
+
   const int rec = (int)packed_scale_record(groups);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
   // With the step loop unrolled, the lane's whole scale record (one byte per
@@ -217,13 +251,29 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
   // select, where one array indexed by a run-time word would go to scratch)
   u32x2_t srec0[kRb], srec1[kRb], srec2[kRb];
 #pragma unroll
-  for (int rb = 0; rb < kRb; ++rb) {
+  for (int rb = 0; rb < kRb && !kScLds; ++rb) {
     const int row = wtile[rb >> 2] * kTileRows + (rb & 3) * 16 + lr;
     srec0[rb] = __builtin_amdgcn_raw_buffer_load_b64(wbuf, (uint32_t)packed_scale_word(groups, row, 0, lq), scale_base, 0);
     srec1[rb] = __builtin_amdgcn_raw_buffer_load_b64(
         wbuf, (uint32_t)packed_scale_word(groups, row, min(1, rec / 8 - 1), lq), scale_base, 0);
     srec2[rb] = __builtin_amdgcn_raw_buffer_load_b64(
         wbuf, (uint32_t)packed_scale_word(groups, row, min(2, rec / 8 - 1), lq), scale_base, 0);
+  }
+  // Scales in LDS: the wave copies its tile's records (rec / 4 KiB) with
+  // buffer-to-LDS loads issued ahead of the ring's first steps (no register
+  // round trip, so no wait); lane (lr, lq) of row block rb finds step s at
+  // sc_lane[rb * 512 + (s / 8) * 2048 + s % 8].
+  static_assert(kWaveTiles == 1, "one scale tile per wave");
+  uint8_t* sc_lds = stage + (gemm_lds_bytes<kDown, kPl>() - kScaleLdsBytes) + wave * kScaleTileLds;
+  const uint8_t* sc_lane = sc_lds + (lr * 4 + lq) * 8;
+  if constexpr (kScLds) {
+    // (inputs <= 3072 wide, checked by check_gemv_shapes: rec <= 24)
+    const uint32_t tile_scales = scale_base + (uint32_t)wtile[0] * (uint32_t)(kTileRows * 4 * rec);
+#pragma unroll
+    for (int i = 0; i < kScaleTileLds / 1024; ++i)
+      if (i < rec / 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wbuf, (__attribute__((address_space(3))) void*)(sc_lds + i * 1024), 16,
+                                                 (uint32_t)(lane * 16 + i * 1024), tile_scales, 0, 0);
   }
   auto a_load = [&](int s, u32x4_t (&a)[kRb]) {
     const bool ok = s < steps && 4 * s + lq < groups;
@@ -261,10 +311,22 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
   // pipeline; blocks past the unit's tokens are neither read nor multiplied).
   auto compute = [&](auto ncb_c, int s, int slot, const u32x4_t (&a_cur)[kRb], const uint32_t (&word)[kRb]) {
     constexpr int kNcb = decltype(ncb_c)::value;
-    const bool live = 4 * s + lq < groups;
     float scale[kRb];
+    if constexpr (kScLds) {
+      // E8M0 e -> 2^(e - 127) as float bits.  Past the last group of a
+      // step the record's padding is 0 (2^-127, finite) and the codes load
+      // as zeros; steps past the last one (the loop's padding) take scale 0.
+      const int soff = (s >> 3) * 2048 + (s & 7);
 #pragma unroll
-    for (int rb = 0; rb < kRb; ++rb) scale[rb] = cvt_scale_operand((word[rb] >> (8 * (s & 3))) & 0xffu, live);
+      for (int rb = 0; rb < kRb; ++rb) {
+        const uint32_t e8 = sc_lane[rb * 512 + soff];
+        scale[rb] = s < steps ? __uint_as_float(max(e8 << 23, 0x00400000u)) : 0.0f;
+      }
+    } else {
+      const bool live = 4 * s + lq < groups;
+#pragma unroll
+      for (int rb = 0; rb < kRb; ++rb) scale[rb] = cvt_scale_operand((word[rb] >> (8 * (s & 3))) & 0xffu, live);
+    }
     const uint8_t* base = stage + slot * kStage;
     // the B operands of a quarter are read one quarter ahead of their MFMAs
     bf16x8_t bq[2][kNcb][kPlanes];
@@ -289,7 +351,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
 #pragma unroll
           for (int rb = 0; rb < kRb; ++rb)
             acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], bq[j & 1][cb][pl], acc[rb][cb], 0, 0, 0);
-      if constexpr (kDown) {
+      if constexpr (kDown && kPlanes == 2) {
         // down (two planes): each quarter's B read, its kRb MFMAs and kRb VALU
         // instructions as one group, in order (330 against 345 us on the
         // 2048-token layer; the same grouping made gate_up spill and slower)
@@ -309,6 +371,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     a_load(i, a_ring[i]);
     b_dma(i, i);
   }
+
   // step s: wait for its own loads (the kRing - 2 later steps' stay in
   // flight), barrier (every wave's B rows of step s have landed and every
   // wave is done with step s - 1), issue step s + kRing - 1 into the slots
@@ -326,7 +389,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
 #pragma unroll
       for (int uu = 0; uu < kRing; ++uu) {
         const int s = s0 + uu;
-        if (uu == 0 || (4 % kRing != 0 && (s & 3) == 0)) scale_words(s, word);
+        if (!kScLds && (uu == 0 || (4 % kRing != 0 && (s & 3) == 0))) scale_words(s, word);
         ring_barrier<(kRing - 2) * kLoadsPerStep>();
         a_load(s + kRing - 1, a_ring[(uu + kRing - 1) % kRing]);
         b_dma(s + kRing - 1, (uu + kRing - 1) % kRing);
@@ -348,7 +411,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     // SwiGLU outputs of the workgroup (128 columns x up to 64 tokens) go
     // through LDS (the ring is idle now), so each token's 128 outputs leave
     // as 16-byte stores instead of 2-byte ones scattered over 16 rows
-    static_assert(kUnitTokensGemm * kYStride * 4 <= gemm_lds_bytes<false>(), "the output tile fits in the LDS");
+    static_assert(kUnitTokensGemm * kYStride * 4 <= gemm_lds_bytes<false, 1>(), "the output tile fits in the LDS");
     float* ytile = reinterpret_cast<float*>(stage);
     __syncthreads();  // every wave is done reading the ring
     if (wave_live) {
@@ -368,8 +431,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
               gate = round_bf16(gate);
               up = round_bf16(up);
             }
-            gate += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h]);
-            up += bf16_to_f32(bias[(int64_t)e * rows + row0 + 2 * h + 1]);
+            const uint32_t b2 = h ? bias4[rb].y : bias4[rb].x;  // rows row0 + 2h, + 1
+            gate += __uint_as_float(b2 << 16);
+            up += __uint_as_float(b2 & 0xffff0000u);
             ytile[c * kYStride + wave * (kRb * 8) + rb * 8 + 2 * lq + h] = swiglu(gate, up, limit);
           }
         }
@@ -380,11 +444,14 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     const int col0 = row_wg * (kGemmRows / 2);
     const int ncols = min(kGemmRows / 2, half - col0);
     constexpr int kPieces = kGemmRows / 16;  // 8-column pieces of a token's outputs
-    for (int i = tid; i < nt * kPieces; i += kGemmThreads) {  // (token, 8-column piece)
+    static_assert(kPieces == 16 && kUnitTokensGemm * kPieces == kGemmCb * kGemmThreads, "thread i covers token i / 16 + 16 it");
+#pragma unroll
+    for (int it = 0; it < kGemmCb; ++it) {  // (token, 8-column piece)
+      const int i = tid + it * kGemmThreads;
       const int c = i / kPieces;
       const int ch = (i % kPieces) * 8;
-      if (ch >= ncols) continue;
-      const int p = pairs[pb + tc + c];
+      if (c >= nt || ch >= ncols) continue;
+      const int p = pcol[it];
       float y[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) y[q] = ytile[c * kYStride + ch + q];
@@ -415,7 +482,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
       if (cb >= ncb) continue;
       const int c = cb * 16 + lr;
       if (c >= nt) continue;
-      const int p = pairs[pb + tc + c];
+      const int p = pcol[cb];
 #pragma unroll
       for (int rb = 0; rb < kRb; ++rb) {
         if (!tile_live[rb >> 2]) continue;
@@ -425,7 +492,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float t = precision == KLC_PRECISION_BF16 ? round_bf16(v4[v]) : v4[v];
-          o[v] = t + bf16_to_f32(bias[(int64_t)e * rows + row0 + v]);
+          const uint32_t b2 = (v & 2) ? bias4[rb].y : bias4[rb].x;
+          o[v] = t + __uint_as_float((v & 1) ? (b2 & 0xffff0000u) : (b2 << 16));
         }
         *reinterpret_cast<float4*>(out + (int64_t)p * rows + row0) = make_float4(o[0], o[1], o[2], o[3]);
       }
@@ -445,7 +513,7 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(hidden / 32);
-  moe_gemm_kernel<false><<<grid, kGemmThreads, gemm_lds_bytes<false>(), stream>>>(
+  moe_gemm_kernel<false, 1><<<grid, kGemmThreads, gemm_lds_bytes<false, 1>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
       0, nullptr, static_cast<uint16_t*>(gated_split), n_pairs * inter, gated_raw, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, groups, (int)k, limit, precision,
@@ -460,7 +528,10 @@ int launch_gemm_down(const void* const* w, const void* bias, const void* gated_s
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(inter / 32);
-  moe_gemm_kernel<true><<<grid, kGemmThreads, gemm_lds_bytes<true>(), stream>>>(
+  // bfloat16 precision: the input is the hi plane alone (its lo plane is zero)
+  auto kernel = precision == KLC_PRECISION_BF16 ? moe_gemm_kernel<true, 1> : moe_gemm_kernel<true, 2>;
+  const int lds = precision == KLC_PRECISION_BF16 ? gemm_lds_bytes<true, 1>() : gemm_lds_bytes<true, 2>();
+  kernel<<<grid, kGemmThreads, lds, stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),
       static_cast<const uint16_t*>(gated_split), n_pairs * inter, eo, nullptr, 0, nullptr, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)hidden, groups, 1, 0.0f, precision,

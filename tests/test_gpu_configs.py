@@ -63,14 +63,14 @@ def expert_fn(workload, layer):
     return fn
 
 
-def oracle(workload, layer, x, host):
+def oracle(workload, layer, x, host, precision="fp32"):
     return olayer.moe_layer_lazy(x, host["router_weight"], host["router_bias"], expert_fn(workload, layer),
-                                 host["gate_up_bias"], host["down_bias"], k=K, workers=WORKERS)
+                                 host["gate_up_bias"], host["down_bias"], k=K, precision=precision, workers=WORKERS)
 
 
-def check_layer_full(gpu, dev_w, x, ref, path):
+def check_layer_full(gpu, dev_w, x, ref, path, precision="fp32"):
     """Fused layer (routing, output) and the step-by-step path (expert outputs) against the oracle."""
-    layer = moe.MoELayer(dev_w, K, path=path)
+    layer = moe.MoELayer(dev_w, K, precision=precision, path=path)
     xt = bf16_tensor(x, gpu)
     ids = torch.empty((x.shape[0], K), dtype=torch.int32, device=gpu)
     wts = torch.empty((x.shape[0], K), dtype=torch.bfloat16, device=gpu)
@@ -80,10 +80,10 @@ def check_layer_full(gpu, dev_w, x, ref, path):
     assert np.array_equal(ids.cpu().numpy(), ref["ids"])
     assert np.array_equal(bf16_bits(wts), ref["weights"])
     n = x.shape[0]
-    assert_close(det["gated"].cpu().numpy().reshape(n, K, -1), ref["gated"], "SwiGLU output")
-    assert_close(det["expert_out"].cpu().numpy().reshape(n, K, -1), ref["expert_out"], "expert output")
+    assert_close(det["gated"].cpu().numpy().reshape(n, K, -1), ref["gated"], "SwiGLU output", precision)
+    assert_close(det["expert_out"].cpu().numpy().reshape(n, K, -1), ref["expert_out"], "expert output", precision)
     assert np.array_equal(bf16_bits(out), bf16_bits(det["out"]))
-    assert_final_close(bf16_bits(out), ref)
+    assert_final_close(bf16_bits(out), ref, precision)
 
 
 @pytest.mark.timeout(300)
@@ -121,17 +121,18 @@ def test_decode_layer_120b_full_size(gpu, n_tok):
 
 
 @pytest.mark.timeout(300)
-def test_prefill_2048_zipf_full_size(gpu):
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_prefill_2048_zipf_full_size(gpu, precision):
     workload, n_tok = 3, 2048  # the benchmark's prefill workload
     host = host_router(workload, 0)
     x = moe.synthetic_hidden(workload, n_tok, H)
     bias, _ = synth.zipf_router_bias(x, host["router_weight"], K, 1.1, 1000 * workload + 11)
     host["router_bias"] = bias
     dev_w = moe.MoELayerWeights.synthetic(workload, 0, H, I, E, gpu, bias)
-    ref = oracle(workload, 0, x, host)
+    ref = oracle(workload, 0, x, host, precision)
     counts = np.bincount(ref["ids"].ravel(), minlength=E)
     assert counts.max() >= 1500  # the hot expert spans many 64-token GEMM units
-    check_layer_full(gpu, dev_w, x, ref, "auto")
+    check_layer_full(gpu, dev_w, x, ref, "auto", precision)
 
 
 @pytest.mark.timeout(400)

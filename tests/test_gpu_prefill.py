@@ -19,7 +19,8 @@ from test_gpu_experts import assert_close, assert_final_close, build, oracle_lay
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("n_tok,k,n_exp,precision", [(256, 4, 16, "fp32"), (40, 4, 8, "fp32"), (130, 2, 4, "bf16")])
+@pytest.mark.parametrize("n_tok,k,n_exp,precision", [(256, 4, 16, "fp32"), (40, 4, 8, "fp32"), (130, 2, 4, "bf16"),
+                                                      (256, 4, 16, "bf16"), (75, 4, 8, "bf16")])
 def test_gemm_layer_matches_oracle(gpu, n_tok, k, n_exp, precision):
     host, dev_w, x = build(gpu, 400 + n_tok, 256, 128, n_exp, n_tok)
     layer = moe.MoELayer(dev_w, experts_per_token=k, precision=precision, path="gemm")
