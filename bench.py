@@ -300,12 +300,17 @@ def prefill_bench(torch, dev, n_tok: int, reps: int) -> dict:
         while time.perf_counter() < settle:
             layers[0].forward(x, out=out)
             torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        # per-kernel times from an event pass; the layer time from a pass without events (an event
+        # record between two kernels costs a few us)
         for r in range(reps):
             layers[r % 2].forward(x, out=out, ids=ids if r == 0 else None, events=evs[r])
         torch.cuda.synchronize()
-        dt = (time.perf_counter() - t0) / reps
         kern = np.array([[evs[r][i].elapsed_time(evs[r][i + 1]) for i in range(6)] for r in range(reps)]).mean(axis=0)
+        t0 = time.perf_counter()
+        for r in range(reps):
+            layers[r % 2].forward(x, out=out)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
         return dt, kern
 
     dt, kern = timed("bf16")
@@ -729,9 +734,10 @@ def _cpu_layer(workload: int, n_exp: int, router_bias=None):
     return torch_ref.Layer(t_bf16(rw), t_bf16(rb), t_bf16(gub), t_bf16(db), {}, TOPK), seed, t_bf16
 
 
-def _cpu_route_sample(layer, seed, xs, warmups: int) -> dict:
+def _cpu_route_sample(layer, seed, xs, warmups: int, precision: str = "fp32") -> dict:
     """Single-token route() calls over xs: cold (every call dequantizes its experts) and warm (the
-    dequantized matrices cached); medians over the calls after ``warmups``."""
+    dequantized matrices cached); medians over the calls after ``warmups``; ``precision`` is the
+    reference's matmul_precision."""
     import statistics
 
     import torch
@@ -747,14 +753,14 @@ def _cpu_route_sample(layer, seed, xs, warmups: int) -> dict:
         out = []
         for i, x in enumerate(xs):
             t0 = time.perf_counter()
-            layer.route(x, warm)
+            layer.route(x, warm, precision)
             if i >= warmups:
                 out.append(time.perf_counter() - t0)
         return out
 
     cold = timed(False)
     for x in xs:  # fill the warm store with the sample's experts
-        layer.route(x, True)
+        layer.route(x, True, precision)
     warm = timed(True)
     return {"warm_us_per_token": round(statistics.median(warm) * 1e6, 1),
             "cold_us_per_token": round(statistics.median(cold) * 1e6, 1),
@@ -848,9 +854,9 @@ def cpu_baseline(n_tokens: int, warmups: int = 2) -> dict:
     bias, _ = synth.zipf_router_bias(x_host, rw.reshape(EXPERTS, HIDDEN), TOPK, 1.1, 1000 * 3 + 11)
     layer, seed, _ = _cpu_layer(3, EXPERTS, bias)
     xs = [t_bf16(row) for row in x_host[:warmups + 6]]
-    c3 = _cpu_route_sample(layer, seed, xs, warmups)
+    c3 = _cpu_route_sample(layer, seed, xs, warmups, "bf16")
     configs["3"] = {"workload": "gpt-oss-120B-shape layer with Zipf(1.1) router bias, 2048 prefill tokens as "
-                                "single-token route() calls", **c3,
+                                "single-token route() calls, matmul_precision bf16", **c3,
                     "extrapolated": "2048 x the per-call medians",
                     "s_total_warm": round(2048 * c3["warm_us_per_token"] / 1e6, 2),
                     "s_total_cold": round(2048 * c3["cold_us_per_token"] / 1e6, 2),
@@ -1021,7 +1027,7 @@ def main() -> int:
         result["route_api"] = route_api_bench(torch, dev, layers[0].w, args.route_calls, args.precision)
         print(f"[bench] route(): {result['route_api']}", file=sys.stderr, flush=True)
     if args.prefill_tokens > 0:
-        result["prefill"] = prefill_bench(torch, dev, args.prefill_tokens, 10)
+        result["prefill"] = prefill_bench(torch, dev, args.prefill_tokens, 20)
         print(f"[bench] prefill: {result['prefill']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del layers

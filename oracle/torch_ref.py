@@ -12,7 +12,9 @@ restatement: the same torch operations, dtypes and rounding points as
 * ``_execute_mxfp4_experts`` and ``_apply_gate`` (:483-529) in the
   executor's default float32 matmul mode (streamed_transformer_executor.py:54):
   ``hidden.float() @ W.float() + b.float()``, interleaved gate/up clamped
-  SwiGLU, the down matmul, and the slot-order bf16 combine.
+  SwiGLU, the down matmul, and the slot-order bf16 combine; or in its
+  ``matmul_precision="bf16"`` mode (:502-511): bf16 operands, the matmul
+  results in bf16, then ``.float() + b.float()``.
 
 Two variants, as the reference's expert store behaves:
 
@@ -79,8 +81,11 @@ class Layer:
             self.cache[key] = m
         return m
 
-    def route(self, hidden: torch.Tensor, warm: bool) -> tuple[torch.Tensor, list[int]]:
-        """One 1-D token through router, top-k, experts and combine (bf16 hidden in, bf16 out)."""
+    def route(self, hidden: torch.Tensor, warm: bool, precision: str = "fp32") -> tuple[torch.Tensor, list[int]]:
+        """One 1-D token through router, top-k, experts and combine (bf16 hidden in, bf16 out);
+        ``precision`` is the reference's matmul_precision ("fp32" or "bf16")."""
+        if precision not in ("fp32", "bf16"):
+            raise ValueError(f"unknown matmul precision {precision!r}")
         logits = torch.nn.functional.linear(hidden, self.router_weight, self.router_bias)
         top = torch.topk(logits.float(), k=min(self.k, logits.numel()))
         experts = top.indices.tolist()
@@ -90,8 +95,14 @@ class Layer:
         for pos, e in enumerate(experts):
             gate_up = self.matrix(e, "gate_up_proj", warm)
             down = self.matrix(e, "down_proj", warm)
-            gu = hidden.float() @ gate_up.float() + self.gate_up_bias[e].float()
+            if precision == "bf16":  # streamed_moe_router.py:502-511
+                gu = (hidden.to(torch.bfloat16) @ gate_up.to(torch.bfloat16)).float() + self.gate_up_bias[e].float()
+            else:
+                gu = hidden.float() @ gate_up.float() + self.gate_up_bias[e].float()
             gated = swiglu(gu, self.limit)
-            out = gated @ down.float() + self.down_bias[e].float()
+            if precision == "bf16":
+                out = (gated.to(torch.bfloat16) @ down.to(torch.bfloat16)).float() + self.down_bias[e].float()
+            else:
+                out = gated @ down.float() + self.down_bias[e].float()
             output += out.to(hidden.dtype) * weights[pos]
         return output, experts
