@@ -40,6 +40,24 @@ def test_gemm_layer_matches_oracle(gpu, n_tok, k, n_exp, precision):
     assert_final_close(bf16_bits(det["out"]), ref, precision)
 
 
+@pytest.mark.parametrize("hidden,inter,precision", [(1024, 2048, "fp32"), (1024, 2048, "bf16"), (896, 960, "bf16"),
+                                                   (3072, 3072, "fp32")])
+def test_gemm_step_counts(gpu, hidden, inter, precision):
+    """Inputs whose 128-wide step counts leave the step loop's padding past
+    the scale records (8 and 16 steps), a 7-step and 7.5-step pair, and the
+    widest supported input (24 steps)."""
+    n_tok, k, n_exp = 72, 4, 8
+    host, dev_w, x = build(gpu, 430 + hidden + inter, hidden, inter, n_exp, n_tok)
+    layer = moe.MoELayer(dev_w, experts_per_token=k, precision=precision, path="gemm")
+    det = layer.forward_detailed(bf16_tensor(x, gpu))
+    torch.cuda.synchronize()
+    ref = oracle_layer(host, x, k, precision)
+    assert np.array_equal(det["ids"].cpu().numpy(), ref["ids"])
+    assert_close(det["gated"].cpu().numpy().reshape(n_tok, k, -1), ref["gated"], "SwiGLU output", precision)
+    assert_close(det["expert_out"].cpu().numpy().reshape(n_tok, k, -1), ref["expert_out"], "expert output", precision)
+    assert_final_close(bf16_bits(det["out"]), ref, precision)
+
+
 def test_gemm_units_span_hot_experts(gpu):
     """Router bias sends every token to the same 4 experts: 300 tokens per expert = 5 GEMM units each."""
     n_exp, n_tok = 8, 300
