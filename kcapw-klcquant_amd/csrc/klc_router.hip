@@ -212,6 +212,8 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_multi_kernel(const 
 // [gridDim.z][256] float64.  host_ids / host_weights (optional): copies of
 // the selection in a host record (SelectionOut); with one token, host_tag
 // (optional) then receives tag_value once they are in host memory.
+// kCls: router_expert_class(n_exp, k), or 0 for any expert count.
+template <int kCls>
 __global__ __launch_bounds__(256) void router_decode_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b, uint16_t* logits,
     int n_tok, int hidden, int n_exp, int k, int32_t* ids, float* values, uint16_t* weights,
@@ -298,8 +300,8 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     // workgroup barrier (the block form below pays one per step).
     if (wave != 0) return;
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp));
-    topk_softmax_row(rows, n_exp, k, 0, SelectionOut{ids, values, weights, tile_ids, host_ids, host_weights},
-                     tie_scratch);
+    topk_softmax_row<kCls>(rows, n_exp, k, 0, SelectionOut{ids, values, weights, tile_ids, host_ids, host_weights},
+                           tie_scratch);
     // the selection's host stores are fenced (SelectionOut::put, lanes < k of this wave): the tag follows
     if (host_tag != nullptr && lane == 0)
       __hip_atomic_store(host_tag, tag_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -312,8 +314,8 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     uint32_t* tie_scratch = reinterpret_cast<uint32_t*>(lds + decode_rows_bytes(n_exp) +
                                                         wave * topk_tie_scratch_bytes(n_exp));
     const SelectionOut sel{ids, values, weights, n_tt == 1 ? tile_ids : nullptr, host_ids, host_weights};
-    topk_softmax_block([&](int t) { return rows + t * n_exp; }, min(kRouterTile, n_tok - t0), n_exp, k, t0, sel,
-                       tie_scratch, tie_list);
+    topk_softmax_block<kCls>([&](int t) { return rows + t * n_exp; }, min(kRouterTile, n_tok - t0), n_exp, k, t0,
+                             sel, tie_scratch, tie_list);
   }
   if (units == nullptr) return;  // routing only: no dispatch
   if (n_tt > 1) {
@@ -399,7 +401,14 @@ int launch_router_decode(const void* x, const void* w, const void* b, void* logi
   size_t lds = 3 * 64 * 4 * sizeof(double);
   lds = std::max(lds, decode_rows_bytes((int)n_exp) + 4 * topk_tie_scratch_bytes((int)n_exp));
   lds = std::max(lds, dispatch_lds_bytes((int)(n_tok * k), (int)n_exp));
-  router_decode_kernel<<<grid, 256, lds, stream>>>(
+  auto kernel = router_decode_kernel<0>;
+  switch (router_expert_class(n_exp, k)) {
+    case 1: kernel = router_decode_kernel<1>; break;
+    case 2: kernel = router_decode_kernel<2>; break;
+    case 4: kernel = router_decode_kernel<4>; break;
+    default: break;
+  }
+  kernel<<<grid, 256, lds, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<const uint16_t*>(b),
       static_cast<uint16_t*>(logits), (int)n_tok, (int)hidden, (int)n_exp, (int)k, ids, values,
       static_cast<uint16_t*>(weights), offsets, sorted, active, n_active, units, counters, partials, host_ids,

@@ -509,12 +509,24 @@ __device__ __forceinline__ int wave_torch_topk_regs(const uint16_t* row, int n, 
   return my_id;
 }
 
+// Expert class of a router: 1, 2 or 4 when k <= 16, k * 64 > n_exp (torch's
+// introselect regime) and n_exp <= 64, 128 or 256 -- the rows then take
+// only the register and 4-tokens-per-wave forms of that size, so a kernel
+// instantiated for the class compiles no other form (the decode router's
+// code drops from ~38,700 to ~12,000 instructions, which shortens its
+// workgroups' start); 0 otherwise (every form compiled, chosen per call).
+__host__ __device__ constexpr int router_expert_class(int64_t n_exp, int64_t k) {
+  return (k > 16 || k * 64 <= n_exp || n_exp > 256) ? 0 : n_exp <= 64 ? 1 : n_exp <= 128 ? 2 : 4;
+}
+
 // torch's order for one tie row by the whole wave: the register form for
 // the rows the 4-tokens-per-wave kernel takes (n <= 256, k <= 16) in the
 // introselect regime, the LDS form otherwise.  Returns the expert of result
-// j in lane out_lane_base + j.
+// j in lane out_lane_base + j.  kCls: router_expert_class(n, k), or 0.
+template <int kCls = 0>
 __device__ __forceinline__ int wave_torch_topk_lanes(const uint16_t* row, int n, int k, uint32_t* scratch, int out_lane_base,
                                      int my_id) {
+  if constexpr (kCls > 0) return wave_torch_topk_regs<kCls>(row, n, k, scratch, out_lane_base, my_id);
   if (k * 64 > n && k <= 16) {
     if (n <= 64) return wave_torch_topk_regs<1>(row, n, k, scratch, out_lane_base, my_id);
     if (n <= 128) return wave_torch_topk_regs<2>(row, n, k, scratch, out_lane_base, my_id);
@@ -631,8 +643,8 @@ struct SelectionOut {
 // value.  If no two of those k + 1 values are equal, torch's order is that
 // descending order; otherwise the wave replays torch's order
 // (wave_torch_topk, tie_scratch: topk_tie_scratch_bytes(n_exp) bytes of
-// the wave's LDS).
-template <int kSlots>
+// the wave's LDS).  kCls: router_expert_class(n_exp, k), or 0.
+template <int kSlots, int kCls = 0>
 __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_exp, int k, int64_t t,
                                                    const SelectionOut& out, uint32_t* tie_scratch) {
   const int lane = threadIdx.x & 63;
@@ -660,14 +672,19 @@ __device__ __forceinline__ void topk_softmax_row_n(const uint16_t* row, int n_ex
     prev = value_key;
     if (lane == r) my_id = (int)(0xffffu - (best & 0xffffu));
   }
-  if (tie) my_id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, my_id);  // uniform: the same maxima
+  if (tie) my_id = wave_torch_topk_lanes<kCls>(row, n_exp, k, tie_scratch, 0, my_id);  // uniform: the same maxima
   const float my_val = bf16_to_f32(row[lane < k ? my_id : 0]);
   const uint32_t w = torch_softmax_bf16(my_val, k);
   if (lane < k) out.put(t * k + lane, my_id, my_val, w);
 }
 
+template <int kCls = 0>
 __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp, int k, int64_t t,
                                                  const SelectionOut& out, uint32_t* tie_scratch) {
+  if constexpr (kCls > 0) {
+    topk_softmax_row_n<kCls, kCls>(row, n_exp, k, t, out, tie_scratch);
+    return;
+  }
   const int slots = (n_exp + kWave - 1) / kWave;  // <= kTopkMaxPerLane (checked on the host)
   if (slots <= 1) topk_softmax_row_n<1>(row, n_exp, k, t, out, tie_scratch);
   else if (slots <= 2) topk_softmax_row_n<2>(row, n_exp, k, t, out, tie_scratch);
@@ -690,8 +707,9 @@ __device__ __forceinline__ void topk_softmax_row(const uint16_t* row, int n_exp,
 // is written at t_base + t.  n_exp <= 16 kSlots, k <= 16.  Every thread of
 // the workgroup must call this (it synchronises the workgroup).
 // tie_scratch: the calling wave's topk_tie_scratch_bytes(n_exp) bytes of
-// LDS; tie_list: 17 ints of LDS shared by the workgroup.
-template <int kSlots, typename RowFn>
+// LDS; tie_list: 17 ints of LDS shared by the workgroup.  kCls:
+// router_expert_class(n_exp, k), or 0.
+template <int kSlots, int kCls, typename RowFn>
 __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block, int n_exp, int k, int64_t t_base,
                                                         const SelectionOut& out, uint32_t* tie_scratch,
                                                         int* tie_list) {
@@ -743,7 +761,7 @@ __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block,
   for (int i = wave; i < n_ties; i += 4) {
     const int t = tie_list[i];
     const uint16_t* row = rows(t);
-    const int id = wave_torch_topk_lanes(row, n_exp, k, tie_scratch, 0, 0);
+    const int id = wave_torch_topk_lanes<kCls>(row, n_exp, k, tie_scratch, 0, 0);
     const float v = bf16_to_f32(row[lane < k ? id : 0]);
     const uint32_t w = torch_softmax_bf16(v, k);
     if (lane < k) out.put((t_base + t) * k + lane, id, v, w);
@@ -755,17 +773,22 @@ __device__ __forceinline__ void topk_softmax_block_quad(RowFn rows, int n_block,
 // row fits (n_exp <= 256, k <= 16), else token by token, 4 per wave.
 // out: where the selections go (SelectionOut).  tie_scratch: the wave's
 // topk_tie_scratch_bytes(n_exp) bytes of LDS; tie_list: 17 ints of LDS.
-// Called by every thread of the workgroup.
-template <typename RowFn>
+// Called by every thread of the workgroup.  kCls: router_expert_class(n_exp,
+// k), or 0.
+template <int kCls = 0, typename RowFn>
 __device__ __forceinline__ void topk_softmax_block(RowFn rows, int n_block, int n_exp, int k, int64_t t_base,
                                                    const SelectionOut& out, uint32_t* tie_scratch, int* tie_list) {
+  if constexpr (kCls > 0) {
+    topk_softmax_block_quad<4 * kCls, kCls>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
+    return;
+  }
   if (k <= 16 && n_exp <= 256) {
     if (n_exp <= 64)
-      topk_softmax_block_quad<4>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
+      topk_softmax_block_quad<4, 0>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
     else if (n_exp <= 128)
-      topk_softmax_block_quad<8>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
+      topk_softmax_block_quad<8, 0>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
     else
-      topk_softmax_block_quad<16>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
+      topk_softmax_block_quad<16, 0>(rows, n_block, n_exp, k, t_base, out, tie_scratch, tie_list);
   } else {
     const int wave = threadIdx.x >> 6;
     for (int q = 4 * wave; q < min(n_block, 4 * wave + 4); ++q)

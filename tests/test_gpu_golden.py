@@ -22,6 +22,7 @@ import pytest
 import torch
 
 from conftest import bf16_bits, bf16_tensor
+from klcquant_amd import _native as nat
 from klcquant_amd import moe, ops, synth
 from oracle import router as orr
 
@@ -96,27 +97,38 @@ def test_combine_matches_torch_bits(gpu, name):
     assert np.array_equal(crc, g["combine_crc"])
 
 
+@pytest.mark.parametrize("n_exp,k", [(128, 4), (32, 4), (200, 4), (256, 4), (128, 1), (64, 20)])
 @pytest.mark.parametrize("n_tok", [1, 16, 64, 128])
-def test_decode_router_replays_torch_order_on_ties(gpu, n_tok):
+def test_decode_router_replays_torch_order_on_ties(gpu, n_tok, n_exp, k):
     """Router rows repeated across experts make many logits equal, so most tokens take the
-    tie replay inside the one-launch decode router (one and several token tiles)."""
-    hidden, inter, n_exp = 256, 64, 128
+    tie replay inside the one-launch decode router (one and several token tiles).  The expert
+    counts cover each compiled form of the router: 32 / 128 / 200 experts with k = 4 (the
+    kernels built for <= 64, 128 and 256 experts in torch's introselect regime) and the
+    general kernel for k * 64 <= n (256 and 128 experts with k = 4 and 1) and k > 16 (20)."""
+    hidden, inter = 256, 64
     weights = moe.MoELayerWeights.synthetic(5, 0, hidden, inter, n_exp, gpu)
     base = synth.random_normal_bf16(501, 3 * hidden, 0.0, 0.02).reshape(3, hidden)
     rw = base[synth.random_ints(502, n_exp, 0, 2)]
     rb = np.zeros(n_exp, np.uint16)
     weights.router_weight.copy_(bf16_tensor(rw, gpu))
     weights.router_bias.copy_(bf16_tensor(rb, gpu))
-    layer = moe.MoELayer(weights, K)
     x = synth.random_normal_bf16(503 + n_tok, n_tok * hidden).reshape(n_tok, hidden)
-    ids = torch.empty((n_tok, K), dtype=torch.int32, device=gpu)
-    wts = torch.empty((n_tok, K), dtype=torch.bfloat16, device=gpu)
-    layer.forward(bf16_tensor(x, gpu), ids=ids, weights=wts)
+    xt = bf16_tensor(x, gpu)
+    ids = torch.empty((n_tok, k), dtype=torch.int32, device=gpu)
+    wts = torch.empty((n_tok, k), dtype=torch.bfloat16, device=gpu)
+    if k <= K:
+        # the layer's own launch: routing, then the dispatch of its experts
+        moe.MoELayer(weights, k).forward(xt, ids=ids, weights=wts)
+    else:
+        # routing only (klc_moe_select: the same one-launch router, no dispatch)
+        ws = torch.zeros(ops.workspace_bytes(n_tok, hidden, inter, n_exp, k), dtype=torch.uint8, device=gpu)
+        nat.call("klc_moe_select", ops._ptr(xt), ops._ptr(weights.router_weight), ops._ptr(weights.router_bias),
+                 n_tok, hidden, n_exp, k, ops._ptr(ws), ws.numel(), ops._ptr(ids), ops._ptr(wts), ops._stream(gpu))
     torch.cuda.synchronize()
     logits = orr.router_logits(x, rw, rb)
-    want_ids, want_vals = orr.topk(logits, K)
+    want_ids, want_vals = orr.topk(logits, k)
     assert np.array_equal(ids.cpu().numpy(), want_ids)
     assert np.array_equal(bf16_bits(wts), orr.softmax_weights(want_vals))
-    # nearly every token has equal values among its 5 largest logits
+    # nearly every token has equal values among its k + 1 largest logits
     srt = np.sort(synth.bf16_bits_to_f32(logits), axis=1)[:, ::-1]
-    assert np.count_nonzero(np.any(srt[:, :K] == srt[:, 1:K + 1], axis=1)) >= n_tok // 2
+    assert np.count_nonzero(np.any(srt[:, :k] == srt[:, 1:k + 1], axis=1)) >= n_tok // 2
