@@ -191,17 +191,33 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     src_row[i] = (int64_t)(kDown ? p : p / k_top) * in_dim;
     piece[i] = lr ^ (r & 15);
   }
+  // The lane's byte offset in its plane is a per-lane constant plus a uniform
+  // step offset of 256 s bytes (no address arithmetic per step), with one
+  // per-lane alternative for the last step, whose pieces past the input are
+  // clamped (every address is inside the plane: planes < 2 GiB, checked on
+  // the host).  (Two named resources: resource descriptors do not form arrays.)
+  uint32_t boff[kBInstr], boff_last[kBInstr];
+#pragma unroll
+  for (int i = 0; i < kBInstr; ++i) {
+    boff[i] = (uint32_t)((src_row[i] + piece[i] * 8) * 2);
+    const int kl = min((steps - 1) * 128 + piece[i] * 8, in_dim - 8);
+    boff_last[i] = (uint32_t)((src_row[i] + kl) * 2 - (int64_t)(steps - 1) * 256);
+  }
+  const __amdgpu_buffer_rsrc_t bbuf0 =
+      __builtin_amdgcn_make_buffer_rsrc((void*)act, (short)0, 0x7fffffff, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t bbuf1 =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(act + (kPlanes > 1 ? act_plane : 0)), (short)0, 0x7fffffff, kBufferWord3);
   auto b_dma = [&](int s, int slot) {
     const int sc = min(s, steps - 1);
+    const bool last = sc == steps - 1;
 #pragma unroll
     for (int pl = 0; pl < kPlanes; ++pl) {
 #pragma unroll
       for (int i = 0; i < kBInstr; ++i) {
-        const int kc = min(sc * 128 + piece[i] * 8, in_dim - 8);
-        const uint16_t* g = act + pl * act_plane + src_row[i] + kc;
-        __attribute__((address_space(3))) uint8_t* dst =
+        __attribute__((address_space(3))) void* dst =
             (__attribute__((address_space(3))) uint8_t*)stage + slot * kStage + pl * kPlaneStage + (kBRowsPerWave * wave + 4 * i) * 256;
-        __builtin_amdgcn_global_load_lds(g, dst, 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(pl == 0 ? bbuf0 : bbuf1, dst, 16, last ? boff_last[i] : boff[i],
+                                                 (uint32_t)sc * 256u, 0, 0);
       }
     }
   };
@@ -239,14 +255,11 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
 
   const int rec = (int)packed_scale_record(groups);
   const uint32_t scale_base = (uint32_t)packed_block_bytes(rows, groups);
-  // With the step loop unrolled, the lane's whole scale record (one byte per
-  // step, <= 24 steps) is loaded once up front: per-step scale words, one
-  // 4-byte load per lane at a 24-byte stride, cost more issue time in the
-  // texture unit than the weight chunks themselves.
-  // The lane's scales for all steps (one byte per step; inputs <= 3072 have
-  // <= 24 steps: three 8-byte words) are loaded once: per-step 4-byte scale
-  // loads cost more issue time in the texture unit than the weight chunks
-  // themselves.  (Words past a shorter record repeat its last word.)
+  // Two-plane down (scales in registers): the lane's scales for all steps
+  // (one byte per step; inputs <= 3072 have <= 24 steps: three 8-byte words)
+  // are loaded once: per-step 4-byte scale loads cost more issue time in the
+  // texture unit than the weight chunks themselves.  (Words past a shorter
+  // record repeat its last word.)
   // (three separately named arrays: the per-step choice among them is a
   // select, where one array indexed by a run-time word would go to scratch)
   u32x2_t srec0[kRb], srec1[kRb], srec2[kRb];
@@ -275,14 +288,17 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wbuf, (__attribute__((address_space(3))) void*)(sc_lds + i * 1024), 16,
                                                  (uint32_t)(lane * 16 + i * 1024), tile_scales, 0, 0);
   }
+  // The wave's 64-row tile as a buffer of its own (empty for a tile past the
+  // matrix): the groups past the input and the steps past the last fall
+  // outside it and load zeros (no traffic) by the range check alone, so a
+  // step's loads cost one address add.
+  const __amdgpu_buffer_rsrc_t abuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(wptr[e] + tile_off[0]), (short)0, tile_live[0] ? groups * 1024 : 0, kBufferWord3);
+  const uint32_t aoff = (uint32_t)(lq * 1024 + lr * 16);
   auto a_load = [&](int s, u32x4_t (&a)[kRb]) {
-    const bool ok = s < steps && 4 * s + lq < groups;
-    const int sc = min(s, steps - 1);
+    const uint32_t v = aoff + 4096u * (uint32_t)s;
 #pragma unroll
-    for (int rb = 0; rb < kRb; ++rb) {
-      const uint32_t v = ok && tile_live[rb >> 2] ? (uint32_t)(lq * 1024 + ((rb & 3) * 16 + lr) * 16) : kOutOfRange;
-      a[rb] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, v, tile_off[rb >> 2] + 4096u * sc, 0);
-    }
+    for (int rb = 0; rb < kRb; ++rb) a[rb] = __builtin_amdgcn_raw_buffer_load_b128(abuf, v, (uint32_t)(rb * 256), 0);
   };
 
   f32x4_t acc[kRb][kGemmCb];
@@ -292,9 +308,15 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     for (int cb = 0; cb < kGemmCb; ++cb) acc[rb][cb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // B read offsets: lane (lr, lq) reads piece 4 lq + j of row 16 cb + lr
-  int b_off[4];
+  // (kept as LDS pointers, one register each: every read of a step is then
+  // one of them plus a constant offset, with no address add per step)
+  typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
+  lds_cptr b_ptr[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) b_off[j] = lr * 256 + (((4 * lq + j) ^ lr) << 4);
+  for (int j = 0; j < 4; ++j) {
+    b_ptr[j] = (lds_cptr)stage + lr * 256 + (((4 * lq + j) ^ lr) << 4);
+    asm volatile("" : "+v"(b_ptr[j]));
+  }
 
   // The lane's scale dword holding step s (4 steps per dword, at most 6 dwords).
   auto scale_words = [&](int s, uint32_t (&word)[kRb]) {
@@ -315,19 +337,22 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
     if constexpr (kScLds) {
       // E8M0 e -> 2^(e - 127) as float bits.  Past the last group of a
       // step the record's padding is 0 (2^-127, finite) and the codes load
-      // as zeros; steps past the last one (the loop's padding) take scale 0.
-      const int soff = (s >> 3) * 2048 + (s & 7);
+      // as zeros.  Steps past the last one (the loop's padding) read the
+      // last step's scales: their codes are zeros, so they add nothing (a
+      // NaN scale there has already made the sum NaN).  No branch: the four
+      // reads go out together.
+      const int sc = min(s, steps - 1);
+      const int soff = (sc >> 3) * 2048 + (sc & 7);
+      uint32_t e8[kRb];
 #pragma unroll
-      for (int rb = 0; rb < kRb; ++rb) {
-        const uint32_t e8 = sc_lane[rb * 512 + soff];
-        scale[rb] = s < steps ? __uint_as_float(max(e8 << 23, 0x00400000u)) : 0.0f;
-      }
+      for (int rb = 0; rb < kRb; ++rb) e8[rb] = sc_lane[rb * 512 + soff];
+#pragma unroll
+      for (int rb = 0; rb < kRb; ++rb) scale[rb] = __uint_as_float(max(e8[rb] << 23, 0x00400000u));
     } else {
       const bool live = 4 * s + lq < groups;
 #pragma unroll
       for (int rb = 0; rb < kRb; ++rb) scale[rb] = cvt_scale_operand((word[rb] >> (8 * (s & 3))) & 0xffu, live);
     }
-    const uint8_t* base = stage + slot * kStage;
     // the B operands of a quarter are read one quarter ahead of their MFMAs
     bf16x8_t bq[2][kNcb][kPlanes];
     auto load_b = [&](int j, bf16x8_t (&dst)[kNcb][kPlanes]) {
@@ -335,7 +360,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
       for (int cb = 0; cb < kNcb; ++cb)
 #pragma unroll
         for (int pl = 0; pl < kPlanes; ++pl)
-          dst[cb][pl] = *reinterpret_cast<const bf16x8_t*>(base + pl * kPlaneStage + cb * 16 * 256 + b_off[j]);
+          dst[cb][pl] = *reinterpret_cast<__attribute__((address_space(3))) const bf16x8_t*>(
+              b_ptr[j] + slot * kStage + pl * kPlaneStage + cb * 16 * 256);
     };
     load_b(0, bq[0]);
 #pragma unroll
@@ -509,6 +535,8 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
                         float* gated_raw, hipStream_t stream) {
   const int64_t n_pairs = n_tok * k;
   const int64_t rows = 2 * inter;
+  KLC_REQUIRE(n_tok * hidden * 2 <= 0x7fffffff, KLC_ERR_UNSUPPORTED,
+              "moe_gemm_kernel<gate_up>: %lld tokens x %lld inputs exceed 2 GiB", (long long)n_tok, (long long)hidden);
   const int row_wgs = (int)((rows + kGemmRows - 1) / kGemmRows);
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
@@ -524,6 +552,9 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
 int launch_gemm_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs, int64_t n_exp,
                      const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
                      int precision, float* eo, hipStream_t stream) {
+  KLC_REQUIRE(n_pairs * inter * 2 <= 0x7fffffff, KLC_ERR_UNSUPPORTED,
+              "moe_gemm_kernel<down>: %lld pairs x %lld inputs exceed 2 GiB per plane", (long long)n_pairs,
+              (long long)inter);
   const int row_wgs = (int)((hidden + kGemmRows - 1) / kGemmRows);
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
