@@ -186,10 +186,7 @@ int klc_moe_pair_norms(const float* gated, const float* expert_out, int64_t n_pa
  * The same expert math as klc_moe_gate_up / klc_moe_down (same arguments,
  * outputs and tolerance) for batches that give experts many tokens: the
  * dispatch's 64-token GEMM units x 256-row tiles, weights decoded in
- * registers into v_mfma_f32_16x16x32_bf16, activations staged in LDS.
- * KLC_ERR_UNSUPPORTED when an activation plane (n_tokens x hidden, or
- * n_pairs x inter, bfloat16) exceeds 2 GiB; klc_moe_layer splits long
- * inputs well below that. */
+ * registers into v_mfma_f32_16x16x32_bf16, activations staged in LDS. */
 int klc_moe_gemm_gate_up(const void* const* w_gate_up, const void* bias, const void* x, int64_t n_tokens, int64_t k,
                          int64_t n_experts, const int32_t* offsets, const int32_t* sorted_pairs, const int32_t* units,
                          int64_t hidden, int64_t inter, float swiglu_limit, int precision, void* gated_split,

@@ -133,11 +133,10 @@ static_assert(2 * gemm_lds_bytes<false, 1>() <= 160 * 1024 && 2 * gemm_lds_bytes
 // [n_tok][in], one plane; writes the down input as hi/lo bfloat16 planes
 // [2][pairs][in_down] (and float32 SwiGLU output to out_raw if set).  down:
 // act = those planes (rows by pair); writes float32 expert outputs.
-#ifndef KLC_GEMM_WAVES_PER_EU
-#define KLC_GEMM_WAVES_PER_EU 2
-#endif
-template <bool kDown, int kPl>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KLC_GEMM_WAVES_PER_EU))) void moe_gemm_kernel(
+// kWide: activation planes past 2 GiB (rows addressed with 64-bit pointers
+// instead of a buffer's 32-bit offsets).
+template <bool kDown, int kPl, bool kWide>
+__device__ __forceinline__ void moe_gemm_body(
     const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
     int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
     float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
@@ -194,8 +193,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
   // The lane's byte offset in its plane is a per-lane constant plus a uniform
   // step offset of 256 s bytes (no address arithmetic per step), with one
   // per-lane alternative for the last step, whose pieces past the input are
-  // clamped (every address is inside the plane: planes < 2 GiB, checked on
-  // the host).  (Two named resources: resource descriptors do not form arrays.)
+  // clamped (every address is inside the plane: planes < 2 GiB; larger ones
+  // take the wide kernels).  (Two named resources: resource descriptors do not form arrays.)
   uint32_t boff[kBInstr], boff_last[kBInstr];
 #pragma unroll
   for (int i = 0; i < kBInstr; ++i) {
@@ -216,8 +215,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
       for (int i = 0; i < kBInstr; ++i) {
         __attribute__((address_space(3))) void* dst =
             (__attribute__((address_space(3))) uint8_t*)stage + slot * kStage + pl * kPlaneStage + (kBRowsPerWave * wave + 4 * i) * 256;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(pl == 0 ? bbuf0 : bbuf1, dst, 16, last ? boff_last[i] : boff[i],
-                                                 (uint32_t)sc * 256u, 0, 0);
+        if constexpr (kWide) {
+          const int kc = min(sc * 128 + piece[i] * 8, in_dim - 8);
+          __builtin_amdgcn_global_load_lds(act + pl * act_plane + src_row[i] + kc, dst, 16, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(pl == 0 ? bbuf0 : bbuf1, dst, 16, last ? boff_last[i] : boff[i],
+                                                   (uint32_t)sc * 256u, 0, 0);
+        }
       }
     }
   };
@@ -527,6 +531,31 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KL
   }
 }
 
+#ifndef KLC_GEMM_WAVES_PER_EU
+#define KLC_GEMM_WAVES_PER_EU 2
+#endif
+// The kernels: planes below 2 GiB (every layer call) and past it.
+template <bool kDown, int kPl>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KLC_GEMM_WAVES_PER_EU))) void moe_gemm_kernel(
+    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
+    int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
+    float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
+    const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
+    float limit, int precision, int row_wgs, int units_per_xcd) {
+  moe_gemm_body<kDown, kPl, false>(wptr, bias, act, act_plane, out, out_split, out_plane, out_raw, offsets, pairs,
+                                   units, n_units, rows, groups, k_top, limit, precision, row_wgs, units_per_xcd);
+}
+template <bool kDown, int kPl>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KLC_GEMM_WAVES_PER_EU))) void moe_gemm_wide_kernel(
+    const uint8_t* const* __restrict__ wptr, const uint16_t* __restrict__ bias, const uint16_t* __restrict__ act,
+    int64_t act_plane, float* __restrict__ out, uint16_t* __restrict__ out_split, int64_t out_plane,
+    float* __restrict__ out_raw, const int32_t* __restrict__ offsets, const int32_t* __restrict__ pairs,
+    const int32_t* __restrict__ units, const int32_t* __restrict__ n_units, int rows, int groups, int k_top,
+    float limit, int precision, int row_wgs, int units_per_xcd) {
+  moe_gemm_body<kDown, kPl, true>(wptr, bias, act, act_plane, out, out_split, out_plane, out_raw, offsets, pairs,
+                                  units, n_units, rows, groups, k_top, limit, precision, row_wgs, units_per_xcd);
+}
+
 }  // namespace
 
 int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, int64_t n_tok, int64_t k,
@@ -535,13 +564,13 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
                         float* gated_raw, hipStream_t stream) {
   const int64_t n_pairs = n_tok * k;
   const int64_t rows = 2 * inter;
-  KLC_REQUIRE(n_tok * hidden * 2 <= 0x7fffffff, KLC_ERR_UNSUPPORTED,
-              "moe_gemm_kernel<gate_up>: %lld tokens x %lld inputs exceed 2 GiB", (long long)n_tok, (long long)hidden);
   const int row_wgs = (int)((rows + kGemmRows - 1) / kGemmRows);
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(hidden / 32);
-  moe_gemm_kernel<false, 1><<<grid, kGemmThreads, gemm_lds_bytes<false, 1>(), stream>>>(
+  // activation planes past 2 GiB take the 64-bit-pointer form
+  auto kernel = n_tok * hidden * 2 > 0x7fffffff ? moe_gemm_wide_kernel<false, 1> : moe_gemm_kernel<false, 1>;
+  kernel<<<grid, kGemmThreads, gemm_lds_bytes<false, 1>(), stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(x),
       0, nullptr, static_cast<uint16_t*>(gated_split), n_pairs * inter, gated_raw, offsets, pairs,
       units + units_offset_gemm(n_pairs, n_exp), units + 2, (int)rows, groups, (int)k, limit, precision,
@@ -552,15 +581,15 @@ int launch_gemm_gate_up(const void* const* w, const void* bias, const void* x, i
 int launch_gemm_down(const void* const* w, const void* bias, const void* gated_split, int64_t n_pairs, int64_t n_exp,
                      const int32_t* offsets, const int32_t* pairs, const int32_t* units, int64_t hidden, int64_t inter,
                      int precision, float* eo, hipStream_t stream) {
-  KLC_REQUIRE(n_pairs * inter * 2 <= 0x7fffffff, KLC_ERR_UNSUPPORTED,
-              "moe_gemm_kernel<down>: %lld pairs x %lld inputs exceed 2 GiB per plane", (long long)n_pairs,
-              (long long)inter);
   const int row_wgs = (int)((hidden + kGemmRows - 1) / kGemmRows);
   const int per_xcd = (int)((units_capacity(n_pairs, n_exp, kUnitTokensGemm) + kXcds - 1) / kXcds);
   const dim3 grid((unsigned)(kXcds * per_xcd * row_wgs));
   const int groups = (int)(inter / 32);
   // bfloat16 precision: the input is the hi plane alone (its lo plane is zero)
-  auto kernel = precision == KLC_PRECISION_BF16 ? moe_gemm_kernel<true, 1> : moe_gemm_kernel<true, 2>;
+  // activation planes past 2 GiB take the 64-bit-pointer form
+  const bool wide = n_pairs * inter * 2 > 0x7fffffff;
+  auto kernel = precision == KLC_PRECISION_BF16 ? (wide ? moe_gemm_wide_kernel<true, 1> : moe_gemm_kernel<true, 1>)
+                                                : (wide ? moe_gemm_wide_kernel<true, 2> : moe_gemm_kernel<true, 2>);
   const int lds = precision == KLC_PRECISION_BF16 ? gemm_lds_bytes<true, 1>() : gemm_lds_bytes<true, 2>();
   kernel<<<grid, kGemmThreads, lds, stream>>>(
       reinterpret_cast<const uint8_t* const*>(w), static_cast<const uint16_t*>(bias),

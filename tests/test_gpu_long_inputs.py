@@ -109,3 +109,22 @@ def test_route_splits_past_layer_limit(gpu):
     assert route["experts"] == ids.cpu().tolist()
     assert route["weights"] == wts.float().cpu().tolist()
     assert len(route["expert_logs"]) == n and route["expert_logs"][-1][0]["expert"] == route["experts"][-1][0]
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_gemm_down_planes_past_2gib(gpu, precision):
+    """47,000 tokens at top-8 with a 2880-wide expert input: each of down's activation planes (pairs x 2880
+    bf16) passes 2 GiB, past what the GEMM's 32-bit buffer offsets reach, so the down GEMM takes its
+    64-bit-pointer form; the result equals two calls of half the rows (planes under 2 GiB), bit for bit."""
+    h, i, e, k, n = 256, 2880, 16, 8, 47000
+    assert n * k * i * 2 > 2**31 - 1 and (n // 2) * k * i * 2 < 2**31 - 1
+    dev_w = moe.MoELayerWeights.synthetic(74, 0, h, i, e, gpu)
+    layer = moe.MoELayer(dev_w, k, precision=precision, path="gemm")
+    x = bf16_tensor(moe.synthetic_hidden(74, n, h), gpu)
+    out = layer.forward(x)
+    cut = n // 2
+    out_a = layer.forward(x[:cut])
+    out_b = layer.forward(x[cut:])
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(out), np.concatenate([bf16_bits(out_a), bf16_bits(out_b)]))
