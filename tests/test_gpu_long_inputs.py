@@ -128,3 +128,33 @@ def test_gemm_down_planes_past_2gib(gpu, precision):
     out_b = layer.forward(x[cut:])
     torch.cuda.synchronize()
     assert np.array_equal(bf16_bits(out), np.concatenate([bf16_bits(out_a), bf16_bits(out_b)]))
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_gemm_gate_up_hidden_plane_past_2gib(gpu, precision):
+    """380,000 tokens of a 2880-wide hidden state (2.19 GB of bf16, one call of the grouped gate_up GEMM at
+    top-1, which has no token cap of its own): past the 32-bit buffer offsets, so gate_up takes its
+    64-bit-pointer form; every (token, slot) row equals the row of two calls on half the tokens each (planes
+    under 2 GiB, the buffer-offset form), bit for bit, in both down-input planes and the float32 SwiGLU
+    output."""
+    h, i, e, k, n = 2880, 64, 4, 1, 380_000
+    assert n * h * 2 > 2**31 - 1 and (n // 2) * h * 2 < 2**31 - 1 and n * k <= nat.DISPATCH_MAX_PAIRS
+    w = moe.MoELayerWeights.synthetic(75, 0, h, i, e, gpu)
+    gen = torch.Generator(device=gpu).manual_seed(75)
+    x = torch.randn((n, h), generator=gen, device=gpu).to(torch.bfloat16)
+    ids = torch.randint(0, e, (n, k), generator=gen, device=gpu, dtype=torch.int32)
+
+    def run(rows):
+        disp = ops.dispatch(ids[rows].contiguous(), e)
+        return ops.gate_up(w.gate_up_table, w.gate_up_bias, x[rows], k, disp, h, i, precision=precision,
+                           want_raw=True, gemm=True)
+
+    split, raw = run(slice(0, n))
+    cut = n // 2
+    split_a, raw_a = run(slice(0, cut))
+    split_b, raw_b = run(slice(cut, n))
+    torch.cuda.synchronize()
+    assert torch.equal(split.view(torch.int16), torch.cat([split_a, split_b], dim=1).view(torch.int16))
+    assert torch.equal(raw.view(torch.int32), torch.cat([raw_a, raw_b]).view(torch.int32))
+    assert bool((split[0].view(torch.int16) != 0).any())
