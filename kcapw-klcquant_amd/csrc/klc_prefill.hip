@@ -452,8 +452,7 @@ __device__ __forceinline__ void moe_gemm_body(
 #pragma unroll
         for (int rb = 0; rb < kRb; ++rb) {
           if (!tile_live[rb >> 2]) continue;
-          const int row0 = tile0 * kTileRows + rb * 16 + 4 * lq;
-          const f32x4_t v4 = acc[rb][cb];
+          const f32x4_t v4 = acc[rb][cb];  // rows rb * 16 + 4 lq .. + 3 of the tile
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             float gate = v4[2 * h], up = v4[2 * h + 1];
@@ -461,7 +460,7 @@ __device__ __forceinline__ void moe_gemm_body(
               gate = round_bf16(gate);
               up = round_bf16(up);
             }
-            const uint32_t b2 = h ? bias4[rb].y : bias4[rb].x;  // rows row0 + 2h, + 1
+            const uint32_t b2 = h ? bias4[rb].y : bias4[rb].x;  // rows 4 lq + 2h, + 1
             gate += __uint_as_float(b2 << 16);
             up += __uint_as_float(b2 & 0xffff0000u);
             ytile[c * kYStride + wave * (kRb * 8) + rb * 8 + 2 * lq + h] = swiglu(gate, up, limit);
