@@ -17,9 +17,10 @@
 // rounded to the cache's type and then to bfloat16 (o_proj's input type).
 //
 // Kernels per step: scores (workgroup = one KV head x 64 keys, its whole
-// query group), per-head max and sum, probabilities x values (workgroup =
-// one query head x 256 keys), and the sum of the splits; a window of at most
-// 256 keys takes the max, sum and context in the value workgroup itself.
+// query group), probabilities x values (workgroup = one query head x 256
+// keys, each taking its head's max and sum over all the scores first), and
+// the sum of the splits; a window of at most 256 keys (one split) writes the
+// context from the value workgroup itself.
 #include <math.h>
 
 #include "klc_common.h"
@@ -98,15 +99,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
   }
 }
 
-// per query head: m = max(scores, sink), l = sum exp(x - m) over [scores, sink];
-// each reduction is a wave shuffle tree plus one exchange of the 4 waves' values
-__global__ __launch_bounds__(kAttnThreads) void attn_stats_kernel(const float* __restrict__ scores,
-                                                                  const uint16_t* __restrict__ sinks, int count,
-                                                                  float* __restrict__ stats) {
+// Query head h's m = max(scores, sink) and l = sum exp(x - m) over [scores,
+// sink], l summed in float64 and rounded once; each reduction is a wave
+// shuffle tree plus one exchange of the 4 waves' values.  Every thread of
+// the workgroup calls it and gets both.
+__device__ __forceinline__ void head_stats(const float* __restrict__ s, int count, const uint16_t* __restrict__ sinks,
+                                           int h, float& m_out, float& l_out) {
   __shared__ float wm[kAttnThreads / kWave];
   __shared__ double wl[kAttnThreads / kWave];
-  const int h = blockIdx.x, lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const float* s = scores + (int64_t)h * count;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   float m = sinks != nullptr ? bf(sinks[h]) : -INFINITY;
   for (int i = threadIdx.x; i < count; i += kAttnThreads) m = fmaxf(m, s[i]);
   for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
@@ -120,21 +121,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_stats_kernel(const float* _
   for (int off = kWave / 2; off > 0; off >>= 1) l += __shfl_xor(l, off);
   if (lane == 0) wl[wave] = l;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (int w = 0; w < kAttnThreads / kWave; ++w) t += wl[w];
-    stats[2 * h] = m;
-    stats[2 * h + 1] = (float)t;
-  }
+  double t = 0.0;
+  for (int w = 0; w < kAttnThreads / kWave; ++w) t += wl[w];
+  m_out = m;
+  l_out = (float)t;
 }
 
 // partial[h][split][d] = sum over the split's keys of p * v, p rounded to the
-// cache type.  kWhole (count <= 256, one split): the workgroup also takes the
-// head's max and sum itself and writes the context, so the step needs
-// neither the stats nor the combine launch.
+// cache type.  Each workgroup first takes its head's max and sum over all
+// the scores (16 KB of L2 reads at 4,096 keys: cheaper than a launch of its
+// own).  kWhole (count <= 256, one split): the workgroup also writes the
+// context, so the step needs no combine launch.
 template <bool kWhole>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __restrict__ scores,
-                                                               const float* __restrict__ stats,
                                                                const uint16_t* __restrict__ sinks,
                                                                const uint16_t* __restrict__ v_cache,
                                                                float* __restrict__ partial,
@@ -146,30 +145,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __re
   const int h = blockIdx.x, split = blockIdx.y, g = nh / nkv, kvh = h / g;
   const int k0 = split * kPvKeys, nk = min(kPvKeys, count - k0);
   float m, l;
-  if constexpr (kWhole) {
-    __shared__ float wm[kAttnThreads / kWave];
-    __shared__ double wl[kAttnThreads / kWave];
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    const float x = (int)threadIdx.x < nk ? scores[(int64_t)h * count + threadIdx.x] : -INFINITY;
-    m = sinks != nullptr ? bf(sinks[h]) : -INFINITY;
-    m = fmaxf(m, x);
-    for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if (lane == 0) wm[wave] = m;
-    __syncthreads();
-    m = wm[0];
-    for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, wm[w]);
-    double e = (int)threadIdx.x < nk ? (double)expf(x - m) : 0.0;
-    if (threadIdx.x == 0 && sinks != nullptr) e += (double)expf(bf(sinks[h]) - m);
-    for (int off = kWave / 2; off > 0; off >>= 1) e += __shfl_xor(e, off);
-    if (lane == 0) wl[wave] = e;
-    __syncthreads();
-    double t = 0.0;
-    for (int w = 0; w < kAttnThreads / kWave; ++w) t += wl[w];
-    l = (float)t;
-  } else {
-    m = stats[2 * h];
-    l = stats[2 * h + 1];
-  }
+  head_stats(scores + (int64_t)h * count, count, sinks, h, m, l);
   for (int i = threadIdx.x; i < nk; i += kAttnThreads) p[i] = rkv(expf(scores[(int64_t)h * count + k0 + i] - m) / l, f16);
   __syncthreads();
   // thread (slice, four dims): slices of keys; each thread issues the 8-byte
@@ -266,7 +242,7 @@ extern "C" int klc_rope_append(const void* q, const void* k, const void* v, cons
 extern "C" int64_t klc_attn_workspace_bytes(int64_t n_heads, int64_t head_dim, int64_t count) {
   if (n_heads <= 0 || head_dim <= 0 || count <= 0)
     return set_error(KLC_ERR_ARGUMENT, "klc_attn_workspace_bytes: bad sizes");
-  return 4 * (n_heads * count + 2 * n_heads + n_heads * attn_splits(count) * head_dim);
+  return 4 * (n_heads * count + n_heads * attn_splits(count) * head_dim);
 }
 
 extern "C" int klc_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* sinks,
@@ -291,8 +267,7 @@ extern "C" int klc_attn_decode(const void* q, const void* k_cache, const void* v
   KLC_REQUIRE(workspace_bytes >= need, KLC_ERR_ARGUMENT, "klc_attn_decode: workspace of %lld bytes, need %lld",
               (long long)workspace_bytes, (long long)need);
   float* scores = static_cast<float*>(workspace);
-  float* stats = scores + n_heads * count;
-  float* partial = stats + 2 * n_heads;
+  float* partial = scores + n_heads * count;
   const int splits = (int)attn_splits(count);
   hipStream_t st = as_stream(stream);
   const uint16_t* qb = static_cast<const uint16_t*>(q);
@@ -306,13 +281,11 @@ extern "C" int klc_attn_decode(const void* q, const void* k_cache, const void* v
   uint16_t* ctx = static_cast<uint16_t*>(context);
   if (splits == 1) {  // a window of at most 256 keys: one workgroup per head does the rest
     attn_pv_kernel<true><<<dim3((unsigned)n_heads, 1u), kAttnThreads, 0, st>>>(
-        scores, stats, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
+        scores, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
     return check_launch("attn_pv_kernel");
   }
-  attn_stats_kernel<<<(unsigned)n_heads, kAttnThreads, 0, st>>>(scores, sk, (int)count, stats);
-  if ((rc = check_launch("attn_stats_kernel"))) return rc;
   attn_pv_kernel<false><<<dim3((unsigned)n_heads, (unsigned)splits), kAttnThreads, 0, st>>>(
-      scores, stats, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
+      scores, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
   if ((rc = check_launch("attn_pv_kernel"))) return rc;
   attn_combine_kernel<<<(unsigned)((n_heads * head_dim + kAttnThreads - 1) / kAttnThreads), kAttnThreads, 0, st>>>(
       partial, splits, (int)n_heads, (int)head_dim, static_cast<uint16_t*>(context), f16);
