@@ -78,21 +78,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     int64_t first, int count, int nh, int nkv, int d, float sqrt_d, bool f16) {
   __shared__ float qs[kMaxGroup][kMaxHeadDim];
   const int g = nh / nkv, kvh = blockIdx.x;
-  for (int i = threadIdx.x; i < g * d; i += blockDim.x) qs[i / d][i % d] = bf(q[(int64_t)(kvh * g + i / d) * d + i % d]);
-  __syncthreads();
   const int key = blockIdx.y * kScoreKeys + (threadIdx.x % kScoreKeys);
   const int part = threadIdx.x / kScoreKeys;  // 4 parts share the group's heads
-  if (key >= count) return;
-  const uint16_t* krow = k_cache + (((first + key) % cap) * nkv + kvh) * d;
+  const bool live = key < count;
+  // the key row goes into registers before the query staging, so its loads
+  // overlap the staging and its barrier
+  uint4 kr[kMaxHeadDim / 8] = {};
+  const uint16_t* krow = k_cache + (((first + (live ? key : 0)) % cap) * nkv + kvh) * d;
+#pragma unroll
+  for (int c = 0; c < kMaxHeadDim / 8; ++c)
+    if (live && c * 8 < d) kr[c] = *reinterpret_cast<const uint4*>(krow + c * 8);
+  for (int i = threadIdx.x; i < g * d; i += blockDim.x) qs[i / d][i % d] = bf(q[(int64_t)(kvh * g + i / d) * d + i % d]);
+  __syncthreads();
+  if (!live) return;
   for (int hh = part; hh < g; hh += kAttnThreads / kScoreKeys) {
     double acc = 0.0;
-    for (int c = 0; c < d; c += 8) {
-      const uint4 w = *reinterpret_cast<const uint4*>(krow + c);
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int c = 0; c < kMaxHeadDim / 8; ++c) {
+      if (c * 8 >= d) break;
+      // opaque per head: the conversions stay in the loop instead of being
+      // hoisted as 128 float64 values
+      uint32_t wd[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+      asm volatile("" : "+v"(wd[0]), "+v"(wd[1]), "+v"(wd[2]), "+v"(wd[3]));
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        acc = fma((double)kv_f((uint16_t)(wd[t] & 0xffffu), f16), (double)qs[hh][c + 2 * t], acc);
-        acc = fma((double)kv_f((uint16_t)(wd[t] >> 16), f16), (double)qs[hh][c + 2 * t + 1], acc);
+        acc = fma((double)kv_f((uint16_t)(wd[t] & 0xffffu), f16), (double)qs[hh][8 * c + 2 * t], acc);
+        acc = fma((double)kv_f((uint16_t)(wd[t] >> 16), f16), (double)qs[hh][8 * c + 2 * t + 1], acc);
       }
     }
     scores[(int64_t)(kvh * g + hh) * count + key] = (float)acc / sqrt_d;
@@ -108,15 +119,35 @@ __device__ __forceinline__ void head_stats(const float* __restrict__ s, int coun
   __shared__ float wm[kAttnThreads / kWave];
   __shared__ double wl[kAttnThreads / kWave];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  // both passes issue 8 loads before using them (a thread's scores are
+  // otherwise a chain of dependent L2 round trips); the sum keeps the
+  // thread's order i, i + 256, ...
+  constexpr int kAhead = 8;
   float m = sinks != nullptr ? bf(sinks[h]) : -INFINITY;
-  for (int i = threadIdx.x; i < count; i += kAttnThreads) m = fmaxf(m, s[i]);
+  int i = threadIdx.x;
+  for (; i + (kAhead - 1) * kAttnThreads < count; i += kAhead * kAttnThreads) {
+    float x[kAhead];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) x[j] = s[i + j * kAttnThreads];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) m = fmaxf(m, x[j]);
+  }
+  for (; i < count; i += kAttnThreads) m = fmaxf(m, s[i]);
   for (int off = kWave / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   if (lane == 0) wm[wave] = m;
   __syncthreads();
   m = wm[0];
   for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, wm[w]);
   double l = 0.0;
-  for (int i = threadIdx.x; i < count; i += kAttnThreads) l += (double)expf(s[i] - m);
+  i = threadIdx.x;
+  for (; i + (kAhead - 1) * kAttnThreads < count; i += kAhead * kAttnThreads) {
+    float x[kAhead];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) x[j] = s[i + j * kAttnThreads];
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) l += (double)expf(x[j] - m);
+  }
+  for (; i < count; i += kAttnThreads) l += (double)expf(s[i] - m);
   if (threadIdx.x == 0 && sinks != nullptr) l += (double)expf(bf(sinks[h]) - m);
   for (int off = kWave / 2; off > 0; off >>= 1) l += __shfl_xor(l, off);
   if (lane == 0) wl[wave] = l;
@@ -203,8 +234,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nh * d) return;
   const int h = i / d, e = i - h * d;
+  const float* src = partial + (int64_t)h * splits * d + e;
+  // 8 loads in flight, summed in split order
   double t = 0.0;
-  for (int s = 0; s < splits; ++s) t += partial[((int64_t)h * splits + s) * d + e];
+  int s = 0;
+  for (; s + 7 < splits; s += 8) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = src[(int64_t)(s + j) * d];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t += x[j];
+  }
+  for (; s < splits; ++s) t += src[(int64_t)s * d];
   context[i] = to_bf(rkv((float)t, f16));  // the cache type's einsum result, then bfloat16
 }
 
