@@ -19,8 +19,8 @@
 // Kernels per step: scores (workgroup = one KV head x 64 keys, its whole
 // query group), probabilities x values (workgroup = one query head x 256
 // keys, each taking its head's max and sum over all the scores first), and
-// the sum of the splits; a window of at most 256 keys (one split) writes the
-// context from the value workgroup itself.
+// the sum of the splits; a window of at most 256 keys (one split) runs as
+// one launch, scores to context, one workgroup per query head.
 #include <math.h>
 
 #include "klc_common.h"
@@ -158,26 +158,25 @@ __device__ __forceinline__ void head_stats(const float* __restrict__ s, int coun
   l_out = (float)t;
 }
 
-// partial[h][split][d] = sum over the split's keys of p * v, p rounded to the
-// cache type.  Each workgroup first takes its head's max and sum over all
-// the scores (16 KB of L2 reads at 4,096 keys: cheaper than a launch of its
-// own).  kWhole (count <= 256, one split): the workgroup also writes the
-// context, so the step needs no combine launch.
+// The body of a value workgroup: partial[h][split][d] = sum over the
+// split's keys of p * v, p rounded to the cache type, for query head
+// h = blockIdx.x whose `count` scores s_head holds (global memory or LDS).
+// The workgroup first takes its head's max and sum over all the scores
+// (16 KB of L2 reads at 4,096 keys: cheaper than a launch of its own).
+// kWhole (count <= 256, one split): it also writes the context, so the step
+// needs no combine launch.
 template <bool kWhole>
-__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __restrict__ scores,
-                                                               const uint16_t* __restrict__ sinks,
-                                                               const uint16_t* __restrict__ v_cache,
-                                                               float* __restrict__ partial,
-                                                               uint16_t* __restrict__ context, int64_t cap,
-                                                               int64_t first, int count, int nh, int nkv, int d,
-                                                               bool f16) {
+__device__ __forceinline__ void pv_body(const float* __restrict__ s_head, const uint16_t* __restrict__ sinks,
+                                        const uint16_t* __restrict__ v_cache, float* __restrict__ partial,
+                                        uint16_t* __restrict__ context, int64_t cap, int64_t first, int count, int nh,
+                                        int nkv, int d, bool f16) {
   __shared__ float p[kPvKeys];
   __shared__ float acc_s[kAttnThreads / 32][kMaxHeadDim];
   const int h = blockIdx.x, split = blockIdx.y, g = nh / nkv, kvh = h / g;
   const int k0 = split * kPvKeys, nk = min(kPvKeys, count - k0);
   float m, l;
-  head_stats(scores + (int64_t)h * count, count, sinks, h, m, l);
-  for (int i = threadIdx.x; i < nk; i += kAttnThreads) p[i] = rkv(expf(scores[(int64_t)h * count + k0 + i] - m) / l, f16);
+  head_stats(s_head, count, sinks, h, m, l);
+  for (int i = threadIdx.x; i < nk; i += kAttnThreads) p[i] = rkv(expf(s_head[k0 + i] - m) / l, f16);
   __syncthreads();
   // thread (slice, four dims): slices of keys; each thread issues the 8-byte
   // loads of four keys before their multiply-adds, so L2 round trips overlap
@@ -225,6 +224,55 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __re
       context[(int64_t)h * d + threadIdx.x] = to_bf(rkv(t, f16));
     }
   }
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __restrict__ scores,
+                                                               const uint16_t* __restrict__ sinks,
+                                                               const uint16_t* __restrict__ v_cache,
+                                                               float* __restrict__ partial,
+                                                               uint16_t* __restrict__ context, int64_t cap,
+                                                               int64_t first, int count, int nh, int nkv, int d,
+                                                               bool f16) {
+  pv_body<false>(scores + (int64_t)blockIdx.x * count, sinks, v_cache, partial, context, cap, first, count, nh, nkv,
+                 d, f16);
+}
+
+// A window of at most 256 keys in one launch: workgroup = query head
+// blockIdx.x.  Its scores (the same float64 dot products as
+// attn_scores_kernel, one key per thread) go to LDS, then the value body
+// takes the max, the sum and the context.
+__global__ __launch_bounds__(kAttnThreads) void attn_window_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ sinks,
+    const uint16_t* __restrict__ v_cache, float* __restrict__ partial, uint16_t* __restrict__ context, int64_t cap,
+    int64_t first, int count, int nh, int nkv, int d, float sqrt_d, bool f16) {
+  __shared__ float qs[kMaxHeadDim];
+  __shared__ float sc[kPvKeys];
+  const int h = blockIdx.x, kvh = h / (nh / nkv);
+  const int key = threadIdx.x;
+  const bool live = key < count;
+  uint4 kr[kMaxHeadDim / 8] = {};
+  const uint16_t* krow = k_cache + (((first + (live ? key : 0)) % cap) * nkv + kvh) * d;
+#pragma unroll
+  for (int c = 0; c < kMaxHeadDim / 8; ++c)
+    if (live && c * 8 < d) kr[c] = *reinterpret_cast<const uint4*>(krow + c * 8);
+  for (int i = threadIdx.x; i < d; i += blockDim.x) qs[i] = bf(q[(int64_t)h * d + i]);
+  __syncthreads();
+  if (live) {
+    double acc = 0.0;
+#pragma unroll
+    for (int c = 0; c < kMaxHeadDim / 8; ++c) {
+      if (c * 8 >= d) break;
+      const uint32_t wd[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc = fma((double)kv_f((uint16_t)(wd[t] & 0xffffu), f16), (double)qs[8 * c + 2 * t], acc);
+        acc = fma((double)kv_f((uint16_t)(wd[t] >> 16), f16), (double)qs[8 * c + 2 * t + 1], acc);
+      }
+    }
+    sc[key] = (float)acc / sqrt_d;
+  }
+  __syncthreads();
+  pv_body<true>(sc, sinks, v_cache, partial, context, cap, first, count, nh, nkv, d, f16);
 }
 
 // context[h][d] = bf16(sum over splits of partial[h][split][d])
@@ -314,18 +362,20 @@ extern "C" int klc_attn_decode(const void* q, const void* k_cache, const void* v
   const uint16_t* qb = static_cast<const uint16_t*>(q);
   const uint16_t* kb = static_cast<const uint16_t*>(k_cache);
   const uint16_t* vb = static_cast<const uint16_t*>(v_cache);
-  attn_scores_kernel<<<dim3((unsigned)n_kv, (unsigned)((count + kScoreKeys - 1) / kScoreKeys)), kAttnThreads, 0, st>>>(
-      qb, kb, scores, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, sqrtf((float)head_dim), f16);
-  int rc = check_launch("attn_scores_kernel");
-  if (rc) return rc;
   const uint16_t* sk = static_cast<const uint16_t*>(sinks);
   uint16_t* ctx = static_cast<uint16_t*>(context);
-  if (splits == 1) {  // a window of at most 256 keys: one workgroup per head does the rest
-    attn_pv_kernel<true><<<dim3((unsigned)n_heads, 1u), kAttnThreads, 0, st>>>(
-        scores, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
-    return check_launch("attn_pv_kernel");
+  const float sqrt_d = sqrtf((float)head_dim);
+  if (splits == 1) {  // a window of at most 256 keys: one launch, one workgroup per query head
+    static_assert(kPvKeys == kAttnThreads, "one key per thread");
+    attn_window_kernel<<<(unsigned)n_heads, kAttnThreads, 0, st>>>(
+        qb, kb, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, sqrt_d, f16);
+    return check_launch("attn_window_kernel");
   }
-  attn_pv_kernel<false><<<dim3((unsigned)n_heads, (unsigned)splits), kAttnThreads, 0, st>>>(
+  attn_scores_kernel<<<dim3((unsigned)n_kv, (unsigned)((count + kScoreKeys - 1) / kScoreKeys)), kAttnThreads, 0, st>>>(
+      qb, kb, scores, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, sqrt_d, f16);
+  int rc = check_launch("attn_scores_kernel");
+  if (rc) return rc;
+  attn_pv_kernel<<<dim3((unsigned)n_heads, (unsigned)splits), kAttnThreads, 0, st>>>(
       scores, sk, vb, partial, ctx, cap, first, (int)count, (int)n_heads, (int)n_kv, (int)head_dim, f16);
   if ((rc = check_launch("attn_pv_kernel"))) return rc;
   attn_combine_kernel<<<(unsigned)((n_heads * head_dim + kAttnThreads - 1) / kAttnThreads), kAttnThreads, 0, st>>>(
